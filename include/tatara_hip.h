@@ -1,0 +1,216 @@
+/*
+ * tatara_hip.h - C ABI of the MI355X (gfx950) training backend for tatara's
+ * GPU hot path (one training step: sparse FT gather, LayerStack dense layers
+ * and loss, FT backward, optimizer).
+ *
+ * The ABI replaces the reference's device backend below its step API:
+ *   - the trainer calls re-export `trait TrainerBackend`
+ *     (crates/nnue-train/src/trainer.rs:273-375) as implemented by GpuTrainer
+ *     (bins/nnue_train/src/trainer_layerstack.rs:1885-2010, via the macro at
+ *     bins/nnue_train/src/trainer_common.rs:276-411);
+ *   - the runtime calls replace the device-runtime surface of
+ *     crates/gpu-runtime/src/lib.rs:50-126 / native_backend.rs:17-300
+ *     (DeviceBuffer::from_host / zeroed / to_host_vec, memset, streams) and
+ *     the driver FFI of crates/cuda-native-runtime/src/runtime.rs:16-78;
+ *   - the op calls are the hot kernels of
+ *     crates/cuda-native-runtime/kernels/native_kernels.cu, one entry point
+ *     per reference kernel family, for kernel-level parity checks.
+ *
+ * Conventions: every function returns int32 status (0 = ok, <0 = error; see
+ * TATARA_* codes); tatara_last_error() returns the thread's last message
+ * ("HIP error {code}: {name}: {msg} [{call}]").  Out-of-memory is reported as
+ * TATARA_ERR_OOM so callers can classify it (native_backend.rs:294-300).
+ * Device pointers are plain void* from tatara_malloc.  Nothing in this header
+ * uses a torch or HIP type.
+ */
+#ifndef TATARA_HIP_H
+#define TATARA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define TATARA_API __attribute__((visibility("default")))
+#else
+#define TATARA_API
+#endif
+
+#define TATARA_OK 0
+#define TATARA_ERR_HIP (-1)
+#define TATARA_ERR_OOM (-2)
+#define TATARA_ERR_INVALID (-3)
+#define TATARA_ERR_STATE (-4)
+
+/* ------------------------------------------------------------------------ */
+/* Runtime (crates/gpu-runtime/src/lib.rs:50-126, :190-400)                 */
+/* ------------------------------------------------------------------------ */
+
+/* Thread-local message of the last failing call (never NULL). */
+TATARA_API const char* tatara_last_error(void);
+/* Library version string. */
+TATARA_API const char* tatara_version(void);
+/* Number of visible GPUs (CudaContext::new ordinal range). */
+TATARA_API int32_t tatara_device_count(int32_t* count);
+/* Selects the device for subsequent calls on this thread. */
+TATARA_API int32_t tatara_set_device(int32_t device);
+/* Device name and compute-unit count (DeviceOccupancy::query). */
+TATARA_API int32_t tatara_device_info(int32_t device, char* name, int32_t name_len, int32_t* cu_count);
+/* DeviceBuffer::zeroed / from_host / to_host_vec / memset_d8_async. */
+TATARA_API int32_t tatara_malloc(void** ptr, uint64_t bytes);
+TATARA_API int32_t tatara_free(void* ptr);
+TATARA_API int32_t tatara_memcpy_htod(void* dst, const void* src, uint64_t bytes);
+TATARA_API int32_t tatara_memcpy_dtoh(void* dst, const void* src, uint64_t bytes);
+TATARA_API int32_t tatara_memset(void* dst, int32_t byte, uint64_t bytes);
+/* Waits for all work on the device (CudaStream::synchronize). */
+TATARA_API int32_t tatara_synchronize(void);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel-level ops (device pointers, default stream, synchronous errors)   */
+/* ------------------------------------------------------------------------ */
+
+/* sparse_ft_forward (native_kernels.cu:162-202; CPU ref
+ * crates/gpu-kernels/src/sparse/sparse_ft_forward.rs:100-122):
+ * out[b][r] = sum_{n<nnz[b]} W[idx[b][n]][r] for valid idx, in n order. */
+TATARA_API int32_t tatara_op_sparse_ft_forward(const float* weight, const int32_t* indices,
+                                    const int32_t* nnz, float* out, uint32_t batch,
+                                    uint32_t rows, uint32_t cols, uint32_t max_active);
+/* sparse_ft_forward x2 + ft_post_perspective_fwd (native_kernels.cu:1499-1527):
+ * raw sums of both perspectives and the pairwise CReLU product `combined`. */
+TATARA_API int32_t tatara_op_ft_forward_pairwise(const float* weight, const int32_t* stm_idx,
+                                      const int32_t* nstm_idx, const int32_t* nnz,
+                                      const float* bias, float* stm_out, float* nstm_out,
+                                      float* combined, uint32_t batch, uint32_t ft_out,
+                                      uint32_t cols, uint32_t max_active, uint32_t piece_inputs,
+                                      float scale);
+/* FT weight gradient of both perspectives (the inverse-index pipeline of
+ * trainer_layerstack.rs:3723-3936; CPU ref sparse_ft_backward.rs:247-267,
+ * stm then nstm): grad[f][c] = sum of dft rows that index f, summed in
+ * (perspective, position) order.  dft is [2][batch][ft_out].  Overwrites
+ * grad rows [0, cols).  Deterministic. */
+TATARA_API int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
+                                 const int32_t* nstm_idx, const int32_t* nnz, float* grad,
+                                 uint32_t batch, uint32_t ft_out, uint32_t cols,
+                                 uint32_t max_active);
+/* ft_fold_virtual / ft_reduce_virtual_grad, Base mode (native_kernels.cu:204-406). */
+TATARA_API int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,
+                                  uint32_t ft_out, uint32_t piece_inputs);
+TATARA_API int32_t tatara_op_ft_reduce_virtual_grad(float* grad, uint32_t ft_in, uint32_t ft_out,
+                                         uint32_t piece_inputs);
+/* radam_step (native_kernels.cu:1291-1327) and ranger_lookahead_lerp (:1842). */
+TATARA_API int32_t tatara_op_radam_step(float* weights, float* m, float* v, float* grad, float lr,
+                             float step_size, int32_t denom, float decay, float beta1,
+                             float beta2, float eps, float min_w, float max_w, uint64_t n);
+TATARA_API int32_t tatara_op_ranger_lookahead_lerp(float* weights, float* slow, float alpha, uint64_t n);
+/* Host pre-compute of RAdam (crates/gpu-kernels/src/pointwise/radam_step.rs:75-97). */
+TATARA_API int32_t tatara_radam_step_size_denom(uint64_t step, float beta1, float beta2,
+                                     float n_sma_threshold, float* step_size, int32_t* denom);
+
+/* ------------------------------------------------------------------------ */
+/* Trainer (trait TrainerBackend, crates/nnue-train/src/trainer.rs:273-375)  */
+/* ------------------------------------------------------------------------ */
+
+typedef struct TataraTrainer TataraTrainer;
+
+#define TATARA_ARCH_LAYERSTACK 0
+#define TATARA_ARCH_SIMPLE 1
+
+#define TATARA_OPT_RANGER 0
+#define TATARA_OPT_RADAM 1
+#define TATARA_OPT_ADAMW 2
+
+/* GpuTrainer::new arguments (trainer_layerstack.rs:781-1064) and the feature
+ * set shape (crates/shogi-features/src/feature_set.rs:103-185). */
+typedef struct TataraTrainerConfig {
+    int32_t arch;          /* TATARA_ARCH_* */
+    int32_t device;
+    int32_t max_batch;     /* workspace capacity in positions (multiple of 16) */
+    int32_t ft_in;         /* base FT input rows of the feature set */
+    int32_t max_active;    /* active-feature slots per perspective (<= 64) */
+    int32_t piece_inputs;  /* factorizer piece inputs; 0 = factorizer off */
+    int32_t ft_out;        /* --ft-out */
+    int32_t l1_out;        /* --l1 */
+    int32_t l2_out;        /* --l2 */
+    int32_t num_buckets;   /* --num-buckets (LayerStack) */
+    int32_t optimizer;     /* TATARA_OPT_* */
+    float ft_weight_decay, dense_weight_decay, bias_weight_decay;
+    float ft_lr_mult, dense_lr_mult, bias_lr_mult;
+    int32_t keep_grads;    /* debug: keep every gradient after the step */
+} TataraTrainerConfig;
+
+/* LossKind (crates/nnue-train/src/trainer.rs:89-135). */
+typedef struct TataraLoss {
+    int32_t kind;  /* 0 Sigmoid{scale}, 1 Wrm{...} */
+    float scale;
+    float nnue2score, in_scaling, in_offset, target_offset, target_scaling;
+    float pow_exp, qp_asymmetry, weight_boost_w1, weight_boost_w2;
+} TataraLoss;
+
+/* BatchData (bins/nnue_train/src/trainer_common.rs:142-153).  Index rows are
+ * [n_pos][max_active], -1 padding; valid slots are [0, nnz[b]).  With
+ * on_device = 0 the arrays are host memory and are copied before the call
+ * returns; with on_device = 1 they are device pointers (tatara_malloc) that
+ * must stay valid until the next train_step/validate_step/flush returns. */
+typedef struct TataraBatch {
+    int32_t n_pos;
+    int32_t max_active;
+    const int32_t* stm_indices;
+    const int32_t* nstm_indices;
+    const int32_t* nnz;
+    const int32_t* bucket_idx; /* LayerStack: bucket per position */
+    const float* score;
+    const float* wdl;
+    int32_t on_device;
+} TataraBatch;
+
+/* GpuTrainer::new with LayerStackInit::default_uniform / SimpleInit (init.rs:252-310). */
+TATARA_API int32_t tatara_trainer_create(const TataraTrainerConfig* config, TataraTrainer** out);
+/* Drop for GpuTrainer: synchronises, then frees. */
+TATARA_API int32_t tatara_trainer_destroy(TataraTrainer* trainer);
+/* TrainerBackend::train_step: one forward+backward+optimizer step.  Returns in
+ * *lagged_loss the sum of squared errors of the PREVIOUS step (0.0 on the
+ * first), as AsyncLossRing does (trainer_common.rs:909-1035). */
+TATARA_API int32_t tatara_trainer_train_step(TataraTrainer* trainer, const TataraBatch* batch, float lr,
+                                  float wdl_lambda, const TataraLoss* loss, double* lagged_loss);
+/* TrainerBackend::flush_pending_loss. */
+TATARA_API int32_t tatara_trainer_flush_pending_loss(TataraTrainer* trainer, double* loss);
+/* TrainerBackend::validate_step: forward + loss only; net_output may be NULL. */
+TATARA_API int32_t tatara_trainer_validate_step(TataraTrainer* trainer, const TataraBatch* batch,
+                                     float wdl_lambda, const TataraLoss* loss, double* sum_sq_err,
+                                     float* net_output);
+/* Number of optimizer steps taken. */
+TATARA_API int32_t tatara_trainer_step_count(TataraTrainer* trainer, uint64_t* steps);
+/* Parameter groups by reference name ("ft_w", "ft_b", "l1_w", "l1_b",
+ * "l1_shared_weight", "l1_shared_bias", "l2_w", "l2_b", "l3_w", "l3_b");
+ * which: 0 weight, 1 m, 2 v, 3 slow, 4 grad.  n is the element count. */
+TATARA_API int32_t tatara_trainer_tensor_size(TataraTrainer* trainer, const char* name, uint64_t* n);
+TATARA_API int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int32_t which,
+                                  float* host, uint64_t n);
+TATARA_API int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int32_t which,
+                                  const float* host, uint64_t n);
+/* Activations of the last step, for parity checks: "ft_stm_out", "ft_nstm_out",
+ * "combined", "net_output", "dft_stm", "dft_nstm".  n = elements to copy. */
+TATARA_API int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const char* name, float* host,
+                                      uint64_t n);
+/* Phase timing (the NNUE_TRAIN_STEP_PROFILE breakdown, trainer_layerstack.rs:
+ * 1885-1921, measured with HIP events on the trainer's stream instead of host
+ * syncs).  While enabled, each step records events between its phases:
+ *   0 prep (sorts)  1 FT gather + post  2 dense forward + loss
+ *   3 dense backward (L1 weight grad, L1 input + FT post grad)
+ *   4 FT backward + optimizer + fold  5 dense optimizer
+ * phase_times sums the elapsed milliseconds of every phase over the steps
+ * run since profiling was enabled (it synchronises). */
+TATARA_API int32_t tatara_trainer_set_profiling(TataraTrainer* trainer, int32_t enable);
+TATARA_API int32_t tatara_trainer_phase_times(TataraTrainer* trainer, double* ms, int32_t n_phases,
+                                   uint64_t* steps);
+/* Rebuilds the forward weight table (factorizer fold) after set_tensor of
+ * ft_w (sync_ft_forward_weights, trainer_layerstack.rs:1787). */
+TATARA_API int32_t tatara_trainer_sync_forward_weights(TataraTrainer* trainer);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TATARA_HIP_H */

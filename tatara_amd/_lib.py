@@ -1,0 +1,171 @@
+"""ctypes binding of libtatara_hip.so (the C ABI declared in include/tatara_hip.h).
+
+The library is built in-tree by tatara_amd/build.py.  Loading fails loudly
+when it is missing: there is no CPU fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libtatara_hip.so"
+
+c_f32p = C.POINTER(C.c_float)
+c_i32p = C.POINTER(C.c_int32)
+c_u64p = C.POINTER(C.c_uint64)
+c_f64p = C.POINTER(C.c_double)
+
+
+class TataraTrainerConfig(C.Structure):
+    _fields_ = [
+        ("arch", C.c_int32),
+        ("device", C.c_int32),
+        ("max_batch", C.c_int32),
+        ("ft_in", C.c_int32),
+        ("max_active", C.c_int32),
+        ("piece_inputs", C.c_int32),
+        ("ft_out", C.c_int32),
+        ("l1_out", C.c_int32),
+        ("l2_out", C.c_int32),
+        ("num_buckets", C.c_int32),
+        ("optimizer", C.c_int32),
+        ("ft_weight_decay", C.c_float),
+        ("dense_weight_decay", C.c_float),
+        ("bias_weight_decay", C.c_float),
+        ("ft_lr_mult", C.c_float),
+        ("dense_lr_mult", C.c_float),
+        ("bias_lr_mult", C.c_float),
+        ("keep_grads", C.c_int32),
+    ]
+
+
+class TataraLoss(C.Structure):
+    _fields_ = [
+        ("kind", C.c_int32),
+        ("scale", C.c_float),
+        ("nnue2score", C.c_float),
+        ("in_scaling", C.c_float),
+        ("in_offset", C.c_float),
+        ("target_offset", C.c_float),
+        ("target_scaling", C.c_float),
+        ("pow_exp", C.c_float),
+        ("qp_asymmetry", C.c_float),
+        ("weight_boost_w1", C.c_float),
+        ("weight_boost_w2", C.c_float),
+    ]
+
+
+class TataraBatch(C.Structure):
+    _fields_ = [
+        ("n_pos", C.c_int32),
+        ("max_active", C.c_int32),
+        ("stm_indices", C.c_void_p),
+        ("nstm_indices", C.c_void_p),
+        ("nnz", C.c_void_p),
+        ("bucket_idx", C.c_void_p),
+        ("score", C.c_void_p),
+        ("wdl", C.c_void_p),
+        ("on_device", C.c_int32),
+    ]
+
+
+# name -> (restype, argtypes); every entry point returns an int32 status
+# except the two string getters.
+SIGNATURES = {
+    "tatara_last_error": (C.c_char_p, []),
+    "tatara_version": (C.c_char_p, []),
+    "tatara_device_count": (C.c_int32, [c_i32p]),
+    "tatara_set_device": (C.c_int32, [C.c_int32]),
+    "tatara_device_info": (C.c_int32, [C.c_int32, C.c_char_p, C.c_int32, c_i32p]),
+    "tatara_malloc": (C.c_int32, [C.POINTER(C.c_void_p), C.c_uint64]),
+    "tatara_free": (C.c_int32, [C.c_void_p]),
+    "tatara_memcpy_htod": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "tatara_memcpy_dtoh": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "tatara_memset": (C.c_int32, [C.c_void_p, C.c_int32, C.c_uint64]),
+    "tatara_synchronize": (C.c_int32, []),
+    "tatara_op_sparse_ft_forward": (C.c_int32, [C.c_void_p] * 4 + [C.c_uint32] * 4),
+    "tatara_op_ft_forward_pairwise": (
+        C.c_int32,
+        [C.c_void_p] * 8 + [C.c_uint32] * 5 + [C.c_float],
+    ),
+    "tatara_op_ft_weight_grad": (C.c_int32, [C.c_void_p] * 5 + [C.c_uint32] * 4),
+    "tatara_op_ft_fold_virtual": (C.c_int32, [C.c_void_p, C.c_void_p] + [C.c_uint32] * 3),
+    "tatara_op_ft_reduce_virtual_grad": (C.c_int32, [C.c_void_p] + [C.c_uint32] * 3),
+    "tatara_op_radam_step": (
+        C.c_int32,
+        [C.c_void_p] * 4
+        + [C.c_float, C.c_float, C.c_int32]
+        + [C.c_float] * 6
+        + [C.c_uint64],
+    ),
+    "tatara_op_ranger_lookahead_lerp": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_float, C.c_uint64]),
+    "tatara_radam_step_size_denom": (
+        C.c_int32,
+        [C.c_uint64, C.c_float, C.c_float, C.c_float, c_f32p, c_i32p],
+    ),
+    "tatara_trainer_create": (C.c_int32, [C.POINTER(TataraTrainerConfig), C.POINTER(C.c_void_p)]),
+    "tatara_trainer_destroy": (C.c_int32, [C.c_void_p]),
+    "tatara_trainer_train_step": (
+        C.c_int32,
+        [C.c_void_p, C.POINTER(TataraBatch), C.c_float, C.c_float, C.POINTER(TataraLoss), c_f64p],
+    ),
+    "tatara_trainer_flush_pending_loss": (C.c_int32, [C.c_void_p, c_f64p]),
+    "tatara_trainer_validate_step": (
+        C.c_int32,
+        [C.c_void_p, C.POINTER(TataraBatch), C.c_float, C.POINTER(TataraLoss), c_f64p, c_f32p],
+    ),
+    "tatara_trainer_step_count": (C.c_int32, [C.c_void_p, c_u64p]),
+    "tatara_trainer_tensor_size": (C.c_int32, [C.c_void_p, C.c_char_p, c_u64p]),
+    "tatara_trainer_get_tensor": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, c_f32p, C.c_uint64]),
+    "tatara_trainer_set_tensor": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, c_f32p, C.c_uint64]),
+    "tatara_trainer_get_activation": (C.c_int32, [C.c_void_p, C.c_char_p, c_f32p, C.c_uint64]),
+    "tatara_trainer_sync_forward_weights": (C.c_int32, [C.c_void_p]),
+    "tatara_trainer_set_profiling": (C.c_int32, [C.c_void_p, C.c_int32]),
+    "tatara_trainer_phase_times": (C.c_int32, [C.c_void_p, c_f64p, C.c_int32, c_u64p]),
+}
+
+
+class TataraError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"status {status}: {message}")
+        self.status = status
+
+
+class OutOfMemory(TataraError):
+    pass
+
+
+_LIB: C.CDLL | None = None
+
+
+def load(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Loads (once) and returns the HIP library with typed entry points."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is missing: build it with `python -m tatara_amd.build` "
+            "(the HIP library is the only implementation of this path)"
+        )
+    lib = C.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def check(status: int) -> None:
+    """Raises TataraError (OutOfMemory for -2) when status is non-zero."""
+    if status == 0:
+        return
+    msg = load().tatara_last_error().decode(errors="replace")
+    if status == -2:
+        raise OutOfMemory(status, msg)
+    raise TataraError(status, msg)

@@ -1,0 +1,738 @@
+// LayerStack dense layers for gfx950.
+//
+// The batch is processed in the bucket-sorted order produced by the stable
+// bin sort (every 16-row tile belongs to one bucket), as the reference's
+// sorted L1 kernels do (crates/cuda-native-runtime/kernels/native_kernels.cu:
+// 2394-2432, 2502-2589).  Per-row arithmetic follows the reference CPU
+// functions in crates/gpu-kernels/src/layerstack/ (dense_mm.rs,
+// dense_mm_bucket.rs, crelu.rs, abs_pow2_scale.rs, concat_l1sqr_main.rs,
+// elementwise.rs, slice2d.rs, ft_post_perspective.rs) and the loss kernels in
+// crates/gpu-kernels/src/pointwise/{loss_wdl,loss_wrm}.rs; the launch order is
+// the one of GpuTrainer::forward/backward (bins/nnue_train/src/
+// trainer_layerstack.rs:2038-3936).
+//
+// MFMA (v_mfma_f32_16x16x4_f32) is used for the FT->L1 contraction only: the
+// L1 forward (bucket + shared weights, K = ft_out) and the L1 weight gradient
+// (K = rows of the batch).  Everything reduced over the batch goes through
+// per-workgroup partials that are summed in a fixed order, so a step is
+// bit-reproducible run to run (no float atomics anywhere).
+#include "dense_kernels.hpp"
+
+#include "common.hpp"
+
+namespace tatara {
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// L1 forward.  One wave per 16-row sorted tile.
+//   bucket part: l1_b[g] + combined . l1_w[g]^T   (accumulator starts at the bias,
+//                as dense_mm_fwd_bucket_tiled_l1_sorted does); 0 for an invalid bucket
+//   shared part: combined . l1s_w + l1s_b         (bias after the sum, as the
+//                reference's sgemm + bias_add_per_row)
+// MFMA operand layout (16x16x4 f32): lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; the result holds D[4*(l/16)+r][l%16] in element r.  Each lane
+// loads float4 column runs and feeds their components to four successive
+// MFMAs, which permutes the K order consistently for A and B.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t tile = blockIdx.x * 4 + wave;
+    if ((uint64_t)tile * 16 >= a.padded_b) return;
+    const int32_t bin = a.sorted_bin[tile * 16];
+    if (bin < 0) return;  // trailing all-padding tile
+    const uint32_t i = lane % 16, q = lane / 16;
+    const uint32_t ft_out = a.ft_out, l1 = a.l1;
+    const int32_t orig = a.perm[tile * 16 + i];
+    const bool bvalid = (uint32_t)bin < a.nb;
+    const bool jvalid = i < l1;
+    const float4* X = orig >= 0 ? reinterpret_cast<const float4*>(a.combined + (uint64_t)orig * ft_out)
+                                : nullptr;
+    const float4* W1 = (bvalid && jvalid)
+                           ? reinterpret_cast<const float4*>(a.l1_w + ((uint64_t)bin * l1 + i) * ft_out)
+                           : nullptr;
+    const float* Ws = a.l1s_w;
+    const float binit = (bvalid && jvalid) ? a.l1_b[bin * l1 + i] : 0.0f;
+    floatx4 accb = {binit, binit, binit, binit};
+    floatx4 accs = {0.f, 0.f, 0.f, 0.f};
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t nk = ft_out / 16;
+    for (uint32_t kb = 0; kb < nk; ++kb) {
+        const float4 x = X ? X[kb * 4 + q] : zero4;
+        const float4 wb = W1 ? W1[kb * 4 + q] : zero4;
+        const uint32_t k = kb * 16 + 4 * q;
+        float ws0 = 0.f, ws1 = 0.f, ws2 = 0.f, ws3 = 0.f;
+        if (jvalid) {
+            ws0 = Ws[(uint64_t)(k + 0) * l1 + i];
+            ws1 = Ws[(uint64_t)(k + 1) * l1 + i];
+            ws2 = Ws[(uint64_t)(k + 2) * l1 + i];
+            ws3 = Ws[(uint64_t)(k + 3) * l1 + i];
+        }
+        accb = mfma4(x.x, wb.x, accb);
+        accs = mfma4(x.x, ws0, accs);
+        accb = mfma4(x.y, wb.y, accb);
+        accs = mfma4(x.y, ws1, accs);
+        accb = mfma4(x.z, wb.z, accb);
+        accs = mfma4(x.z, ws2, accs);
+        accb = mfma4(x.w, wb.w, accb);
+        accs = mfma4(x.w, ws3, accs);
+    }
+    const uint32_t j = lane % 16;
+    if (j >= l1) return;
+    const float bs = a.l1s_b[j];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint64_t row = (uint64_t)tile * 16 + 4 * q + r;
+        float* o = a.l1_sorted + row * 2 * l1;
+        o[j] = bvalid ? accb[r] : 0.0f;
+        o[l1 + j] = accs[r] + bs;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Extended-WRM weight sum (wrm_weight_sum, native_kernels.cu:520-544), as a
+// deterministic two-level f64 reduction in position order.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wrm_weight_dev(float s, const LossParams& lp) {
+    const float tp = 1.0f / (1.0f + expf(-((s - lp.target_offset) / lp.target_scaling)));
+    const float tn = 1.0f / (1.0f + expf(-((-s - lp.target_offset) / lp.target_scaling)));
+    const float t = 0.5f * (1.0f + tp - tn);
+    const float wb = (t - 0.5f) * (t - 0.5f) * t * (1.0f - t);
+    return 1.0f + (powf(2.0f, lp.w1) - 1.0f) * powf(wb, lp.w2);
+}
+
+__global__ __launch_bounds__(256) void wrm_weight_partial_kernel(const float* __restrict__ score,
+                                                                 uint32_t n, LossParams lp,
+                                                                 double* __restrict__ partial) {
+    __shared__ double s[256];
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    s[threadIdx.x] = i < n ? (double)wrm_weight_dev(score[i], lp) : 0.0;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int k = 0; k < 256; ++k) acc += s[k];
+        partial[blockIdx.x] = acc;
+    }
+}
+
+__global__ void sum_partials_f64_kernel(const double* __restrict__ partial, uint32_t n,
+                                        double* __restrict__ out) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    double acc = 0.0;
+    for (uint32_t k = 0; k < n; ++k) acc += partial[k];
+    *out = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Tail: one thread per sorted row.
+// ---------------------------------------------------------------------------
+template <int L1, int L2>
+__global__ __launch_bounds__(kTailRows) void ls_tail_kernel(LsDenseArgs a, int32_t train) {
+    constexpr int LE = L1 - 1;
+    constexpr int LIN = 2 * LE;
+    constexpr int R = kTailRows;
+    __shared__ float s_l2in[R][LIN + 1];
+    __shared__ float s_dl2o[R][L2 + 1];
+    __shared__ float s_l2a[R][L2 + 1];
+    __shared__ float s_dl1[R][L1 + 1];
+    __shared__ float s_dy[R];
+    __shared__ int32_t s_bin[R];
+    __shared__ double s_loss[R];
+    __shared__ uint32_t s_lo[16], s_hi[16];
+
+    const uint32_t t = threadIdx.x;
+    const uint64_t row = (uint64_t)blockIdx.x * R + t;
+    const uint32_t nb = a.nb;
+    int32_t bin = -1, orig = -1;
+    if (row < a.padded_b) {
+        bin = a.sorted_bin[row];
+        orig = a.perm[row];
+    }
+    const bool real = orig >= 0;
+    const bool bvalid = real && (uint32_t)bin < nb;
+    const int g = bvalid ? bin : 0;
+
+    float l1t[L1];
+    float l2pre[LIN], l2in[LIN], l2o[L2], l2a[L2];
+    float net = 0.0f, dy = 0.0f;
+    double loss_c = 0.0;
+    if (real) {
+        const float* l1v = a.l1_sorted + row * 2 * L1;
+#pragma unroll
+        for (int o = 0; o < L1; ++o) l1t[o] = l1v[o] + l1v[L1 + o];  // elementwise_add
+        const float skip = l1t[L1 - 1];                                // slice_extract_2d
+#pragma unroll
+        for (int k = 0; k < LE; ++k) {
+            const float mk = l1t[k];
+            l2pre[k] = mk * mk * a.l1_sqr_scale;  // abs_pow2_scale_fwd
+            l2pre[LE + k] = mk;                   // concat_l1sqr_main_fwd
+        }
+#pragma unroll
+        for (int k = 0; k < LIN; ++k) l2in[k] = crelu01(l2pre[k]);
+        const float* W2 = a.l2_w + (uint64_t)g * L2 * LIN;
+#pragma unroll
+        for (int o = 0; o < L2; ++o) {
+            float acc = bvalid ? a.l2_b[g * L2 + o] : 0.0f;
+            if (bvalid) {
+#pragma unroll
+                for (int k = 0; k < LIN; ++k) acc += l2in[k] * W2[o * LIN + k];
+            }
+            l2o[o] = bvalid ? acc : 0.0f;
+            l2a[o] = crelu01(l2o[o]);
+        }
+        float l3 = 0.0f;
+        if (bvalid) {
+            l3 = a.l3_b[g];
+#pragma unroll
+            for (int o = 0; o < L2; ++o) l3 += l2a[o] * a.l3_w[g * L2 + o];
+        }
+        net = l3 + skip;
+        a.net_output[orig] = net;
+        // loss (loss_wdl / loss_wrm)
+        const float sc = a.score[orig];
+        const float wd = a.wdl[orig];
+        const float lam = a.wdl_lambda;
+        const LossParams& lp = a.loss;
+        if (lp.kind == 0) {
+            const float p = sigmoidf_(net * lp.scale);
+            const float ys = sigmoidf_(sc * lp.scale);
+            const float y = lam * wd + (1.0f - lam) * ys;
+            const float err = p - y;
+            loss_c = (double)err * (double)err;
+            dy = 2.0f * err * p * (1.0f - p) * lp.scale * a.per_pos_norm;
+        } else {
+            const float tp = 1.0f / (1.0f + expf(-((sc - lp.target_offset) / lp.target_scaling)));
+            const float tn = 1.0f / (1.0f + expf(-((-sc - lp.target_offset) / lp.target_scaling)));
+            const float twrm = 0.5f * (1.0f + tp - tn);
+            const float target = lam * wd + (1.0f - lam) * twrm;
+            const float sn = net * lp.nnue2score;
+            const float q = 1.0f / (1.0f + expf(-((sn - lp.in_offset) / lp.in_scaling)));
+            const float qm = 1.0f / (1.0f + expf(-((-sn - lp.in_offset) / lp.in_scaling)));
+            const float pred = 0.5f * (1.0f + q - qm);
+            const float err = pred - target;
+            if (!lp.extended) {
+                dy = err * (lp.nnue2score / lp.in_scaling) * (q * (1.0f - q) + qm * (1.0f - qm)) *
+                     a.per_pos_norm;
+                loss_c = (double)err * (double)err;
+            } else {
+                const float wb = (twrm - 0.5f) * (twrm - 0.5f) * twrm * (1.0f - twrm);
+                const float weight = 1.0f + (powf(2.0f, lp.w1) - 1.0f) * powf(wb, lp.w2);
+                const float asym = pred > target ? 1.0f + lp.qp_asymmetry : 1.0f;
+                const float ae = fabsf(err);
+                const float ap = powf(ae, lp.pow_exp - 1.0f);
+                const float sp = err < 0.0f ? -ap : ap;
+                const float inv = (float)(1.0 / a.weight_sum[0]);
+                const float pg = 0.5f * (lp.nnue2score / lp.in_scaling) * (q * (1.0f - q) + qm * (1.0f - qm));
+                dy = (weight * inv) * (asym * lp.pow_exp * sp) * pg;
+                loss_c = (double)(asym * powf(ae, lp.pow_exp) * weight * (float)a.batch * inv);
+            }
+        }
+    }
+    s_loss[t] = loss_c;
+    if (!train) {
+        __syncthreads();
+        if (t == 0) {
+            double acc = 0.0;
+            for (int k = 0; k < R; ++k) acc += s_loss[k];
+            a.loss_partial[blockIdx.x] = acc;
+        }
+        return;
+    }
+
+    // backward through L3, L2 and the L1 tail
+    float dl1[L1];
+#pragma unroll
+    for (int o = 0; o < L1; ++o) dl1[o] = 0.0f;
+    float dl2o[L2];
+    if (real) {
+        float dl2a[L2];
+#pragma unroll
+        for (int o = 0; o < L2; ++o) {
+            float acc = 0.0f;  // dense_mm_bwd_input_bucket, out_dim 1
+            if (bvalid) acc += dy * a.l3_w[g * L2 + o];
+            dl2a[o] = acc;
+            dl2o[o] = (l2o[o] > 0.0f && l2o[o] < 1.0f) ? dl2a[o] : 0.0f;  // crelu_grad
+        }
+        const float* W2 = a.l2_w + (uint64_t)g * L2 * LIN;
+        float dl2pre[LIN];
+#pragma unroll
+        for (int k = 0; k < LIN; ++k) {
+            float acc = 0.0f;
+            if (bvalid) {
+#pragma unroll
+                for (int o = 0; o < L2; ++o) acc += dl2o[o] * W2[o * LIN + k];
+            }
+            dl2pre[k] = (l2pre[k] > 0.0f && l2pre[k] < 1.0f) ? acc : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < LE; ++k) {
+            const float from_sqr = 2.0f * l1t[k] * a.l1_sqr_scale * dl2pre[k];  // abs_pow2_scale_grad
+            dl1[k] = dl2pre[LE + k] + from_sqr;                                  // elementwise_add
+        }
+        dl1[L1 - 1] = dy;  // slice_scatter_2d of the skip gradient
+    } else {
+#pragma unroll
+        for (int o = 0; o < L2; ++o) dl2o[o] = 0.0f;
+    }
+    if (row < a.padded_b) {
+        float* d = a.dl1_sorted + row * L1;
+#pragma unroll
+        for (int o = 0; o < L1; ++o) d[o] = dl1[o];
+    }
+#pragma unroll
+    for (int k = 0; k < LIN; ++k) s_l2in[t][k] = real ? l2in[k] : 0.0f;
+#pragma unroll
+    for (int o = 0; o < L2; ++o) {
+        s_dl2o[t][o] = dl2o[o];
+        s_l2a[t][o] = real ? l2a[o] : 0.0f;
+    }
+#pragma unroll
+    for (int o = 0; o < L1; ++o) s_dl1[t][o] = dl1[o];
+    s_dy[t] = dy;
+    s_bin[t] = bvalid ? bin : -1;
+    __syncthreads();
+
+    if (t == 0) {
+        double acc = 0.0;
+        for (int k = 0; k < R; ++k) acc += s_loss[k];
+        a.loss_partial[blockIdx.x] = acc;
+        for (uint32_t gg = 0; gg < nb; ++gg) {
+            s_lo[gg] = R;
+            s_hi[gg] = 0;
+        }
+        for (int k = 0; k < R; ++k) {
+            const int32_t bk = s_bin[k];
+            if (bk >= 0) {
+                if ((uint32_t)k < s_lo[bk]) s_lo[bk] = k;
+                s_hi[bk] = k + 1;
+            }
+        }
+    }
+    __syncthreads();
+
+    const TailDims td{(uint32_t)L1, (uint32_t)L2, nb};
+    const uint32_t cells = td.cells();
+    float* part = a.tail_partial + (uint64_t)blockIdx.x * nb * cells;
+    for (uint32_t c = t; c < cells; c += R) {
+        for (uint32_t gg = 0; gg < nb; ++gg) {
+            const uint32_t lo = s_lo[gg], hi = s_hi[gg];
+            float acc = 0.0f;
+            if (c < td.off_b2()) {
+                const uint32_t o = c / LIN, k = c % LIN;
+                for (uint32_t r = lo; r < hi; ++r)
+                    if (s_bin[r] == (int32_t)gg) acc += s_l2in[r][k] * s_dl2o[r][o];
+            } else if (c < td.off_w3()) {
+                const uint32_t o = c - td.off_b2();
+                for (uint32_t r = lo; r < hi; ++r)
+                    if (s_bin[r] == (int32_t)gg) acc += s_dl2o[r][o];
+            } else if (c < td.off_b3()) {
+                const uint32_t o = c - td.off_w3();
+                for (uint32_t r = lo; r < hi; ++r)
+                    if (s_bin[r] == (int32_t)gg) acc += s_l2a[r][o] * s_dy[r];
+            } else if (c < td.off_b1()) {
+                for (uint32_t r = lo; r < hi; ++r)
+                    if (s_bin[r] == (int32_t)gg) acc += s_dy[r];
+            } else {
+                const uint32_t o = c - td.off_b1();
+                for (uint32_t r = lo; r < hi; ++r)
+                    if (s_bin[r] == (int32_t)gg) acc += s_dl1[r][o];
+            }
+            part[(uint64_t)gg * cells + c] = acc;
+        }
+    }
+    // shared L1 bias: every real row, including rows of an invalid bucket
+    if (t < (uint32_t)L1) {
+        float acc = 0.0f;
+        for (int r = 0; r < R; ++r) acc += s_dl1[r][t];
+        a.b1s_partial[(uint64_t)blockIdx.x * L1 + t] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Chunk table for the L1 weight gradient: every bin (including the invalid
+// bin nb, whose rows still feed the shared weight) is split into chunks of at
+// most kChunkTiles 16-row tiles.
+// ---------------------------------------------------------------------------
+__global__ void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
+                                      const uint32_t* __restrict__ bin_count, uint32_t nb,
+                                      uint32_t max_chunks, uint32_t* __restrict__ info) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    uint32_t c = 0;
+    for (uint32_t g = 0; g <= nb; ++g) {
+        const uint32_t t0 = bin_start[g] / 16;
+        const uint32_t t1 = (bin_start[g] + bin_count[g] + 15) / 16;
+        for (uint32_t t = t0; t < t1 && c < max_chunks; t += kChunkTiles) {
+            info[3 * c + 0] = g;
+            info[3 * c + 1] = t;
+            info[3 * c + 2] = min(kChunkTiles, t1 - t);
+            ++c;
+        }
+    }
+    info[3 * max_chunks] = c;
+}
+
+// ---------------------------------------------------------------------------
+// L1 weight gradient partials: P[chunk][o][k] = sum over the chunk's rows of
+// dl1[row][o] * combined[row][k].  One wave owns 64 columns; lane (k, q) loads
+// a float4 of combined so block c of its four MFMAs holds columns k0+4k+c.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t n_chunks = a.chunk_info[3 * a.max_chunks];
+    const uint32_t chunk = blockIdx.x;
+    if (chunk >= n_chunks) return;
+    const uint32_t k0 = (blockIdx.y * 4 + wave) * 64;
+    if (k0 >= a.ft_out) return;
+    const uint32_t t0 = a.chunk_info[3 * chunk + 1], nt = a.chunk_info[3 * chunk + 2];
+    const uint32_t o = lane % 16, q = lane / 16, kk = lane % 16;
+    const uint32_t l1 = a.l1, ft_out = a.ft_out;
+    const bool ovalid = o < l1;
+    const bool kvalid = k0 + 4 * kk < ft_out;
+    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+    for (uint32_t tt = 0; tt < nt; ++tt) {
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) {
+            const uint64_t row = (uint64_t)(t0 + tt) * 16 + 4 * s + q;
+            const int32_t orig = a.perm[row];
+            const float d = ovalid ? a.dl1_sorted[row * l1 + o] : 0.0f;
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (orig >= 0 && kvalid)
+                x = reinterpret_cast<const float4*>(a.combined + (uint64_t)orig * ft_out + k0)[kk];
+            acc0 = mfma4(d, x.x, acc0);
+            acc1 = mfma4(d, x.y, acc1);
+            acc2 = mfma4(d, x.z, acc2);
+            acc3 = mfma4(d, x.w, acc3);
+        }
+    }
+    if (!kvalid) return;
+    float* P = a.w1_partial + (uint64_t)chunk * l1 * ft_out;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t oo = 4 * q + r;
+        if (oo >= l1) continue;
+        float* dst = P + (uint64_t)oo * ft_out + k0 + 4 * kk;
+        dst[0] = acc0[r];
+        dst[1] = acc1[r];
+        dst[2] = acc2[r];
+        dst[3] = acc3[r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// L1 input gradient fused with the FT-post gradient.
+// dcombined[c] = sum_o dl1[o] * l1_w[g][o][c]  +  sum_o dl1[o] * l1s_w[c][o]
+// (the reference's two input-gradient kernels, added as in
+// ft_post_perspective_grad_fused), then the pairwise CReLU gradient into dft
+// (native_kernels.cu:2260-2302).  A workgroup owns kPostTiles sorted tiles and
+// writes its ft_b gradient partial per perspective.
+// ---------------------------------------------------------------------------
+template <int L1>
+__global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t ft_out = a.ft_out, half = ft_out / 2, n4 = ft_out / 4;
+    const uint64_t batch = a.batch;
+    const uint32_t tile0 = blockIdx.x * kPostTiles;
+    float* part = a.ftb_partial + (uint64_t)blockIdx.x * 2 * ft_out;
+    for (uint32_t qq = t; qq < n4; qq += 128) {
+        const uint32_t c0 = 4 * qq;
+        const uint32_t persp = c0 < half ? 0 : 1;
+        const uint32_t p0 = c0 - persp * half;
+        const float* ft = persp ? a.ft_nstm : a.ft_stm;
+        float* dft = a.dft + persp * batch * ft_out;
+        float ws[4][L1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int o = 0; o < L1; ++o) ws[e][o] = a.l1s_w[(uint64_t)(c0 + e) * L1 + o];
+        const float4 ba = reinterpret_cast<const float4*>(a.ft_b)[p0 / 4];
+        const float4 bb = reinterpret_cast<const float4*>(a.ft_b)[(p0 + half) / 4];
+        float4 w1[L1];
+        int32_t cur_bin = -2;
+        float4 acc_a = make_float4(0.f, 0.f, 0.f, 0.f), acc_b = acc_a;
+        for (uint32_t tt = 0; tt < kPostTiles; ++tt) {
+            const uint64_t tile = tile0 + tt;
+            if (tile * 16 >= a.padded_b) break;
+            const int32_t bin = a.sorted_bin[tile * 16];
+            if (bin < 0) continue;
+            const bool bvalid = (uint32_t)bin < a.nb;
+            if (bin != cur_bin) {
+                cur_bin = bin;
+#pragma unroll
+                for (int o = 0; o < L1; ++o)
+                    w1[o] = bvalid ? reinterpret_cast<const float4*>(
+                                         a.l1_w + ((uint64_t)bin * L1 + o) * ft_out)[qq]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            for (uint32_t r = 0; r < 16; ++r) {
+                const uint64_t row = tile * 16 + r;
+                const int32_t orig = a.perm[row];
+                if (orig < 0) continue;
+                float d[L1];
+                const float* dsrc = a.dl1_sorted + row * L1;
+#pragma unroll
+                for (int o = 0; o < L1; ++o) d[o] = dsrc[o];
+                float dyv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float da = 0.0f;
+                    if (bvalid) {
+#pragma unroll
+                        for (int o = 0; o < L1; ++o) {
+                            const float wv = e == 0 ? w1[o].x : e == 1 ? w1[o].y : e == 2 ? w1[o].z : w1[o].w;
+                            da += d[o] * wv;
+                        }
+                    }
+                    float db = 0.0f;
+#pragma unroll
+                    for (int o = 0; o < L1; ++o) db += d[o] * ws[e][o];
+                    dyv[e] = da + db;
+                }
+                const float4 xa4 = reinterpret_cast<const float4*>(ft + (uint64_t)orig * ft_out)[p0 / 4];
+                const float4 xb4 =
+                    reinterpret_cast<const float4*>(ft + (uint64_t)orig * ft_out)[(p0 + half) / 4];
+                const float xa[4] = {xa4.x + ba.x, xa4.y + ba.y, xa4.z + ba.z, xa4.w + ba.w};
+                const float xb[4] = {xb4.x + bb.x, xb4.y + bb.y, xb4.z + bb.z, xb4.w + bb.w};
+                float ga[4], gb[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float ya = crelu01(xa[e]), yb = crelu01(xb[e]);
+                    ga[e] = (xa[e] > 0.0f && xa[e] < 1.0f) ? dyv[e] * yb * a.ft_post_scale : 0.0f;
+                    gb[e] = (xb[e] > 0.0f && xb[e] < 1.0f) ? dyv[e] * ya * a.ft_post_scale : 0.0f;
+                }
+                float4* drow = reinterpret_cast<float4*>(dft + (uint64_t)orig * ft_out);
+                drow[p0 / 4] = make_float4(ga[0], ga[1], ga[2], ga[3]);
+                drow[(p0 + half) / 4] = make_float4(gb[0], gb[1], gb[2], gb[3]);
+                acc_a.x += ga[0];
+                acc_a.y += ga[1];
+                acc_a.z += ga[2];
+                acc_a.w += ga[3];
+                acc_b.x += gb[0];
+                acc_b.y += gb[1];
+                acc_b.z += gb[2];
+                acc_b.w += gb[3];
+            }
+        }
+        float* pp = part + persp * ft_out;
+        reinterpret_cast<float4*>(pp)[p0 / 4] = acc_a;
+        reinterpret_cast<float4*>(pp)[(p0 + half) / 4] = acc_b;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dense gradient finalize + optimizer: one thread per parameter element of
+// the nine non-FT groups (uniform_optim_group_layout order,
+// trainer_layerstack.rs:676-705).
+// ---------------------------------------------------------------------------
+struct GroupTable {
+    LsDenseGroup g[9];
+    uint64_t start[10];
+};
+
+__global__ __launch_bounds__(256) void ls_dense_finalize_kernel(LsDenseArgs a, GroupTable gt,
+                                                                OptScalars dense, OptScalars bias,
+                                                                int32_t apply_update,
+                                                                int32_t keep_grads, uint32_t n_tail,
+                                                                uint32_t n_post) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= gt.start[9]) return;
+    int gi = 0;
+    while (i >= gt.start[gi + 1]) ++gi;
+    const uint64_t e = i - gt.start[gi];
+    const uint32_t l1 = a.l1, l2 = a.l2, nb = a.nb, ft_out = a.ft_out;
+    const TailDims td{l1, l2, nb};
+    const uint32_t cells = td.cells();
+    const uint32_t n_chunks = a.chunk_info[3 * a.max_chunks];
+    float grad = 0.0f;
+    auto tail_sum = [&](uint32_t g, uint32_t cell) {
+        float s = 0.0f;
+        for (uint32_t w = 0; w < n_tail; ++w) s += a.tail_partial[((uint64_t)w * nb + g) * cells + cell];
+        return s;
+    };
+    switch (gi) {
+        case 0: {  // ft_b: stm partials then nstm partials
+            float s = 0.0f;
+            for (uint32_t w = 0; w < n_post; ++w) s += a.ftb_partial[(uint64_t)w * 2 * ft_out + e];
+            for (uint32_t w = 0; w < n_post; ++w)
+                s += a.ftb_partial[(uint64_t)w * 2 * ft_out + ft_out + e];
+            grad = s;
+            break;
+        }
+        case 1: {  // l1_w [nb][l1][ft_out]
+            const uint32_t g = (uint32_t)(e / ((uint64_t)l1 * ft_out));
+            const uint64_t ok = e - (uint64_t)g * l1 * ft_out;
+            float s = 0.0f;
+            for (uint32_t c = 0; c < n_chunks; ++c)
+                if (a.chunk_info[3 * c] == g) s += a.w1_partial[(uint64_t)c * l1 * ft_out + ok];
+            grad = s;
+            break;
+        }
+        case 2: {  // l1_b [nb][l1]
+            const uint32_t g = (uint32_t)(e / l1), o = (uint32_t)(e % l1);
+            grad = tail_sum(g, td.off_b1() + o);
+            break;
+        }
+        case 3: {  // l1s_w [ft_out][l1]
+            const uint32_t k = (uint32_t)(e / l1), o = (uint32_t)(e % l1);
+            float s = 0.0f;
+            for (uint32_t c = 0; c < n_chunks; ++c)
+                s += a.w1_partial[(uint64_t)c * l1 * ft_out + (uint64_t)o * ft_out + k];
+            grad = s;
+            break;
+        }
+        case 4: {  // l1s_b [l1]
+            float s = 0.0f;
+            for (uint32_t w = 0; w < n_tail; ++w) s += a.b1s_partial[(uint64_t)w * l1 + e];
+            grad = s;
+            break;
+        }
+        case 5: {  // l2_w [nb][l2][l2_in]
+            const uint32_t per = l2 * td.l2_in();
+            const uint32_t g = (uint32_t)(e / per), c = (uint32_t)(e % per);
+            grad = tail_sum(g, td.off_w2() + c);
+            break;
+        }
+        case 6: {  // l2_b [nb][l2]
+            grad = tail_sum((uint32_t)(e / l2), td.off_b2() + (uint32_t)(e % l2));
+            break;
+        }
+        case 7: {  // l3_w [nb][l2]
+            grad = tail_sum((uint32_t)(e / l2), td.off_w3() + (uint32_t)(e % l2));
+            break;
+        }
+        default: {  // l3_b [nb]
+            grad = tail_sum((uint32_t)e, td.off_b3());
+            break;
+        }
+    }
+    const LsDenseGroup& G = gt.g[gi];
+    if (!apply_update) {
+        G.grad[e] = grad;
+        return;
+    }
+    OptScalars s = G.kind == 2 ? bias : dense;
+    s.min_w = G.min_w;
+    s.max_w = G.max_w;
+    float W = G.w[e], M = G.m[e], V = G.v[e];
+    radam_elem(W, M, V, grad, s);
+    if (s.lookahead) {
+        float S = G.slow[e];
+        lerp_elem(W, S, s.alpha);
+        G.slow[e] = S;
+    }
+    G.w[e] = W;
+    G.m[e] = M;
+    G.v[e] = V;
+    G.grad[e] = keep_grads ? grad : 0.0f;
+}
+
+__global__ void ls_loss_reduce_kernel(const double* __restrict__ partial, uint32_t n,
+                                      double* __restrict__ out) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    double acc = 0.0;
+    for (uint32_t k = 0; k < n; ++k) acc += partial[k];
+    *out = acc;
+}
+
+}  // namespace
+
+uint32_t ls_tail_workgroups(uint32_t padded_b) { return ceil_div(padded_b, kTailRows); }
+uint32_t ls_post_workgroups(uint32_t padded_b) { return ceil_div(padded_b / 16, kPostTiles); }
+uint32_t ls_max_chunks(uint32_t padded_b, uint32_t nb) {
+    return ceil_div(padded_b / 16, kChunkTiles) + nb + 1;
+}
+
+int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream) {
+    TATARA_REQUIRE(a.l1 >= 2 && a.l1 <= 16, "l1 must be in [2, 16]");
+    TATARA_REQUIRE(a.ft_out % 16 == 0, "ft_out must be a multiple of 16");
+    const uint32_t tiles = a.padded_b / 16;
+    if (tiles == 0) return kOk;
+    ls_l1_fwd_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    TATARA_LAUNCHED("ls_l1_forward");
+    return kOk;
+}
+
+int32_t launch_wrm_weight_sum(const float* score, uint32_t n, const LossParams& lp, double* out,
+                              double* scratch, hipStream_t stream) {
+    const uint32_t blocks = ceil_div(n, 256);
+    if (blocks) {
+        wrm_weight_partial_kernel<<<blocks, 256, 0, stream>>>(score, n, lp, scratch);
+        TATARA_LAUNCHED("wrm_weight_sum");
+    }
+    sum_partials_f64_kernel<<<1, 64, 0, stream>>>(scratch, blocks, out);
+    TATARA_LAUNCHED("wrm_weight_sum_reduce");
+    return kOk;
+}
+
+int32_t launch_ls_tail(const LsDenseArgs& a, int32_t train, hipStream_t stream) {
+    TATARA_REQUIRE(a.nb <= 16, "num_buckets must be <= 16");
+    const uint32_t blocks = ls_tail_workgroups(a.padded_b);
+    if (blocks == 0) return kOk;
+    if (a.l1 == 16 && a.l2 == 32) {
+        ls_tail_kernel<16, 32><<<blocks, kTailRows, 0, stream>>>(a, train);
+    } else if (a.l1 == 8 && a.l2 == 32) {
+        ls_tail_kernel<8, 32><<<blocks, kTailRows, 0, stream>>>(a, train);
+    } else {
+        TATARA_REQUIRE(false, "LayerStack (l1, l2) must be (16, 32) or (8, 32)");
+    }
+    TATARA_LAUNCHED("ls_tail");
+    return kOk;
+}
+
+int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream) {
+    ls_chunk_table_kernel<<<1, 64, 0, stream>>>(a.bin_start, a.bin_count, a.nb, a.max_chunks,
+                                               a.chunk_info);
+    TATARA_LAUNCHED("ls_chunk_table");
+    dim3 grid(a.max_chunks, ceil_div(a.ft_out, 256));
+    ls_l1_wgrad_kernel<<<grid, 256, 0, stream>>>(a);
+    TATARA_LAUNCHED("ls_l1_weight_grad");
+    return kOk;
+}
+
+int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
+    const uint32_t blocks = ls_post_workgroups(a.padded_b);
+    if (blocks == 0) return kOk;
+    if (a.l1 == 16) {
+        ls_l1_input_post_kernel<16><<<blocks, 128, 0, stream>>>(a);
+    } else if (a.l1 == 8) {
+        ls_l1_input_post_kernel<8><<<blocks, 128, 0, stream>>>(a);
+    } else {
+        TATARA_REQUIRE(false, "l1 must be 16 or 8");
+    }
+    TATARA_LAUNCHED("ls_l1_input_post");
+    return kOk;
+}
+
+int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups,
+                                 const OptScalars& dense, const OptScalars& bias,
+                                 int32_t apply_update, int32_t keep_grads, hipStream_t stream) {
+    GroupTable gt;
+    gt.start[0] = 0;
+    for (int k = 0; k < 9; ++k) {
+        gt.g[k] = groups[k];
+        gt.start[k + 1] = gt.start[k] + groups[k].n;
+    }
+    const uint64_t n = gt.start[9];
+    ls_dense_finalize_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(a, gt, dense, bias, apply_update,
+                                                                    keep_grads,
+                                                                    ls_tail_workgroups(a.padded_b),
+                                                                    ls_post_workgroups(a.padded_b));
+    TATARA_LAUNCHED("ls_dense_finalize");
+    return kOk;
+}
+
+int32_t launch_ls_loss_reduce(const LsDenseArgs& a, hipStream_t stream) {
+    ls_loss_reduce_kernel<<<1, 64, 0, stream>>>(a.loss_partial, ls_tail_workgroups(a.padded_b),
+                                               a.loss_out);
+    TATARA_LAUNCHED("ls_loss_reduce");
+    return kOk;
+}
+
+}  // namespace tatara

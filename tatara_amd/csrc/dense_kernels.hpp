@@ -1,0 +1,114 @@
+// Host launchers of the LayerStack dense-layer kernels (see dense_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "optim.hpp"
+
+namespace tatara {
+
+// Loss selection, mirroring LossKind (crates/nnue-train/src/trainer.rs:89-221).
+struct LossParams {
+    int32_t kind;  // 0 sigmoid-MSE, 1 WRM
+    float scale;   // sigmoid
+    float nnue2score, in_scaling, in_offset, target_offset, target_scaling;
+    float pow_exp, qp_asymmetry, w1, w2;
+    int32_t extended;  // WRM extended form (pow != 2 || asym != 0 || w1 != 0)
+};
+
+// Layout of the per-workgroup gradient partials written by the tail kernel.
+struct TailDims {
+    uint32_t l1, l2, nb;
+    __host__ __device__ uint32_t l2_in() const { return 2 * (l1 - 1); }
+    // cells per bucket: W2 (l2*l2_in), b2 (l2), W3 (l2), b3 (1), b1 (l1)
+    __host__ __device__ uint32_t cells() const { return l2 * l2_in() + l2 + l2 + 1 + l1; }
+    __host__ __device__ uint32_t off_w2() const { return 0; }
+    __host__ __device__ uint32_t off_b2() const { return l2 * l2_in(); }
+    __host__ __device__ uint32_t off_w3() const { return off_b2() + l2; }
+    __host__ __device__ uint32_t off_b3() const { return off_w3() + l2; }
+    __host__ __device__ uint32_t off_b1() const { return off_b3() + 1; }
+};
+
+constexpr uint32_t kTailRows = 128;      // sorted rows per tail workgroup
+constexpr uint32_t kChunkTiles = 64;     // 16-row tiles per L1 weight-gradient chunk
+constexpr uint32_t kPostTiles = 8;       // 16-row tiles per L1-input/FT-post workgroup
+
+struct LsDenseArgs {
+    // shapes
+    uint32_t batch, padded_b, ft_out, l1, l2, nb;
+    // bucket sort
+    const int32_t* perm;        // [padded_b] sorted row -> original row, -1 padding
+    const int32_t* sorted_bin;  // [padded_b] bin (nb = invalid bucket), -1 padding
+    const uint32_t* bin_start;  // [nb + 2]
+    const uint32_t* bin_count;  // [nb + 1]
+    // chunk table for the L1 weight gradient
+    uint32_t* chunk_info;       // [max_chunks][3] (bin, first tile, n tiles); [max_chunks*3] = count
+    uint32_t max_chunks;
+    // activations
+    const float* combined;      // [batch][ft_out]
+    const float* ft_stm;        // [batch][ft_out] raw FT sums
+    const float* ft_nstm;
+    float* l1_sorted;           // [padded_b][2*l1]  bucket part | shared part (biases added)
+    float* dl1_sorted;          // [padded_b][l1]
+    float* net_output;          // [batch]
+    float* dft;                 // [2][batch][ft_out]
+    // inputs
+    const float* score;
+    const float* wdl;
+    float per_pos_norm;
+    float wdl_lambda;
+    LossParams loss;
+    double* weight_sum;         // [1] extended WRM sum of weights
+    // weights
+    const float* ft_b;
+    const float* l1_w;          // [nb][l1][ft_out]
+    const float* l1_b;          // [nb][l1]
+    const float* l1s_w;         // [ft_out][l1]
+    const float* l1s_b;         // [l1]
+    const float* l2_w;          // [nb][l2][l2_in]
+    const float* l2_b;          // [nb][l2]
+    const float* l3_w;          // [nb][l2]
+    const float* l3_b;          // [nb]
+    float ft_post_scale, l1_sqr_scale;
+    // partials
+    float* tail_partial;        // [n_tail_wg][nb][cells]
+    float* b1s_partial;         // [n_tail_wg][l1]
+    double* loss_partial;       // [n_tail_wg]
+    float* w1_partial;          // [max_chunks][l1][ft_out]
+    float* ftb_partial;         // [n_post_wg][2][ft_out]
+    double* loss_out;           // [1] reduced loss
+};
+
+uint32_t ls_tail_workgroups(uint32_t padded_b);
+uint32_t ls_post_workgroups(uint32_t padded_b);
+uint32_t ls_max_chunks(uint32_t padded_b, uint32_t nb);
+
+// Forward: L1 (bucket + shared) on sorted tiles.
+int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream);
+// Extended WRM: sum of position weights (before the tail).
+int32_t launch_wrm_weight_sum(const float* score, uint32_t n, const LossParams& lp, double* out,
+                              double* scratch, hipStream_t stream);
+// Tail: L1 glue, L2, L3, loss, and (train) their backward with gradient partials.
+int32_t launch_ls_tail(const LsDenseArgs& a, int32_t train, hipStream_t stream);
+// Backward: L1 weight-gradient partials (chunk table built on device).
+int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream);
+// Backward: L1 input gradient fused with the FT-post gradient -> dft, ft_b partials.
+int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream);
+
+// Reduces every dense-group gradient from its partials and applies the
+// optimizer.  grads_out receives the gradients (keep_grads) or zeros.
+struct LsDenseGroup {
+    float *w, *m, *v, *slow, *grad;
+    uint64_t n;
+    float min_w, max_w;
+    int32_t kind;  // 0 ft (unused here), 1 dense, 2 bias
+};
+int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups /*9*/,
+                                 const OptScalars& dense, const OptScalars& bias,
+                                 int32_t apply_update, int32_t keep_grads, hipStream_t stream);
+// Sums the tail loss partials into a.loss_out (deterministic order).
+int32_t launch_ls_loss_reduce(const LsDenseArgs& a, hipStream_t stream);
+
+}  // namespace tatara

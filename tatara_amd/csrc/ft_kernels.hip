@@ -1,0 +1,533 @@
+// Feature-transformer (FT) kernels for gfx950: the sparse gather forward with
+// the FT post activation fused into its store, the deterministic backward
+// (sorted occurrence lists + one sequential accumulator per weight cell) with
+// the RAdam/Ranger update and the factorizer fold fused in, and the
+// scheduling sorts they rely on.
+//
+// Reference semantics:
+//   forward   crates/gpu-kernels/src/sparse/sparse_ft_forward.rs:100-122
+//   post      crates/gpu-kernels/src/layerstack/ft_post_perspective.rs (fwd)
+//             crates/cuda-native-runtime/kernels/native_kernels.cu:1406-1427 (Simple)
+//   backward  crates/gpu-kernels/src/sparse/sparse_ft_backward.rs:247-267 in the
+//             trainer's stm-then-nstm order (gpu_cpu_equivalence_tests.rs:4257-4275)
+//   reduce    crates/gpu-kernels/src/sparse/ft_factorize.rs (ft_reduce_virtual_grad_cpu)
+//   fold      crates/gpu-kernels/src/sparse/ft_factorize.rs (ft_fold_virtual_cpu)
+//   optimizer crates/gpu-kernels/src/pointwise/radam_step.rs:116-149
+#include "ft_kernels.hpp"
+
+#include <hipcub/hipcub.hpp>
+
+#include "common.hpp"
+#include "optim.hpp"
+
+namespace tatara {
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kMaxActive = 64;  // one index per lane
+
+__device__ __forceinline__ float4 f4add(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// Loads the position's active indices into per-wave LDS in slot order,
+// keeping only valid ones (slot < nnz and 0 <= idx < cols), and returns how
+// many there are.  Skipping invalid slots here matches the reference, which
+// skips them in the sum (adding nothing).
+__device__ __forceinline__ int compact_indices(const int32_t* __restrict__ idx_row, int nnz,
+                                               uint32_t cols, uint32_t max_active, int* s_idx) {
+    const int lane = __lane_id();
+    const int n = nnz < (int)max_active ? nnz : (int)max_active;  // never read past the row
+    int v = -1;
+    if (lane < n) v = idx_row[lane];
+    const bool ok = lane < n && v >= 0 && (uint32_t)v < cols;
+    const uint64_t mask = __ballot(ok);
+    const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+    if (ok) s_idx[rank] = v;
+    __builtin_amdgcn_wave_barrier();
+    return __popcll(mask);
+}
+
+// Sums rows idx[0..nv) of W (row length ft_out) at float4 column q (and q2 if
+// TWO), in slot order, starting from +0.0.  Loads of UNROLL rows are issued
+// before their adds so that many 16-byte loads are in flight per lane.
+template <bool TWO, int UNROLL>
+__device__ __forceinline__ void gather_rows(const float* __restrict__ W, uint64_t ft_out,
+                                            const int* s_idx, int nv, uint32_t q, uint32_t q2,
+                                            bool active, float4& a0, float4& a1) {
+    a0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    a1 = a0;
+    if (!active) return;
+    const float4* __restrict__ W4 = reinterpret_cast<const float4*>(W);
+    const uint64_t row4 = ft_out / 4;
+    int k = 0;
+    for (; k + UNROLL <= nv; k += UNROLL) {
+        float4 w0[UNROLL], w1[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const uint64_t r = (uint32_t)__builtin_amdgcn_readfirstlane(s_idx[k + u]);
+            w0[u] = W4[r * row4 + q];
+            if (TWO) w1[u] = W4[r * row4 + q2];
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            a0 = f4add(a0, w0[u]);
+            if (TWO) a1 = f4add(a1, w1[u]);
+        }
+    }
+    for (; k < nv; ++k) {
+        const uint64_t r = (uint32_t)__builtin_amdgcn_readfirstlane(s_idx[k]);
+        const float4 w0 = W4[r * row4 + q];
+        a0 = f4add(a0, w0);
+        if (TWO) {
+            const float4 w1 = W4[r * row4 + q2];
+            a1 = f4add(a1, w1);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward gather.
+//
+// One wave = one task (position, column chunk).  Lane j of chunk c owns float4
+// column q = 64c + j of the row (PAIR mode: q and its pair partner q + half/4,
+// so both halves of each CReLU pair sit in one lane).  Tasks are enumerated
+// (perspective, chunk, position-in-schedule) and the schedule lists positions
+// grouped by king block, so concurrently running waves read rows of the same
+// king block (a few MB) and hit in L2; the XCD swizzle keeps neighbouring
+// tasks on one XCD.
+// ---------------------------------------------------------------------------
+
+enum FwdMode : int { kRaw = 0, kPair = 1, kConcat = 2 };
+
+template <int MODE>
+__global__ __launch_bounds__(256) void ft_forward_kernel(
+    const float* __restrict__ W, const int32_t* __restrict__ idx_stm,
+    const int32_t* __restrict__ idx_nstm, const int32_t* __restrict__ nnz,
+    const int32_t* __restrict__ schedule,  // [n_persp][batch] position order, or null
+    const float* __restrict__ bias, float* __restrict__ out_stm, float* __restrict__ out_nstm,
+    float* __restrict__ combined, uint32_t batch, uint32_t ft_out, uint32_t cols,
+    uint32_t max_active, uint32_t n_chunks, uint32_t n_persp, float scale) {
+    __shared__ int s_idx_all[kWavesPerBlock][kMaxActive];
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
+    const uint64_t per_persp = (uint64_t)n_chunks * batch;
+    if (task >= per_persp * n_persp) return;
+    const uint32_t persp = (uint32_t)(task / per_persp);
+    const uint64_t rem = task - (uint64_t)persp * per_persp;
+    const uint32_t chunk = (uint32_t)(rem / batch);
+    const uint32_t slot = (uint32_t)(rem - (uint64_t)chunk * batch);
+    const uint32_t pos = schedule ? (uint32_t)schedule[(uint64_t)persp * batch + slot] : slot;
+    if (pos >= batch) return;  // a schedule always lists every position once
+
+    const int32_t* idx = persp == 0 ? idx_stm : idx_nstm;
+    float* out = persp == 0 ? out_stm : out_nstm;
+    int* s_idx = s_idx_all[wave];
+    const int nv = compact_indices(idx + (uint64_t)pos * max_active, nnz[pos], cols, max_active, s_idx);
+
+    const uint32_t half4 = ft_out / 8;
+    const uint32_t row4 = ft_out / 4;
+    const uint32_t q = chunk * kWave + lane;
+    float4 a0, a1;
+    if (MODE == kPair) {
+        const bool active = q < half4;
+        gather_rows<true, 8>(W, ft_out, s_idx, nv, q, q + half4, active, a0, a1);
+        if (!active) return;
+        float4* o4 = reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out);
+        o4[q] = a0;
+        o4[q + half4] = a1;
+        const float4 b0 = reinterpret_cast<const float4*>(bias)[q];
+        const float4 b1 = reinterpret_cast<const float4*>(bias)[q + half4];
+        float4 c;
+        c.x = crelu01(a0.x + b0.x) * crelu01(a1.x + b1.x) * scale;
+        c.y = crelu01(a0.y + b0.y) * crelu01(a1.y + b1.y) * scale;
+        c.z = crelu01(a0.z + b0.z) * crelu01(a1.z + b1.z) * scale;
+        c.w = crelu01(a0.w + b0.w) * crelu01(a1.w + b1.w) * scale;
+        reinterpret_cast<float4*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2))[q] = c;
+    } else {
+        const bool active = q < row4;
+        gather_rows<false, 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
+        if (!active) return;
+        if (MODE == kRaw) {
+            reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out)[q] = a0;
+        } else {
+            // Simple: ft_out += bias in place, combined[off + c] = crelu(x).
+            const float4 b0 = reinterpret_cast<const float4*>(bias)[q];
+            const float4 x = f4add(a0, b0);
+            reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out)[q] = x;
+            float4 c;
+            c.x = crelu01(x.x);
+            c.y = crelu01(x.y);
+            c.z = crelu01(x.z);
+            c.w = crelu01(x.w);
+            reinterpret_cast<float4*>(combined + (uint64_t)pos * 2 * ft_out + persp * ft_out)[q] = c;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward schedule keys: item p*batch + b gets key p*n_bins + (king block of
+// position b in perspective p), where the king block is the first valid
+// index divided by piece_inputs.  A stable bin sort of these keys yields,
+// per perspective, the positions grouped by king block in ascending order.
+// ---------------------------------------------------------------------------
+
+__global__ void king_block_keys_kernel(const int32_t* __restrict__ idx_stm,
+                                       const int32_t* __restrict__ idx_nstm,
+                                       const int32_t* __restrict__ nnz, uint8_t* __restrict__ keys,
+                                       uint32_t batch, uint32_t max_active, uint32_t cols,
+                                       uint32_t piece_inputs, uint32_t n_bins) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 2ull * batch) return;
+    const uint32_t persp = i >= batch ? 1u : 0u;
+    const uint32_t b = (uint32_t)(i - (uint64_t)persp * batch);
+    const int32_t* row = (persp ? idx_nstm : idx_stm) + (uint64_t)b * max_active;
+    const int n = nnz[b] < (int)max_active ? nnz[b] : (int)max_active;
+    uint32_t k = 0;
+    for (int s = 0; s < n; ++s) {
+        const int32_t v = row[s];
+        if (v >= 0 && (uint32_t)v < cols) {
+            k = piece_inputs ? (uint32_t)v / piece_inputs : 0u;
+            if (k >= n_bins) k = n_bins - 1;
+            break;
+        }
+    }
+    keys[i] = (uint8_t)(persp * n_bins + k);
+}
+
+// ---------------------------------------------------------------------------
+// Occurrence lists for the backward: key = 2*feature + perspective, value =
+// perspective*batch + position (a row of the concatenated [2][batch][ft_out]
+// dft buffer).  Items are emitted in (perspective, position, slot) order and
+// sorted stably, so each key's list is in ascending position order: the same
+// order in which the reference CPU backward accumulates.
+// ---------------------------------------------------------------------------
+
+__global__ void build_occurrence_keys_kernel(const int32_t* __restrict__ idx_stm,
+                                             const int32_t* __restrict__ idx_nstm,
+                                             const int32_t* __restrict__ nnz,
+                                             uint32_t* __restrict__ keys,
+                                             uint32_t* __restrict__ vals,
+                                             uint32_t* __restrict__ counts, uint32_t batch,
+                                             uint32_t max_active, uint32_t cols) {
+    const uint64_t per = (uint64_t)batch * max_active;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 2 * per) return;
+    const uint32_t persp = i >= per ? 1u : 0u;
+    const uint64_t j = i - persp * per;
+    const uint32_t b = (uint32_t)(j / max_active);
+    const uint32_t slot = (uint32_t)(j - (uint64_t)b * max_active);
+    const int32_t v = (persp ? idx_nstm : idx_stm)[j];
+    const bool ok = (int)slot < nnz[b] && v >= 0 && (uint32_t)v < cols;
+    const uint32_t key = ok ? 2u * (uint32_t)v + persp : 2u * cols;
+    keys[i] = key;
+    vals[i] = persp * batch + b;
+    if (ok) atomicAdd(&counts[key], 1u);
+}
+
+// ---------------------------------------------------------------------------
+// Backward + optimizer + fold.
+//
+// One wave = one task (row group g, column chunk c).  A group is the rows
+// g + j*stride for j < count (for the factorizer: the king-bucket copies of
+// piece g) followed by the virtual row virt_base + g when has_virtual.
+// For each real row f the gradient is the sequential sum, from +0.0, of the
+// dft rows listed in its occurrence segment [off[2f], off[2f+2]) - stm
+// occurrences in ascending position order, then nstm ones - which is exactly
+// the order of the reference CPU backward.  The virtual row's gradient is the
+// sequential sum of the group's real-row gradients in ascending row order
+// (ft_reduce_virtual_grad_cpu).  Each row is then updated with RAdam (+ the
+// Ranger lerp on lookahead steps) and, with a virtual row, the forward table
+// comb = w + w_virtual is rewritten for the group.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float4 segment_sum(const float4* __restrict__ dft4, uint64_t row4,
+                                              const uint32_t* __restrict__ vals, uint32_t s,
+                                              uint32_t e, uint32_t q) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    constexpr int U = 8;
+    uint32_t i = s;
+    for (; i + U <= e; i += U) {
+        float4 d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i + u]);
+            d[u] = dft4[r * row4 + q];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = f4add(acc, d[u]);
+    }
+    for (; i < e; ++i) {
+        const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i]);
+        acc = f4add(acc, dft4[r * row4 + q]);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ void opt_update4(float* __restrict__ w, float* __restrict__ m,
+                                            float* __restrict__ v, float* __restrict__ slow,
+                                            uint64_t off4, float4 g, const OptScalars& s) {
+    float4 W = reinterpret_cast<float4*>(w)[off4];
+    float4 M = reinterpret_cast<float4*>(m)[off4];
+    float4 V = reinterpret_cast<float4*>(v)[off4];
+    radam_elem(W.x, M.x, V.x, g.x, s);
+    radam_elem(W.y, M.y, V.y, g.y, s);
+    radam_elem(W.z, M.z, V.z, g.z, s);
+    radam_elem(W.w, M.w, V.w, g.w, s);
+    if (s.lookahead) {
+        float4 S = reinterpret_cast<float4*>(slow)[off4];
+        lerp_elem(W.x, S.x, s.alpha);
+        lerp_elem(W.y, S.y, s.alpha);
+        lerp_elem(W.z, S.z, s.alpha);
+        lerp_elem(W.w, S.w, s.alpha);
+        reinterpret_cast<float4*>(slow)[off4] = S;
+    }
+    reinterpret_cast<float4*>(w)[off4] = W;
+    reinterpret_cast<float4*>(m)[off4] = M;
+    reinterpret_cast<float4*>(v)[off4] = V;
+}
+
+__global__ __launch_bounds__(256) void ft_backward_optimizer_kernel(
+    const float* __restrict__ dft,  // [2][batch][ft_out]
+    const uint32_t* __restrict__ occ_vals, const uint32_t* __restrict__ occ_off,
+    float* __restrict__ w, float* __restrict__ m, float* __restrict__ v, float* __restrict__ slow,
+    float* __restrict__ comb,      // forward table, written when has_virtual (may be null)
+    float* __restrict__ grad_out,  // optional: the gradient each row received (may be null)
+    uint32_t ft_out, uint32_t n_groups, uint32_t stride, uint32_t count, uint32_t has_virtual,
+    uint32_t virt_base, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t task = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
+    if (task >= (uint64_t)n_groups * n_chunks) return;
+    // Chunk-major enumeration: concurrently running waves share a column chunk
+    // and walk king blocks in step, so the dft rows they gather overlap.
+    const uint32_t chunk = (uint32_t)(task / n_groups);
+    const uint32_t g = (uint32_t)(task - (uint64_t)chunk * n_groups);
+    const uint32_t row4 = ft_out / 4;
+    const uint32_t q = chunk * kWave + lane;
+    const bool active = q < row4;
+    const float4* dft4 = reinterpret_cast<const float4*>(dft);
+    float4 vsum = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t j = 0; j < count; ++j) {
+        const uint32_t f = g + j * stride;
+        const uint32_t s0 = __builtin_amdgcn_readfirstlane(occ_off[2 * f]);
+        const uint32_t s1 = __builtin_amdgcn_readfirstlane(occ_off[2 * f + 2]);
+        if (!active) continue;
+        const float4 gr = segment_sum(dft4, row4, occ_vals, s0, s1, q);
+        if (has_virtual) vsum = f4add(vsum, gr);
+        const uint64_t off4 = (uint64_t)f * row4 + q;
+        if (grad_out) reinterpret_cast<float4*>(grad_out)[off4] = gr;
+        if (apply_update) opt_update4(w, m, v, slow, off4, gr, s);
+    }
+    if (!active || !has_virtual) return;
+    const uint64_t voff4 = (uint64_t)(virt_base + g) * row4 + q;
+    if (grad_out) reinterpret_cast<float4*>(grad_out)[voff4] = vsum;
+    if (!apply_update) return;
+    opt_update4(w, m, v, slow, voff4, vsum, s);
+    if (!comb) return;
+    const float4 wv = reinterpret_cast<const float4*>(w)[voff4];
+    for (uint32_t j = 0; j < count; ++j) {
+        const uint64_t off4 = (uint64_t)(g + j * stride) * row4 + q;
+        const float4 wr = reinterpret_cast<const float4*>(w)[off4];
+        reinterpret_cast<float4*>(comb)[off4] = f4add(wr, wv);
+    }
+}
+
+// Standalone fold / reduce (Base mode), used when they are not fused.
+__global__ void ft_fold_kernel(const float* __restrict__ w, float* __restrict__ comb,
+                               uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs) {
+    const uint64_t n4 = (uint64_t)ft_in * ft_out / 4;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const uint32_t row4 = ft_out / 4;
+    const uint64_t f = i / row4;
+    const uint32_t c = (uint32_t)(i - f * row4);
+    const uint64_t vrow = ft_in + f % piece_inputs;
+    reinterpret_cast<float4*>(comb)[i] =
+        f4add(reinterpret_cast<const float4*>(w)[i], reinterpret_cast<const float4*>(w)[vrow * row4 + c]);
+}
+
+__global__ void ft_reduce_kernel(float* __restrict__ grad, uint32_t ft_in, uint32_t ft_out,
+                                 uint32_t piece_inputs) {
+    const uint64_t n = (uint64_t)piece_inputs * ft_out;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t v = i / ft_out;
+    const uint32_t c = (uint32_t)(i - v * ft_out);
+    float sum = 0.0f;
+    for (uint64_t f = v; f < ft_in; f += piece_inputs) sum += grad[f * ft_out + c];
+    grad[((uint64_t)ft_in + v) * ft_out + c] = sum;
+}
+
+__global__ void radam_kernel(float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
+                             float* __restrict__ g, float* __restrict__ slow, uint64_t n,
+                             OptScalars s) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float W = w[i], M = m[i], V = v[i];
+    radam_elem(W, M, V, g[i], s);
+    if (s.lookahead) {
+        float S = slow[i];
+        lerp_elem(W, S, s.alpha);
+        slow[i] = S;
+    }
+    w[i] = W;
+    m[i] = M;
+    v[i] = V;
+    g[i] = 0.0f;
+}
+
+__global__ void lerp_kernel(float* __restrict__ w, float* __restrict__ slow, uint64_t n,
+                            float alpha) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float W = w[i], S = slow[i];
+    lerp_elem(W, S, alpha);
+    w[i] = W;
+    slow[i] = S;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+
+int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
+    TATARA_REQUIRE(a.max_active <= (uint32_t)kMaxActive, "max_active must be <= 64");
+    TATARA_REQUIRE(a.ft_out % 8 == 0, "ft_out must be a multiple of 8");
+    TATARA_REQUIRE(a.n_persp == 1 || a.n_persp == 2, "n_persp must be 1 or 2");
+    if (a.batch == 0) return kOk;
+    const uint32_t lanes_needed = a.mode == kPair ? a.ft_out / 8 : a.ft_out / 4;
+    const uint32_t n_chunks = ceil_div(lanes_needed, kWave);
+    const uint64_t tasks = (uint64_t)a.n_persp * n_chunks * a.batch;
+    const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+    switch (a.mode) {
+        case kRaw:
+            ft_forward_kernel<kRaw><<<blocks, 256, 0, stream>>>(
+                a.W, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm,
+                a.combined, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale);
+            break;
+        case kPair:
+            ft_forward_kernel<kPair><<<blocks, 256, 0, stream>>>(
+                a.W, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm,
+                a.combined, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale);
+            break;
+        case kConcat:
+            ft_forward_kernel<kConcat><<<blocks, 256, 0, stream>>>(
+                a.W, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm,
+                a.combined, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale);
+            break;
+        default:
+            TATARA_REQUIRE(false, "unknown forward mode");
+    }
+    TATARA_LAUNCHED("ft_forward");
+    return kOk;
+}
+
+int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm,
+                               const int32_t* nnz, uint8_t* keys, uint32_t batch,
+                               uint32_t max_active, uint32_t cols, uint32_t piece_inputs,
+                               uint32_t n_bins, hipStream_t stream) {
+    if (batch == 0) return kOk;
+    TATARA_REQUIRE(2 * n_bins <= 256, "king block keys: 2*n_bins <= 256");
+    king_block_keys_kernel<<<ceil_div(2ull * batch, 256), 256, 0, stream>>>(
+        idx_stm, idx_nstm, nnz, keys, batch, max_active, cols, piece_inputs, n_bins);
+    TATARA_LAUNCHED("king_block_keys");
+    return kOk;
+}
+
+uint32_t occurrence_key_bits(uint32_t cols) {
+    uint32_t bits = 1;
+    while ((1ull << bits) <= 2ull * cols) ++bits;
+    return bits;
+}
+
+size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols) {
+    const uint32_t key_bits = occurrence_key_bits(cols);
+    size_t bytes = 0;
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                       (const uint32_t*)nullptr, (uint32_t*)nullptr, (int)n_items,
+                                       0, (int)key_bits);
+    size_t scan_bytes = 0;
+    (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, (const uint32_t*)nullptr,
+                                           (uint32_t*)nullptr, (int)(2ull * cols + 2));
+    return bytes > scan_bytes ? bytes : scan_bytes;
+}
+
+int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) {
+    const uint64_t n_items = 2ull * a.batch * a.max_active;
+    const uint32_t n_keys = 2 * a.cols + 1;
+    TATARA_HIP(hipMemsetAsync(a.counts, 0, sizeof(uint32_t) * (n_keys + 1), stream),
+               "memset occurrence counts");
+    if (n_items > 0) {
+        build_occurrence_keys_kernel<<<ceil_div(n_items, 256), 256, 0, stream>>>(
+            a.idx_stm, a.idx_nstm, a.nnz, a.keys_in, a.vals_in, a.counts, a.batch, a.max_active,
+            a.cols);
+        TATARA_LAUNCHED("build_occurrence_keys");
+        size_t bytes = a.temp_bytes;
+        TATARA_HIP(hipcub::DeviceRadixSort::SortPairs(a.temp, bytes, a.keys_in, a.keys_out,
+                                                      a.vals_in, a.vals_out, (int)n_items, 0,
+                                                      (int)occurrence_key_bits(a.cols), stream),
+                   "occurrence radix sort");
+    }
+    size_t bytes = a.temp_bytes;
+    TATARA_HIP(hipcub::DeviceScan::ExclusiveSum(a.temp, bytes, a.counts, a.offsets, (int)n_keys + 1,
+                                                stream),
+               "occurrence offsets scan");
+    return kOk;
+}
+
+int32_t launch_ft_backward_optimizer(const FtBackwardArgs& a, hipStream_t stream) {
+    TATARA_REQUIRE(a.ft_out % 4 == 0, "ft_out must be a multiple of 4");
+    const uint32_t n_chunks = ceil_div(a.ft_out / 4, kWave);
+    const uint64_t tasks = (uint64_t)a.n_groups * n_chunks;
+    if (tasks == 0) return kOk;
+    const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+    ft_backward_optimizer_kernel<<<blocks, 256, 0, stream>>>(
+        a.dft, a.occ_vals, a.occ_off, a.w, a.m, a.v, a.slow, a.comb, a.grad_out, a.ft_out,
+        a.n_groups, a.stride, a.count, a.has_virtual, a.virt_base, n_chunks, a.apply_update, a.opt);
+    TATARA_LAUNCHED("ft_backward_optimizer");
+    return kOk;
+}
+
+int32_t launch_ft_fold(const float* w, float* comb, uint32_t ft_in, uint32_t ft_out,
+                       uint32_t piece_inputs, hipStream_t stream) {
+    TATARA_REQUIRE(ft_out % 4 == 0 && piece_inputs > 0, "fold: ft_out%4==0, piece_inputs>0");
+    const uint64_t n4 = (uint64_t)ft_in * ft_out / 4;
+    if (n4 == 0) return kOk;
+    ft_fold_kernel<<<ceil_div(n4, 256), 256, 0, stream>>>(w, comb, ft_in, ft_out, piece_inputs);
+    TATARA_LAUNCHED("ft_fold");
+    return kOk;
+}
+
+int32_t launch_ft_reduce(float* grad, uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs,
+                         hipStream_t stream) {
+    TATARA_REQUIRE(piece_inputs > 0, "reduce: piece_inputs > 0");
+    const uint64_t n = (uint64_t)piece_inputs * ft_out;
+    if (n == 0) return kOk;
+    ft_reduce_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(grad, ft_in, ft_out, piece_inputs);
+    TATARA_LAUNCHED("ft_reduce");
+    return kOk;
+}
+
+int32_t launch_radam(float* w, float* m, float* v, float* g, float* slow, uint64_t n,
+                     const OptScalars& s, hipStream_t stream) {
+    if (n == 0) return kOk;
+    radam_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(w, m, v, g, slow, n, s);
+    TATARA_LAUNCHED("radam_step");
+    return kOk;
+}
+
+int32_t launch_lerp(float* w, float* slow, uint64_t n, float alpha, hipStream_t stream) {
+    if (n == 0) return kOk;
+    lerp_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(w, slow, n, alpha);
+    TATARA_LAUNCHED("ranger_lookahead_lerp");
+    return kOk;
+}
+
+}  // namespace tatara

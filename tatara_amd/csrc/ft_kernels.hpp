@@ -1,0 +1,73 @@
+// Host launchers of the FT kernels (see ft_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "optim.hpp"
+
+namespace tatara {
+
+struct FtForwardArgs {
+    int mode;  // 0 raw sum, 1 LayerStack pairwise post, 2 Simple concat post
+    const float* W;
+    const int32_t* idx_stm;
+    const int32_t* idx_nstm;
+    const int32_t* nnz;
+    const int32_t* schedule;  // [n_persp][batch] or null (identity order)
+    const float* bias;
+    float* out_stm;
+    float* out_nstm;
+    float* combined;
+    uint32_t batch, ft_out, cols, max_active, n_persp;
+    float scale;
+};
+
+struct OccurrenceSortArgs {
+    const int32_t* idx_stm;
+    const int32_t* idx_nstm;
+    const int32_t* nnz;
+    uint32_t batch, max_active, cols;
+    uint32_t* keys_in;   // [2*batch*max_active]
+    uint32_t* vals_in;
+    uint32_t* keys_out;
+    uint32_t* vals_out;  // sorted dft row ids
+    uint32_t* counts;    // [2*cols + 2]
+    uint32_t* offsets;   // [2*cols + 2]; key k occupies [offsets[k], offsets[k+1])
+    void* temp;
+    size_t temp_bytes;
+};
+
+struct FtBackwardArgs {
+    const float* dft;          // [2][batch][ft_out]
+    const uint32_t* occ_vals;  // sorted dft row ids
+    const uint32_t* occ_off;   // offsets by key 2*f+p
+    float *w, *m, *v, *slow;
+    float* comb;               // forward table (factorized) or null
+    float* grad_out;           // optional gradient dump or null
+    uint32_t ft_out;
+    uint32_t n_groups, stride, count;  // group g = rows g + j*stride, j < count
+    uint32_t has_virtual, virt_base;   // virtual row virt_base + g
+    int32_t apply_update;              // 0: only dump gradients
+    OptScalars opt;
+};
+
+int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream);
+int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm, const int32_t* nnz,
+                               uint8_t* keys, uint32_t batch, uint32_t max_active, uint32_t cols,
+                               uint32_t piece_inputs, uint32_t n_bins, hipStream_t stream);
+uint32_t occurrence_key_bits(uint32_t cols);
+size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols);
+int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream);
+int32_t launch_ft_backward_optimizer(const FtBackwardArgs& a, hipStream_t stream);
+int32_t launch_ft_fold(const float* w, float* comb, uint32_t ft_in, uint32_t ft_out,
+                       uint32_t piece_inputs, hipStream_t stream);
+int32_t launch_ft_reduce(float* grad, uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs,
+                         hipStream_t stream);
+int32_t launch_radam(float* w, float* m, float* v, float* g, float* slow, uint64_t n,
+                     const OptScalars& s, hipStream_t stream);
+int32_t launch_lerp(float* w, float* slow, uint64_t n, float alpha, hipStream_t stream);
+
+}  // namespace tatara

@@ -1,0 +1,300 @@
+// C ABI: error reporting, device runtime surface and kernel-level ops.
+//
+// The runtime calls mirror crates/gpu-runtime/src/lib.rs:50-126 and
+// native_backend.rs:17-300 (DeviceBuffer, memset, synchronize, device
+// queries); the op calls wrap one reference kernel family each so that tests
+// can check them against the CPU oracle kernel by kernel, as
+// bins/nnue_train/src/tests/gpu_cpu_equivalence_tests.rs does.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/tatara_hip.h"
+#include "binsort.hpp"
+#include "common.hpp"
+#include "ft_kernels.hpp"
+
+namespace tatara {
+
+namespace {
+thread_local std::string g_last_error = "no error";
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+const char* last_error() { return g_last_error.c_str(); }
+
+int32_t hip_status(hipError_t e, const char* what) {
+    std::string msg = "HIP error " + std::to_string((int)e) + ": " + hipGetErrorName(e) + ": " +
+                      hipGetErrorString(e) + " [" + what + "]";
+    set_error(msg);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return kErrOutOfMemory;
+    return kErrHip;
+}
+
+// Scoped device allocation for the standalone ops.
+struct DevScratch {
+    void* p = nullptr;
+    ~DevScratch() {
+        if (p) (void)hipFree(p);
+    }
+    int32_t alloc(size_t bytes) {
+        if (bytes == 0) bytes = 4;
+        TATARA_HIP(hipMalloc(&p, bytes), "hipMalloc scratch");
+        return kOk;
+    }
+    template <class T>
+    T* as() {
+        return static_cast<T*>(p);
+    }
+};
+
+}  // namespace tatara
+
+using namespace tatara;
+
+extern "C" {
+
+const char* tatara_last_error(void) { return last_error(); }
+const char* tatara_version(void) { return "tatara-mi355x 0.1.0 (gfx950)"; }
+
+int32_t tatara_device_count(int32_t* count) {
+    TATARA_REQUIRE(count, "count is null");
+    int n = 0;
+    TATARA_HIP(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    *count = n;
+    return kOk;
+}
+
+int32_t tatara_set_device(int32_t device) {
+    TATARA_HIP(hipSetDevice(device), "hipSetDevice");
+    return kOk;
+}
+
+int32_t tatara_device_info(int32_t device, char* name, int32_t name_len, int32_t* cu_count) {
+    hipDeviceProp_t prop;
+    TATARA_HIP(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (name && name_len > 0) {
+        std::strncpy(name, prop.gcnArchName, (size_t)name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    return kOk;
+}
+
+int32_t tatara_malloc(void** ptr, uint64_t bytes) {
+    TATARA_REQUIRE(ptr, "ptr is null");
+    *ptr = nullptr;
+    TATARA_HIP(hipMalloc(ptr, bytes ? bytes : 4), "hipMalloc");
+    return kOk;
+}
+
+int32_t tatara_free(void* ptr) {
+    if (ptr) TATARA_HIP(hipFree(ptr), "hipFree");
+    return kOk;
+}
+
+int32_t tatara_memcpy_htod(void* dst, const void* src, uint64_t bytes) {
+    if (bytes) TATARA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    return kOk;
+}
+
+int32_t tatara_memcpy_dtoh(void* dst, const void* src, uint64_t bytes) {
+    if (bytes) TATARA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return kOk;
+}
+
+int32_t tatara_memset(void* dst, int32_t byte, uint64_t bytes) {
+    if (bytes) TATARA_HIP(hipMemset(dst, byte, bytes), "hipMemset");
+    return kOk;
+}
+
+int32_t tatara_synchronize(void) {
+    TATARA_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return kOk;
+}
+
+int32_t tatara_radam_step_size_denom(uint64_t step, float beta1, float beta2,
+                                     float n_sma_threshold, float* step_size, int32_t* denom) {
+    TATARA_REQUIRE(step >= 1, "step must be >= 1");
+    TATARA_REQUIRE(step_size && denom, "null output");
+    const float step_f = (float)step;
+    const float beta2_t = std::pow(beta2, step_f);
+    const float n_sma_max = 2.0f / (1.0f - beta2) - 1.0f;
+    const float n_sma = n_sma_max - 2.0f * step_f * beta2_t / (1.0f - beta2_t);
+    const float bc1 = 1.0f - std::pow(beta1, step_f);
+    float ss;
+    if (n_sma > n_sma_threshold) {
+        const float p1 = (n_sma - 4.0f) / (n_sma_max - 4.0f);
+        const float p2 = (n_sma - 2.0f) / n_sma;
+        const float p3 = n_sma_max / (n_sma_max - 2.0f);
+        ss = std::sqrt((1.0f - beta2_t) * p1 * p2 * p3) / bc1;
+    } else {
+        ss = 1.0f / bc1;
+    }
+    *step_size = ss;
+    *denom = n_sma > n_sma_threshold ? 1 : 0;
+    return kOk;
+}
+
+int32_t tatara_op_sparse_ft_forward(const float* weight, const int32_t* indices,
+                                    const int32_t* nnz, float* out, uint32_t batch, uint32_t rows,
+                                    uint32_t cols, uint32_t max_active) {
+    TATARA_REQUIRE(rows % 8 == 0, "rows must be a multiple of 8");
+    FtForwardArgs a{};
+    a.mode = 0;
+    a.W = weight;
+    a.idx_stm = indices;
+    a.idx_nstm = indices;
+    a.nnz = nnz;
+    a.out_stm = out;
+    a.out_nstm = out;
+    a.batch = batch;
+    a.ft_out = rows;
+    a.cols = cols;
+    a.max_active = max_active;
+    a.n_persp = 1;
+    int32_t st = launch_ft_forward(a, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "sparse_ft_forward");
+    return kOk;
+}
+
+int32_t tatara_op_ft_forward_pairwise(const float* weight, const int32_t* stm_idx,
+                                      const int32_t* nstm_idx, const int32_t* nnz,
+                                      const float* bias, float* stm_out, float* nstm_out,
+                                      float* combined, uint32_t batch, uint32_t ft_out,
+                                      uint32_t cols, uint32_t max_active, uint32_t piece_inputs,
+                                      float scale) {
+    TATARA_REQUIRE(ft_out % 8 == 0, "ft_out must be a multiple of 8");
+    DevScratch keys, sched, hist, bstart, bcount;
+    int32_t* schedule = nullptr;
+    if (piece_inputs > 0 && batch > 0) {
+        uint32_t n_bins = ceil_div(cols, piece_inputs);
+        if (n_bins > 128) n_bins = 128;
+        int32_t st;
+        if ((st = keys.alloc(2ull * batch)) || (st = sched.alloc(8ull * batch)) ||
+            (st = hist.alloc(4ull * 2 * n_bins * binsort_tiles(2 * batch))) ||
+            (st = bstart.alloc(4ull * (2 * n_bins + 1))) || (st = bcount.alloc(4ull * 2 * n_bins)))
+            return st;
+        st = launch_king_block_keys(stm_idx, nstm_idx, nnz, keys.as<uint8_t>(), batch, max_active,
+                                    cols, piece_inputs, n_bins, 0);
+        if (st) return st;
+        BinSortArgs bs{};
+        bs.keys = keys.as<uint8_t>();
+        bs.n_items = 2 * batch;
+        bs.n_bins = 2 * n_bins;
+        bs.align = 1;
+        bs.value_mod = batch;
+        bs.hist = hist.as<uint32_t>();
+        bs.bin_start = bstart.as<uint32_t>();
+        bs.bin_count = bcount.as<uint32_t>();
+        bs.out = sched.as<int32_t>();
+        st = launch_binsort(bs, 0);
+        if (st) return st;
+        schedule = sched.as<int32_t>();
+    }
+    FtForwardArgs a{};
+    a.mode = 1;
+    a.W = weight;
+    a.idx_stm = stm_idx;
+    a.idx_nstm = nstm_idx;
+    a.nnz = nnz;
+    a.schedule = schedule;
+    a.bias = bias;
+    a.out_stm = stm_out;
+    a.out_nstm = nstm_out;
+    a.combined = combined;
+    a.batch = batch;
+    a.ft_out = ft_out;
+    a.cols = cols;
+    a.max_active = max_active;
+    a.n_persp = 2;
+    a.scale = scale;
+    int32_t st = launch_ft_forward(a, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "ft_forward_pairwise");
+    return kOk;
+}
+
+int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
+                                 const int32_t* nstm_idx, const int32_t* nnz, float* grad,
+                                 uint32_t batch, uint32_t ft_out, uint32_t cols,
+                                 uint32_t max_active) {
+    TATARA_REQUIRE(ft_out % 4 == 0, "ft_out must be a multiple of 4");
+    const uint64_t n_items = 2ull * batch * max_active;
+    const uint32_t n_keys = 2 * cols + 1;
+    DevScratch ki, vi, ko, vo, cnt, off, tmp;
+    const size_t tb = occurrence_sort_temp_bytes(n_items, cols);
+    int32_t st;
+    if ((st = ki.alloc(4 * n_items)) || (st = vi.alloc(4 * n_items)) || (st = ko.alloc(4 * n_items)) ||
+        (st = vo.alloc(4 * n_items)) || (st = cnt.alloc(4ull * (n_keys + 1))) ||
+        (st = off.alloc(4ull * (n_keys + 1))) || (st = tmp.alloc(tb)))
+        return st;
+    OccurrenceSortArgs os{};
+    os.idx_stm = stm_idx;
+    os.idx_nstm = nstm_idx;
+    os.nnz = nnz;
+    os.batch = batch;
+    os.max_active = max_active;
+    os.cols = cols;
+    os.keys_in = ki.as<uint32_t>();
+    os.vals_in = vi.as<uint32_t>();
+    os.keys_out = ko.as<uint32_t>();
+    os.vals_out = vo.as<uint32_t>();
+    os.counts = cnt.as<uint32_t>();
+    os.offsets = off.as<uint32_t>();
+    os.temp = tmp.p;
+    os.temp_bytes = tb;
+    if ((st = launch_occurrence_sort(os, 0))) return st;
+    FtBackwardArgs b{};
+    b.dft = dft;
+    b.occ_vals = vo.as<uint32_t>();
+    b.occ_off = off.as<uint32_t>();
+    b.grad_out = grad;
+    b.ft_out = ft_out;
+    b.n_groups = cols;
+    b.stride = 0;
+    b.count = 1;
+    b.has_virtual = 0;
+    b.apply_update = 0;
+    if ((st = launch_ft_backward_optimizer(b, 0))) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "ft_weight_grad");
+    return kOk;
+}
+
+int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,
+                                  uint32_t ft_out, uint32_t piece_inputs) {
+    int32_t st = launch_ft_fold(weight, comb, ft_in, ft_out, piece_inputs, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "ft_fold_virtual");
+    return kOk;
+}
+
+int32_t tatara_op_ft_reduce_virtual_grad(float* grad, uint32_t ft_in, uint32_t ft_out,
+                                         uint32_t piece_inputs) {
+    int32_t st = launch_ft_reduce(grad, ft_in, ft_out, piece_inputs, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "ft_reduce_virtual_grad");
+    return kOk;
+}
+
+int32_t tatara_op_radam_step(float* weights, float* m, float* v, float* grad, float lr,
+                             float step_size, int32_t denom, float decay, float beta1,
+                             float beta2, float eps, float min_w, float max_w, uint64_t n) {
+    OptScalars s{lr, step_size, denom, decay, beta1, beta2, eps, min_w, max_w, 0, 0.0f};
+    int32_t st = launch_radam(weights, m, v, grad, nullptr, n, s, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "radam_step");
+    return kOk;
+}
+
+int32_t tatara_op_ranger_lookahead_lerp(float* weights, float* slow, float alpha, uint64_t n) {
+    int32_t st = launch_lerp(weights, slow, n, alpha, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "ranger_lookahead_lerp");
+    return kOk;
+}
+
+}  // extern "C"

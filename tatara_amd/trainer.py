@@ -1,0 +1,362 @@
+"""Host-side mirror of tatara's step API over the HIP C ABI.
+
+`LayerStackTrainer` follows `trait TrainerBackend`
+(crates/nnue-train/src/trainer.rs:273-375) as GpuTrainer implements it
+(bins/nnue_train/src/trainer_layerstack.rs:1885-2010): `train_step` returns
+the previous step's sum of squared errors (0.0 on the first call),
+`flush_pending_loss` drains the last one, `validate_step` runs forward + loss
+only.  `Batch` mirrors crates/nnue-train/src/dataloader.rs:355-369 and
+`Sigmoid` / `Wrm` mirror `LossKind` (trainer.rs:89-135).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from ._lib import TataraBatch, TataraLoss, TataraTrainerConfig, check
+
+OPTIMIZERS = {"ranger": 0, "radam": 1, "adamw": 2}
+GROUPS = (
+    "ft_w",
+    "ft_b",
+    "l1_w",
+    "l1_b",
+    "l1_shared_weight",
+    "l1_shared_bias",
+    "l2_w",
+    "l2_b",
+    "l3_w",
+    "l3_b",
+)
+WHICH = {"w": 0, "m": 1, "v": 2, "slow": 3, "grad": 4}
+
+
+@dataclass(frozen=True)
+class Sigmoid:
+    """LossKind::Sigmoid (sigmoid-MSE); LayerStack default scale 1/290."""
+
+    scale: float = 1.0 / 290.0
+
+    def to_c(self) -> TataraLoss:
+        return TataraLoss(kind=0, scale=self.scale)
+
+
+@dataclass(frozen=True)
+class Wrm:
+    """LossKind::Wrm (win-rate-model loss)."""
+
+    nnue2score: float = 600.0
+    in_scaling: float = 340.0
+    in_offset: float = 270.0
+    target_offset: float = 270.0
+    target_scaling: float = 380.0
+    pow_exp: float = 2.0
+    qp_asymmetry: float = 0.0
+    weight_boost_w1: float = 0.0
+    weight_boost_w2: float = 0.5
+
+    @property
+    def extended(self) -> bool:
+        return self.pow_exp != 2.0 or self.qp_asymmetry != 0.0 or self.weight_boost_w1 != 0.0
+
+    def to_c(self) -> TataraLoss:
+        return TataraLoss(
+            kind=1,
+            scale=0.0,
+            nnue2score=self.nnue2score,
+            in_scaling=self.in_scaling,
+            in_offset=self.in_offset,
+            target_offset=self.target_offset,
+            target_scaling=self.target_scaling,
+            pow_exp=self.pow_exp,
+            qp_asymmetry=self.qp_asymmetry,
+            weight_boost_w1=self.weight_boost_w1,
+            weight_boost_w2=self.weight_boost_w2,
+        )
+
+
+@dataclass
+class Batch:
+    """One training batch: [n_pos, max_active] index rows (-1 padding)."""
+
+    stm_indices: np.ndarray
+    nstm_indices: np.ndarray
+    nnz: np.ndarray
+    score: np.ndarray
+    wdl: np.ndarray
+
+    def __post_init__(self):
+        self.stm_indices = np.ascontiguousarray(self.stm_indices, dtype=np.int32)
+        self.nstm_indices = np.ascontiguousarray(self.nstm_indices, dtype=np.int32)
+        self.nnz = np.ascontiguousarray(self.nnz, dtype=np.int32)
+        self.score = np.ascontiguousarray(self.score, dtype=np.float32)
+        self.wdl = np.ascontiguousarray(self.wdl, dtype=np.float32)
+        if self.stm_indices.ndim != 2 or self.stm_indices.shape != self.nstm_indices.shape:
+            raise ValueError("index arrays must both be [n_pos, max_active]")
+
+    @property
+    def n_positions(self) -> int:
+        return int(self.stm_indices.shape[0])
+
+    @property
+    def max_active(self) -> int:
+        return int(self.stm_indices.shape[1])
+
+
+class DeviceArray:
+    """A device allocation owned by the library (DeviceBuffer::from_host)."""
+
+    def __init__(self, host: np.ndarray):
+        host = np.ascontiguousarray(host)
+        self.dtype = host.dtype
+        self.shape = host.shape
+        self.nbytes = host.nbytes
+        lib = _lib.load()
+        ptr = C.c_void_p()
+        check(lib.tatara_malloc(C.byref(ptr), self.nbytes))
+        self.ptr = ptr.value
+        check(lib.tatara_memcpy_htod(self.ptr, host.ctypes.data, self.nbytes))
+
+    @classmethod
+    def empty(cls, shape, dtype) -> "DeviceArray":
+        return cls(np.zeros(shape, dtype=dtype))
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        check(_lib.load().tatara_memcpy_dtoh(out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            _lib.load().tatara_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class DeviceBatch:
+    """A batch resident in device memory (inputs already in HBM)."""
+
+    n_pos: int
+    max_active: int
+    arrays: dict = field(default_factory=dict)
+
+    @classmethod
+    def upload(cls, batch: Batch, bucket_idx: np.ndarray) -> "DeviceBatch":
+        db = cls(batch.n_positions, batch.max_active)
+        db.arrays = {
+            "stm": DeviceArray(batch.stm_indices),
+            "nstm": DeviceArray(batch.nstm_indices),
+            "nnz": DeviceArray(batch.nnz),
+            "bucket": DeviceArray(np.ascontiguousarray(bucket_idx, dtype=np.int32)),
+            "score": DeviceArray(batch.score),
+            "wdl": DeviceArray(batch.wdl),
+        }
+        return db
+
+    def to_c(self) -> TataraBatch:
+        a = self.arrays
+        return TataraBatch(
+            n_pos=self.n_pos,
+            max_active=self.max_active,
+            stm_indices=a["stm"].ptr,
+            nstm_indices=a["nstm"].ptr,
+            nnz=a["nnz"].ptr,
+            bucket_idx=a["bucket"].ptr,
+            score=a["score"].ptr,
+            wdl=a["wdl"].ptr,
+            on_device=1,
+        )
+
+
+def _host_batch(batch: Batch, bucket_idx: np.ndarray) -> tuple[TataraBatch, tuple]:
+    if len(bucket_idx) != batch.n_positions:
+        raise ValueError(
+            f"bucket_idx len ({len(bucket_idx)}) must equal batch.n_positions ({batch.n_positions})"
+        )
+    bucket = np.ascontiguousarray(bucket_idx, dtype=np.int32)
+    keep = (batch.stm_indices, batch.nstm_indices, batch.nnz, bucket, batch.score, batch.wdl)
+    cb = TataraBatch(
+        n_pos=batch.n_positions,
+        max_active=batch.max_active,
+        stm_indices=batch.stm_indices.ctypes.data,
+        nstm_indices=batch.nstm_indices.ctypes.data,
+        nnz=batch.nnz.ctypes.data,
+        bucket_idx=bucket.ctypes.data,
+        score=batch.score.ctypes.data,
+        wdl=batch.wdl.ctypes.data,
+        on_device=0,
+    )
+    return cb, keep
+
+
+@dataclass
+class LayerStackConfig:
+    """GpuTrainer::new arguments for the LayerStack architecture."""
+
+    ft_in: int
+    max_active: int
+    piece_inputs: int = 0  # factorizer piece inputs (0: off)
+    ft_out: int = 1536
+    l1_out: int = 16
+    l2_out: int = 32
+    num_buckets: int = 9
+    max_batch: int = 16384
+    optimizer: str = "ranger"
+    weight_decay: float = 0.01
+    ft_weight_decay: Optional[float] = None
+    dense_weight_decay: Optional[float] = None
+    bias_weight_decay: Optional[float] = None
+    ft_lr_mult: float = 1.0
+    dense_lr_mult: float = 1.0
+    bias_lr_mult: float = 1.0
+    device: int = 0
+    keep_grads: bool = False
+
+    def to_c(self) -> TataraTrainerConfig:
+        wd = self.weight_decay
+        return TataraTrainerConfig(
+            arch=0,
+            device=self.device,
+            max_batch=self.max_batch,
+            ft_in=self.ft_in,
+            max_active=self.max_active,
+            piece_inputs=self.piece_inputs,
+            ft_out=self.ft_out,
+            l1_out=self.l1_out,
+            l2_out=self.l2_out,
+            num_buckets=self.num_buckets,
+            optimizer=OPTIMIZERS[self.optimizer],
+            ft_weight_decay=wd if self.ft_weight_decay is None else self.ft_weight_decay,
+            dense_weight_decay=wd if self.dense_weight_decay is None else self.dense_weight_decay,
+            bias_weight_decay=wd if self.bias_weight_decay is None else self.bias_weight_decay,
+            ft_lr_mult=self.ft_lr_mult,
+            dense_lr_mult=self.dense_lr_mult,
+            bias_lr_mult=self.bias_lr_mult,
+            keep_grads=1 if self.keep_grads else 0,
+        )
+
+    @property
+    def train_ft_in(self) -> int:
+        return self.ft_in + self.piece_inputs
+
+
+class LayerStackTrainer:
+    """TrainerBackend for the LayerStack architecture on one MI355X."""
+
+    def __init__(self, config: LayerStackConfig):
+        self.config = config
+        self._lib = _lib.load()
+        h = C.c_void_p()
+        cfg = config.to_c()
+        check(self._lib.tatara_trainer_create(C.byref(cfg), C.byref(h)))
+        self._h = h.value
+        self._keep = None  # host arrays referenced by the in-flight step
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.tatara_trainer_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- TrainerBackend -----------------------------------------------------
+    def train_step(self, batch, bucket_idx=None, lr: float = 8.75e-4, wdl_lambda: float = 0.0,
+                   loss=Sigmoid()) -> float:
+        """One training step; returns the previous step's sum of squared errors."""
+        if isinstance(batch, DeviceBatch):
+            cb = batch.to_c()
+        else:
+            cb, self._keep = _host_batch(batch, bucket_idx)
+        cl = loss.to_c()
+        out = C.c_double()
+        check(self._lib.tatara_trainer_train_step(self._h, C.byref(cb), lr, wdl_lambda,
+                                                  C.byref(cl), C.byref(out)))
+        return out.value
+
+    def flush_pending_loss(self) -> float:
+        out = C.c_double()
+        check(self._lib.tatara_trainer_flush_pending_loss(self._h, C.byref(out)))
+        return out.value
+
+    def validate_step(self, batch, bucket_idx=None, wdl_lambda: float = 0.0, loss=Sigmoid()):
+        """Forward + loss only: returns (sum_sq_err, net_output)."""
+        if isinstance(batch, DeviceBatch):
+            cb = batch.to_c()
+            n = batch.n_pos
+        else:
+            cb, self._keep = _host_batch(batch, bucket_idx)
+            n = batch.n_positions
+        cl = loss.to_c()
+        sse = C.c_double()
+        net = np.zeros(n, dtype=np.float32)
+        check(self._lib.tatara_trainer_validate_step(
+            self._h, C.byref(cb), wdl_lambda, C.byref(cl), C.byref(sse),
+            net.ctypes.data_as(_lib.c_f32p)))
+        return sse.value, net
+
+    # -- state access (parity tests, checkpoints) --------------------------
+    @property
+    def step_count(self) -> int:
+        out = C.c_uint64()
+        check(self._lib.tatara_trainer_step_count(self._h, C.byref(out)))
+        return out.value
+
+    def tensor_size(self, name: str) -> int:
+        out = C.c_uint64()
+        check(self._lib.tatara_trainer_tensor_size(self._h, name.encode(), C.byref(out)))
+        return out.value
+
+    def get(self, name: str, which: str = "w") -> np.ndarray:
+        n = self.tensor_size(name)
+        out = np.empty(n, dtype=np.float32)
+        check(self._lib.tatara_trainer_get_tensor(self._h, name.encode(), WHICH[which],
+                                                  out.ctypes.data_as(_lib.c_f32p), n))
+        return out
+
+    def set(self, name: str, values: np.ndarray, which: str = "w") -> None:
+        v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        check(self._lib.tatara_trainer_set_tensor(self._h, name.encode(), WHICH[which],
+                                                  v.ctypes.data_as(_lib.c_f32p), v.size))
+
+    def activation(self, name: str, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        check(self._lib.tatara_trainer_get_activation(self._h, name.encode(),
+                                                      out.ctypes.data_as(_lib.c_f32p), n))
+        return out
+
+    PHASES = ("prep", "ft_forward", "dense_forward", "dense_backward", "ft_backward_opt",
+              "dense_opt")
+
+    def set_profiling(self, enable: bool) -> None:
+        """Per-phase GPU timing with HIP events on the trainer's stream."""
+        check(self._lib.tatara_trainer_set_profiling(self._h, 1 if enable else 0))
+
+    def phase_times(self) -> tuple[dict, int]:
+        """Summed milliseconds per phase and the number of profiled steps."""
+        ms = (C.c_double * len(self.PHASES))()
+        steps = C.c_uint64()
+        check(self._lib.tatara_trainer_phase_times(self._h, ms, len(self.PHASES), C.byref(steps)))
+        return dict(zip(self.PHASES, list(ms))), steps.value
+
+    def state(self) -> dict:
+        return {g: {k: self.get(g, k) for k in ("w", "m", "v", "slow")} for g in GROUPS}

@@ -1,0 +1,72 @@
+"""The C ABI library builds for gfx950, loads, and exports every declared symbol.
+
+CPU-only: no compute call is made here.
+"""
+import re
+from pathlib import Path
+
+import pytest
+
+from tatara_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "tatara_hip.h").read_text()
+    return sorted(set(re.findall(r"^TATARA_API\s+[\w\s\*]+?\b(tatara_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert len(syms) >= 25
+    assert "tatara_trainer_train_step" in syms and "tatara_op_sparse_ft_forward" in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    assert set(declared_symbols()) <= set(_lib.SIGNATURES), set(declared_symbols()) - set(_lib.SIGNATURES)
+
+
+def test_library_is_built_for_gfx950_only():
+    data = _lib.LIB_PATH.read_bytes()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert b"amdgcn-amd-amdhsa--" + other not in data
+
+
+def test_version_and_error_strings():
+    lib = _lib.load()
+    assert b"gfx950" in lib.tatara_version()
+    assert lib.tatara_last_error() is not None
+
+
+def test_invalid_arguments_fail_loudly_without_gpu_work():
+    import ctypes as C
+
+    lib = _lib.load()
+    # a null config is rejected before any device call
+    assert lib.tatara_trainer_create(None, None) == -3
+    assert b"invalid argument" in lib.tatara_last_error()
+    # step >= 1 precondition of the RAdam pre-compute
+    ss, dn = C.c_float(), C.c_int32()
+    assert lib.tatara_radam_step_size_denom(0, 0.9, 0.999, 5.0, C.byref(ss), C.byref(dn)) == -3
+
+
+def test_radam_host_precompute_matches_oracle():
+    import ctypes as C
+
+    from oracle import ffi
+
+    lib = _lib.load()
+    for step in (1, 2, 5, 6, 7, 100, 1000, 123456):
+        for beta1 in (0.9, 0.99):
+            ss, dn = C.c_float(), C.c_int32()
+            assert lib.tatara_radam_step_size_denom(step, beta1, 0.999, 5.0, C.byref(ss), C.byref(dn)) == 0
+            ess, edn = ffi.radam_step_size_denom(step, beta1, 0.999, 5.0)
+            assert (ss.value, dn.value) == (ess, edn)

@@ -1,0 +1,146 @@
+"""Kernel-level parity of the HIP ops against the CPU oracle (GPU).
+
+Bar: bit-exact for the sparse gather, the FT post activation, the
+deterministic FT weight gradient, the factorizer fold/reduce and the
+optimizer element update (the reference itself asserts tolerance 0.0 for the
+gather, gpu_cpu_equivalence_tests.rs:3836-3844).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import ffi
+from tatara_amd.trainer import DeviceArray
+from tatara_amd._lib import check
+
+pytestmark = pytest.mark.gpu
+
+SC = np.float32(127.0 / 128.0)
+
+
+def dev(a):
+    return DeviceArray(np.ascontiguousarray(a))
+
+
+def ragged_indices(rng, b, ma, cols, oob=True):
+    idx = rng.integers(0, cols, (b, ma)).astype(np.int32)
+    nnz = rng.integers(0, ma + 1, b).astype(np.int32)
+    if oob:
+        m = rng.random((b, ma))
+        idx[m < 0.05] = -1
+        idx[(m >= 0.05) & (m < 0.08)] = cols + 3  # out of range: skipped
+    # slots past nnz hold garbage that must be ignored
+    for i in range(b):
+        idx[i, nnz[i]:] = rng.integers(-5, cols, ma - nnz[i])
+    nnz[0] = ma
+    if b > 1:
+        nnz[1] = 0
+    # duplicate index inside one row
+    if ma >= 3 and b > 2:
+        idx[2, 1] = idx[2, 0]
+        nnz[2] = max(nnz[2], 3)
+    return idx, nnz
+
+
+def test_sparse_forward_reference_fixture(gpu):
+    # sparse_ft_forward.rs:132 fixture (rows=2) embedded in rows=8 columns
+    rows, cols = 8, 3
+    w = np.zeros((cols, rows), np.float32)
+    w[:, :2] = np.array([[0, 1], [2, 3], [4, 5]], np.float32)
+    idx = np.array([[0, 1, -1, -1], [2, 2, 1, 0]], np.int32)
+    nnz = np.array([2, 4], np.int32)
+    W, I, N = dev(w), dev(idx), dev(nnz)
+    out = DeviceArray.empty((2, rows), np.float32)
+    check(gpu.tatara_op_sparse_ft_forward(W.ptr, I.ptr, N.ptr, out.ptr, 2, rows, cols, 4))
+    got = out.to_host()
+    assert got[:, :2].ravel().tolist() == [2.0, 4.0, 10.0, 14.0]
+    assert not got[:, 2:].any()
+
+
+@pytest.mark.parametrize("b,ma,cols,rows", [(37, 40, 300, 64), (256, 38, 2000, 256), (64, 40, 500, 1536)])
+def test_sparse_forward_bit_exact(gpu, b, ma, cols, rows):
+    rng = np.random.default_rng(b + rows)
+    w = rng.standard_normal((cols, rows)).astype(np.float32)
+    idx, nnz = ragged_indices(rng, b, ma, cols)
+    exp = ffi.sparse_ft_forward(w, idx, nnz, b, rows, cols, ma)
+    W, I, N = dev(w), dev(idx), dev(nnz)
+    out = DeviceArray.empty((b, rows), np.float32)
+    check(gpu.tatara_op_sparse_ft_forward(W.ptr, I.ptr, N.ptr, out.ptr, b, rows, cols, ma))
+    assert np.array_equal(out.to_host().ravel(), exp)
+
+
+@pytest.mark.parametrize("pi", [0, 50])
+@pytest.mark.parametrize("ft_out", [256, 768, 1536])
+def test_ft_forward_pairwise_bit_exact(gpu, pi, ft_out):
+    rng = np.random.default_rng(ft_out + pi)
+    b, ma, cols = 96, 40, 600
+    w = (rng.standard_normal((cols, ft_out)) * 0.05 + 0.02).astype(np.float32)
+    bias = (rng.standard_normal(ft_out) * 0.1 + 0.2).astype(np.float32)
+    si, nnz = ragged_indices(rng, b, ma, cols)
+    ni, _ = ragged_indices(rng, b, ma, cols)
+    s_exp = ffi.sparse_ft_forward(w, si, nnz, b, ft_out, cols, ma)
+    n_exp = ffi.sparse_ft_forward(w, ni, nnz, b, ft_out, cols, ma)
+    c_exp = ffi.ft_post_perspective_fwd(s_exp, n_exp, bias, b, ft_out, SC)
+    W, S, Nn, N, B = dev(w), dev(si), dev(ni), dev(nnz), dev(bias)
+    so = DeviceArray.empty((b, ft_out), np.float32)
+    no = DeviceArray.empty((b, ft_out), np.float32)
+    co = DeviceArray.empty((b, ft_out), np.float32)
+    check(gpu.tatara_op_ft_forward_pairwise(W.ptr, S.ptr, Nn.ptr, N.ptr, B.ptr, so.ptr, no.ptr, co.ptr,
+                                            b, ft_out, cols, ma, pi, float(SC)))
+    assert np.array_equal(so.to_host().ravel(), s_exp)
+    assert np.array_equal(no.to_host().ravel(), n_exp)
+    assert np.array_equal(co.to_host().ravel(), c_exp)
+
+
+@pytest.mark.parametrize("b,ma,cols,ft_out", [(48, 40, 200, 256), (200, 38, 3000, 1536), (16, 4, 7, 64)])
+def test_ft_weight_grad_bit_exact(gpu, b, ma, cols, ft_out):
+    rng = np.random.default_rng(cols)
+    si, nnz = ragged_indices(rng, b, ma, cols)
+    ni, _ = ragged_indices(rng, b, ma, cols)
+    dft = rng.standard_normal((2, b, ft_out)).astype(np.float32)
+    exp = np.zeros(cols * ft_out, np.float32)
+    ffi.sparse_ft_backward_nnz(dft[0].ravel(), si, nnz, exp, b, ft_out, cols, ma)
+    ffi.sparse_ft_backward_nnz(dft[1].ravel(), ni, nnz, exp, b, ft_out, cols, ma)
+    D, S, Nn, N = dev(dft), dev(si), dev(ni), dev(nnz)
+    g = DeviceArray(np.full(cols * ft_out, 7.0, np.float32))
+    check(gpu.tatara_op_ft_weight_grad(D.ptr, S.ptr, Nn.ptr, N.ptr, g.ptr, b, ft_out, cols, ma))
+    assert np.array_equal(g.to_host(), exp)
+
+
+def test_fold_reduce_bit_exact(gpu):
+    rng = np.random.default_rng(9)
+    ft_in, ft_out, pi = 45 * 12, 256, 12
+    w = rng.standard_normal((ft_in + pi) * ft_out).astype(np.float32)
+    W = dev(w)
+    comb = DeviceArray.empty(ft_in * ft_out, np.float32)
+    check(gpu.tatara_op_ft_fold_virtual(W.ptr, comb.ptr, ft_in, ft_out, pi))
+    assert np.array_equal(comb.to_host(), ffi.ft_fold_virtual(w, ft_in, ft_out, pi))
+    g = rng.standard_normal((ft_in + pi) * ft_out).astype(np.float32)
+    G = dev(g)
+    check(gpu.tatara_op_ft_reduce_virtual_grad(G.ptr, ft_in, ft_out, pi))
+    exp = g.copy()
+    ffi.ft_reduce_virtual_grad(exp, ft_in, ft_out, pi)
+    assert np.array_equal(G.to_host(), exp)
+
+
+@pytest.mark.parametrize("denom", [0, 1])
+def test_radam_and_lerp_bit_exact(gpu, denom):
+    rng = np.random.default_rng(denom)
+    n = 10_007
+    w = rng.standard_normal(n).astype(np.float32)
+    m = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    v = (rng.random(n) * 1e-5).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    args = (1e-3, 12.5, denom, 0.01, 0.99, 0.999, 1e-8, -1.984375, 1.984375)
+    ew, em, ev, eg = w.copy(), m.copy(), v.copy(), g.copy()
+    ffi.radam_step(ew, em, ev, eg, *args)
+    W, M, V, G = dev(w), dev(m), dev(v), dev(g)
+    check(gpu.tatara_op_radam_step(W.ptr, M.ptr, V.ptr, G.ptr, *args, n))
+    for d, e in ((W, ew), (M, em), (V, ev), (G, eg)):
+        assert np.array_equal(d.to_host(), e)
+    s = rng.standard_normal(n).astype(np.float32)
+    S = dev(s)
+    check(gpu.tatara_op_ranger_lookahead_lerp(W.ptr, S.ptr, 0.5, n))
+    ffi.ranger_lookahead_lerp(ew, s, 0.5)
+    assert np.array_equal(W.to_host(), ew) and np.array_equal(S.to_host(), s)

@@ -1,0 +1,199 @@
+"""LayerStack training-step parity: HIP trainer vs the CPU oracle step (GPU).
+
+Bars:
+  - initial weights and the FT forward (raw sums, combined): bit-exact;
+  - net output, gradients, post-step weights and optimizer state: within
+    1e-5 relative / 1e-6 absolute, looser where a
+    batch-reduced sum is compared element-wise against a different order;
+  - the step is deterministic: two runs give bit-identical state.
+"""
+import numpy as np
+import pytest
+
+from oracle import layerstack as ols
+from tatara_amd.synthetic import small_spec, structured_batch, HALFKA_HM_MERGED
+from tatara_amd.trainer import (DeviceBatch, LayerStackConfig, LayerStackTrainer, Sigmoid, Wrm,
+                                GROUPS)
+
+pytestmark = pytest.mark.gpu
+
+SPEC = small_spec(king_buckets=10, piece_inputs=64, max_active=40)
+
+
+def close(got, exp, rtol, atol_frac=0.0, atol=0.0, what=""):
+    got = np.asarray(got, np.float64)
+    exp = np.asarray(exp, np.float64)
+    scale = np.abs(exp).max() if exp.size else 0.0
+    tol = atol + atol_frac * scale + rtol * np.abs(exp)
+    err = np.abs(got - exp)
+    bad = err > tol
+    assert not bad.any(), (
+        f"{what}: {bad.sum()} / {bad.size} outside tolerance; worst abs err {err.max():.3e} "
+        f"at {int(err.argmax())} (got {got.ravel()[err.argmax()]:.9g}, exp {exp.ravel()[err.argmax()]:.9g})"
+    )
+
+
+def make(nb=8, ft_out=256, l1=16, optimizer="ranger", b=256, keep=True, factorize=True):
+    sh = ols.LsShape(ft_in=SPEC["ft_in"], max_active=SPEC["max_active"],
+                     piece_inputs=SPEC["piece_inputs"] if factorize else 0, ft_out=ft_out, l1=l1,
+                     l2=32, nb=nb)
+    cfg = LayerStackConfig(ft_in=sh.ft_in, max_active=sh.max_active, piece_inputs=sh.piece_inputs,
+                           ft_out=ft_out, l1_out=l1, l2_out=32, num_buckets=nb, max_batch=b,
+                           optimizer=optimizer, keep_grads=keep)
+    return sh, cfg
+
+
+def batch_for(seed, b, nb, invalid_buckets=True):
+    batch, bucket = structured_batch(b, SPEC, num_buckets=nb, seed=seed, nnz_min=30)
+    if invalid_buckets:
+        bucket[3] = -1
+        bucket[7] = nb  # out of range -> no bucket layers
+    return batch, bucket
+
+
+def as_dict(batch, bucket):
+    return dict(stm=batch.stm_indices, nstm=batch.nstm_indices, nnz=batch.nnz, bucket=bucket,
+                score=batch.score, wdl=batch.wdl)
+
+
+def loss_dict(loss):
+    if isinstance(loss, Sigmoid):
+        return {"kind": "sigmoid", "scale": loss.scale}
+    return {"kind": "wrm", "nnue2score": loss.nnue2score, "in_scaling": loss.in_scaling,
+            "in_offset": loss.in_offset, "target_offset": loss.target_offset,
+            "target_scaling": loss.target_scaling, "pow_exp": loss.pow_exp,
+            "qp_asymmetry": loss.qp_asymmetry, "w1": loss.weight_boost_w1,
+            "w2": loss.weight_boost_w2}
+
+
+def test_initial_weights_bit_exact(gpu):
+    sh, cfg = make()
+    with LayerStackTrainer(cfg) as t:
+        st = ols.default_init(sh)
+        for g in GROUPS:
+            assert np.array_equal(t.get(g), st[g]["w"]), g
+            assert not t.get(g, "m").any() and not t.get(g, "slow").any()
+
+
+@pytest.mark.parametrize("loss", [Sigmoid(), Wrm(), Wrm(pow_exp=2.5, qp_asymmetry=0.2, weight_boost_w1=1.0)],
+                         ids=["sigmoid", "wrm", "wrm_ext"])
+@pytest.mark.parametrize("optimizer", ["ranger", "adamw"])
+def test_one_step_matches_oracle(gpu, loss, optimizer):
+    sh, cfg = make(optimizer=optimizer)
+    b = cfg.max_batch
+    batch, bucket = batch_for(1, b, sh.nb)
+    lr, lam = 8.75e-4, 0.25
+    with LayerStackTrainer(cfg) as t:
+        assert t.train_step(batch, bucket, lr, lam, loss) == 0.0
+        st = ols.default_init(sh)
+        opt = ols.OptConfig(optimizer=optimizer, weight_decay=0.01)
+        acc, a, g = ols.train_step(sh, st, as_dict(batch, bucket), opt, lr, lam, loss_dict(loss), 1)
+        # forward: bit-exact FT path
+        bf = b * sh.ft_out
+        assert np.array_equal(t.activation("ft_stm_out", bf), a["ft_stm"])
+        assert np.array_equal(t.activation("ft_nstm_out", bf), a["ft_nstm"])
+        assert np.array_equal(t.activation("combined", bf), a["combined"])
+        close(t.activation("net_output", b), a["net"], 1e-5, atol=1e-6, what="net_output")
+        dmax = max(np.abs(a["dft_stm"]).max(), 1e-30)
+        close(t.activation("dft_stm", bf), a["dft_stm"], 1e-4, atol=1e-5 * dmax, what="dft_stm")
+        close(t.activation("dft_nstm", bf), a["dft_nstm"], 1e-4, atol=1e-5 * dmax, what="dft_nstm")
+        # gradients (kept for the check)
+        for name in GROUPS:
+            close(t.get(name, "grad"), g[name], 1e-4, atol_frac=1e-5, what=f"grad {name}")
+        # post-step state
+        for name in GROUPS:
+            for k in ("w", "m", "v"):
+                close(t.get(name, k), st[name][k], 1e-5, atol=1e-6 if k == "w" else 0.0,
+                      atol_frac=1e-5 if k != "w" else 0.0, what=f"{name}.{k}")
+        close([t.flush_pending_loss()], [acc], 1e-6, what="loss")
+        assert t.step_count == 1
+
+
+def test_multi_step_ranger_with_lookahead(gpu):
+    sh, cfg = make(optimizer="ranger")
+    b = cfg.max_batch
+    st = ols.default_init(sh)
+    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+    loss = Sigmoid()
+    losses_gpu, losses_ref = [], []
+    with LayerStackTrainer(cfg) as t:
+        for step in range(1, 8):  # lookahead fires at step 6
+            batch, bucket = batch_for(100 + step % 3, b, sh.nb)
+            lagged = t.train_step(batch, bucket, 1e-3, 0.0, loss)
+            if step > 1:
+                losses_gpu.append(lagged)
+            acc, _, _ = ols.train_step(sh, st, as_dict(batch, bucket), opt, 1e-3, 0.0, loss_dict(loss), step)
+            losses_ref.append(acc)
+        losses_gpu.append(t.flush_pending_loss())
+        close(losses_gpu, losses_ref, 1e-5, what="lagged losses")
+        for name in GROUPS:
+            close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"{name}.w after 7 steps")
+            close(t.get(name, "slow"), st[name]["slow"], 1e-5, atol=1e-6, what=f"{name}.slow")
+
+
+def test_unfactorized_and_l1_8(gpu):
+    sh, cfg = make(factorize=False, l1=8, nb=9, optimizer="radam")
+    b = cfg.max_batch
+    batch, bucket = batch_for(5, b, sh.nb)
+    with LayerStackTrainer(cfg) as t:
+        t.train_step(batch, bucket, 1e-3, 0.5, Sigmoid())
+        st = ols.default_init(sh)
+        opt = ols.OptConfig(optimizer="radam")
+        acc, a, g = ols.train_step(sh, st, as_dict(batch, bucket), opt, 1e-3, 0.5, loss_dict(Sigmoid()), 1)
+        assert np.array_equal(t.activation("combined", b * sh.ft_out), a["combined"])
+        for name in GROUPS:
+            close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=name)
+
+
+def test_validate_step_and_ragged_batch(gpu):
+    sh, cfg = make(b=512)
+    batch, bucket = batch_for(7, 160, sh.nb)  # smaller than capacity, multiple of 16
+    with LayerStackTrainer(cfg) as t:
+        sse, net = t.validate_step(batch, bucket, 0.0, Sigmoid())
+        st = ols.default_init(sh)
+        a, acc = ols.forward(sh, st, as_dict(batch, bucket), 0.0, loss_dict(Sigmoid()))
+        close(net, a["net"], 1e-5, atol=1e-6, what="validate net")
+        close([sse], [acc], 1e-6, what="validate sse")
+        assert t.step_count == 0
+        # a batch that is not a multiple of 16 is rejected
+        bad, bb = batch_for(7, 24, sh.nb)
+        from tatara_amd._lib import TataraError
+        with pytest.raises(TataraError):
+            t.train_step(bad.__class__(bad.stm_indices[:20], bad.nstm_indices[:20], bad.nnz[:20],
+                                       bad.score[:20], bad.wdl[:20]), bb[:20])
+
+
+def test_device_batch_and_determinism(gpu):
+    sh, cfg = make(keep=False)
+    b = cfg.max_batch
+    batches = [batch_for(s, b, sh.nb) for s in (11, 12, 13)]
+    states = []
+    for run in range(2):
+        with LayerStackTrainer(cfg) as t:
+            dbs = [DeviceBatch.upload(bt, bk) for bt, bk in batches]
+            for db in dbs:
+                t.train_step(db, None, 1e-3, 0.0, Sigmoid())
+            t.flush_pending_loss()
+            states.append({g: t.get(g) for g in GROUPS})
+    for g in GROUPS:
+        assert np.array_equal(states[0][g], states[1][g]), g
+
+
+def test_full_shape_step_properties(gpu):
+    """LS ft-1536/16/32, halfka-hm-merged shape, b=4096: finite, deterministic, learns."""
+    spec = HALFKA_HM_MERGED
+    b = 4096
+    cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=40, piece_inputs=spec["piece_inputs"],
+                           ft_out=1536, num_buckets=8, max_batch=b, optimizer="ranger")
+    batch, bucket = structured_batch(b, spec, num_buckets=8, seed=3)
+    with LayerStackTrainer(cfg) as t:
+        db = DeviceBatch.upload(batch, bucket)
+        sse0, _ = t.validate_step(db, None, 0.0, Sigmoid())
+        for _ in range(5):
+            t.train_step(db, None, 5e-3, 0.0, Sigmoid())
+        t.flush_pending_loss()
+        sse1, net = t.validate_step(db, None, 0.0, Sigmoid())
+        assert np.isfinite(net).all()
+        assert sse1 < sse0
+        w = t.get("ft_w")
+        assert np.isfinite(w).all()
