@@ -38,7 +38,7 @@ __device__ __forceinline__ float radam_elem(float& w, float& m, float& v, float 
     m = mi;
     v = vi;
     float val = mi;
-    if (s.denom != 0) val /= __fsqrt_rn(vi) + s.eps;
+    if (s.denom != 0) val /= sqrtf(vi) + s.eps;  // correctly rounded (llvm.sqrt.f32); __fsqrt_rn is native
     p -= rate * val;
     p = p < s.min_w ? s.min_w : (p > s.max_w ? s.max_w : p);
     w = p;

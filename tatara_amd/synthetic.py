@@ -34,7 +34,20 @@ def small_spec(king_buckets: int = 10, piece_inputs: int = 64, max_active: int =
 
 
 def _distinct_rows(rng, n: int, k: int, lo: int, hi: int) -> np.ndarray:
-    """n rows of k distinct integers in [lo, hi) (rows with a repeat are redrawn)."""
+    """n rows of k distinct integers in [lo, hi).
+
+    Dense draws (k comparable to the range) take the first k entries of a
+    random permutation per row; sparse draws redraw the rows that repeat.
+    """
+    span = hi - lo
+    if k > span:
+        raise ValueError(f"cannot draw {k} distinct values from {span}")
+    if k * k > 6 * span:  # P(no repeat) = exp(-k^2 / 2 span) < 5%: rejection would crawl
+        out = np.empty((n, k), dtype=np.int64)
+        for r0 in range(0, n, 4096):
+            r1 = min(n, r0 + 4096)
+            out[r0:r1] = np.argsort(rng.random((r1 - r0, span)), axis=1)[:, :k] + lo
+        return out
     out = rng.integers(lo, hi, (n, k))
     todo = np.arange(n)
     while todo.size:
