@@ -365,6 +365,10 @@ struct LayerStackTrainer {
         s.lr = lr * mult;
         s.lookahead = (opt == TATARA_OPT_RANGER && step % kRangerK == 0) ? 1 : 0;
         s.alpha = kAlpha;
+        // the FT weight has no clamp (W_CLAMP_NONE); the dense groups get
+        // their per-group bounds in the finalize kernel
+        s.min_w = std::numeric_limits<float>::lowest();
+        s.max_w = std::numeric_limits<float>::max();
         return s;
     }
 
