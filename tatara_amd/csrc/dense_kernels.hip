@@ -366,7 +366,9 @@ __global__ void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
                                       uint32_t max_chunks, uint32_t* __restrict__ info) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     uint32_t c = 0;
+    uint32_t* seg = info + 3 * max_chunks + 1;  // seg[g] = first chunk of bin g, seg[nb+1] = end
     for (uint32_t g = 0; g <= nb; ++g) {
+        seg[g] = c;
         const uint32_t t0 = bin_start[g] / 16;
         const uint32_t t1 = (bin_start[g] + bin_count[g] + 15) / 16;
         for (uint32_t t = t0; t < t1 && c < max_chunks; t += kChunkTiles) {
@@ -377,6 +379,33 @@ __global__ void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
         }
     }
     info[3 * max_chunks] = c;
+    seg[nb + 1] = c;
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic column sums of a partial matrix P[rows][n_cols]:
+// out[seg][c] = sum over the segment's rows of P[r][c].  Thread (c, phase)
+// sums rows phase, phase+4, ... sequentially; the four phase sums are added
+// in a fixed order.  Segment s covers rows [seg_rows[s], seg_rows[s+1]) when
+// seg_rows is given, else all rows.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void reduce_rows_kernel(const float* __restrict__ P,
+                                                          uint32_t n_rows, uint32_t n_cols,
+                                                          const uint32_t* __restrict__ seg_rows,
+                                                          float* __restrict__ out) {
+    __shared__ float part[4][64];
+    const uint32_t lane = threadIdx.x % 64, phase = threadIdx.x / 64;
+    const uint32_t c = blockIdx.x * 64 + lane;
+    const uint32_t seg = blockIdx.y;
+    const uint32_t r0 = seg_rows ? seg_rows[seg] : 0;
+    const uint32_t r1 = seg_rows ? seg_rows[seg + 1] : n_rows;
+    float acc = 0.0f;
+    if (c < n_cols)
+        for (uint32_t r = r0 + phase; r < r1; r += 4) acc += P[(uint64_t)r * n_cols + c];
+    part[phase][lane] = acc;
+    __syncthreads();
+    if (phase == 0 && c < n_cols)
+        out[(uint64_t)seg * n_cols + c] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
 }
 
 // ---------------------------------------------------------------------------
@@ -431,17 +460,19 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
 // dcombined[c] = sum_o dl1[o] * l1_w[g][o][c]  +  sum_o dl1[o] * l1s_w[c][o]
 // (the reference's two input-gradient kernels, added as in
 // ft_post_perspective_grad_fused), then the pairwise CReLU gradient into dft
-// (native_kernels.cu:2260-2302).  A workgroup owns kPostTiles sorted tiles and
-// writes its ft_b gradient partial per perspective.
+// (native_kernels.cu:2260-2302).  Grid (column block, row block): a thread
+// owns one float4 column group of kPostTiles sorted tiles and writes its ft_b
+// gradient partial per perspective for that row block.
 // ---------------------------------------------------------------------------
 template <int L1>
 __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
-    const uint32_t t = threadIdx.x;
     const uint32_t ft_out = a.ft_out, half = ft_out / 2, n4 = ft_out / 4;
     const uint64_t batch = a.batch;
-    const uint32_t tile0 = blockIdx.x * kPostTiles;
-    float* part = a.ftb_partial + (uint64_t)blockIdx.x * 2 * ft_out;
-    for (uint32_t qq = t; qq < n4; qq += 128) {
+    const uint32_t tile0 = blockIdx.y * kPostTiles;
+    float* part = a.ftb_partial + (uint64_t)blockIdx.y * 2 * ft_out;
+    {
+        const uint32_t qq = blockIdx.x * 128 + threadIdx.x;
+        if (qq >= n4) return;
         const uint32_t c0 = 4 * qq;
         const uint32_t persp = c0 < half ? 0 : 1;
         const uint32_t p0 = c0 - persp * half;
@@ -539,8 +570,7 @@ struct GroupTable {
 __global__ __launch_bounds__(256) void ls_dense_finalize_kernel(LsDenseArgs a, GroupTable gt,
                                                                 OptScalars dense, OptScalars bias,
                                                                 int32_t apply_update,
-                                                                int32_t keep_grads, uint32_t n_tail,
-                                                                uint32_t n_post) {
+                                                                int32_t keep_grads) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= gt.start[9]) return;
     int gi = 0;
@@ -549,68 +579,43 @@ __global__ __launch_bounds__(256) void ls_dense_finalize_kernel(LsDenseArgs a, G
     const uint32_t l1 = a.l1, l2 = a.l2, nb = a.nb, ft_out = a.ft_out;
     const TailDims td{l1, l2, nb};
     const uint32_t cells = td.cells();
-    const uint32_t n_chunks = a.chunk_info[3 * a.max_chunks];
     float grad = 0.0f;
-    auto tail_sum = [&](uint32_t g, uint32_t cell) {
-        float s = 0.0f;
-        for (uint32_t w = 0; w < n_tail; ++w) s += a.tail_partial[((uint64_t)w * nb + g) * cells + cell];
-        return s;
-    };
+    auto tail_sum = [&](uint32_t g, uint32_t cell) { return a.tail_sum[(uint64_t)g * cells + cell]; };
     switch (gi) {
-        case 0: {  // ft_b: stm partials then nstm partials
-            float s = 0.0f;
-            for (uint32_t w = 0; w < n_post; ++w) s += a.ftb_partial[(uint64_t)w * 2 * ft_out + e];
-            for (uint32_t w = 0; w < n_post; ++w)
-                s += a.ftb_partial[(uint64_t)w * 2 * ft_out + ft_out + e];
-            grad = s;
+        case 0:  // ft_b: stm sum then nstm sum
+            grad = a.ftb_sum[e] + a.ftb_sum[ft_out + e];
             break;
-        }
-        case 1: {  // l1_w [nb][l1][ft_out]
-            const uint32_t g = (uint32_t)(e / ((uint64_t)l1 * ft_out));
-            const uint64_t ok = e - (uint64_t)g * l1 * ft_out;
-            float s = 0.0f;
-            for (uint32_t c = 0; c < n_chunks; ++c)
-                if (a.chunk_info[3 * c] == g) s += a.w1_partial[(uint64_t)c * l1 * ft_out + ok];
-            grad = s;
+        case 1:  // l1_w [nb][l1][ft_out]: bucket segments of the chunk partials
+            grad = a.w1_seg[e];
             break;
-        }
         case 2: {  // l1_b [nb][l1]
-            const uint32_t g = (uint32_t)(e / l1), o = (uint32_t)(e % l1);
-            grad = tail_sum(g, td.off_b1() + o);
+            grad = tail_sum((uint32_t)(e / l1), td.off_b1() + (uint32_t)(e % l1));
             break;
         }
-        case 3: {  // l1s_w [ft_out][l1]
+        case 3: {  // l1s_w [ft_out][l1]: every bin's segment, invalid bin included
             const uint32_t k = (uint32_t)(e / l1), o = (uint32_t)(e % l1);
             float s = 0.0f;
-            for (uint32_t c = 0; c < n_chunks; ++c)
-                s += a.w1_partial[(uint64_t)c * l1 * ft_out + (uint64_t)o * ft_out + k];
+            for (uint32_t g = 0; g <= nb; ++g) s += a.w1_seg[((uint64_t)g * l1 + o) * ft_out + k];
             grad = s;
             break;
         }
-        case 4: {  // l1s_b [l1]
-            float s = 0.0f;
-            for (uint32_t w = 0; w < n_tail; ++w) s += a.b1s_partial[(uint64_t)w * l1 + e];
-            grad = s;
+        case 4:  // l1s_b [l1]
+            grad = a.b1s_sum[e];
             break;
-        }
         case 5: {  // l2_w [nb][l2][l2_in]
             const uint32_t per = l2 * td.l2_in();
-            const uint32_t g = (uint32_t)(e / per), c = (uint32_t)(e % per);
-            grad = tail_sum(g, td.off_w2() + c);
+            grad = tail_sum((uint32_t)(e / per), td.off_w2() + (uint32_t)(e % per));
             break;
         }
-        case 6: {  // l2_b [nb][l2]
+        case 6:  // l2_b [nb][l2]
             grad = tail_sum((uint32_t)(e / l2), td.off_b2() + (uint32_t)(e % l2));
             break;
-        }
-        case 7: {  // l3_w [nb][l2]
+        case 7:  // l3_w [nb][l2]
             grad = tail_sum((uint32_t)(e / l2), td.off_w3() + (uint32_t)(e % l2));
             break;
-        }
-        default: {  // l3_b [nb]
+        default:  // l3_b [nb]
             grad = tail_sum((uint32_t)e, td.off_b3());
             break;
-        }
     }
     const LsDenseGroup& G = gt.g[gi];
     if (!apply_update) {
@@ -697,12 +702,13 @@ int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream) {
 }
 
 int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
-    const uint32_t blocks = ls_post_workgroups(a.padded_b);
-    if (blocks == 0) return kOk;
+    const uint32_t rows = ls_post_workgroups(a.padded_b);
+    if (rows == 0) return kOk;
+    const dim3 grid(ceil_div(a.ft_out / 4, 128), rows);
     if (a.l1 == 16) {
-        ls_l1_input_post_kernel<16><<<blocks, 128, 0, stream>>>(a);
+        ls_l1_input_post_kernel<16><<<grid, 128, 0, stream>>>(a);
     } else if (a.l1 == 8) {
-        ls_l1_input_post_kernel<8><<<blocks, 128, 0, stream>>>(a);
+        ls_l1_input_post_kernel<8><<<grid, 128, 0, stream>>>(a);
     } else {
         TATARA_REQUIRE(false, "l1 must be 16 or 8");
     }
@@ -720,10 +726,21 @@ int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups,
         gt.start[k + 1] = gt.start[k] + groups[k].n;
     }
     const uint64_t n = gt.start[9];
+    const TailDims td{a.l1, a.l2, a.nb};
+    const uint32_t n_tail = ls_tail_workgroups(a.padded_b);
+    const uint32_t n_post = ls_post_workgroups(a.padded_b);
+    const uint32_t tail_cols = a.nb * td.cells();
+    reduce_rows_kernel<<<dim3(ceil_div(tail_cols, 64), 1), 256, 0, stream>>>(
+        a.tail_partial, n_tail, tail_cols, nullptr, a.tail_sum);
+    reduce_rows_kernel<<<dim3(ceil_div(a.l1, 64), 1), 256, 0, stream>>>(a.b1s_partial, n_tail, a.l1,
+                                                                        nullptr, a.b1s_sum);
+    reduce_rows_kernel<<<dim3(ceil_div(2 * a.ft_out, 64), 1), 256, 0, stream>>>(
+        a.ftb_partial, n_post, 2 * a.ft_out, nullptr, a.ftb_sum);
+    reduce_rows_kernel<<<dim3(ceil_div(a.l1 * a.ft_out, 64), a.nb + 1), 256, 0, stream>>>(
+        a.w1_partial, 0, a.l1 * a.ft_out, a.chunk_info + 3 * a.max_chunks + 1, a.w1_seg);
+    TATARA_LAUNCHED("reduce_rows");
     ls_dense_finalize_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(a, gt, dense, bias, apply_update,
-                                                                    keep_grads,
-                                                                    ls_tail_workgroups(a.padded_b),
-                                                                    ls_post_workgroups(a.padded_b));
+                                                                    keep_grads);
     TATARA_LAUNCHED("ls_dense_finalize");
     return kOk;
 }

@@ -33,7 +33,7 @@ struct TailDims {
 
 constexpr uint32_t kTailRows = 128;      // sorted rows per tail workgroup
 constexpr uint32_t kChunkTiles = 64;     // 16-row tiles per L1 weight-gradient chunk
-constexpr uint32_t kPostTiles = 8;       // 16-row tiles per L1-input/FT-post workgroup
+constexpr uint32_t kPostTiles = 4;       // 16-row tiles per L1-input/FT-post row block
 
 struct LsDenseArgs {
     // shapes
@@ -44,7 +44,8 @@ struct LsDenseArgs {
     const uint32_t* bin_start;  // [nb + 2]
     const uint32_t* bin_count;  // [nb + 1]
     // chunk table for the L1 weight gradient
-    uint32_t* chunk_info;       // [max_chunks][3] (bin, first tile, n tiles); [max_chunks*3] = count
+    uint32_t* chunk_info;       // [max_chunks][3] (bin, first tile, n tiles); [max_chunks*3] = count,
+                                // then [nb + 2] first chunk of each bin (last = count)
     uint32_t max_chunks;
     // activations
     const float* combined;      // [batch][ft_out]
@@ -79,6 +80,11 @@ struct LsDenseArgs {
     float* w1_partial;          // [max_chunks][l1][ft_out]
     float* ftb_partial;         // [n_post_wg][2][ft_out]
     double* loss_out;           // [1] reduced loss
+    // fixed-order reductions of the partials
+    float* tail_sum;            // [nb][cells]
+    float* b1s_sum;             // [l1]
+    float* ftb_sum;             // [2][ft_out]
+    float* w1_seg;              // [nb + 1][l1][ft_out]
 };
 
 uint32_t ls_tail_workgroups(uint32_t padded_b);

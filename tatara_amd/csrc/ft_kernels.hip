@@ -211,8 +211,7 @@ __global__ void build_occurrence_keys_kernel(const int32_t* __restrict__ idx_stm
                                              const int32_t* __restrict__ idx_nstm,
                                              const int32_t* __restrict__ nnz,
                                              uint32_t* __restrict__ keys,
-                                             uint32_t* __restrict__ vals,
-                                             uint32_t* __restrict__ counts, uint32_t batch,
+                                             uint32_t* __restrict__ vals, uint32_t batch,
                                              uint32_t max_active, uint32_t cols) {
     const uint64_t per = (uint64_t)batch * max_active;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -226,23 +225,33 @@ __global__ void build_occurrence_keys_kernel(const int32_t* __restrict__ idx_stm
     const uint32_t key = ok ? 2u * (uint32_t)v + persp : 2u * cols;
     keys[i] = key;
     vals[i] = persp * batch + b;
-    if (ok) atomicAdd(&counts[key], 1u);
+}
+
+// Segment offsets from the sorted keys: offsets[k] = first sorted position
+// with key >= k, for k in [0, n_keys]; offsets[n_keys] = n_items.  Each entry
+// is written by exactly one thread (the one at the boundary it falls in), so
+// no histogram, atomics or scan are needed.
+__global__ void occurrence_offsets_kernel(const uint32_t* __restrict__ sorted_keys,
+                                          uint64_t n_items, uint32_t n_keys,
+                                          uint32_t* __restrict__ offsets) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > n_items) return;
+    const int64_t prev = i == 0 ? -1 : (int64_t)sorted_keys[i - 1];
+    const int64_t cur = i == n_items ? (int64_t)n_keys : (int64_t)sorted_keys[i];
+    for (int64_t k = prev + 1; k <= cur; ++k) offsets[k] = (uint32_t)i;
 }
 
 // ---------------------------------------------------------------------------
-// Backward + optimizer + fold.
-//
-// One wave = one task (row group g, column chunk c).  A group is the rows
-// g + j*stride for j < count (for the factorizer: the king-bucket copies of
-// piece g) followed by the virtual row virt_base + g when has_virtual.
-// For each real row f the gradient is the sequential sum, from +0.0, of the
-// dft rows listed in its occurrence segment [off[2f], off[2f+2]) - stm
-// occurrences in ascending position order, then nstm ones - which is exactly
-// the order of the reference CPU backward.  The virtual row's gradient is the
-// sequential sum of the group's real-row gradients in ascending row order
-// (ft_reduce_virtual_grad_cpu).  Each row is then updated with RAdam (+ the
-// Ranger lerp on lookahead steps) and, with a virtual row, the forward table
-// comb = w + w_virtual is rewritten for the group.
+// Backward + optimizer, phase A: one wave = one task (column chunk c, real row
+// f).  The gradient of row f is the sequential sum, from +0.0, of the dft rows
+// listed in its occurrence segment [off[2f], off[2f+2]) - stm occurrences in
+// ascending position order, then nstm ones - which is exactly the order of the
+// reference CPU backward (sparse_ft_backward_cpu, stm then nstm).  The row is
+// then updated with RAdam (+ the Ranger lerp on lookahead steps) and its
+// gradient stored for the factorizer's virtual rows (phase B).
+// Tasks are chunk-major and swizzled so that an XCD walks consecutive rows of
+// one chunk: those rows share a king block, whose occurrences come from the
+// same few thousand positions, so the gathered dft rows stay in L2.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ float4 segment_sum(const float4* __restrict__ dft4, uint64_t row4,
@@ -291,49 +300,81 @@ __device__ __forceinline__ void opt_update4(float* __restrict__ w, float* __rest
     reinterpret_cast<float4*>(v)[off4] = V;
 }
 
-__global__ __launch_bounds__(256) void ft_backward_optimizer_kernel(
+__global__ __launch_bounds__(256) void ft_grad_update_kernel(
     const float* __restrict__ dft,  // [2][batch][ft_out]
     const uint32_t* __restrict__ occ_vals, const uint32_t* __restrict__ occ_off,
     float* __restrict__ w, float* __restrict__ m, float* __restrict__ v, float* __restrict__ slow,
-    float* __restrict__ comb,      // forward table, written when has_virtual (may be null)
-    float* __restrict__ grad_out,  // optional: the gradient each row received (may be null)
-    uint32_t ft_out, uint32_t n_groups, uint32_t stride, uint32_t count, uint32_t has_virtual,
-    uint32_t virt_base, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
+    float* __restrict__ grad_out,  // gradient per row (may be null without a factorizer)
+    uint32_t ft_out, uint32_t rows, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
+    if (task >= (uint64_t)rows * n_chunks) return;
+    const uint32_t chunk = (uint32_t)(task / rows);
+    const uint32_t f = (uint32_t)(task - (uint64_t)chunk * rows);
+    const uint32_t row4 = ft_out / 4;
+    const uint32_t q = chunk * kWave + lane;
+    const uint32_t s0 = __builtin_amdgcn_readfirstlane(occ_off[2 * f]);
+    const uint32_t s1 = __builtin_amdgcn_readfirstlane(occ_off[2 * f + 2]);
+    if (q >= row4) return;
+    const float4 gr = segment_sum(reinterpret_cast<const float4*>(dft), row4, occ_vals, s0, s1, q);
+    const uint64_t off4 = (uint64_t)f * row4 + q;
+    if (grad_out) reinterpret_cast<float4*>(grad_out)[off4] = gr;
+    if (apply_update) opt_update4(w, m, v, slow, off4, gr, s);
+}
+
+// ---------------------------------------------------------------------------
+// Backward + optimizer, phase B (factorizer): one wave = (column chunk, piece
+// p).  The virtual row's gradient is the sequential sum of the piece's
+// king-bucket rows p, p + pi, p + 2 pi, ... (ft_reduce_virtual_grad_cpu's
+// order); the virtual row is updated, and the forward table
+// comb = w + w_virtual is rewritten for the piece's rows (ft_fold_virtual).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void ft_virtual_fold_kernel(
+    float* __restrict__ grad, float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
+    float* __restrict__ slow, float* __restrict__ comb, uint32_t ft_out, uint32_t ft_in,
+    uint32_t piece_inputs, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint64_t task = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
-    if (task >= (uint64_t)n_groups * n_chunks) return;
-    // Chunk-major enumeration: concurrently running waves share a column chunk
-    // and walk king blocks in step, so the dft rows they gather overlap.
-    const uint32_t chunk = (uint32_t)(task / n_groups);
-    const uint32_t g = (uint32_t)(task - (uint64_t)chunk * n_groups);
+    if (task >= (uint64_t)piece_inputs * n_chunks) return;
+    const uint32_t chunk = (uint32_t)(task / piece_inputs);
+    const uint32_t p = (uint32_t)(task - (uint64_t)chunk * piece_inputs);
     const uint32_t row4 = ft_out / 4;
     const uint32_t q = chunk * kWave + lane;
-    const bool active = q < row4;
-    const float4* dft4 = reinterpret_cast<const float4*>(dft);
+    if (q >= row4) return;
+    const uint32_t count = ft_in / piece_inputs;
+    const float4* g4 = reinterpret_cast<const float4*>(grad);
     float4 vsum = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t j = 0; j < count; ++j) {
-        const uint32_t f = g + j * stride;
-        const uint32_t s0 = __builtin_amdgcn_readfirstlane(occ_off[2 * f]);
-        const uint32_t s1 = __builtin_amdgcn_readfirstlane(occ_off[2 * f + 2]);
-        if (!active) continue;
-        const float4 gr = segment_sum(dft4, row4, occ_vals, s0, s1, q);
-        if (has_virtual) vsum = f4add(vsum, gr);
-        const uint64_t off4 = (uint64_t)f * row4 + q;
-        if (grad_out) reinterpret_cast<float4*>(grad_out)[off4] = gr;
-        if (apply_update) opt_update4(w, m, v, slow, off4, gr, s);
+    constexpr int U = 8;
+    uint32_t j = 0;
+    for (; j + U <= count; j += U) {
+        float4 d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) d[u] = g4[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q];
+#pragma unroll
+        for (int u = 0; u < U; ++u) vsum = f4add(vsum, d[u]);
     }
-    if (!active || !has_virtual) return;
-    const uint64_t voff4 = (uint64_t)(virt_base + g) * row4 + q;
-    if (grad_out) reinterpret_cast<float4*>(grad_out)[voff4] = vsum;
+    for (; j < count; ++j) vsum = f4add(vsum, g4[(uint64_t)(p + j * piece_inputs) * row4 + q]);
+    const uint64_t voff4 = (uint64_t)(ft_in + p) * row4 + q;
+    reinterpret_cast<float4*>(grad)[voff4] = vsum;
     if (!apply_update) return;
     opt_update4(w, m, v, slow, voff4, vsum, s);
     if (!comb) return;
     const float4 wv = reinterpret_cast<const float4*>(w)[voff4];
-    for (uint32_t j = 0; j < count; ++j) {
-        const uint64_t off4 = (uint64_t)(g + j * stride) * row4 + q;
-        const float4 wr = reinterpret_cast<const float4*>(w)[off4];
-        reinterpret_cast<float4*>(comb)[off4] = f4add(wr, wv);
+    for (j = 0; j + U <= count; j += U) {
+        float4 wr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) wr[u] = reinterpret_cast<const float4*>(w)[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            reinterpret_cast<float4*>(comb)[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q] = f4add(wr[u], wv);
+    }
+    for (; j < count; ++j) {
+        const uint64_t off4 = (uint64_t)(p + j * piece_inputs) * row4 + q;
+        reinterpret_cast<float4*>(comb)[off4] = f4add(reinterpret_cast<const float4*>(w)[off4], wv);
     }
 }
 
@@ -448,26 +489,20 @@ uint32_t occurrence_key_bits(uint32_t cols) {
 }
 
 size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols) {
-    const uint32_t key_bits = occurrence_key_bits(cols);
     size_t bytes = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                       (const uint32_t*)nullptr, (uint32_t*)nullptr, (int)n_items,
-                                       0, (int)key_bits);
-    size_t scan_bytes = 0;
-    (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, (const uint32_t*)nullptr,
-                                           (uint32_t*)nullptr, (int)(2ull * cols + 2));
-    return bytes > scan_bytes ? bytes : scan_bytes;
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr,
+                                             (uint32_t*)nullptr, (const uint32_t*)nullptr,
+                                             (uint32_t*)nullptr, (int)n_items, 0,
+                                             (int)occurrence_key_bits(cols));
+    return bytes;
 }
 
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) {
     const uint64_t n_items = 2ull * a.batch * a.max_active;
-    const uint32_t n_keys = 2 * a.cols + 1;
-    TATARA_HIP(hipMemsetAsync(a.counts, 0, sizeof(uint32_t) * (n_keys + 1), stream),
-               "memset occurrence counts");
+    const uint32_t n_keys = 2 * a.cols + 1;  // keys 0..2*cols (2*cols = invalid slot)
     if (n_items > 0) {
         build_occurrence_keys_kernel<<<ceil_div(n_items, 256), 256, 0, stream>>>(
-            a.idx_stm, a.idx_nstm, a.nnz, a.keys_in, a.vals_in, a.counts, a.batch, a.max_active,
-            a.cols);
+            a.idx_stm, a.idx_nstm, a.nnz, a.keys_in, a.vals_in, a.batch, a.max_active, a.cols);
         TATARA_LAUNCHED("build_occurrence_keys");
         size_t bytes = a.temp_bytes;
         TATARA_HIP(hipcub::DeviceRadixSort::SortPairs(a.temp, bytes, a.keys_in, a.keys_out,
@@ -475,23 +510,37 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) 
                                                       (int)occurrence_key_bits(a.cols), stream),
                    "occurrence radix sort");
     }
-    size_t bytes = a.temp_bytes;
-    TATARA_HIP(hipcub::DeviceScan::ExclusiveSum(a.temp, bytes, a.counts, a.offsets, (int)n_keys + 1,
-                                                stream),
-               "occurrence offsets scan");
+    occurrence_offsets_kernel<<<ceil_div(n_items + 1, 256), 256, 0, stream>>>(a.keys_out, n_items,
+                                                                              n_keys, a.offsets);
+    TATARA_LAUNCHED("occurrence_offsets");
     return kOk;
 }
 
-int32_t launch_ft_backward_optimizer(const FtBackwardArgs& a, hipStream_t stream) {
+int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.ft_out % 4 == 0, "ft_out must be a multiple of 4");
     const uint32_t n_chunks = ceil_div(a.ft_out / 4, kWave);
-    const uint64_t tasks = (uint64_t)a.n_groups * n_chunks;
+    const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-    ft_backward_optimizer_kernel<<<blocks, 256, 0, stream>>>(
-        a.dft, a.occ_vals, a.occ_off, a.w, a.m, a.v, a.slow, a.comb, a.grad_out, a.ft_out,
-        a.n_groups, a.stride, a.count, a.has_virtual, a.virt_base, n_chunks, a.apply_update, a.opt);
-    TATARA_LAUNCHED("ft_backward_optimizer");
+    ft_grad_update_kernel<<<blocks, 256, 0, stream>>>(a.dft, a.occ_vals, a.occ_off, a.w, a.m, a.v,
+                                                      a.slow, a.grad, a.ft_out, a.rows, n_chunks,
+                                                      a.apply_update, a.opt);
+    TATARA_LAUNCHED("ft_grad_update");
+    return kOk;
+}
+
+int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb,
+                               hipStream_t stream) {
+    TATARA_REQUIRE(piece_inputs > 0 && a.rows % piece_inputs == 0,
+                   "virtual fold: rows must be a multiple of piece_inputs");
+    TATARA_REQUIRE(a.grad, "virtual fold needs the real-row gradients");
+    const uint32_t n_chunks = ceil_div(a.ft_out / 4, kWave);
+    const uint64_t tasks = (uint64_t)piece_inputs * n_chunks;
+    const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+    ft_virtual_fold_kernel<<<blocks, 256, 0, stream>>>(a.grad, a.w, a.m, a.v, a.slow, comb, a.ft_out,
+                                                       a.rows, piece_inputs, n_chunks,
+                                                       a.apply_update, a.opt);
+    TATARA_LAUNCHED("ft_virtual_fold");
     return kOk;
 }
 

@@ -34,23 +34,20 @@ struct OccurrenceSortArgs {
     uint32_t* vals_in;
     uint32_t* keys_out;
     uint32_t* vals_out;  // sorted dft row ids
-    uint32_t* counts;    // [2*cols + 2]
     uint32_t* offsets;   // [2*cols + 2]; key k occupies [offsets[k], offsets[k+1])
     void* temp;
     size_t temp_bytes;
 };
 
-struct FtBackwardArgs {
+struct FtGradArgs {
     const float* dft;          // [2][batch][ft_out]
     const uint32_t* occ_vals;  // sorted dft row ids
     const uint32_t* occ_off;   // offsets by key 2*f+p
     float *w, *m, *v, *slow;
-    float* comb;               // forward table (factorized) or null
-    float* grad_out;           // optional gradient dump or null
+    float* grad;               // gradient per row (required with a factorizer)
     uint32_t ft_out;
-    uint32_t n_groups, stride, count;  // group g = rows g + j*stride, j < count
-    uint32_t has_virtual, virt_base;   // virtual row virt_base + g
-    int32_t apply_update;              // 0: only dump gradients
+    uint32_t rows;             // real FT rows (ft_in)
+    int32_t apply_update;      // 0: only write gradients
     OptScalars opt;
 };
 
@@ -61,7 +58,9 @@ int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm, 
 uint32_t occurrence_key_bits(uint32_t cols);
 size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols);
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream);
-int32_t launch_ft_backward_optimizer(const FtBackwardArgs& a, hipStream_t stream);
+int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream);
+int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb,
+                               hipStream_t stream);
 int32_t launch_ft_fold(const float* w, float* comb, uint32_t ft_in, uint32_t ft_out,
                        uint32_t piece_inputs, hipStream_t stream);
 int32_t launch_ft_reduce(float* grad, uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs,

@@ -223,14 +223,14 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
                                  uint32_t batch, uint32_t ft_out, uint32_t cols,
                                  uint32_t max_active) {
     TATARA_REQUIRE(ft_out % 4 == 0, "ft_out must be a multiple of 4");
+    TATARA_REQUIRE(max_active <= 64, "max_active must be <= 64");
     const uint64_t n_items = 2ull * batch * max_active;
     const uint32_t n_keys = 2 * cols + 1;
-    DevScratch ki, vi, ko, vo, cnt, off, tmp;
+    DevScratch ki, vi, ko, vo, off, tmp;
     const size_t tb = occurrence_sort_temp_bytes(n_items, cols);
     int32_t st;
     if ((st = ki.alloc(4 * n_items)) || (st = vi.alloc(4 * n_items)) || (st = ko.alloc(4 * n_items)) ||
-        (st = vo.alloc(4 * n_items)) || (st = cnt.alloc(4ull * (n_keys + 1))) ||
-        (st = off.alloc(4ull * (n_keys + 1))) || (st = tmp.alloc(tb)))
+        (st = vo.alloc(4 * n_items)) || (st = off.alloc(4ull * (n_keys + 1))) || (st = tmp.alloc(tb)))
         return st;
     OccurrenceSortArgs os{};
     os.idx_stm = stm_idx;
@@ -243,23 +243,19 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
     os.vals_in = vi.as<uint32_t>();
     os.keys_out = ko.as<uint32_t>();
     os.vals_out = vo.as<uint32_t>();
-    os.counts = cnt.as<uint32_t>();
     os.offsets = off.as<uint32_t>();
     os.temp = tmp.p;
     os.temp_bytes = tb;
     if ((st = launch_occurrence_sort(os, 0))) return st;
-    FtBackwardArgs b{};
-    b.dft = dft;
-    b.occ_vals = vo.as<uint32_t>();
-    b.occ_off = off.as<uint32_t>();
-    b.grad_out = grad;
-    b.ft_out = ft_out;
-    b.n_groups = cols;
-    b.stride = 0;
-    b.count = 1;
-    b.has_virtual = 0;
-    b.apply_update = 0;
-    if ((st = launch_ft_backward_optimizer(b, 0))) return st;
+    FtGradArgs g{};
+    g.dft = dft;
+    g.occ_vals = vo.as<uint32_t>();
+    g.occ_off = off.as<uint32_t>();
+    g.grad = grad;
+    g.ft_out = ft_out;
+    g.rows = cols;
+    g.apply_update = 0;
+    if ((st = launch_ft_grad_update(g, 0))) return st;
     TATARA_HIP(hipDeviceSynchronize(), "ft_weight_grad");
     return kOk;
 }

@@ -113,7 +113,7 @@ struct LayerStackTrainer {
     uint32_t *bkt_hist = nullptr, *bin_start = nullptr, *bin_count = nullptr;
     // occurrence sort
     uint32_t *occ_ki = nullptr, *occ_vi = nullptr, *occ_ko = nullptr, *occ_vo = nullptr;
-    uint32_t *occ_cnt = nullptr, *occ_off = nullptr;
+    uint32_t* occ_off = nullptr;
     void* occ_tmp = nullptr;
     size_t occ_tmp_bytes = 0;
     // activations
@@ -124,6 +124,7 @@ struct LayerStackTrainer {
           *ftb_partial = nullptr;
     double* loss_partial = nullptr;
     uint32_t* chunk_info = nullptr;
+    float *tail_sum = nullptr, *b1s_sum = nullptr, *ftb_sum = nullptr, *w1_seg = nullptr;
     uint32_t max_chunks = 0;
     double *loss_out = nullptr, *weight_sum = nullptr, *wrm_scratch = nullptr;
     // lagged loss ring
@@ -237,7 +238,8 @@ struct LayerStackTrainer {
         const uint32_t l2_in = 2 * (l1 - 1);
 
         int32_t st;
-        if ((st = alloc_group(ft, "ft_w", (uint64_t)train_ft_in * ft_out, fmin, fmax, 0, keep)))
+        if ((st = alloc_group(ft, "ft_w", (uint64_t)train_ft_in * ft_out, fmin, fmax, 0,
+                              keep || c.piece_inputs > 0)))
             return st;
         const struct {
             const char* name;
@@ -299,7 +301,7 @@ struct LayerStackTrainer {
         occ_tmp_bytes = occurrence_sort_temp_bytes(n_items, ft_in);
         if ((st = arena.alloc(&occ_ki, n_items, false)) || (st = arena.alloc(&occ_vi, n_items, false)) ||
             (st = arena.alloc(&occ_ko, n_items, false)) || (st = arena.alloc(&occ_vo, n_items, false)) ||
-            (st = arena.alloc(&occ_cnt, 2ull * ft_in + 2)) || (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
+            (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
         if ((st = arena.alloc(&ft_stm, B * ft_out, false)) || (st = arena.alloc(&ft_nstm, B * ft_out, false)) ||
@@ -314,7 +316,10 @@ struct LayerStackTrainer {
             (st = arena.alloc(&b1s_partial, n_tail * l1)) || (st = arena.alloc(&loss_partial, n_tail)) ||
             (st = arena.alloc(&w1_partial, (uint64_t)max_chunks * l1 * ft_out)) ||
             (st = arena.alloc(&ftb_partial, n_post * 2 * ft_out)) ||
-            (st = arena.alloc(&chunk_info, 3ull * max_chunks + 1)) ||
+            (st = arena.alloc(&chunk_info, 3ull * max_chunks + 1 + nb + 2)) ||
+            (st = arena.alloc(&tail_sum, (uint64_t)nb * td.cells())) || (st = arena.alloc(&b1s_sum, l1)) ||
+            (st = arena.alloc(&ftb_sum, 2ull * ft_out)) ||
+            (st = arena.alloc(&w1_seg, (uint64_t)(nb + 1) * l1 * ft_out)) ||
             (st = arena.alloc(&loss_out, 2)) || (st = arena.alloc(&weight_sum, 1)) ||
             (st = arena.alloc(&wrm_scratch, ceil_div(B, 256) + 1)))
             return st;
@@ -499,6 +504,10 @@ struct LayerStackTrainer {
         a.loss_partial = loss_partial;
         a.w1_partial = w1_partial;
         a.ftb_partial = ftb_partial;
+        a.tail_sum = tail_sum;
+        a.b1s_sum = b1s_sum;
+        a.ftb_sum = ftb_sum;
+        a.w1_seg = w1_seg;
         a.loss_out = loss_out + slot;
         return a;
     }
@@ -559,7 +568,6 @@ struct LayerStackTrainer {
             os.vals_in = occ_vi;
             os.keys_out = occ_ko;
             os.vals_out = occ_vo;
-            os.counts = occ_cnt;
             os.offsets = occ_off;
             os.temp = occ_tmp;
             os.temp_bytes = occ_tmp_bytes;
@@ -621,7 +629,7 @@ struct LayerStackTrainer {
         const OptScalars sf = scalars(0, lr, step_count);
         const OptScalars sd = scalars(1, lr, step_count);
         const OptScalars sb = scalars(2, lr, step_count);
-        FtBackwardArgs fb{};
+        FtGradArgs fb{};
         fb.dft = dft;
         fb.occ_vals = occ_vo;
         fb.occ_off = occ_off;
@@ -629,24 +637,13 @@ struct LayerStackTrainer {
         fb.m = ft.m;
         fb.v = ft.v;
         fb.slow = ft.slow;
-        fb.comb = comb;
-        fb.grad_out = ft.grad;
+        fb.grad = ft.grad;
         fb.ft_out = ft_out;
-        if (factorized) {
-            fb.n_groups = pi;
-            fb.stride = pi;
-            fb.count = ft_in / pi;
-            fb.has_virtual = 1;
-            fb.virt_base = ft_in;
-        } else {
-            fb.n_groups = ft_in;
-            fb.stride = 0;
-            fb.count = 1;
-            fb.has_virtual = 0;
-        }
+        fb.rows = ft_in;
         fb.apply_update = 1;
         fb.opt = sf;
-        if ((st = launch_ft_backward_optimizer(fb, stream))) return st;
+        if ((st = launch_ft_grad_update(fb, stream))) return st;
+        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;
         if ((st = prof_mark(5))) return st;
         LsDenseGroup groups[9];
         for (int k = 0; k < 9; ++k) {
@@ -795,6 +792,7 @@ int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int3
     TATARA_REQUIRE(n == g->n, "element count mismatch");
     TATARA_HIP(hipStreamSynchronize(t.stream), "get_tensor sync");
     float* src = group_ptr(g, which);
+    if (which == 4 && !t.cfg.keep_grads) src = nullptr;  // the optimizer leaves zero gradients
     if (!src) {
         TATARA_REQUIRE(which == 4, "which must be 0..4");
         // gradients are zeroed by the optimizer; without keep_grads none are kept
