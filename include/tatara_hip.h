@@ -104,6 +104,10 @@ TATARA_API int32_t tatara_op_radam_step(float* weights, float* m, float* v, floa
                              float step_size, int32_t denom, float decay, float beta1,
                              float beta2, float eps, float min_w, float max_w, uint64_t n);
 TATARA_API int32_t tatara_op_ranger_lookahead_lerp(float* weights, float* slow, float alpha, uint64_t n);
+/* Plain device-to-device copy (float4 grid-stride loop): the known-size
+ * reference kernel used to calibrate HBM byte counters (FETCH_SIZE,
+ * WRITE_SIZE).  bytes must be a multiple of 16.  No reference counterpart. */
+TATARA_API int32_t tatara_op_copy(void* dst, const void* src, uint64_t bytes);
 /* Host pre-compute of RAdam (crates/gpu-kernels/src/pointwise/radam_step.rs:75-97). */
 TATARA_API int32_t tatara_radam_step_size_denom(uint64_t step, float beta1, float beta2,
                                      float n_sma_threshold, float* step_size, int32_t* denom);
@@ -199,7 +203,8 @@ TATARA_API int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const c
  * syncs).  While enabled, each step records events between its phases:
  *   0 prep (sorts)  1 FT gather + post  2 dense forward + loss
  *   3 dense backward (L1 weight grad, L1 input + FT post grad)
- *   4 FT backward + optimizer + fold  5 dense optimizer
+ *   4 FT gradient + optimizer (real rows)  5 factorizer virtual rows + fold
+ *   6 dense optimizer
  * phase_times sums the elapsed milliseconds of every phase over the steps
  * run since profiling was enabled (it synchronises). */
 TATARA_API int32_t tatara_trainer_set_profiling(TataraTrainer* trainer, int32_t enable);

@@ -100,6 +100,7 @@ SIGNATURES = {
         + [C.c_uint64],
     ),
     "tatara_op_ranger_lookahead_lerp": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_float, C.c_uint64]),
+    "tatara_op_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "tatara_radam_step_size_denom": (
         C.c_int32,
         [C.c_uint64, C.c_float, C.c_float, C.c_float, c_f32p, c_i32p],

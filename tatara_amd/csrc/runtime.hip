@@ -50,6 +50,12 @@ struct DevScratch {
     }
 };
 
+__global__ void copy_f4_kernel(const float4* __restrict__ src, float4* __restrict__ dst, uint64_t n4) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+        dst[i] = src[i];
+}
+
 }  // namespace tatara
 
 using namespace tatara;
@@ -112,6 +118,16 @@ int32_t tatara_memset(void* dst, int32_t byte, uint64_t bytes) {
 
 int32_t tatara_synchronize(void) {
     TATARA_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return kOk;
+}
+
+int32_t tatara_op_copy(void* dst, const void* src, uint64_t bytes) {
+    TATARA_REQUIRE(bytes % 16 == 0, "bytes must be a multiple of 16");
+    const uint64_t n4 = bytes / 16;
+    if (n4 == 0) return kOk;
+    copy_f4_kernel<<<2048, 256, 0, 0>>>(static_cast<const float4*>(src), static_cast<float4*>(dst), n4);
+    TATARA_LAUNCHED("copy_f4");
+    TATARA_HIP(hipDeviceSynchronize(), "copy_f4");
     return kOk;
 }
 

@@ -137,10 +137,10 @@ struct LayerStackTrainer {
     uint32_t last_b = 0;
 
     // phase profiling: events recorded between phases of each profiled step
-    static constexpr int kPhases = 6;
+    static constexpr int kPhases = 7;
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;  // (kPhases + 1) per profiled step
-    double phase_ms[kPhases] = {0, 0, 0, 0, 0, 0};
+    double phase_ms[kPhases] = {0, 0, 0, 0, 0, 0, 0};
     uint64_t prof_steps = 0;
     int prof_cursor = -1;  // first event of the current step
 
@@ -643,8 +643,9 @@ struct LayerStackTrainer {
         fb.apply_update = 1;
         fb.opt = sf;
         if ((st = launch_ft_grad_update(fb, stream))) return st;
-        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;
         if ((st = prof_mark(5))) return st;
+        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;
+        if ((st = prof_mark(6))) return st;
         LsDenseGroup groups[9];
         for (int k = 0; k < 9; ++k) {
             groups[k].w = small[k].w;
@@ -658,7 +659,7 @@ struct LayerStackTrainer {
             groups[k].kind = small[k].kind;
         }
         if ((st = launch_ls_dense_finalize(da, groups, sd, sb, 1, cfg.keep_grads, stream))) return st;
-        if ((st = prof_mark(6))) return st;
+        if ((st = prof_mark(7))) return st;
 
         // lagged loss (AsyncLossRing::read_and_queue_next)
         double prev = 0.0;

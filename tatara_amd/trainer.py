@@ -344,8 +344,8 @@ class LayerStackTrainer:
                                                       out.ctypes.data_as(_lib.c_f32p), n))
         return out
 
-    PHASES = ("prep", "ft_forward", "dense_forward", "dense_backward", "ft_backward_opt",
-              "dense_opt")
+    PHASES = ("prep", "ft_forward", "dense_forward", "dense_backward", "ft_grad_update",
+              "ft_virtual_fold", "dense_opt")
 
     def set_profiling(self, enable: bool) -> None:
         """Per-phase GPU timing with HIP events on the trainer's stream."""
