@@ -32,6 +32,20 @@ __device__ __forceinline__ float4 f4add(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
+// Streamed data (outputs written once, optimizer state touched once per step)
+// uses non-temporal accesses so it does not evict the gathered rows from L2.
+typedef float nt_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void st_nt(float4* p, float4 v) {
+    nt_f4 x = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(p));
+}
+
+__device__ __forceinline__ float4 ld_nt(const float4* p) {
+    const nt_f4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(p));
+    return make_float4(x.x, x.y, x.z, x.w);
+}
+
 // Loads the position's active indices into per-wave LDS in slot order,
 // keeping only valid ones (slot < nnz and 0 <= idx < cols), and returns how
 // many there are.  Skipping invalid slots here matches the reference, which
@@ -138,8 +152,8 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
         gather_rows<true, 8>(W, ft_out, s_idx, nv, q, q + half4, active, a0, a1);
         if (!active) return;
         float4* o4 = reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out);
-        o4[q] = a0;
-        o4[q + half4] = a1;
+        st_nt(o4 + q, a0);
+        st_nt(o4 + q + half4, a1);
         const float4 b0 = reinterpret_cast<const float4*>(bias)[q];
         const float4 b1 = reinterpret_cast<const float4*>(bias)[q + half4];
         float4 c;
@@ -147,7 +161,7 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
         c.y = crelu01(a0.y + b0.y) * crelu01(a1.y + b1.y) * scale;
         c.z = crelu01(a0.z + b0.z) * crelu01(a1.z + b1.z) * scale;
         c.w = crelu01(a0.w + b0.w) * crelu01(a1.w + b1.w) * scale;
-        reinterpret_cast<float4*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2))[q] = c;
+        st_nt(reinterpret_cast<float4*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2)) + q, c);
     } else {
         const bool active = q < row4;
         gather_rows<false, 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
@@ -280,24 +294,24 @@ __device__ __forceinline__ float4 segment_sum(const float4* __restrict__ dft4, u
 __device__ __forceinline__ void opt_update4(float* __restrict__ w, float* __restrict__ m,
                                             float* __restrict__ v, float* __restrict__ slow,
                                             uint64_t off4, float4 g, const OptScalars& s) {
-    float4 W = reinterpret_cast<float4*>(w)[off4];
-    float4 M = reinterpret_cast<float4*>(m)[off4];
-    float4 V = reinterpret_cast<float4*>(v)[off4];
+    float4 W = ld_nt(reinterpret_cast<float4*>(w) + off4);
+    float4 M = ld_nt(reinterpret_cast<float4*>(m) + off4);
+    float4 V = ld_nt(reinterpret_cast<float4*>(v) + off4);
     radam_elem(W.x, M.x, V.x, g.x, s);
     radam_elem(W.y, M.y, V.y, g.y, s);
     radam_elem(W.z, M.z, V.z, g.z, s);
     radam_elem(W.w, M.w, V.w, g.w, s);
     if (s.lookahead) {
-        float4 S = reinterpret_cast<float4*>(slow)[off4];
+        float4 S = ld_nt(reinterpret_cast<float4*>(slow) + off4);
         lerp_elem(W.x, S.x, s.alpha);
         lerp_elem(W.y, S.y, s.alpha);
         lerp_elem(W.z, S.z, s.alpha);
         lerp_elem(W.w, S.w, s.alpha);
-        reinterpret_cast<float4*>(slow)[off4] = S;
+        st_nt(reinterpret_cast<float4*>(slow) + off4, S);
     }
-    reinterpret_cast<float4*>(w)[off4] = W;
-    reinterpret_cast<float4*>(m)[off4] = M;
-    reinterpret_cast<float4*>(v)[off4] = V;
+    st_nt(reinterpret_cast<float4*>(w) + off4, W);
+    st_nt(reinterpret_cast<float4*>(m) + off4, M);
+    st_nt(reinterpret_cast<float4*>(v) + off4, V);
 }
 
 __global__ __launch_bounds__(256) void ft_grad_update_kernel(
@@ -320,7 +334,7 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(
     if (q >= row4) return;
     const float4 gr = segment_sum(reinterpret_cast<const float4*>(dft), row4, occ_vals, s0, s1, q);
     const uint64_t off4 = (uint64_t)f * row4 + q;
-    if (grad_out) reinterpret_cast<float4*>(grad_out)[off4] = gr;
+    if (grad_out) st_nt(reinterpret_cast<float4*>(grad_out) + off4, gr);
     if (apply_update) opt_update4(w, m, v, slow, off4, gr, s);
 }
 
