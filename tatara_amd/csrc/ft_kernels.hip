@@ -105,9 +105,11 @@ __device__ __forceinline__ void gather_rows(const float* __restrict__ W, uint64_
 // ---------------------------------------------------------------------------
 // Forward gather.
 //
-// One wave = one task (position, column chunk).  Lane j of chunk c owns float4
-// column q = 64c + j of the row (PAIR mode: q and its pair partner q + half/4,
-// so both halves of each CReLU pair sit in one lane).  Tasks are enumerated
+// One wave = one task (position, column chunk); each lane owns one float4
+// column, so a task reads 1 KB of every gathered row.  RAW/CONCAT: lane j of
+// chunk c owns column q = 64c + j.  PAIR: chunk c covers 32 CReLU pairs; lane
+// j < 32 owns q = 32c + j of the first half and lane j + 32 its partner
+// q + ft_out/8, and the pair meets with one cross-lane swap.  Tasks are enumerated
 // (perspective, chunk, position-in-schedule) and the schedule lists positions
 // grouped by king block, so concurrently running waves read rows of the same
 // king block (a few MB) and hit in L2; the XCD swizzle keeps neighbouring
@@ -145,24 +147,33 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
 
     const uint32_t half4 = ft_out / 8;
     const uint32_t row4 = ft_out / 4;
-    const uint32_t q = chunk * kWave + lane;
     float4 a0, a1;
     if (MODE == kPair) {
-        const bool active = q < half4;
-        gather_rows<true, 8>(W, ft_out, s_idx, nv, q, q + half4, active, a0, a1);
+        const uint32_t j = lane & 31u;
+        const uint32_t qp = chunk * 32 + j;  // pair index
+        const bool active = qp < half4;
+        const uint32_t q = lane < 32 ? qp : qp + half4;
+        gather_rows<false, 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
+        // first-half lanes receive their partner's sums from lane + 32
+        float4 p;
+        p.x = __shfl_xor(a0.x, 32);
+        p.y = __shfl_xor(a0.y, 32);
+        p.z = __shfl_xor(a0.z, 32);
+        p.w = __shfl_xor(a0.w, 32);
         if (!active) return;
         float4* o4 = reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out);
         st_nt(o4 + q, a0);
-        st_nt(o4 + q + half4, a1);
-        const float4 b0 = reinterpret_cast<const float4*>(bias)[q];
-        const float4 b1 = reinterpret_cast<const float4*>(bias)[q + half4];
+        if (lane >= 32) return;
+        const float4 b0 = reinterpret_cast<const float4*>(bias)[qp];
+        const float4 b1 = reinterpret_cast<const float4*>(bias)[qp + half4];
         float4 c;
-        c.x = crelu01(a0.x + b0.x) * crelu01(a1.x + b1.x) * scale;
-        c.y = crelu01(a0.y + b0.y) * crelu01(a1.y + b1.y) * scale;
-        c.z = crelu01(a0.z + b0.z) * crelu01(a1.z + b1.z) * scale;
-        c.w = crelu01(a0.w + b0.w) * crelu01(a1.w + b1.w) * scale;
-        st_nt(reinterpret_cast<float4*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2)) + q, c);
+        c.x = crelu01(a0.x + b0.x) * crelu01(p.x + b1.x) * scale;
+        c.y = crelu01(a0.y + b0.y) * crelu01(p.y + b1.y) * scale;
+        c.z = crelu01(a0.z + b0.z) * crelu01(p.z + b1.z) * scale;
+        c.w = crelu01(a0.w + b0.w) * crelu01(p.w + b1.w) * scale;
+        st_nt(reinterpret_cast<float4*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2)) + qp, c);
     } else {
+        const uint32_t q = chunk * kWave + lane;
         const bool active = q < row4;
         gather_rows<false, 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
         if (!active) return;
@@ -457,8 +468,7 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.ft_out % 8 == 0, "ft_out must be a multiple of 8");
     TATARA_REQUIRE(a.n_persp == 1 || a.n_persp == 2, "n_persp must be 1 or 2");
     if (a.batch == 0) return kOk;
-    const uint32_t lanes_needed = a.mode == kPair ? a.ft_out / 8 : a.ft_out / 4;
-    const uint32_t n_chunks = ceil_div(lanes_needed, kWave);
+    const uint32_t n_chunks = a.mode == kPair ? ceil_div(a.ft_out / 8, 32) : ceil_div(a.ft_out / 4, kWave);
     const uint64_t tasks = (uint64_t)a.n_persp * n_chunks * a.batch;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
     switch (a.mode) {
