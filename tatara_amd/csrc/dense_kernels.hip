@@ -30,7 +30,6 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ---------------------------------------------------------------------------
 // L1 forward.  One wave per 16-row sorted tile.
@@ -101,14 +100,6 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
 // Extended-WRM weight sum (wrm_weight_sum, native_kernels.cu:520-544), as a
 // deterministic two-level f64 reduction in position order.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wrm_weight_dev(float s, const LossParams& lp) {
-    const float tp = 1.0f / (1.0f + expf(-((s - lp.target_offset) / lp.target_scaling)));
-    const float tn = 1.0f / (1.0f + expf(-((-s - lp.target_offset) / lp.target_scaling)));
-    const float t = 0.5f * (1.0f + tp - tn);
-    const float wb = (t - 0.5f) * (t - 0.5f) * t * (1.0f - t);
-    return 1.0f + (powf(2.0f, lp.w1) - 1.0f) * powf(wb, lp.w2);
-}
-
 __global__ __launch_bounds__(256) void wrm_weight_partial_kernel(const float* __restrict__ score,
                                                                  uint32_t n, LossParams lp,
                                                                  double* __restrict__ partial) {
@@ -197,44 +188,8 @@ __global__ __launch_bounds__(kTailRows) void ls_tail_kernel(LsDenseArgs a, int32
         net = l3 + skip;
         a.net_output[orig] = net;
         // loss (loss_wdl / loss_wrm)
-        const float sc = a.score[orig];
-        const float wd = a.wdl[orig];
-        const float lam = a.wdl_lambda;
-        const LossParams& lp = a.loss;
-        if (lp.kind == 0) {
-            const float p = sigmoidf_(net * lp.scale);
-            const float ys = sigmoidf_(sc * lp.scale);
-            const float y = lam * wd + (1.0f - lam) * ys;
-            const float err = p - y;
-            loss_c = (double)err * (double)err;
-            dy = 2.0f * err * p * (1.0f - p) * lp.scale * a.per_pos_norm;
-        } else {
-            const float tp = 1.0f / (1.0f + expf(-((sc - lp.target_offset) / lp.target_scaling)));
-            const float tn = 1.0f / (1.0f + expf(-((-sc - lp.target_offset) / lp.target_scaling)));
-            const float twrm = 0.5f * (1.0f + tp - tn);
-            const float target = lam * wd + (1.0f - lam) * twrm;
-            const float sn = net * lp.nnue2score;
-            const float q = 1.0f / (1.0f + expf(-((sn - lp.in_offset) / lp.in_scaling)));
-            const float qm = 1.0f / (1.0f + expf(-((-sn - lp.in_offset) / lp.in_scaling)));
-            const float pred = 0.5f * (1.0f + q - qm);
-            const float err = pred - target;
-            if (!lp.extended) {
-                dy = err * (lp.nnue2score / lp.in_scaling) * (q * (1.0f - q) + qm * (1.0f - qm)) *
-                     a.per_pos_norm;
-                loss_c = (double)err * (double)err;
-            } else {
-                const float wb = (twrm - 0.5f) * (twrm - 0.5f) * twrm * (1.0f - twrm);
-                const float weight = 1.0f + (powf(2.0f, lp.w1) - 1.0f) * powf(wb, lp.w2);
-                const float asym = pred > target ? 1.0f + lp.qp_asymmetry : 1.0f;
-                const float ae = fabsf(err);
-                const float ap = powf(ae, lp.pow_exp - 1.0f);
-                const float sp = err < 0.0f ? -ap : ap;
-                const float inv = (float)(1.0 / a.weight_sum[0]);
-                const float pg = 0.5f * (lp.nnue2score / lp.in_scaling) * (q * (1.0f - q) + qm * (1.0f - qm));
-                dy = (weight * inv) * (asym * lp.pow_exp * sp) * pg;
-                loss_c = (double)(asym * powf(ae, lp.pow_exp) * weight * (float)a.batch * inv);
-            }
-        }
+        loss_c = position_loss(net, a.score[orig], a.wdl[orig], a.wdl_lambda, a.loss, a.per_pos_norm,
+                               a.weight_sum, a.batch, dy);
     }
     s_loss[t] = loss_c;
     if (!train) {
@@ -638,14 +593,6 @@ __global__ __launch_bounds__(256) void ls_dense_finalize_kernel(LsDenseArgs a, G
     G.grad[e] = keep_grads ? grad : 0.0f;
 }
 
-__global__ void ls_loss_reduce_kernel(const double* __restrict__ partial, uint32_t n,
-                                      double* __restrict__ out) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    double acc = 0.0;
-    for (uint32_t k = 0; k < n; ++k) acc += partial[k];
-    *out = acc;
-}
-
 }  // namespace
 
 uint32_t ls_tail_workgroups(uint32_t padded_b) { return ceil_div(padded_b, kTailRows); }
@@ -746,9 +693,22 @@ int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups,
 }
 
 int32_t launch_ls_loss_reduce(const LsDenseArgs& a, hipStream_t stream) {
-    ls_loss_reduce_kernel<<<1, 64, 0, stream>>>(a.loss_partial, ls_tail_workgroups(a.padded_b),
-                                               a.loss_out);
-    TATARA_LAUNCHED("ls_loss_reduce");
+    return launch_sum_f64(a.loss_partial, ls_tail_workgroups(a.padded_b), a.loss_out, stream);
+}
+
+int32_t launch_reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols,
+                           const uint32_t* seg_rows, uint32_t n_seg, float* out, hipStream_t stream) {
+    TATARA_REQUIRE(seg_rows || n_seg == 1, "reduce_rows: n_seg must be 1 without segments");
+    if (n_cols == 0 || n_seg == 0) return kOk;
+    reduce_rows_kernel<<<dim3(ceil_div(n_cols, 64), n_seg), 256, 0, stream>>>(P, n_rows, n_cols,
+                                                                               seg_rows, out);
+    TATARA_LAUNCHED("reduce_rows");
+    return kOk;
+}
+
+int32_t launch_sum_f64(const double* partial, uint32_t n, double* out, hipStream_t stream) {
+    sum_partials_f64_kernel<<<1, 64, 0, stream>>>(partial, n, out);
+    TATARA_LAUNCHED("sum_f64");
     return kOk;
 }
 

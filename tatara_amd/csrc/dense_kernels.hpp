@@ -5,18 +5,10 @@
 
 #include <cstdint>
 
+#include "loss.hpp"
 #include "optim.hpp"
 
 namespace tatara {
-
-// Loss selection, mirroring LossKind (crates/nnue-train/src/trainer.rs:89-221).
-struct LossParams {
-    int32_t kind;  // 0 sigmoid-MSE, 1 WRM
-    float scale;   // sigmoid
-    float nnue2score, in_scaling, in_offset, target_offset, target_scaling;
-    float pow_exp, qp_asymmetry, w1, w2;
-    int32_t extended;  // WRM extended form (pow != 2 || asym != 0 || w1 != 0)
-};
 
 // Layout of the per-workgroup gradient partials written by the tail kernel.
 struct TailDims {
@@ -116,5 +108,14 @@ int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups /*9*
                                  int32_t apply_update, int32_t keep_grads, hipStream_t stream);
 // Sums the tail loss partials into a.loss_out (deterministic order).
 int32_t launch_ls_loss_reduce(const LsDenseArgs& a, hipStream_t stream);
+
+// Deterministic column sums of a row-major partial matrix P[n_rows][n_cols]:
+// out[s][c] = sum of P[r][c] over segment s, whose rows are
+// [seg_rows[s], seg_rows[s+1]) (device array) or all rows when seg_rows is
+// null (n_seg must then be 1).  The summation order is fixed.
+int32_t launch_reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols,
+                           const uint32_t* seg_rows, uint32_t n_seg, float* out, hipStream_t stream);
+// out[0] = sum of partial[0..n) in index order (f64).
+int32_t launch_sum_f64(const double* partial, uint32_t n, double* out, hipStream_t stream);
 
 }  // namespace tatara

@@ -1,0 +1,435 @@
+// Simple architecture (FT -> L1 -> L2 -> L3 with CReLU) dense layers for gfx950.
+//
+// Forward/backward follow SimpleGpuTrainer::run_forward_kernels /
+// run_backward_kernels (bins/nnue_train/src/trainer_simple.rs:857-2347):
+// combined = [crelu(ft_stm + b), crelu(ft_nstm + b)] of width 2*ft_out, then
+// row-major x . W + bias layers (W stored [in][out], as the cuBLAS row-major
+// wrappers of trainer_common.rs:752-860 read it), the loss, and the chain rule
+// back to dft.  Per-element arithmetic restates the CPU functions the
+// reference pins those layers to (crates/gpu-kernels/src/layerstack/
+// dense_mm.rs, crelu.rs; loss_wdl.rs / loss_wrm.rs): a dense sum starts at the
+// bias and adds k in ascending order.
+//
+// MFMA (v_mfma_f32_16x16x4_f32) carries the two FT->L1 contractions (the L1
+// forward, K = 2*ft_out, and the L1 weight gradient, K = rows); the tiny L2/L3
+// layers run one row per thread.  Batch reductions go through per-workgroup
+// partials summed in a fixed order: no float atomics, bit-reproducible steps.
+#include "simple_kernels.hpp"
+
+#include "common.hpp"
+#include "dense_kernels.hpp"
+
+namespace tatara {
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// L1 forward: one wave per 16-row tile, L1/16 output blocks of 16 columns.
+// MFMA operand layout (16x16x4 f32): lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; element r of the result is D[4*(l/16)+r][l%16].  Lane (i, q)
+// loads a float4 of row i at k = 16*kb + 4q and feeds its components to four
+// successive MFMAs with the matching rows k..k+3 of W.
+// ---------------------------------------------------------------------------
+template <int L1>
+__global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
+    constexpr int NB = L1 / 16;
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t tile = blockIdx.x * 4 + wave;
+    const uint32_t batch = a.batch;
+    if (tile * 16 >= batch) return;
+    const uint32_t i = lane % 16, q = lane / 16;
+    const uint32_t K = 2 * a.ft_out;
+    const uint32_t row_a = tile * 16 + i;
+    const float4* X = row_a < batch ? reinterpret_cast<const float4*>(a.combined + (uint64_t)row_a * K)
+                                    : nullptr;
+    floatx4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const float b = a.l1_b[16 * nb + i];  // dense_mm_fwd_cpu: the sum starts at the bias
+        acc[nb] = floatx4{b, b, b, b};
+    }
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t kb = 0; kb < K / 16; ++kb) {
+        const float4 x = X ? X[kb * 4 + q] : zero4;
+        const float* w = a.l1_w + (uint64_t)(kb * 16 + 4 * q) * L1 + i;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            acc[nb] = mfma4(x.x, w[0 * L1 + 16 * nb], acc[nb]);
+            acc[nb] = mfma4(x.y, w[1 * L1 + 16 * nb], acc[nb]);
+            acc[nb] = mfma4(x.z, w[2 * L1 + 16 * nb], acc[nb]);
+            acc[nb] = mfma4(x.w, w[3 * L1 + 16 * nb], acc[nb]);
+        }
+    }
+    // the bias seeded every row of column i; lane (j = i, q) holds rows 4q + r
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t row = tile * 16 + 4 * q + r;
+        if (row >= batch) continue;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) a.l1_pre[(uint64_t)row * L1 + 16 * nb + i] = acc[nb][r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Output kernel: one thread per row.  CReLU, L2, CReLU, L3, loss; with train
+// the backward to dl1 and this workgroup's gradient partials (rows in order).
+// ---------------------------------------------------------------------------
+template <int L1, int L2>
+__global__ __launch_bounds__(kSimpleTailRows) void simple_tail_kernel(SimpleDenseArgs a,
+                                                                      int32_t train) {
+    constexpr int R = kSimpleTailRows;
+    __shared__ float s_l1a[R][L1 + 1];
+    __shared__ float s_dl2[R][L2 + 1];
+    __shared__ float s_l2a[R][L2 + 1];
+    __shared__ float s_dl1[R][L1 + 1];
+    __shared__ float s_dy[R];
+    __shared__ double s_loss[R];
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t row = blockIdx.x * R + t;
+    const bool real = row < a.batch;
+    float l1p[L1], l1a[L1], l2p[L2], l2a[L2];
+    float dy = 0.0f;
+    double loss_c = 0.0;
+    if (real) {
+        const float* src = a.l1_pre + (uint64_t)row * L1;
+#pragma unroll
+        for (int k = 0; k < L1; ++k) {
+            l1p[k] = src[k];
+            l1a[k] = crelu01(l1p[k]);
+        }
+#pragma unroll
+        for (int o = 0; o < L2; ++o) {
+            float acc = a.l2_b[o];
+#pragma unroll
+            for (int k = 0; k < L1; ++k) acc += l1a[k] * a.l2_w[k * L2 + o];
+            l2p[o] = acc;
+            l2a[o] = crelu01(acc);
+        }
+        float net = a.l3_b[0];
+#pragma unroll
+        for (int k = 0; k < L2; ++k) net += l2a[k] * a.l3_w[k];
+        a.net_output[row] = net;
+        loss_c = position_loss(net, a.score[row], a.wdl[row], a.wdl_lambda, a.loss, a.per_pos_norm,
+                               a.weight_sum, a.batch, dy);
+    }
+    s_loss[t] = loss_c;
+    if (!train) {
+        __syncthreads();
+        if (t == 0) {
+            double acc = 0.0;
+            for (int k = 0; k < R; ++k) acc += s_loss[k];
+            a.loss_partial[blockIdx.x] = acc;
+        }
+        return;
+    }
+
+    float dl2[L2], dl1[L1];
+    if (real) {
+#pragma unroll
+        for (int o = 0; o < L2; ++o) {
+            const float g = dy * a.l3_w[o];                    // x . W^T with out_dim 1
+            dl2[o] = (l2p[o] > 0.0f && l2p[o] < 1.0f) ? g : 0.0f;  // crelu_grad
+        }
+#pragma unroll
+        for (int k = 0; k < L1; ++k) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int o = 0; o < L2; ++o) acc += dl2[o] * a.l2_w[k * L2 + o];
+            dl1[k] = (l1p[k] > 0.0f && l1p[k] < 1.0f) ? acc : 0.0f;
+        }
+        float* d = a.dl1 + (uint64_t)row * L1;
+#pragma unroll
+        for (int k = 0; k < L1; ++k) d[k] = dl1[k];
+    } else {
+#pragma unroll
+        for (int o = 0; o < L2; ++o) dl2[o] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < L1; ++k) dl1[k] = 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < L1; ++k) {
+        s_l1a[t][k] = real ? l1a[k] : 0.0f;
+        s_dl1[t][k] = dl1[k];
+    }
+#pragma unroll
+    for (int o = 0; o < L2; ++o) {
+        s_dl2[t][o] = dl2[o];
+        s_l2a[t][o] = real ? l2a[o] : 0.0f;
+    }
+    s_dy[t] = dy;
+    __syncthreads();
+    if (t == 0) {
+        double acc = 0.0;
+        for (int k = 0; k < R; ++k) acc += s_loss[k];
+        a.loss_partial[blockIdx.x] = acc;
+    }
+    const SimpleTailDims td{(uint32_t)L1, (uint32_t)L2};
+    const uint32_t cells = td.cells();
+    float* part = a.tail_partial + (uint64_t)blockIdx.x * cells;
+    for (uint32_t c = t; c < cells; c += R) {
+        float acc = 0.0f;
+        if (c < td.off_b2()) {
+            const uint32_t k = c / L2, o = c % L2;
+            for (int r = 0; r < R; ++r) acc += s_l1a[r][k] * s_dl2[r][o];
+        } else if (c < td.off_w3()) {
+            const uint32_t o = c - td.off_b2();
+            for (int r = 0; r < R; ++r) acc += s_dl2[r][o];
+        } else if (c < td.off_b3()) {
+            const uint32_t o = c - td.off_w3();
+            for (int r = 0; r < R; ++r) acc += s_l2a[r][o] * s_dy[r];
+        } else if (c < td.off_b1()) {
+            for (int r = 0; r < R; ++r) acc += s_dy[r];
+        } else {
+            const uint32_t k = c - td.off_b1();
+            for (int r = 0; r < R; ++r) acc += s_dl1[r][k];
+        }
+        part[c] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// L1 weight-gradient partials: P[chunk][k][o] = sum over the chunk's rows of
+// combined[row][k] * dl1[row][o].  One wave owns 64 columns k; lane (o, q)
+// supplies dl1 of row 4s + q as the A operand and lane (q, kk) a float4 of
+// combined at k0 + 4kk as B, so block c of its four MFMAs holds k0 + 4kk + c.
+// ---------------------------------------------------------------------------
+template <int L1>
+__global__ __launch_bounds__(256) void simple_l1_wgrad_kernel(SimpleDenseArgs a) {
+    constexpr int NB = L1 / 16;
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t K = 2 * a.ft_out;
+    const uint32_t k0 = (blockIdx.y * 4 + wave) * 64;
+    if (k0 >= K) return;
+    const uint32_t chunk = blockIdx.x;
+    const uint32_t r0 = chunk * kSimpleChunkRows;
+    const uint32_t r1 = min(r0 + kSimpleChunkRows, a.batch);
+    const uint32_t o = lane % 16, q = lane / 16, kk = lane % 16;
+    const bool kvalid = k0 + 4 * kk < K;
+    floatx4 acc[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[nb][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t base = r0; base < r1; base += 4) {
+        const uint32_t row = base + q;
+        const bool rv = row < r1;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rv && kvalid) x = reinterpret_cast<const float4*>(a.combined + (uint64_t)row * K + k0)[kk];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const float d = rv ? a.dl1[(uint64_t)row * L1 + 16 * nb + o] : 0.0f;
+            acc[nb][0] = mfma4(d, x.x, acc[nb][0]);
+            acc[nb][1] = mfma4(d, x.y, acc[nb][1]);
+            acc[nb][2] = mfma4(d, x.z, acc[nb][2]);
+            acc[nb][3] = mfma4(d, x.w, acc[nb][3]);
+        }
+    }
+    if (!kvalid) return;
+    float* P = a.w1_partial + (uint64_t)chunk * K * L1;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                P[(uint64_t)(k0 + 4 * kk + c) * L1 + 16 * nb + 4 * q + r] = acc[nb][c][r];
+}
+
+// ---------------------------------------------------------------------------
+// L1 input gradient fused with the FT CReLU gradient.  Thread c owns FT
+// column c of both perspectives: dcombined[row][p*ft_out + c] =
+// sum_o dl1[row][o] * l1_w[p*ft_out + c][o] (o ascending, from 0), then
+// dft_p[row][c] passes it where 0 < x < 1 (simple_bwd_ft_act_crelu_fused,
+// native_kernels.cu:1452).  The ft_b partial adds stm + nstm per row, rows in
+// order (simple_bias_grad_dual, native_kernels.cu:1572).
+// ---------------------------------------------------------------------------
+template <int L1>
+__global__ __launch_bounds__(256) void simple_l1_input_post_kernel(SimpleDenseArgs a) {
+    constexpr int R = kSimplePostRows;
+    __shared__ float s_d[R][L1];
+    const uint32_t ft_out = a.ft_out;
+    const uint32_t batch = a.batch;
+    const uint32_t r0 = blockIdx.y * R;
+    const uint32_t nr = min((uint32_t)R, batch - r0);
+    for (uint32_t e = threadIdx.x; e < nr * L1; e += 256)
+        s_d[e / L1][e % L1] = a.dl1[(uint64_t)r0 * L1 + e];
+    __syncthreads();
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= ft_out) return;
+    float ws[L1], wn[L1];
+#pragma unroll
+    for (int o = 0; o < L1; ++o) {
+        ws[o] = a.l1_w[(uint64_t)c * L1 + o];
+        wn[o] = a.l1_w[(uint64_t)(ft_out + c) * L1 + o];
+    }
+    float* dft_s = a.dft;
+    float* dft_n = a.dft + (uint64_t)batch * ft_out;
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < nr; ++r) {
+        const uint64_t i = (uint64_t)(r0 + r) * ft_out + c;
+        float da = 0.0f, db = 0.0f;
+#pragma unroll
+        for (int o = 0; o < L1; ++o) {
+            da += s_d[r][o] * ws[o];
+            db += s_d[r][o] * wn[o];
+        }
+        const float xs = a.ft_stm[i], xn = a.ft_nstm[i];
+        const float gs = (xs > 0.0f && xs < 1.0f) ? da : 0.0f;
+        const float gn = (xn > 0.0f && xn < 1.0f) ? db : 0.0f;
+        dft_s[i] = gs;
+        dft_n[i] = gn;
+        acc += gs + gn;
+    }
+    a.ftb_partial[(uint64_t)blockIdx.y * ft_out + c] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Dense gradients from the reduced partials + RAdam/Ranger/AdamW, one thread
+// per element of ft_b, l1_w, l1_b, l2_w, l2_b, l3_w, l3_b.
+// ---------------------------------------------------------------------------
+struct SimpleGroupTable {
+    SimpleDenseGroup g[7];
+    uint64_t start[8];
+};
+
+__global__ __launch_bounds__(256) void simple_dense_finalize_kernel(SimpleDenseArgs a,
+                                                                    SimpleGroupTable gt,
+                                                                    OptScalars dense,
+                                                                    OptScalars bias,
+                                                                    int32_t keep_grads) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= gt.start[7]) return;
+    int gi = 0;
+    while (i >= gt.start[gi + 1]) ++gi;
+    const uint64_t e = i - gt.start[gi];
+    const SimpleTailDims td{a.l1, a.l2};
+    float grad;
+    switch (gi) {
+        case 0: grad = a.ftb_sum[e]; break;
+        case 1: grad = a.w1_sum[e]; break;
+        case 2: grad = a.tail_sum[td.off_b1() + e]; break;
+        case 3: grad = a.tail_sum[td.off_w2() + e]; break;
+        case 4: grad = a.tail_sum[td.off_b2() + e]; break;
+        case 5: grad = a.tail_sum[td.off_w3() + e]; break;
+        default: grad = a.tail_sum[td.off_b3()]; break;
+    }
+    const SimpleDenseGroup& G = gt.g[gi];
+    OptScalars s = G.kind == 2 ? bias : dense;
+    s.min_w = G.min_w;
+    s.max_w = G.max_w;
+    float W = G.w[e], M = G.m[e], V = G.v[e];
+    radam_elem(W, M, V, grad, s);
+    if (s.lookahead) {
+        float S = G.slow[e];
+        lerp_elem(W, S, s.alpha);
+        G.slow[e] = S;
+    }
+    G.w[e] = W;
+    G.m[e] = M;
+    G.v[e] = V;
+    G.grad[e] = keep_grads ? grad : 0.0f;
+}
+
+}  // namespace
+
+uint32_t simple_tail_workgroups(uint32_t batch) { return ceil_div(batch, kSimpleTailRows); }
+uint32_t simple_chunks(uint32_t batch) { return ceil_div(batch, kSimpleChunkRows); }
+uint32_t simple_post_workgroups(uint32_t batch) { return ceil_div(batch, kSimplePostRows); }
+
+static int32_t check_dims(const SimpleDenseArgs& a) {
+    TATARA_REQUIRE(a.l1 == 16 || a.l1 == 32, "Simple l1 must be 16 or 32");
+    TATARA_REQUIRE(a.l2 == 32, "Simple l2 must be 32");
+    TATARA_REQUIRE(a.ft_out % 8 == 0, "Simple ft_out must be a multiple of 8");
+    return kOk;
+}
+
+int32_t launch_simple_l1_forward(const SimpleDenseArgs& a, hipStream_t stream) {
+    int32_t st = check_dims(a);
+    if (st) return st;
+    const uint32_t tiles = ceil_div(a.batch, 16);
+    if (tiles == 0) return kOk;
+    if (a.l1 == 32)
+        simple_l1_fwd_kernel<32><<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    else
+        simple_l1_fwd_kernel<16><<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    TATARA_LAUNCHED("simple_l1_forward");
+    return kOk;
+}
+
+int32_t launch_simple_tail(const SimpleDenseArgs& a, int32_t train, hipStream_t stream) {
+    int32_t st = check_dims(a);
+    if (st) return st;
+    const uint32_t blocks = simple_tail_workgroups(a.batch);
+    if (blocks == 0) return kOk;
+    if (a.l1 == 32)
+        simple_tail_kernel<32, 32><<<blocks, kSimpleTailRows, 0, stream>>>(a, train);
+    else
+        simple_tail_kernel<16, 32><<<blocks, kSimpleTailRows, 0, stream>>>(a, train);
+    TATARA_LAUNCHED("simple_tail");
+    return kOk;
+}
+
+int32_t launch_simple_l1_weight_grad(const SimpleDenseArgs& a, hipStream_t stream) {
+    int32_t st = check_dims(a);
+    if (st) return st;
+    const uint32_t chunks = simple_chunks(a.batch);
+    if (chunks == 0) return kOk;
+    const dim3 grid(chunks, ceil_div(2 * a.ft_out, 256));
+    if (a.l1 == 32)
+        simple_l1_wgrad_kernel<32><<<grid, 256, 0, stream>>>(a);
+    else
+        simple_l1_wgrad_kernel<16><<<grid, 256, 0, stream>>>(a);
+    TATARA_LAUNCHED("simple_l1_weight_grad");
+    return kOk;
+}
+
+int32_t launch_simple_l1_input_post(const SimpleDenseArgs& a, hipStream_t stream) {
+    int32_t st = check_dims(a);
+    if (st) return st;
+    const uint32_t rows = simple_post_workgroups(a.batch);
+    if (rows == 0) return kOk;
+    const dim3 grid(ceil_div(a.ft_out, 256), rows);
+    if (a.l1 == 32)
+        simple_l1_input_post_kernel<32><<<grid, 256, 0, stream>>>(a);
+    else
+        simple_l1_input_post_kernel<16><<<grid, 256, 0, stream>>>(a);
+    TATARA_LAUNCHED("simple_l1_input_post");
+    return kOk;
+}
+
+int32_t launch_simple_dense_finalize(const SimpleDenseArgs& a, SimpleDenseGroup* groups,
+                                     const OptScalars& dense, const OptScalars& bias,
+                                     int32_t keep_grads, hipStream_t stream) {
+    int32_t st = check_dims(a);
+    if (st) return st;
+    const SimpleTailDims td{a.l1, a.l2};
+    const uint32_t K = 2 * a.ft_out;
+    if ((st = launch_reduce_rows(a.tail_partial, simple_tail_workgroups(a.batch), td.cells(), nullptr,
+                                 1, a.tail_sum, stream)))
+        return st;
+    if ((st = launch_reduce_rows(a.w1_partial, simple_chunks(a.batch), K * a.l1, nullptr, 1, a.w1_sum,
+                                 stream)))
+        return st;
+    if ((st = launch_reduce_rows(a.ftb_partial, simple_post_workgroups(a.batch), a.ft_out, nullptr, 1,
+                                 a.ftb_sum, stream)))
+        return st;
+    SimpleGroupTable gt;
+    gt.start[0] = 0;
+    for (int k = 0; k < 7; ++k) {
+        gt.g[k] = groups[k];
+        gt.start[k + 1] = gt.start[k] + groups[k].n;
+    }
+    simple_dense_finalize_kernel<<<ceil_div(gt.start[7], 256), 256, 0, stream>>>(a, gt, dense, bias,
+                                                                                 keep_grads);
+    TATARA_LAUNCHED("simple_dense_finalize");
+    return kOk;
+}
+
+}  // namespace tatara

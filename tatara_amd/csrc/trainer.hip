@@ -32,18 +32,16 @@
 #include "dense_kernels.hpp"
 #include "ft_kernels.hpp"
 #include "init.hpp"
+#include "trainer_base.hpp"
 
 namespace tatara {
+
+TrainerBase* new_simple_trainer();
 
 namespace {
 
 constexpr float kFtPostScale = 127.0f / 128.0f;  // arch.rs FT_POST_SCALE
 constexpr float kL1SqrScale = 127.0f / 128.0f;   // arch.rs L1_SQR_SCALE
-constexpr float kBeta2 = 0.999f;                 // RangerParams::DEFAULT
-constexpr float kEps = 1e-8f;
-constexpr float kAlpha = 0.5f;
-constexpr uint64_t kRangerK = 6;
-constexpr float kNSmaThreshold = 5.0f;
 constexpr float kQuantClamp = 127.0f / 64.0f;    // i8::MAX / QB
 
 __global__ void bucket_keys_kernel(const int32_t* __restrict__ bucket, uint8_t* __restrict__ keys,
@@ -59,38 +57,10 @@ uint32_t padded_sort_batch(uint32_t b, uint32_t nb) {
     return (raw + 15) / 16 * 16;
 }
 
-struct DeviceArena {
-    std::vector<void*> ptrs;
-    ~DeviceArena() {
-        for (void* p : ptrs) (void)hipFree(p);
-    }
-    template <class T>
-    int32_t alloc(T** out, uint64_t count, bool zero = true) {
-        void* p = nullptr;
-        const uint64_t bytes = count * sizeof(T) ? count * sizeof(T) : 4;
-        TATARA_HIP(hipMalloc(&p, bytes), "hipMalloc trainer buffer");
-        ptrs.push_back(p);
-        if (zero) TATARA_HIP(hipMemset(p, 0, bytes), "hipMemset trainer buffer");
-        *out = static_cast<T*>(p);
-        return kOk;
-    }
-};
-
-struct ParamGroup {
-    const char* name;
-    float *w = nullptr, *m = nullptr, *v = nullptr, *slow = nullptr, *grad = nullptr;
-    uint64_t n = 0;
-    float min_w, max_w;
-    int32_t kind;  // 0 ft, 1 dense, 2 bias
-};
-
 }  // namespace
 
-struct LayerStackTrainer {
-    TataraTrainerConfig cfg{};
-    hipStream_t stream = nullptr;
-    DeviceArena arena;
-
+class LayerStackTrainer final : public TrainerBase {
+   public:
     uint32_t ft_in = 0, train_ft_in = 0, max_active = 0, pi = 0, ft_out = 0, l1 = 0, l2 = 0, nb = 0;
     uint32_t max_b = 0, max_p = 0;
     bool factorized = false;
@@ -99,9 +69,6 @@ struct LayerStackTrainer {
     ParamGroup small[9];    // uniform_optim_group_layout order
     float* comb = nullptr;  // factorized forward table [ft_in][ft_out]
 
-    // device copies of host batches
-    int32_t *in_stm = nullptr, *in_nstm = nullptr, *in_nnz = nullptr, *in_bucket = nullptr;
-    float *in_score = nullptr, *in_wdl = nullptr;
     // schedule
     uint32_t n_king_bins = 1;
     uint8_t* sched_keys = nullptr;
@@ -127,81 +94,8 @@ struct LayerStackTrainer {
     float *tail_sum = nullptr, *b1s_sum = nullptr, *ftb_sum = nullptr, *w1_seg = nullptr;
     uint32_t max_chunks = 0;
     double *loss_out = nullptr, *weight_sum = nullptr, *wrm_scratch = nullptr;
-    // lagged loss ring
-    double* pinned_loss = nullptr;
-    hipEvent_t loss_ev[2] = {nullptr, nullptr};
-    int pending = -1;  // slot holding the last queued loss
-    int next_slot = 0;
 
-    uint64_t step_count = 0;
-    uint32_t last_b = 0;
-
-    // phase profiling: events recorded between phases of each profiled step
-    static constexpr int kPhases = 7;
-    bool profiling = false;
-    std::vector<hipEvent_t> prof_events;  // (kPhases + 1) per profiled step
-    double phase_ms[kPhases] = {0, 0, 0, 0, 0, 0, 0};
-    uint64_t prof_steps = 0;
-    int prof_cursor = -1;  // first event of the current step
-
-    int32_t prof_mark(int k) {
-        if (!profiling) return kOk;
-        hipEvent_t e = nullptr;
-        TATARA_HIP(hipEventCreate(&e), "hipEventCreate (profiling)");
-        TATARA_HIP(hipEventRecord(e, stream), "hipEventRecord (profiling)");
-        if (k == 0) prof_cursor = (int)prof_events.size();
-        prof_events.push_back(e);
-        return kOk;
-    }
-
-    int32_t prof_collect() {
-        TATARA_HIP(hipStreamSynchronize(stream), "profiling sync");
-        const size_t per = kPhases + 1;
-        for (size_t s = 0; s + per <= prof_events.size(); s += per) {
-            for (int k = 0; k < kPhases; ++k) {
-                float ms = 0.f;
-                TATARA_HIP(hipEventElapsedTime(&ms, prof_events[s + k], prof_events[s + k + 1]),
-                           "hipEventElapsedTime");
-                phase_ms[k] += ms;
-            }
-            prof_steps += 1;
-        }
-        for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
-        prof_events.clear();
-        return kOk;
-    }
-
-    ~LayerStackTrainer() {
-        if (stream) (void)hipStreamSynchronize(stream);
-        for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
-        for (auto& e : loss_ev)
-            if (e) (void)hipEventDestroy(e);
-        if (pinned_loss) (void)hipHostFree(pinned_loss);
-        if (stream) (void)hipStreamDestroy(stream);
-    }
-
-    int32_t alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx, int kind,
-                        bool with_grad) {
-        g.name = name;
-        g.n = n;
-        g.min_w = mn;
-        g.max_w = mx;
-        g.kind = kind;
-        int32_t st;
-        if ((st = arena.alloc(&g.w, n)) || (st = arena.alloc(&g.m, n)) ||
-            (st = arena.alloc(&g.v, n)) || (st = arena.alloc(&g.slow, n)))
-            return st;
-        if (with_grad && (st = arena.alloc(&g.grad, n))) return st;
-        return kOk;
-    }
-
-    int32_t upload(float* dst, const std::vector<float>& src) {
-        TATARA_HIP(hipMemcpy(dst, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice),
-                   "upload init weights");
-        return kOk;
-    }
-
-    int32_t create(const TataraTrainerConfig& c) {
+    int32_t create(const TataraTrainerConfig& c) override {
         cfg = c;
         TATARA_REQUIRE(c.arch == TATARA_ARCH_LAYERSTACK, "only the LayerStack architecture is built");
         TATARA_REQUIRE(c.max_batch > 0 && c.max_batch % 16 == 0, "max_batch must be a positive multiple of 16");
@@ -214,12 +108,8 @@ struct LayerStackTrainer {
         TATARA_REQUIRE(c.piece_inputs >= 0, "piece_inputs >= 0");
         if (c.piece_inputs > 0)
             TATARA_REQUIRE(c.ft_in % c.piece_inputs == 0, "ft_in must be a multiple of piece_inputs");
-        TATARA_HIP(hipSetDevice(c.device), "hipSetDevice");
-        TATARA_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
-        TATARA_HIP(hipEventCreateWithFlags(&loss_ev[0], hipEventDisableTiming), "hipEventCreate");
-        TATARA_HIP(hipEventCreateWithFlags(&loss_ev[1], hipEventDisableTiming), "hipEventCreate");
-        TATARA_HIP(hipHostMalloc((void**)&pinned_loss, 2 * sizeof(double), hipHostMallocDefault),
-                   "hipHostMalloc loss ring");
+        int32_t st;
+        if ((st = init_runtime(c.device))) return st;
 
         ft_in = c.ft_in;
         pi = c.piece_inputs;
@@ -237,7 +127,6 @@ struct LayerStackTrainer {
         const float fmax = std::numeric_limits<float>::max();
         const uint32_t l2_in = 2 * (l1 - 1);
 
-        int32_t st;
         if ((st = alloc_group(ft, "ft_w", (uint64_t)train_ft_in * ft_out, fmin, fmax, 0,
                               keep || c.piece_inputs > 0)))
             return st;
@@ -281,10 +170,7 @@ struct LayerStackTrainer {
 
         // workspace
         const uint64_t B = max_b, P = max_p;
-        if ((st = arena.alloc(&in_stm, B * max_active)) || (st = arena.alloc(&in_nstm, B * max_active)) ||
-            (st = arena.alloc(&in_nnz, B)) || (st = arena.alloc(&in_bucket, B)) ||
-            (st = arena.alloc(&in_score, B)) || (st = arena.alloc(&in_wdl, B)))
-            return st;
+        if ((st = alloc_inputs(B, max_active))) return st;
         n_king_bins = factorized ? ceil_div(ft_in, pi) : 1;
         if (n_king_bins > 128) n_king_bins = 128;
         if ((st = arena.alloc(&sched_keys, 2 * B)) || (st = arena.alloc(&schedule, 2 * B)) ||
@@ -327,7 +213,7 @@ struct LayerStackTrainer {
         return sync_forward_weights();
     }
 
-    int32_t sync_forward_weights() {
+    int32_t sync_forward_weights() override {
         if (!factorized) return kOk;
         int32_t st = launch_ft_fold(ft.w, comb, ft_in, ft_out, pi, stream);
         if (st) return st;
@@ -335,129 +221,11 @@ struct LayerStackTrainer {
         return kOk;
     }
 
-    ParamGroup* find(const char* name) {
+    ParamGroup* find(const char* name) override {
         if (!std::strcmp(name, "ft_w")) return &ft;
         for (auto& g : small)
             if (!std::strcmp(name, g.name)) return &g;
         return nullptr;
-    }
-
-    OptScalars scalars(int kind, float lr, uint64_t step) const {
-        OptScalars s{};
-        const int opt = cfg.optimizer;
-        s.beta1 = opt == TATARA_OPT_RANGER ? 0.99f : 0.9f;
-        s.beta2 = kBeta2;
-        s.eps = kEps;
-        if (opt == TATARA_OPT_ADAMW) {
-            s.step_size = 1.0f;
-            s.denom = 1;
-        } else {
-            (void)tatara_radam_step_size_denom(step, s.beta1, kBeta2, kNSmaThreshold, &s.step_size,
-                                               &s.denom);
-        }
-        float wd, mult;
-        if (kind == 0) {
-            wd = cfg.ft_weight_decay;
-            mult = cfg.ft_lr_mult;
-        } else if (kind == 1) {
-            wd = cfg.dense_weight_decay;
-            mult = cfg.dense_lr_mult;
-        } else {
-            wd = cfg.bias_weight_decay;
-            mult = cfg.bias_lr_mult;
-        }
-        s.decay = wd;
-        s.lr = lr * mult;
-        s.lookahead = (opt == TATARA_OPT_RANGER && step % kRangerK == 0) ? 1 : 0;
-        s.alpha = kAlpha;
-        // the FT weight has no clamp (W_CLAMP_NONE); the dense groups get
-        // their per-group bounds in the finalize kernel
-        s.min_w = std::numeric_limits<float>::lowest();
-        s.max_w = std::numeric_limits<float>::max();
-        return s;
-    }
-
-    struct BatchPtrs {
-        const int32_t *stm, *nstm, *nnz, *bucket;
-        const float *score, *wdl;
-        uint32_t b;
-    };
-
-    int32_t stage_batch(const TataraBatch* bt, BatchPtrs& p) {
-        TATARA_REQUIRE(bt, "batch is null");
-        TATARA_REQUIRE(bt->n_pos >= 0 && bt->n_pos % 16 == 0,
-                       "batch.n_pos must be a multiple of 16 (tiled kernels require b % 16 == 0)");
-        TATARA_REQUIRE((uint32_t)bt->n_pos <= max_b, "batch exceeds workspace capacity");
-        TATARA_REQUIRE((uint32_t)bt->max_active == max_active, "batch.max_active != feature set max_active");
-        p.b = bt->n_pos;
-        if (p.b == 0) return kOk;
-        TATARA_REQUIRE(bt->stm_indices && bt->nstm_indices && bt->nnz && bt->bucket_idx && bt->score &&
-                           bt->wdl,
-                       "batch array is null");
-        if (bt->on_device) {
-            p.stm = bt->stm_indices;
-            p.nstm = bt->nstm_indices;
-            p.nnz = bt->nnz;
-            p.bucket = bt->bucket_idx;
-            p.score = bt->score;
-            p.wdl = bt->wdl;
-            return kOk;
-        }
-        const uint64_t b = p.b;
-        TATARA_HIP(hipMemcpyAsync(in_stm, bt->stm_indices, 4 * b * max_active, hipMemcpyHostToDevice, stream), "H2D stm");
-        TATARA_HIP(hipMemcpyAsync(in_nstm, bt->nstm_indices, 4 * b * max_active, hipMemcpyHostToDevice, stream), "H2D nstm");
-        TATARA_HIP(hipMemcpyAsync(in_nnz, bt->nnz, 4 * b, hipMemcpyHostToDevice, stream), "H2D nnz");
-        TATARA_HIP(hipMemcpyAsync(in_bucket, bt->bucket_idx, 4 * b, hipMemcpyHostToDevice, stream), "H2D bucket");
-        TATARA_HIP(hipMemcpyAsync(in_score, bt->score, 4 * b, hipMemcpyHostToDevice, stream), "H2D score");
-        TATARA_HIP(hipMemcpyAsync(in_wdl, bt->wdl, 4 * b, hipMemcpyHostToDevice, stream), "H2D wdl");
-        // pageable sources: make sure they were consumed before returning
-        TATARA_HIP(hipStreamSynchronize(stream), "H2D batch");
-        p.stm = in_stm;
-        p.nstm = in_nstm;
-        p.nnz = in_nnz;
-        p.bucket = in_bucket;
-        p.score = in_score;
-        p.wdl = in_wdl;
-        return kOk;
-    }
-
-    LossParams loss_params(const TataraLoss* l) const {
-        LossParams lp{};
-        lp.kind = l->kind;
-        lp.scale = l->scale;
-        lp.nnue2score = l->nnue2score;
-        lp.in_scaling = l->in_scaling;
-        lp.in_offset = l->in_offset;
-        lp.target_offset = l->target_offset;
-        lp.target_scaling = l->target_scaling;
-        lp.pow_exp = l->pow_exp;
-        lp.qp_asymmetry = l->qp_asymmetry;
-        lp.w1 = l->weight_boost_w1;
-        lp.w2 = l->weight_boost_w2;
-        lp.extended = (l->kind == 1 &&
-                       (l->pow_exp != 2.0f || l->qp_asymmetry != 0.0f || l->weight_boost_w1 != 0.0f))
-                          ? 1
-                          : 0;
-        return lp;
-    }
-
-    int32_t check_loss(const TataraLoss* l) {
-        TATARA_REQUIRE(l, "loss is null");
-        if (l->kind == 0) {
-            TATARA_REQUIRE(std::isfinite(l->scale) && l->scale > 0.0f, "loss scale must be finite and > 0");
-        } else {
-            TATARA_REQUIRE(l->kind == 1, "unknown loss kind");
-            TATARA_REQUIRE(std::isfinite(l->nnue2score) && l->nnue2score > 0.0f, "wrm nnue2score must be finite and > 0");
-            TATARA_REQUIRE(std::isfinite(l->in_scaling) && l->in_scaling > 0.0f, "wrm in_scaling must be finite and > 0");
-            TATARA_REQUIRE(std::isfinite(l->in_offset), "wrm in_offset must be finite");
-            TATARA_REQUIRE(std::isfinite(l->target_offset), "wrm target_offset must be finite");
-            TATARA_REQUIRE(std::isfinite(l->target_scaling) && l->target_scaling > 0.0f, "wrm target_scaling must be finite and > 0");
-            TATARA_REQUIRE(std::isfinite(l->pow_exp) && l->pow_exp >= 1.0f, "wrm pow_exp must be finite and >= 1");
-            TATARA_REQUIRE(std::isfinite(l->qp_asymmetry) && l->qp_asymmetry >= 0.0f, "wrm qp_asymmetry must be finite and >= 0");
-            TATARA_REQUIRE(std::isfinite(l->weight_boost_w1) && l->weight_boost_w1 >= 0.0f, "wrm weight_boost_w1 must be finite and >= 0");
-            TATARA_REQUIRE(std::isfinite(l->weight_boost_w2) && l->weight_boost_w2 >= 0.0f, "wrm weight_boost_w2 must be finite and >= 0");
-        }
-        return kOk;
     }
 
     LsDenseArgs dense_args(const BatchPtrs& p, uint32_t padded, float wdl_lambda, const LossParams& lp,
@@ -605,11 +373,11 @@ struct LayerStackTrainer {
     }
 
     int32_t train_step(const TataraBatch* bt, float lr, float wdl_lambda, const TataraLoss* l,
-                       double* lagged) {
+                       double* lagged) override {
         int32_t st;
         if ((st = check_loss(l))) return st;
         BatchPtrs p{};
-        if ((st = stage_batch(bt, p))) return st;
+        if ((st = stage_batch(bt, p, true, 16, max_b))) return st;
         if (p.b == 0) {
             if (lagged) *lagged = 0.0;
             return kOk;
@@ -662,40 +430,17 @@ struct LayerStackTrainer {
         if ((st = prof_mark(7))) return st;
 
         // lagged loss (AsyncLossRing::read_and_queue_next)
-        double prev = 0.0;
-        if (pending >= 0) {
-            TATARA_HIP(hipEventSynchronize(loss_ev[pending]), "loss ring event");
-            prev = pinned_loss[pending];
-        }
-        TATARA_HIP(hipMemcpyAsync(pinned_loss + slot, loss_out + slot, sizeof(double),
-                                  hipMemcpyDeviceToHost, stream),
-                   "loss D2H");
-        TATARA_HIP(hipEventRecord(loss_ev[slot], stream), "loss ring record");
-        pending = slot;
-        next_slot = 1 - slot;
         last_b = p.b;
-        if (lagged) *lagged = prev;
-        return kOk;
-    }
-
-    int32_t flush(double* out) {
-        double v = 0.0;
-        if (pending >= 0) {
-            TATARA_HIP(hipEventSynchronize(loss_ev[pending]), "loss ring flush");
-            v = pinned_loss[pending];
-            pending = -1;
-        }
-        if (out) *out = v;
-        return kOk;
+        return queue_loss(loss_out, slot, lagged);
     }
 
     int32_t validate(const TataraBatch* bt, float wdl_lambda, const TataraLoss* l, double* sse,
-                     float* net_host) {
+                     float* net_host) override {
         int32_t st;
         if ((st = check_loss(l))) return st;
         TATARA_HIP(hipStreamSynchronize(stream), "validate sync");
         BatchPtrs p{};
-        if ((st = stage_batch(bt, p))) return st;
+        if ((st = stage_batch(bt, p, true, 16, max_b))) return st;
         if (p.b == 0) {
             if (sse) *sse = 0.0;
             return kOk;
@@ -713,6 +458,19 @@ struct LayerStackTrainer {
         if (sse) *sse = v;
         return kOk;
     }
+
+    const float* activation(const char* name, uint64_t& cap) override {
+        const uint64_t bf = (uint64_t)last_b * ft_out;
+        cap = bf;
+        if (!std::strcmp(name, "ft_stm_out")) return ft_stm;
+        if (!std::strcmp(name, "ft_nstm_out")) return ft_nstm;
+        if (!std::strcmp(name, "combined")) return combined;
+        if (!std::strcmp(name, "dft_stm")) return dft;
+        if (!std::strcmp(name, "dft_nstm")) return dft + bf;
+        cap = last_b;
+        if (!std::strcmp(name, "net_output")) return net_out;
+        return nullptr;
+    }
 };
 
 }  // namespace tatara
@@ -720,7 +478,7 @@ struct LayerStackTrainer {
 using namespace tatara;
 
 struct TataraTrainer {
-    std::unique_ptr<LayerStackTrainer> ls;
+    std::unique_ptr<TrainerBase> t;
 };
 
 extern "C" {
@@ -728,11 +486,16 @@ extern "C" {
 int32_t tatara_trainer_create(const TataraTrainerConfig* config, TataraTrainer** out) {
     TATARA_REQUIRE(config && out, "null argument");
     *out = nullptr;
-    auto t = std::make_unique<TataraTrainer>();
-    t->ls = std::make_unique<LayerStackTrainer>();
-    const int32_t st = t->ls->create(*config);
+    auto h = std::make_unique<TataraTrainer>();
+    if (config->arch == TATARA_ARCH_LAYERSTACK) {
+        h->t = std::make_unique<LayerStackTrainer>();
+    } else {
+        TATARA_REQUIRE(config->arch == TATARA_ARCH_SIMPLE, "unknown architecture");
+        h->t.reset(new_simple_trainer());
+    }
+    const int32_t st = h->t->create(*config);
     if (st) return st;
-    *out = t.release();
+    *out = h.release();
     return kOk;
 }
 
@@ -744,30 +507,30 @@ int32_t tatara_trainer_destroy(TataraTrainer* trainer) {
 int32_t tatara_trainer_train_step(TataraTrainer* trainer, const TataraBatch* batch, float lr,
                                   float wdl_lambda, const TataraLoss* loss, double* lagged_loss) {
     TATARA_REQUIRE(trainer, "trainer is null");
-    return trainer->ls->train_step(batch, lr, wdl_lambda, loss, lagged_loss);
+    return trainer->t->train_step(batch, lr, wdl_lambda, loss, lagged_loss);
 }
 
 int32_t tatara_trainer_flush_pending_loss(TataraTrainer* trainer, double* loss) {
     TATARA_REQUIRE(trainer, "trainer is null");
-    return trainer->ls->flush(loss);
+    return trainer->t->flush(loss);
 }
 
 int32_t tatara_trainer_validate_step(TataraTrainer* trainer, const TataraBatch* batch,
                                      float wdl_lambda, const TataraLoss* loss, double* sum_sq_err,
                                      float* net_output) {
     TATARA_REQUIRE(trainer, "trainer is null");
-    return trainer->ls->validate(batch, wdl_lambda, loss, sum_sq_err, net_output);
+    return trainer->t->validate(batch, wdl_lambda, loss, sum_sq_err, net_output);
 }
 
 int32_t tatara_trainer_step_count(TataraTrainer* trainer, uint64_t* steps) {
     TATARA_REQUIRE(trainer && steps, "null argument");
-    *steps = trainer->ls->step_count;
+    *steps = trainer->t->step_count;
     return kOk;
 }
 
 int32_t tatara_trainer_tensor_size(TataraTrainer* trainer, const char* name, uint64_t* n) {
     TATARA_REQUIRE(trainer && name && n, "null argument");
-    ParamGroup* g = trainer->ls->find(name);
+    ParamGroup* g = trainer->t->find(name);
     TATARA_REQUIRE(g, std::string("unknown tensor ") + name);
     *n = g->n;
     return kOk;
@@ -787,16 +550,16 @@ static float* group_ptr(ParamGroup* g, int32_t which) {
 int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int32_t which,
                                   float* host, uint64_t n) {
     TATARA_REQUIRE(trainer && name && host, "null argument");
-    LayerStackTrainer& t = *trainer->ls;
+    TrainerBase& t = *trainer->t;
     ParamGroup* g = t.find(name);
     TATARA_REQUIRE(g, std::string("unknown tensor ") + name);
+    TATARA_REQUIRE(which >= 0 && which <= 4, "which must be 0..4");
     TATARA_REQUIRE(n == g->n, "element count mismatch");
     TATARA_HIP(hipStreamSynchronize(t.stream), "get_tensor sync");
     float* src = group_ptr(g, which);
-    if (which == 4 && !t.cfg.keep_grads) src = nullptr;  // the optimizer leaves zero gradients
+    if (which == 4 && !t.cfg.keep_grads) src = nullptr;
     if (!src) {
-        TATARA_REQUIRE(which == 4, "which must be 0..4");
-        // gradients are zeroed by the optimizer; without keep_grads none are kept
+        // the optimizer leaves zero gradients; without keep_grads none are kept
         std::memset(host, 0, n * sizeof(float));
         return kOk;
     }
@@ -807,7 +570,7 @@ int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int3
 int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int32_t which,
                                   const float* host, uint64_t n) {
     TATARA_REQUIRE(trainer && name && host, "null argument");
-    LayerStackTrainer& t = *trainer->ls;
+    TrainerBase& t = *trainer->t;
     ParamGroup* g = t.find(name);
     TATARA_REQUIRE(g, std::string("unknown tensor ") + name);
     TATARA_REQUIRE(n == g->n, "element count mismatch");
@@ -815,23 +578,16 @@ int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int3
     TATARA_REQUIRE(dst, "tensor not allocated (which)");
     TATARA_HIP(hipStreamSynchronize(t.stream), "set_tensor sync");
     TATARA_HIP(hipMemcpy(dst, host, n * sizeof(float), hipMemcpyHostToDevice), "set_tensor");
-    if (g == &t.ft && which == 0) return t.sync_forward_weights();
+    if (!std::strcmp(name, "ft_w") && which == 0) return t.sync_forward_weights();
     return kOk;
 }
 
 int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const char* name, float* host,
                                       uint64_t n) {
     TATARA_REQUIRE(trainer && name && host, "null argument");
-    LayerStackTrainer& t = *trainer->ls;
-    const uint64_t bf = (uint64_t)t.last_b * t.ft_out;
-    const float* src = nullptr;
+    TrainerBase& t = *trainer->t;
     uint64_t cap = 0;
-    if (!std::strcmp(name, "ft_stm_out")) { src = t.ft_stm; cap = bf; }
-    else if (!std::strcmp(name, "ft_nstm_out")) { src = t.ft_nstm; cap = bf; }
-    else if (!std::strcmp(name, "combined")) { src = t.combined; cap = bf; }
-    else if (!std::strcmp(name, "net_output")) { src = t.net_out; cap = t.last_b; }
-    else if (!std::strcmp(name, "dft_stm")) { src = t.dft; cap = bf; }
-    else if (!std::strcmp(name, "dft_nstm")) { src = t.dft + bf; cap = bf; }
+    const float* src = t.activation(name, cap);
     TATARA_REQUIRE(src, std::string("unknown activation ") + name);
     TATARA_REQUIRE(n <= cap, "activation request exceeds the last batch");
     TATARA_HIP(hipStreamSynchronize(t.stream), "get_activation sync");
@@ -841,7 +597,7 @@ int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const char* name, 
 
 int32_t tatara_trainer_set_profiling(TataraTrainer* trainer, int32_t enable) {
     TATARA_REQUIRE(trainer, "trainer is null");
-    LayerStackTrainer& t = *trainer->ls;
+    TrainerBase& t = *trainer->t;
     int32_t st = t.prof_collect();
     if (st) return st;
     for (double& v : t.phase_ms) v = 0.0;
@@ -853,17 +609,17 @@ int32_t tatara_trainer_set_profiling(TataraTrainer* trainer, int32_t enable) {
 int32_t tatara_trainer_phase_times(TataraTrainer* trainer, double* ms, int32_t n_phases,
                                    uint64_t* steps) {
     TATARA_REQUIRE(trainer && ms, "null argument");
-    LayerStackTrainer& t = *trainer->ls;
+    TrainerBase& t = *trainer->t;
     int32_t st = t.prof_collect();
     if (st) return st;
-    for (int k = 0; k < n_phases && k < LayerStackTrainer::kPhases; ++k) ms[k] = t.phase_ms[k];
+    for (int k = 0; k < n_phases && k < TrainerBase::kPhases; ++k) ms[k] = t.phase_ms[k];
     if (steps) *steps = t.prof_steps;
     return kOk;
 }
 
 int32_t tatara_trainer_sync_forward_weights(TataraTrainer* trainer) {
     TATARA_REQUIRE(trainer, "trainer is null");
-    return trainer->ls->sync_forward_weights();
+    return trainer->t->sync_forward_weights();
 }
 
 }  // extern "C"

@@ -1,0 +1,236 @@
+// Shared trainer services (see trainer_base.hpp).
+#include "trainer_base.hpp"
+
+#include <cmath>
+#include <limits>
+
+namespace tatara {
+
+namespace {
+constexpr float kBeta2 = 0.999f;  // RangerParams::DEFAULT (crates/nnue-train/src/optimizer.rs)
+constexpr float kEps = 1e-8f;
+constexpr float kAlpha = 0.5f;
+constexpr uint64_t kRangerK = 6;
+constexpr float kNSmaThreshold = 5.0f;
+}  // namespace
+
+TrainerBase::~TrainerBase() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
+    for (auto& e : loss_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (pinned_loss) (void)hipHostFree(pinned_loss);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+int32_t TrainerBase::init_runtime(int device) {
+    TATARA_HIP(hipSetDevice(device), "hipSetDevice");
+    TATARA_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    TATARA_HIP(hipEventCreateWithFlags(&loss_ev[0], hipEventDisableTiming), "hipEventCreate");
+    TATARA_HIP(hipEventCreateWithFlags(&loss_ev[1], hipEventDisableTiming), "hipEventCreate");
+    TATARA_HIP(hipHostMalloc((void**)&pinned_loss, 2 * sizeof(double), hipHostMallocDefault),
+               "hipHostMalloc loss ring");
+    return kOk;
+}
+
+int32_t TrainerBase::alloc_inputs(uint64_t B, uint32_t max_active) {
+    in_max_active = max_active;
+    int32_t st;
+    if ((st = arena.alloc(&in_stm, B * max_active)) || (st = arena.alloc(&in_nstm, B * max_active)) ||
+        (st = arena.alloc(&in_nnz, B)) || (st = arena.alloc(&in_bucket, B)) ||
+        (st = arena.alloc(&in_score, B)) || (st = arena.alloc(&in_wdl, B)))
+        return st;
+    return kOk;
+}
+
+int32_t TrainerBase::alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx,
+                                 int kind, bool with_grad) {
+    g.name = name;
+    g.n = n;
+    g.min_w = mn;
+    g.max_w = mx;
+    g.kind = kind;
+    int32_t st;
+    if ((st = arena.alloc(&g.w, n)) || (st = arena.alloc(&g.m, n)) || (st = arena.alloc(&g.v, n)) ||
+        (st = arena.alloc(&g.slow, n)))
+        return st;
+    if (with_grad && (st = arena.alloc(&g.grad, n))) return st;
+    return kOk;
+}
+
+int32_t TrainerBase::upload(float* dst, const std::vector<float>& src) {
+    TATARA_HIP(hipMemcpy(dst, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice),
+               "upload init weights");
+    return kOk;
+}
+
+int32_t TrainerBase::stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_bucket,
+                                 uint32_t multiple, uint32_t max_b) {
+    TATARA_REQUIRE(bt, "batch is null");
+    TATARA_REQUIRE(bt->n_pos >= 0, "batch.n_pos must be >= 0");
+    if (multiple > 1)
+        TATARA_REQUIRE(bt->n_pos % multiple == 0,
+                       "batch.n_pos must be a multiple of 16 (tiled kernels require b % 16 == 0)");
+    TATARA_REQUIRE((uint32_t)bt->n_pos <= max_b, "batch exceeds workspace capacity");
+    TATARA_REQUIRE((uint32_t)bt->max_active == in_max_active, "batch.max_active != feature set max_active");
+    p.b = bt->n_pos;
+    if (p.b == 0) return kOk;
+    TATARA_REQUIRE(bt->stm_indices && bt->nstm_indices && bt->nnz && bt->score && bt->wdl,
+                   "batch array is null");
+    if (need_bucket) TATARA_REQUIRE(bt->bucket_idx, "batch.bucket_idx is null");
+    if (bt->on_device) {
+        p.stm = bt->stm_indices;
+        p.nstm = bt->nstm_indices;
+        p.nnz = bt->nnz;
+        p.bucket = bt->bucket_idx;
+        p.score = bt->score;
+        p.wdl = bt->wdl;
+        return kOk;
+    }
+    const uint64_t b = p.b, ma = in_max_active;
+    TATARA_HIP(hipMemcpyAsync(in_stm, bt->stm_indices, 4 * b * ma, hipMemcpyHostToDevice, stream), "H2D stm");
+    TATARA_HIP(hipMemcpyAsync(in_nstm, bt->nstm_indices, 4 * b * ma, hipMemcpyHostToDevice, stream), "H2D nstm");
+    TATARA_HIP(hipMemcpyAsync(in_nnz, bt->nnz, 4 * b, hipMemcpyHostToDevice, stream), "H2D nnz");
+    if (need_bucket)
+        TATARA_HIP(hipMemcpyAsync(in_bucket, bt->bucket_idx, 4 * b, hipMemcpyHostToDevice, stream), "H2D bucket");
+    TATARA_HIP(hipMemcpyAsync(in_score, bt->score, 4 * b, hipMemcpyHostToDevice, stream), "H2D score");
+    TATARA_HIP(hipMemcpyAsync(in_wdl, bt->wdl, 4 * b, hipMemcpyHostToDevice, stream), "H2D wdl");
+    // pageable sources: make sure they were consumed before returning
+    TATARA_HIP(hipStreamSynchronize(stream), "H2D batch");
+    p.stm = in_stm;
+    p.nstm = in_nstm;
+    p.nnz = in_nnz;
+    p.bucket = need_bucket ? in_bucket : nullptr;
+    p.score = in_score;
+    p.wdl = in_wdl;
+    return kOk;
+}
+
+OptScalars TrainerBase::scalars(int kind, float lr, uint64_t step) const {
+    OptScalars s{};
+    const int opt = cfg.optimizer;
+    s.beta1 = opt == TATARA_OPT_RANGER ? 0.99f : 0.9f;
+    s.beta2 = kBeta2;
+    s.eps = kEps;
+    if (opt == TATARA_OPT_ADAMW) {
+        s.step_size = 1.0f;
+        s.denom = 1;
+    } else {
+        (void)tatara_radam_step_size_denom(step, s.beta1, kBeta2, kNSmaThreshold, &s.step_size, &s.denom);
+    }
+    float wd, mult;
+    if (kind == 0) {
+        wd = cfg.ft_weight_decay;
+        mult = cfg.ft_lr_mult;
+    } else if (kind == 1) {
+        wd = cfg.dense_weight_decay;
+        mult = cfg.dense_lr_mult;
+    } else {
+        wd = cfg.bias_weight_decay;
+        mult = cfg.bias_lr_mult;
+    }
+    s.decay = wd;
+    s.lr = lr * mult;
+    s.lookahead = (opt == TATARA_OPT_RANGER && step % kRangerK == 0) ? 1 : 0;
+    s.alpha = kAlpha;
+    // no clamp by default (W_CLAMP_NONE); groups with a quantised clamp set
+    // their bounds where they are updated
+    s.min_w = std::numeric_limits<float>::lowest();
+    s.max_w = std::numeric_limits<float>::max();
+    return s;
+}
+
+LossParams TrainerBase::loss_params(const TataraLoss* l) const {
+    LossParams lp{};
+    lp.kind = l->kind;
+    lp.scale = l->scale;
+    lp.nnue2score = l->nnue2score;
+    lp.in_scaling = l->in_scaling;
+    lp.in_offset = l->in_offset;
+    lp.target_offset = l->target_offset;
+    lp.target_scaling = l->target_scaling;
+    lp.pow_exp = l->pow_exp;
+    lp.qp_asymmetry = l->qp_asymmetry;
+    lp.w1 = l->weight_boost_w1;
+    lp.w2 = l->weight_boost_w2;
+    lp.extended =
+        (l->kind == 1 && (l->pow_exp != 2.0f || l->qp_asymmetry != 0.0f || l->weight_boost_w1 != 0.0f))
+            ? 1
+            : 0;
+    return lp;
+}
+
+int32_t TrainerBase::check_loss(const TataraLoss* l) const {
+    TATARA_REQUIRE(l, "loss is null");
+    if (l->kind == 0) {
+        TATARA_REQUIRE(std::isfinite(l->scale) && l->scale > 0.0f, "loss scale must be finite and > 0");
+    } else {
+        TATARA_REQUIRE(l->kind == 1, "unknown loss kind");
+        TATARA_REQUIRE(std::isfinite(l->nnue2score) && l->nnue2score > 0.0f, "wrm nnue2score must be finite and > 0");
+        TATARA_REQUIRE(std::isfinite(l->in_scaling) && l->in_scaling > 0.0f, "wrm in_scaling must be finite and > 0");
+        TATARA_REQUIRE(std::isfinite(l->in_offset), "wrm in_offset must be finite");
+        TATARA_REQUIRE(std::isfinite(l->target_offset), "wrm target_offset must be finite");
+        TATARA_REQUIRE(std::isfinite(l->target_scaling) && l->target_scaling > 0.0f, "wrm target_scaling must be finite and > 0");
+        TATARA_REQUIRE(std::isfinite(l->pow_exp) && l->pow_exp >= 1.0f, "wrm pow_exp must be finite and >= 1");
+        TATARA_REQUIRE(std::isfinite(l->qp_asymmetry) && l->qp_asymmetry >= 0.0f, "wrm qp_asymmetry must be finite and >= 0");
+        TATARA_REQUIRE(std::isfinite(l->weight_boost_w1) && l->weight_boost_w1 >= 0.0f, "wrm weight_boost_w1 must be finite and >= 0");
+        TATARA_REQUIRE(std::isfinite(l->weight_boost_w2) && l->weight_boost_w2 >= 0.0f, "wrm weight_boost_w2 must be finite and >= 0");
+    }
+    return kOk;
+}
+
+int32_t TrainerBase::queue_loss(const double* loss_dev, int slot, double* lagged) {
+    double prev = 0.0;
+    if (pending >= 0) {
+        TATARA_HIP(hipEventSynchronize(loss_ev[pending]), "loss ring event");
+        prev = pinned_loss[pending];
+    }
+    TATARA_HIP(hipMemcpyAsync(pinned_loss + slot, loss_dev + slot, sizeof(double), hipMemcpyDeviceToHost,
+                              stream),
+               "loss D2H");
+    TATARA_HIP(hipEventRecord(loss_ev[slot], stream), "loss ring record");
+    pending = slot;
+    next_slot = 1 - slot;
+    if (lagged) *lagged = prev;
+    return kOk;
+}
+
+int32_t TrainerBase::flush(double* out) {
+    double v = 0.0;
+    if (pending >= 0) {
+        TATARA_HIP(hipEventSynchronize(loss_ev[pending]), "loss ring flush");
+        v = pinned_loss[pending];
+        pending = -1;
+    }
+    if (out) *out = v;
+    return kOk;
+}
+
+int32_t TrainerBase::prof_mark(int k) {
+    if (!profiling) return kOk;
+    hipEvent_t e = nullptr;
+    TATARA_HIP(hipEventCreate(&e), "hipEventCreate (profiling)");
+    TATARA_HIP(hipEventRecord(e, stream), "hipEventRecord (profiling)");
+    prof_events.push_back(e);
+    (void)k;
+    return kOk;
+}
+
+int32_t TrainerBase::prof_collect() {
+    TATARA_HIP(hipStreamSynchronize(stream), "profiling sync");
+    const size_t per = kPhases + 1;
+    for (size_t s = 0; s + per <= prof_events.size(); s += per) {
+        for (int k = 0; k < kPhases; ++k) {
+            float ms = 0.f;
+            TATARA_HIP(hipEventElapsedTime(&ms, prof_events[s + k], prof_events[s + k + 1]),
+                       "hipEventElapsedTime");
+            phase_ms[k] += ms;
+        }
+        prof_steps += 1;
+    }
+    for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
+    prof_events.clear();
+    return kOk;
+}
+
+}  // namespace tatara

@@ -1,0 +1,107 @@
+// State and services shared by the LayerStack and Simple trainers: the
+// stream, parameter groups, batch staging, optimizer scalars, the lagged loss
+// ring (AsyncLossRing, bins/nnue_train/src/trainer_common.rs:909-1035) and
+// phase profiling.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "../../include/tatara_hip.h"
+#include "common.hpp"
+#include "loss.hpp"
+#include "optim.hpp"
+
+namespace tatara {
+
+struct DeviceArena {
+    std::vector<void*> ptrs;
+    ~DeviceArena() {
+        for (void* p : ptrs) (void)hipFree(p);
+    }
+    template <class T>
+    int32_t alloc(T** out, uint64_t count, bool zero = true) {
+        void* p = nullptr;
+        const uint64_t bytes = count * sizeof(T) ? count * sizeof(T) : 4;
+        TATARA_HIP(hipMalloc(&p, bytes), "hipMalloc trainer buffer");
+        ptrs.push_back(p);
+        if (zero) TATARA_HIP(hipMemset(p, 0, bytes), "hipMemset trainer buffer");
+        *out = static_cast<T*>(p);
+        return kOk;
+    }
+};
+
+struct ParamGroup {
+    const char* name = "";
+    float *w = nullptr, *m = nullptr, *v = nullptr, *slow = nullptr, *grad = nullptr;
+    uint64_t n = 0;
+    float min_w = 0.f, max_w = 0.f;
+    int32_t kind = 0;  // 0 ft, 1 dense, 2 bias
+};
+
+struct BatchPtrs {
+    const int32_t *stm = nullptr, *nstm = nullptr, *nnz = nullptr, *bucket = nullptr;
+    const float *score = nullptr, *wdl = nullptr;
+    uint32_t b = 0;
+};
+
+class TrainerBase {
+   public:
+    static constexpr int kPhases = 7;  // prep, ft_forward, dense_forward, dense_backward,
+                                       // ft_grad_update, ft_virtual_fold, dense_opt
+
+    TataraTrainerConfig cfg{};
+    hipStream_t stream = nullptr;
+    DeviceArena arena;
+    uint64_t step_count = 0;
+    uint32_t last_b = 0;
+    bool profiling = false;
+    double phase_ms[kPhases] = {0, 0, 0, 0, 0, 0, 0};
+    uint64_t prof_steps = 0;
+
+    virtual ~TrainerBase();
+    virtual int32_t create(const TataraTrainerConfig& c) = 0;
+    virtual ParamGroup* find(const char* name) = 0;
+    virtual int32_t train_step(const TataraBatch* bt, float lr, float wdl_lambda, const TataraLoss* l,
+                               double* lagged) = 0;
+    virtual int32_t validate(const TataraBatch* bt, float wdl_lambda, const TataraLoss* l, double* sse,
+                             float* net_host) = 0;
+    virtual int32_t sync_forward_weights() = 0;
+    // Device activation of the last batch and its element capacity, or null.
+    virtual const float* activation(const char* name, uint64_t& cap) = 0;
+
+    int32_t flush(double* out);
+    int32_t prof_collect();
+
+   protected:
+    // device copies of host batches
+    int32_t *in_stm = nullptr, *in_nstm = nullptr, *in_nnz = nullptr, *in_bucket = nullptr;
+    float *in_score = nullptr, *in_wdl = nullptr;
+    uint32_t in_max_active = 0;
+    // lagged loss ring
+    double* pinned_loss = nullptr;
+    hipEvent_t loss_ev[2] = {nullptr, nullptr};
+    int pending = -1;  // slot holding the last queued loss
+    int next_slot = 0;
+    // phase profiling: kPhases + 1 events per profiled step
+    std::vector<hipEvent_t> prof_events;
+
+    int32_t init_runtime(int device);
+    int32_t alloc_inputs(uint64_t max_b, uint32_t max_active);
+    int32_t alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx, int kind,
+                        bool with_grad);
+    int32_t upload(float* dst, const std::vector<float>& src);
+    // need_bucket: bucket_idx is required; multiple: n_pos must be a multiple of it
+    int32_t stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_bucket, uint32_t multiple,
+                        uint32_t max_b);
+    OptScalars scalars(int kind, float lr, uint64_t step) const;
+    LossParams loss_params(const TataraLoss* l) const;
+    int32_t check_loss(const TataraLoss* l) const;
+    // Queues this step's loss (device f64 at loss_dev[slot]) and returns the previous one.
+    int32_t queue_loss(const double* loss_dev, int slot, double* lagged);
+    int32_t prof_mark(int k);
+};
+
+}  // namespace tatara

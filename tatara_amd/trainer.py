@@ -1,8 +1,9 @@
 """Host-side mirror of tatara's step API over the HIP C ABI.
 
-`LayerStackTrainer` follows `trait TrainerBackend`
-(crates/nnue-train/src/trainer.rs:273-375) as GpuTrainer implements it
-(bins/nnue_train/src/trainer_layerstack.rs:1885-2010): `train_step` returns
+`LayerStackTrainer` and `SimpleTrainer` follow `trait TrainerBackend`
+(crates/nnue-train/src/trainer.rs:273-375) as GpuTrainer
+(bins/nnue_train/src/trainer_layerstack.rs:1885-2010) and SimpleGpuTrainer
+(bins/nnue_train/src/trainer_simple.rs:742-856) implement it: `train_step` returns
 the previous step's sum of squared errors (0.0 on the first call),
 `flush_pending_loss` drains the last one, `validate_step` runs forward + loss
 only.  `Batch` mirrors crates/nnue-train/src/dataloader.rs:355-369 and
@@ -32,6 +33,7 @@ GROUPS = (
     "l3_w",
     "l3_b",
 )
+SIMPLE_GROUPS = ("ft_w", "ft_b", "l1_w", "l1_b", "l2_w", "l2_b", "l3_w", "l3_b")
 WHICH = {"w": 0, "m": 1, "v": 2, "slow": 3, "grad": 4}
 
 
@@ -151,16 +153,18 @@ class DeviceBatch:
     arrays: dict = field(default_factory=dict)
 
     @classmethod
-    def upload(cls, batch: Batch, bucket_idx: np.ndarray) -> "DeviceBatch":
+    def upload(cls, batch: Batch, bucket_idx: Optional[np.ndarray] = None) -> "DeviceBatch":
+        """bucket_idx: LayerStack bucket per position; None for Simple."""
         db = cls(batch.n_positions, batch.max_active)
         db.arrays = {
             "stm": DeviceArray(batch.stm_indices),
             "nstm": DeviceArray(batch.nstm_indices),
             "nnz": DeviceArray(batch.nnz),
-            "bucket": DeviceArray(np.ascontiguousarray(bucket_idx, dtype=np.int32)),
             "score": DeviceArray(batch.score),
             "wdl": DeviceArray(batch.wdl),
         }
+        if bucket_idx is not None:
+            db.arrays["bucket"] = DeviceArray(np.ascontiguousarray(bucket_idx, dtype=np.int32))
         return db
 
     def to_c(self) -> TataraBatch:
@@ -171,19 +175,21 @@ class DeviceBatch:
             stm_indices=a["stm"].ptr,
             nstm_indices=a["nstm"].ptr,
             nnz=a["nnz"].ptr,
-            bucket_idx=a["bucket"].ptr,
+            bucket_idx=a["bucket"].ptr if "bucket" in a else None,
             score=a["score"].ptr,
             wdl=a["wdl"].ptr,
             on_device=1,
         )
 
 
-def _host_batch(batch: Batch, bucket_idx: np.ndarray) -> tuple[TataraBatch, tuple]:
-    if len(bucket_idx) != batch.n_positions:
-        raise ValueError(
-            f"bucket_idx len ({len(bucket_idx)}) must equal batch.n_positions ({batch.n_positions})"
-        )
-    bucket = np.ascontiguousarray(bucket_idx, dtype=np.int32)
+def _host_batch(batch: Batch, bucket_idx: Optional[np.ndarray]) -> tuple[TataraBatch, tuple]:
+    bucket = None
+    if bucket_idx is not None:
+        if len(bucket_idx) != batch.n_positions:
+            raise ValueError(
+                f"bucket_idx len ({len(bucket_idx)}) must equal batch.n_positions ({batch.n_positions})"
+            )
+        bucket = np.ascontiguousarray(bucket_idx, dtype=np.int32)
     keep = (batch.stm_indices, batch.nstm_indices, batch.nnz, bucket, batch.score, batch.wdl)
     cb = TataraBatch(
         n_pos=batch.n_positions,
@@ -191,7 +197,7 @@ def _host_batch(batch: Batch, bucket_idx: np.ndarray) -> tuple[TataraBatch, tupl
         stm_indices=batch.stm_indices.ctypes.data,
         nstm_indices=batch.nstm_indices.ctypes.data,
         nnz=batch.nnz.ctypes.data,
-        bucket_idx=bucket.ctypes.data,
+        bucket_idx=bucket.ctypes.data if bucket is not None else None,
         score=batch.score.ctypes.data,
         wdl=batch.wdl.ctypes.data,
         on_device=0,
@@ -250,10 +256,60 @@ class LayerStackConfig:
         return self.ft_in + self.piece_inputs
 
 
-class LayerStackTrainer:
-    """TrainerBackend for the LayerStack architecture on one MI355X."""
+@dataclass
+class SimpleConfig:
+    """SimpleGpuTrainer::new arguments (bins/nnue_train/src/trainer_simple.rs:392-600).
 
-    def __init__(self, config: LayerStackConfig):
+    The reference applies one weight decay and one learning rate to every
+    group; the per-kind fields exist for symmetry with LayerStackConfig.
+    """
+
+    ft_in: int
+    max_active: int
+    piece_inputs: int = 0
+    ft_out: int = 256
+    l1_out: int = 32
+    l2_out: int = 32
+    max_batch: int = 16384
+    optimizer: str = "adamw"
+    weight_decay: float = 0.01
+    device: int = 0
+    keep_grads: bool = False
+
+    def to_c(self) -> TataraTrainerConfig:
+        wd = self.weight_decay
+        return TataraTrainerConfig(
+            arch=1,
+            device=self.device,
+            max_batch=self.max_batch,
+            ft_in=self.ft_in,
+            max_active=self.max_active,
+            piece_inputs=self.piece_inputs,
+            ft_out=self.ft_out,
+            l1_out=self.l1_out,
+            l2_out=self.l2_out,
+            num_buckets=1,
+            optimizer=OPTIMIZERS[self.optimizer],
+            ft_weight_decay=wd,
+            dense_weight_decay=wd,
+            bias_weight_decay=wd,
+            ft_lr_mult=1.0,
+            dense_lr_mult=1.0,
+            bias_lr_mult=1.0,
+            keep_grads=1 if self.keep_grads else 0,
+        )
+
+    @property
+    def train_ft_in(self) -> int:
+        return self.ft_in + self.piece_inputs
+
+
+class _Trainer:
+    """Shared TrainerBackend surface over an opaque C trainer handle."""
+
+    GROUPS: tuple = ()
+
+    def __init__(self, config):
         self.config = config
         self._lib = _lib.load()
         h = C.c_void_p()
@@ -359,4 +415,28 @@ class LayerStackTrainer:
         return dict(zip(self.PHASES, list(ms))), steps.value
 
     def state(self) -> dict:
-        return {g: {k: self.get(g, k) for k in ("w", "m", "v", "slow")} for g in GROUPS}
+        return {g: {k: self.get(g, k) for k in ("w", "m", "v", "slow")} for g in self.GROUPS}
+
+
+class LayerStackTrainer(_Trainer):
+    """TrainerBackend for the LayerStack architecture on one MI355X."""
+
+    GROUPS = GROUPS
+
+    def __init__(self, config: LayerStackConfig):
+        super().__init__(config)
+
+
+class SimpleTrainer(_Trainer):
+    """TrainerBackend for the Simple architecture on one MI355X (no buckets)."""
+
+    GROUPS = SIMPLE_GROUPS
+
+    def __init__(self, config: SimpleConfig):
+        super().__init__(config)
+
+    def train_step(self, batch, lr: float = 1e-3, wdl_lambda: float = 0.0, loss=None) -> float:
+        return super().train_step(batch, None, lr, wdl_lambda, Wrm() if loss is None else loss)
+
+    def validate_step(self, batch, wdl_lambda: float = 0.0, loss=None):
+        return super().validate_step(batch, None, wdl_lambda, Wrm() if loss is None else loss)
