@@ -1,10 +1,13 @@
 #!/usr/bin/env python3
 """Training-step throughput of the MI355X backend on the BASELINE headline workload.
 
-Workload: LayerStack, halfka-hm-merged with the
-factorizer, ft-out 1536 / l1 16 / l2 32, fp32, batch 65536, 8 output
-buckets, Ranger, sigmoid-MSE loss at scale 1/290 (the LayerStack default),
-on one GPU.  A step is one forward + backward + optimizer pass over one
+Default workload: LayerStack, halfka-hm-merged
+with the factorizer, ft-out 1536 / l1 16 / l2 32, fp32, batch 65536, 8
+output buckets, Ranger, sigmoid-MSE loss at scale 1/290 (the LayerStack
+default), on one GPU.  `--workload ls768` runs configs[2] (ft-out 768 / l1 8,
+9 buckets) and `--workload simple` configs[1] (Simple HalfKP 256x2-32-32,
+AdamW lr 1e-3 wd 0.01, WRM with every scaling at 290 as README.md:57-62
+runs it).  A step is one forward + backward + optimizer pass over one
 batch; 8 distinct seeded synthetic batches are uploaded to HBM before the
 timed region and cycled (inputs resident in HBM, as the metric asks).
 
@@ -28,20 +31,62 @@ import time
 
 import numpy as np
 
-METRIC = "train pos/s @ batch 65536 (LayerStack ft-1536, 1 GPU); FT gather % HBM peak"
 HBM_PEAK_GBS = 8000.0
-REF_RTX5090_FP32 = 2.45e6  # BASELINE.md section 1 (README.md:41), LayerStack 1536 fp32
+
+# name -> workload; ref = the reference's published fp32 pos/s at b=65536 on
+# RTX 5090 (README.md:41-43)
+WORKLOADS = {
+    "ls1536": dict(
+        metric="train pos/s @ batch 65536 (LayerStack ft-1536, 1 GPU); FT gather % HBM peak",
+        arch="layerstack", spec="halfka-hm-merged", ft_out=1536, l1=16, l2=32, nb=8,
+        optimizer="ranger", lr=8.75e-4, ref=2.45e6, ref_src="README.md:41",
+        desc="LayerStack halfka-hm-merged ft-out 1536/16/32 fp32, batch 65536, 8 buckets, "
+             "Ranger, sigmoid loss 1/290, factorizer on (BASELINE configs[3])"),
+    "ls768": dict(
+        metric="train pos/s @ batch 65536 (LayerStack ft-768, 1 GPU); FT gather % HBM peak",
+        arch="layerstack", spec="halfka-hm-merged", ft_out=768, l1=8, l2=32, nb=9,
+        optimizer="ranger", lr=8.75e-4, ref=4.24e6, ref_src="README.md:42",
+        desc="LayerStack halfka-hm-merged ft-out 768/8/32 fp32, batch 65536, 9 buckets, "
+             "Ranger, sigmoid loss 1/290, factorizer on (BASELINE configs[2])"),
+    "simple": dict(
+        metric="train pos/s @ batch 65536 (Simple HalfKP 256x2-32-32, 1 GPU); FT gather % HBM peak",
+        arch="simple", spec="halfkp", ft_out=256, l1=32, l2=32, nb=1,
+        optimizer="adamw", lr=1e-3, ref=11.29e6, ref_src="README.md:43",
+        desc="Simple HalfKP 256x2-32-32 fp32 crelu, batch 65536, AdamW lr 1e-3 wd 0.01, "
+             "WRM with every scaling 290, factorizer on (BASELINE configs[1])"),
+}
+
+
+def hbm_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of a kernel from the committed counter summary.
+
+    profiles/hbm_traffic.md holds FETCH_SIZE / WRITE_SIZE per dispatch from
+    two rocprofv3 --pmc passes of this script, scaled by a plain-copy
+    calibration; returns None when the kernel was not profiled.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 7 and cells[0] == workload and cells[1].startswith(kernel):
+                    return int(cells[6])
+    except OSError:
+        return None
+    return None
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(batches, ft_out, ft_in, max_active, lookahead_frac):
+def algorithmic_bytes(batches, ft_out, ft_in, max_active, lookahead_frac, out_rows):
     """Per-launch algorithmic bytes of the two FT kernels, averaged over the batches.
 
-    ft_forward: gathered fp32 rows of both perspectives + raw sums (x2) and
-    combined written + index rows + nnz.
+    ft_forward: gathered fp32 rows of both perspectives + the per-perspective
+    sums and combined written (out_rows rows of ft_out floats per position:
+    3 for LayerStack, whose combined is ft_out wide; 4 for Simple, 2*ft_out)
+    + index rows + nnz.
     ft_grad_update: gathered fp32 dft rows (one per occurrence) + occurrence
     list + w, m, v read and written for every real row (+ slow on the
     lookahead step, 1 in 6) + the row gradient written for the virtual rows.
@@ -49,35 +94,54 @@ def algorithmic_bytes(batches, ft_out, ft_in, max_active, lookahead_frac):
     nnz_total = np.mean([float(b.nnz.sum()) for b, _ in batches])
     b = batches[0][0].n_positions
     gather = 2.0 * nnz_total * ft_out * 4
-    fwd = gather + 3.0 * b * ft_out * 4 + 2.0 * b * max_active * 4 + 4.0 * b
+    fwd = gather + out_rows * b * ft_out * 4 + 2.0 * b * max_active * 4 + 4.0 * b
     rows = ft_in * ft_out * 4.0
     grad = gather + 2.0 * nnz_total * 4 + 6.0 * rows + lookahead_frac * 2.0 * rows + rows
     return fwd, grad
 
 
-def cpu_baseline(batch, bucket, threads: int) -> dict:
-    """Oracle (CPU restatement) step on this host, bounded sample."""
+WRM290 = {"kind": "wrm", "nnue2score": 290.0, "in_scaling": 290.0, "in_offset": 0.0,
+          "target_offset": 0.0, "target_scaling": 290.0, "pow_exp": 2.0, "qp_asymmetry": 0.0,
+          "w1": 0.0, "w2": 0.5}
+SIGMOID = {"kind": "sigmoid", "scale": 1.0 / 290.0}
+
+
+def cpu_baseline(w: dict, spec: dict, batch, bucket, threads: int) -> dict:
+    """Oracle (CPU restatement) step on this host, bounded sample of the same workload."""
     from oracle import ffi
-    from oracle import layerstack as ols
 
     used = ffi.set_threads(threads)
-    n = 16384
-    sh = ols.LsShape(ft_in=45 * 1629, max_active=40, piece_inputs=1629, ft_out=1536, l1=16, l2=32, nb=8)
-    st = ols.default_init(sh)
+    n = 16384 if w["arch"] == "layerstack" else 32768
     bd = dict(stm=batch.stm_indices[:n], nstm=batch.nstm_indices[:n], nnz=batch.nnz[:n],
-              bucket=bucket[:n], score=batch.score[:n], wdl=batch.wdl[:n])
-    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
-    loss = {"kind": "sigmoid", "scale": 1.0 / 290.0}
-    t0 = time.perf_counter()
-    ols.train_step(sh, st, bd, opt, 8.75e-4, 0.0, loss, 1)
-    dt = time.perf_counter() - t0
+              bucket=None if bucket is None else bucket[:n], score=batch.score[:n], wdl=batch.wdl[:n])
+    if w["arch"] == "layerstack":
+        from oracle import layerstack as ols
+
+        sh = ols.LsShape(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
+                         ft_out=w["ft_out"], l1=w["l1"], l2=w["l2"], nb=w["nb"])
+        st = ols.default_init(sh)
+        opt = ols.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
+        t0 = time.perf_counter()
+        ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, 1)
+        dt = time.perf_counter() - t0
+    else:
+        from oracle import simple as osi
+
+        sh = osi.SimpleShape(ft_in=spec["ft_in"], max_active=spec["max_active"],
+                             piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1=w["l1"], l2=w["l2"])
+        st = osi.default_init(sh)
+        opt = osi.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
+        t0 = time.perf_counter()
+        osi.train_step(sh, st, bd, opt, w["lr"], 0.0, WRM290, 1)
+        dt = time.perf_counter() - t0
+    n_ft = (spec["ft_in"] + spec["piece_inputs"]) * w["ft_out"]
     return {
         "value": round(n / dt, 1),
         "unit": "pos/s",
         "cores": used,
         "kind": "port",
-        "sample": f"1 full oracle step (fwd+bwd+Ranger over all 115.1M FT params) at b={n} "
-                  f"of the same workload, {dt:.1f} s",
+        "sample": f"1 full oracle step (fwd+bwd+{w['optimizer']} over all {n_ft / 1e6:.1f}M FT params) "
+                  f"at b={n} of the same workload, {dt:.1f} s",
     }
 
 
@@ -86,6 +150,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="ls1536")
     ap.add_argument("--batch", type=int, default=65536)
     ap.add_argument("--n-batches", type=int, default=8)
     ap.add_argument("--profile-steps", type=int, default=12)
@@ -102,9 +167,11 @@ def main() -> int:
         return 2
 
     from tatara_amd import _lib
-    from tatara_amd.synthetic import HALFKA_HM_MERGED, structured_batch
-    from tatara_amd.trainer import DeviceBatch, LayerStackConfig, LayerStackTrainer, Sigmoid
+    from tatara_amd.synthetic import HALFKA_HM_MERGED, HALFKP, structured_batch
+    from tatara_amd.trainer import (DeviceBatch, LayerStackConfig, LayerStackTrainer, Sigmoid,
+                                    SimpleConfig, SimpleTrainer, Wrm)
 
+    w = WORKLOADS[args.workload]
     lib = _lib.load()
     if args.copy_calibration_mb:
         import ctypes as C
@@ -119,26 +186,38 @@ def main() -> int:
         _lib.check(lib.tatara_free(src.value))
         _lib.check(lib.tatara_free(dst.value))
         log(f"copied {args.copy_calibration_mb} MiB x3 (counter calibration)")
-    spec = HALFKA_HM_MERGED
+    spec = HALFKA_HM_MERGED if w["spec"] == "halfka-hm-merged" else HALFKP
     b = args.batch
-    log(f"generating {args.n_batches} synthetic batches of {b} positions")
-    batches = [structured_batch(b, spec, num_buckets=8, seed=1000 + i) for i in range(args.n_batches)]
-    cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
-                           piece_inputs=spec["piece_inputs"], ft_out=1536, l1_out=16, l2_out=32,
-                           num_buckets=8, max_batch=b, optimizer="ranger", weight_decay=0.01)
-    loss = Sigmoid(1.0 / 290.0)
-    lr = 8.75e-4
-    with LayerStackTrainer(cfg) as t:
-        dev = [DeviceBatch.upload(bt, bk) for bt, bk in batches]
+    log(f"{args.workload}: generating {args.n_batches} synthetic batches of {b} positions")
+    batches = [structured_batch(b, spec, num_buckets=w["nb"], seed=1000 + i) for i in range(args.n_batches)]
+    lr = w["lr"]
+    if w["arch"] == "layerstack":
+        cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
+                               piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
+                               l2_out=w["l2"], num_buckets=w["nb"], max_batch=b,
+                               optimizer=w["optimizer"], weight_decay=0.01)
+        trainer = LayerStackTrainer(cfg)
+        loss = Sigmoid(1.0 / 290.0)
+        step = lambda t, db: t.train_step(db, None, lr, 0.0, loss)  # noqa: E731
+    else:
+        cfg = SimpleConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
+                           piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
+                           l2_out=w["l2"], max_batch=b, optimizer=w["optimizer"], weight_decay=0.01)
+        trainer = SimpleTrainer(cfg)
+        loss = Wrm(nnue2score=290.0, in_scaling=290.0, in_offset=0.0, target_offset=0.0,
+                   target_scaling=290.0)
+        step = lambda t, db: t.train_step(db, lr, 0.0, loss)  # noqa: E731
+    with trainer as t:
+        dev = [DeviceBatch.upload(bt, bk if w["arch"] == "layerstack" else None) for bt, bk in batches]
         log(f"warm-up {args.warmup} steps")
         for i in range(args.warmup):
-            t.train_step(dev[i % len(dev)], None, lr, 0.0, loss)
+            step(t, dev[i % len(dev)])
         t.flush_pending_loss()
         _lib.check(lib.tatara_synchronize())
         log(f"timing {args.steps} steps")
         t0 = time.perf_counter()
         for i in range(args.steps):
-            t.train_step(dev[i % len(dev)], None, lr, 0.0, loss)
+            step(t, dev[i % len(dev)])
         last = t.flush_pending_loss()
         _lib.check(lib.tatara_synchronize())
         elapsed = time.perf_counter() - t0
@@ -149,7 +228,7 @@ def main() -> int:
         # phase profile (HIP events on the trainer's stream)
         t.set_profiling(True)
         for i in range(args.profile_steps):
-            t.train_step(dev[i % len(dev)], None, lr, 0.0, loss)
+            step(t, dev[i % len(dev)])
         t.flush_pending_loss()
         phases, nprof = t.phase_times()
         t.set_profiling(False)
@@ -157,8 +236,10 @@ def main() -> int:
     phase_avg = {k: v / max(nprof, 1) for k, v in phases.items()}
     log("phases (ms/step): " + ", ".join(f"{k} {v:.3f}" for k, v in phase_avg.items()))
 
-    fwd_bytes, grad_bytes = algorithmic_bytes(batches, 1536, spec["ft_in"], spec["max_active"],
-                                              lookahead_frac=1.0 / 6.0)
+    la = 1.0 / 6.0 if w["optimizer"] == "ranger" else 0.0
+    fwd_bytes, grad_bytes = algorithmic_bytes(batches, w["ft_out"], spec["ft_in"], spec["max_active"],
+                                              lookahead_frac=la,
+                                              out_rows=3 if w["arch"] == "layerstack" else 4)
     kernels = {
         "ft_forward_kernel": (phase_avg["ft_forward"], fwd_bytes),
         "ft_grad_update_kernel": (phase_avg["ft_grad_update"], grad_bytes),
@@ -166,6 +247,7 @@ def main() -> int:
     dom = max(kernels, key=lambda k: kernels[k][0])
     ms, byts = kernels[dom]
     achieved = byts / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    traffic = hbm_traffic(args.workload, dom)
     roofline = {
         "bound": "hbm",
         "kernel": dom,
@@ -173,24 +255,31 @@ def main() -> int:
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": traffic,
         "avg_launch_ms": round(ms, 4),
         "algorithmic_bytes_per_launch": int(byts),
+        # the algorithmic (logical) bytes include gathered rows served by L2 /
+        # Infinity Cache; the physical HBM rate is traffic / duration
+        "hbm_GBps": round(traffic / (ms * 1e-3) / 1e9, 1) if (traffic and ms > 0) else None,
+        "hbm_frac": round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if (traffic and ms > 0) else None,
+        "traffic_source": "profiles/hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
     }
     other = {k: {"avg_launch_ms": round(v[0], 4),
-                 "algorithmic_GBps": round(v[1] / (v[0] * 1e-3) / 1e9, 1) if v[0] > 0 else None}
+                 "algorithmic_GBps": round(v[1] / (v[0] * 1e-3) / 1e9, 1) if v[0] > 0 else None,
+                 "hbm_bytes": hbm_traffic(args.workload, k)}
              for k, v in kernels.items()}
 
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle step)")
         try:
-            cpu = cpu_baseline(batches[0][0], batches[0][1], args.cpu_threads)
+            cpu = cpu_baseline(w, spec, batches[0][0], batches[0][1] if w["arch"] == "layerstack" else None,
+                               args.cpu_threads)
         except Exception as e:  # the baseline must not hide the GPU result
             cpu = {"value": None, "error": repr(e)}
 
     line = {
-        "metric": METRIC,
+        "metric": w["metric"],
         "value": round(pos_s, 1),
         "unit": "pos/s",
         "n_gpus": 1,
@@ -199,16 +288,15 @@ def main() -> int:
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(pos_s / REF_RTX5090_FP32, 4),
+        "vs_baseline": round(pos_s / w["ref"], 4),
         "dtype": "f32",
-        "data": "synthetic (seeded king-blocked halfka-hm-merged index batches, resident in HBM)",
+        "data": f"synthetic (seeded king-blocked {w['spec']} index batches, resident in HBM)",
         "config": {
-            "workload": "LayerStack halfka-hm-merged ft-out 1536/16/32 fp32, batch 65536, "
-                        "8 buckets, Ranger, sigmoid loss 1/290, factorizer on (BASELINE configs[3])",
+            "workload": w["desc"],
             "global_batch": b,
-            "ft_out": 1536, "l1": 16, "l2": 32, "num_buckets": 8,
+            "ft_out": w["ft_out"], "l1": w["l1"], "l2": w["l2"], "num_buckets": w["nb"],
             "n_batches_cycled": args.n_batches,
-            "vs_baseline_ref": "RTX 5090 fp32 2.45M pos/s (BASELINE.md, README.md:41)",
+            "vs_baseline_ref": f"RTX 5090 fp32 {w['ref'] / 1e6:.2f}M pos/s (BASELINE.md, {w['ref_src']})",
             "step_count_end": step_count,
         },
         "roofline": roofline,
