@@ -53,36 +53,50 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
     const int32_t orig = a.perm[tile * 16 + i];
     const bool bvalid = (uint32_t)bin < a.nb;
     const bool jvalid = i < l1;
-    const float4* X = orig >= 0 ? reinterpret_cast<const float4*>(a.combined + (uint64_t)orig * ft_out)
-                                : nullptr;
-    const float4* W1 = (bvalid && jvalid)
-                           ? reinterpret_cast<const float4*>(a.l1_w + ((uint64_t)bin * l1 + i) * ft_out)
-                           : nullptr;
-    const float* Ws = a.l1s_w;
+    // Operands are loaded unconditionally from always-valid addresses (row 0,
+    // bucket 0, column l1-1) and masked afterwards: a guarded load would be
+    // split into predicated dword loads and lose the 16-byte accesses.
+    const bool xvalid = orig >= 0, wbvalid = bvalid && jvalid;
+    const uint32_t ic = jvalid ? i : l1 - 1;
+    const float4* X = reinterpret_cast<const float4*>(a.combined + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
+    const float4* W1 = reinterpret_cast<const float4*>(
+        a.l1_w + ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
+    const float* Ws = a.l1s_w + ic;
     const float binit = (bvalid && jvalid) ? a.l1_b[bin * l1 + i] : 0.0f;
     floatx4 accb = {binit, binit, binit, binit};
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    // ft_out % 64 == 0: whole groups of kU K-blocks; a group's operands are
+    // loaded before its MFMAs so each wave keeps several loads in flight
     const uint32_t nk = ft_out / 16;
-    for (uint32_t kb = 0; kb < nk; ++kb) {
-        const float4 x = X ? X[kb * 4 + q] : zero4;
-        const float4 wb = W1 ? W1[kb * 4 + q] : zero4;
-        const uint32_t k = kb * 16 + 4 * q;
-        float ws0 = 0.f, ws1 = 0.f, ws2 = 0.f, ws3 = 0.f;
-        if (jvalid) {
-            ws0 = Ws[(uint64_t)(k + 0) * l1 + i];
-            ws1 = Ws[(uint64_t)(k + 1) * l1 + i];
-            ws2 = Ws[(uint64_t)(k + 2) * l1 + i];
-            ws3 = Ws[(uint64_t)(k + 3) * l1 + i];
+    constexpr uint32_t kU = 4;
+    for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
+        float4 x[kU], wb[kU];
+        float ws[kU][4];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) {
+            const uint32_t kb = kb0 + u;
+            x[u] = X[kb * 4 + q];
+            wb[u] = W1[kb * 4 + q];
+            const uint32_t k = kb * 16 + 4 * q;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ws[u][c] = Ws[(uint64_t)(k + c) * l1];
         }
-        accb = mfma4(x.x, wb.x, accb);
-        accs = mfma4(x.x, ws0, accs);
-        accb = mfma4(x.y, wb.y, accb);
-        accs = mfma4(x.y, ws1, accs);
-        accb = mfma4(x.z, wb.z, accb);
-        accs = mfma4(x.z, ws2, accs);
-        accb = mfma4(x.w, wb.w, accb);
-        accs = mfma4(x.w, ws3, accs);
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) {
+            const float4 xv = xvalid ? x[u] : zero4;
+            const float4 wv = wbvalid ? wb[u] : zero4;
+            const float w0 = jvalid ? ws[u][0] : 0.f, w1 = jvalid ? ws[u][1] : 0.f;
+            const float w2 = jvalid ? ws[u][2] : 0.f, w3 = jvalid ? ws[u][3] : 0.f;
+            accb = mfma4(xv.x, wv.x, accb);
+            accs = mfma4(xv.x, w0, accs);
+            accb = mfma4(xv.y, wv.y, accb);
+            accs = mfma4(xv.y, w1, accs);
+            accb = mfma4(xv.z, wv.z, accb);
+            accs = mfma4(xv.z, w2, accs);
+            accb = mfma4(xv.w, wv.w, accb);
+            accs = mfma4(xv.w, w3, accs);
+        }
     }
     const uint32_t j = lane % 16;
     if (j >= l1) return;
@@ -114,12 +128,21 @@ __global__ __launch_bounds__(256) void wrm_weight_partial_kernel(const float* __
     }
 }
 
-__global__ void sum_partials_f64_kernel(const double* __restrict__ partial, uint32_t n,
-                                        double* __restrict__ out) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// out[0] = sum of partial[0..n): thread t adds t, t + 256, ... in order, then
+// the 256 thread sums are combined by a fixed pairwise tree (deterministic).
+__global__ __launch_bounds__(256) void sum_partials_f64_kernel(const double* __restrict__ partial,
+                                                               uint32_t n, double* __restrict__ out) {
+    __shared__ double s[256];
+    const uint32_t t = threadIdx.x;
     double acc = 0.0;
-    for (uint32_t k = 0; k < n; ++k) acc += partial[k];
-    *out = acc;
+    for (uint32_t k = t; k < n; k += 256) acc += partial[k];
+    s[t] = acc;
+    __syncthreads();
+    for (uint32_t w = 128; w > 0; w >>= 1) {
+        if (t < w) s[t] = s[t] + s[t + w];
+        __syncthreads();
+    }
+    if (t == 0) *out = s[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -340,27 +363,33 @@ __global__ void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
 // ---------------------------------------------------------------------------
 // Deterministic column sums of a partial matrix P[rows][n_cols]:
 // out[seg][c] = sum over the segment's rows of P[r][c].  Thread (c, phase)
-// sums rows phase, phase+4, ... sequentially; the four phase sums are added
-// in a fixed order.  Segment s covers rows [seg_rows[s], seg_rows[s+1]) when
-// seg_rows is given, else all rows.
+// sums rows phase, phase + 16, ... sequentially; the 16 phase sums are then
+// combined by a fixed pairwise tree.  Segment s covers rows
+// [seg_rows[s], seg_rows[s+1]) when seg_rows is given, else all rows.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void reduce_rows_kernel(const float* __restrict__ P,
-                                                          uint32_t n_rows, uint32_t n_cols,
-                                                          const uint32_t* __restrict__ seg_rows,
-                                                          float* __restrict__ out) {
-    __shared__ float part[4][64];
+constexpr uint32_t kReducePhases = 16;
+
+__global__ __launch_bounds__(64 * kReducePhases) void reduce_rows_kernel(
+    const float* __restrict__ P, uint32_t n_rows, uint32_t n_cols, const uint32_t* __restrict__ seg_rows,
+    float* __restrict__ out) {
+    __shared__ float part[kReducePhases][64];
     const uint32_t lane = threadIdx.x % 64, phase = threadIdx.x / 64;
     const uint32_t c = blockIdx.x * 64 + lane;
     const uint32_t seg = blockIdx.y;
     const uint32_t r0 = seg_rows ? seg_rows[seg] : 0;
     const uint32_t r1 = seg_rows ? seg_rows[seg + 1] : n_rows;
     float acc = 0.0f;
-    if (c < n_cols)
-        for (uint32_t r = r0 + phase; r < r1; r += 4) acc += P[(uint64_t)r * n_cols + c];
+    if (c < n_cols) {
+#pragma unroll 8
+        for (uint32_t r = r0 + phase; r < r1; r += kReducePhases) acc += P[(uint64_t)r * n_cols + c];
+    }
     part[phase][lane] = acc;
     __syncthreads();
-    if (phase == 0 && c < n_cols)
-        out[(uint64_t)seg * n_cols + c] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+    for (uint32_t w = kReducePhases / 2; w > 0; w >>= 1) {
+        if (phase < w) part[phase][lane] = part[phase][lane] + part[phase + w][lane];
+        __syncthreads();
+    }
+    if (phase == 0 && c < n_cols) out[(uint64_t)seg * n_cols + c] = part[0][lane];
 }
 
 // ---------------------------------------------------------------------------
@@ -381,15 +410,27 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
     const bool ovalid = o < l1;
     const bool kvalid = k0 + 4 * kk < ft_out;
     floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t kc = kvalid ? k0 + 4 * kk : 0;  // always-valid column, masked below
+    const uint32_t oc = ovalid ? o : 0;
     for (uint32_t tt = 0; tt < nt; ++tt) {
+        // the tile's 16 rows are loaded before its 16 MFMAs (unconditional
+        // loads from valid addresses, masked after the load)
+        float4 xs[4];
+        float ds[4];
+        bool rvs[4];
 #pragma unroll
         for (uint32_t s = 0; s < 4; ++s) {
             const uint64_t row = (uint64_t)(t0 + tt) * 16 + 4 * s + q;
             const int32_t orig = a.perm[row];
-            const float d = ovalid ? a.dl1_sorted[row * l1 + o] : 0.0f;
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (orig >= 0 && kvalid)
-                x = reinterpret_cast<const float4*>(a.combined + (uint64_t)orig * ft_out + k0)[kk];
+            rvs[s] = orig >= 0;
+            xs[s] = *reinterpret_cast<const float4*>(a.combined + (uint64_t)(orig >= 0 ? orig : 0) * ft_out + kc);
+            ds[s] = a.dl1_sorted[row * l1 + oc];
+        }
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) {
+            const float d = ovalid ? ds[s] : 0.0f;
+            const float4 x = (rvs[s] && kvalid) ? xs[s] : zero4;
             acc0 = mfma4(d, x.x, acc0);
             acc1 = mfma4(d, x.y, acc1);
             acc2 = mfma4(d, x.z, acc2);
@@ -457,9 +498,27 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                                          a.l1_w + ((uint64_t)bin * L1 + o) * ft_out)[qq]
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+            // the FT sums of row r + 1 are loaded before row r is computed
+            const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            int32_t orig_n = a.perm[tile * 16];
+            float4 xa_n = zero4, xb_n = zero4;
+            if (orig_n >= 0) {
+                const float4* src = reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out);
+                xa_n = src[p0 / 4];
+                xb_n = src[(p0 + half) / 4];
+            }
             for (uint32_t r = 0; r < 16; ++r) {
                 const uint64_t row = tile * 16 + r;
-                const int32_t orig = a.perm[row];
+                const int32_t orig = orig_n;
+                const float4 xa4 = xa_n, xb4 = xb_n;
+                if (r + 1 < 16) {
+                    orig_n = a.perm[row + 1];
+                    if (orig_n >= 0) {
+                        const float4* src = reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out);
+                        xa_n = src[p0 / 4];
+                        xb_n = src[(p0 + half) / 4];
+                    }
+                }
                 if (orig < 0) continue;
                 float d[L1];
                 const float* dsrc = a.dl1_sorted + row * L1;
@@ -481,9 +540,6 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                     for (int o = 0; o < L1; ++o) db += d[o] * ws[e][o];
                     dyv[e] = da + db;
                 }
-                const float4 xa4 = reinterpret_cast<const float4*>(ft + (uint64_t)orig * ft_out)[p0 / 4];
-                const float4 xb4 =
-                    reinterpret_cast<const float4*>(ft + (uint64_t)orig * ft_out)[(p0 + half) / 4];
                 const float xa[4] = {xa4.x + ba.x, xa4.y + ba.y, xa4.z + ba.z, xa4.w + ba.w};
                 const float xb[4] = {xb4.x + bb.x, xb4.y + bb.y, xb4.z + bb.z, xb4.w + bb.w};
                 float ga[4], gb[4];
@@ -603,7 +659,7 @@ uint32_t ls_max_chunks(uint32_t padded_b, uint32_t nb) {
 
 int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.l1 >= 2 && a.l1 <= 16, "l1 must be in [2, 16]");
-    TATARA_REQUIRE(a.ft_out % 16 == 0, "ft_out must be a multiple of 16");
+    TATARA_REQUIRE(a.ft_out % 64 == 0, "ft_out must be a multiple of 64");
     const uint32_t tiles = a.padded_b / 16;
     if (tiles == 0) return kOk;
     ls_l1_fwd_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
@@ -618,7 +674,7 @@ int32_t launch_wrm_weight_sum(const float* score, uint32_t n, const LossParams& 
         wrm_weight_partial_kernel<<<blocks, 256, 0, stream>>>(score, n, lp, scratch);
         TATARA_LAUNCHED("wrm_weight_sum");
     }
-    sum_partials_f64_kernel<<<1, 64, 0, stream>>>(scratch, blocks, out);
+    sum_partials_f64_kernel<<<1, 256, 0, stream>>>(scratch, blocks, out);
     TATARA_LAUNCHED("wrm_weight_sum_reduce");
     return kOk;
 }
@@ -677,13 +733,13 @@ int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups,
     const uint32_t n_tail = ls_tail_workgroups(a.padded_b);
     const uint32_t n_post = ls_post_workgroups(a.padded_b);
     const uint32_t tail_cols = a.nb * td.cells();
-    reduce_rows_kernel<<<dim3(ceil_div(tail_cols, 64), 1), 256, 0, stream>>>(
+    reduce_rows_kernel<<<dim3(ceil_div(tail_cols, 64), 1), 64 * kReducePhases, 0, stream>>>(
         a.tail_partial, n_tail, tail_cols, nullptr, a.tail_sum);
-    reduce_rows_kernel<<<dim3(ceil_div(a.l1, 64), 1), 256, 0, stream>>>(a.b1s_partial, n_tail, a.l1,
+    reduce_rows_kernel<<<dim3(ceil_div(a.l1, 64), 1), 64 * kReducePhases, 0, stream>>>(a.b1s_partial, n_tail, a.l1,
                                                                         nullptr, a.b1s_sum);
-    reduce_rows_kernel<<<dim3(ceil_div(2 * a.ft_out, 64), 1), 256, 0, stream>>>(
+    reduce_rows_kernel<<<dim3(ceil_div(2 * a.ft_out, 64), 1), 64 * kReducePhases, 0, stream>>>(
         a.ftb_partial, n_post, 2 * a.ft_out, nullptr, a.ftb_sum);
-    reduce_rows_kernel<<<dim3(ceil_div(a.l1 * a.ft_out, 64), a.nb + 1), 256, 0, stream>>>(
+    reduce_rows_kernel<<<dim3(ceil_div(a.l1 * a.ft_out, 64), a.nb + 1), 64 * kReducePhases, 0, stream>>>(
         a.w1_partial, 0, a.l1 * a.ft_out, a.chunk_info + 3 * a.max_chunks + 1, a.w1_seg);
     TATARA_LAUNCHED("reduce_rows");
     ls_dense_finalize_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(a, gt, dense, bias, apply_update,
@@ -700,14 +756,14 @@ int32_t launch_reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols,
                            const uint32_t* seg_rows, uint32_t n_seg, float* out, hipStream_t stream) {
     TATARA_REQUIRE(seg_rows || n_seg == 1, "reduce_rows: n_seg must be 1 without segments");
     if (n_cols == 0 || n_seg == 0) return kOk;
-    reduce_rows_kernel<<<dim3(ceil_div(n_cols, 64), n_seg), 256, 0, stream>>>(P, n_rows, n_cols,
+    reduce_rows_kernel<<<dim3(ceil_div(n_cols, 64), n_seg), 64 * kReducePhases, 0, stream>>>(P, n_rows, n_cols,
                                                                                seg_rows, out);
     TATARA_LAUNCHED("reduce_rows");
     return kOk;
 }
 
 int32_t launch_sum_f64(const double* partial, uint32_t n, double* out, hipStream_t stream) {
-    sum_partials_f64_kernel<<<1, 64, 0, stream>>>(partial, n, out);
+    sum_partials_f64_kernel<<<1, 256, 0, stream>>>(partial, n, out);
     TATARA_LAUNCHED("sum_f64");
     return kOk;
 }

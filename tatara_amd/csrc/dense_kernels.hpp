@@ -24,7 +24,7 @@ struct TailDims {
 };
 
 constexpr uint32_t kTailRows = 128;      // sorted rows per tail workgroup
-constexpr uint32_t kChunkTiles = 64;     // 16-row tiles per L1 weight-gradient chunk
+constexpr uint32_t kChunkTiles = 16;     // 16-row tiles per L1 weight-gradient chunk
 constexpr uint32_t kPostTiles = 4;       // 16-row tiles per L1-input/FT-post row block
 
 struct LsDenseArgs {

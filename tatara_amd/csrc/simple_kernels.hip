@@ -46,8 +46,10 @@ __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
     const uint32_t i = lane % 16, q = lane / 16;
     const uint32_t K = 2 * a.ft_out;
     const uint32_t row_a = tile * 16 + i;
-    const float4* X = row_a < batch ? reinterpret_cast<const float4*>(a.combined + (uint64_t)row_a * K)
-                                    : nullptr;
+    // rows past the batch load row 0 (always valid) and are zeroed after the
+    // load: a guarded load would be split into predicated dword loads
+    const bool xvalid = row_a < batch;
+    const float4* X = reinterpret_cast<const float4*>(a.combined + (uint64_t)(xvalid ? row_a : 0) * K);
     floatx4 acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -55,15 +57,33 @@ __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
         acc[nb] = floatx4{b, b, b, b};
     }
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t kb = 0; kb < K / 16; ++kb) {
-        const float4 x = X ? X[kb * 4 + q] : zero4;
-        const float* w = a.l1_w + (uint64_t)(kb * 16 + 4 * q) * L1 + i;
+    // K / 16 is a multiple of kU (ft_out % 32 == 0); a group's operands are
+    // loaded before its MFMAs so each wave keeps several loads in flight
+    const uint32_t nk = K / 16;
+    constexpr uint32_t kU = 4;
+    for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
+        float4 x[kU];
+        float w[kU][4][NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            acc[nb] = mfma4(x.x, w[0 * L1 + 16 * nb], acc[nb]);
-            acc[nb] = mfma4(x.y, w[1 * L1 + 16 * nb], acc[nb]);
-            acc[nb] = mfma4(x.z, w[2 * L1 + 16 * nb], acc[nb]);
-            acc[nb] = mfma4(x.w, w[3 * L1 + 16 * nb], acc[nb]);
+        for (uint32_t u = 0; u < kU; ++u) {
+            const uint32_t kb = kb0 + u;
+            x[u] = X[kb * 4 + q];
+            const float* wp = a.l1_w + (uint64_t)(kb * 16 + 4 * q) * L1 + i;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) w[u][c][nb] = wp[c * L1 + 16 * nb];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) {
+            const float4 xv = xvalid ? x[u] : zero4;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                acc[nb] = mfma4(xv.x, w[u][0][nb], acc[nb]);
+                acc[nb] = mfma4(xv.y, w[u][1][nb], acc[nb]);
+                acc[nb] = mfma4(xv.z, w[u][2][nb], acc[nb]);
+                acc[nb] = mfma4(xv.w, w[u][3][nb], acc[nb]);
+            }
         }
     }
     // the bias seeded every row of column i; lane (j = i, q) holds rows 4q + r
@@ -217,14 +237,18 @@ __global__ __launch_bounds__(256) void simple_l1_wgrad_kernel(SimpleDenseArgs a)
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[nb][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t kc = kvalid ? k0 + 4 * kk : 0;  // always-valid column for the masked lanes
     for (uint32_t base = r0; base < r1; base += 4) {
         const uint32_t row = base + q;
         const bool rv = row < r1;
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (rv && kvalid) x = reinterpret_cast<const float4*>(a.combined + (uint64_t)row * K + k0)[kk];
+        const uint32_t rc = rv ? row : r0;  // always-valid row, masked below
+        const float4 xl = *reinterpret_cast<const float4*>(a.combined + (uint64_t)rc * K + kc);
+        const float4 x = (rv && kvalid) ? xl : zero4;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const float d = rv ? a.dl1[(uint64_t)row * L1 + 16 * nb + o] : 0.0f;
+            const float dl = a.dl1[(uint64_t)rc * L1 + 16 * nb + o];
+            const float d = rv ? dl : 0.0f;
             acc[nb][0] = mfma4(d, x.x, acc[nb][0]);
             acc[nb][1] = mfma4(d, x.y, acc[nb][1]);
             acc[nb][2] = mfma4(d, x.z, acc[nb][2]);
@@ -346,7 +370,7 @@ uint32_t simple_post_workgroups(uint32_t batch) { return ceil_div(batch, kSimple
 static int32_t check_dims(const SimpleDenseArgs& a) {
     TATARA_REQUIRE(a.l1 == 16 || a.l1 == 32, "Simple l1 must be 16 or 32");
     TATARA_REQUIRE(a.l2 == 32, "Simple l2 must be 32");
-    TATARA_REQUIRE(a.ft_out % 8 == 0, "Simple ft_out must be a multiple of 8");
+    TATARA_REQUIRE(a.ft_out % 32 == 0, "Simple ft_out must be a multiple of 32");
     return kOk;
 }
 

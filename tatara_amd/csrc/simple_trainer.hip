@@ -66,7 +66,7 @@ class SimpleTrainer final : public TrainerBase {
         cfg = c;
         TATARA_REQUIRE(c.max_batch > 0, "max_batch must be positive");
         TATARA_REQUIRE(c.ft_in > 0 && c.max_active > 0 && c.max_active <= 64, "ft_in > 0, 0 < max_active <= 64");
-        TATARA_REQUIRE(c.ft_out > 0 && c.ft_out % 8 == 0, "ft_out must be a positive multiple of 8");
+        TATARA_REQUIRE(c.ft_out > 0 && c.ft_out % 32 == 0, "ft_out must be a positive multiple of 32");
         TATARA_REQUIRE((c.l1_out == 32 || c.l1_out == 16) && c.l2_out == 32,
                        "Simple (l1, l2) must be (32, 32) or (16, 32)");
         TATARA_REQUIRE(c.optimizer >= 0 && c.optimizer <= 2, "unknown optimizer");
@@ -238,6 +238,27 @@ class SimpleTrainer final : public TrainerBase {
         int32_t st;
         const uint32_t b = p.b;
         if (train && (st = prof_mark(0))) return st;
+        if (train) {
+            // occurrence lists for the FT backward, on the side stream: they
+            // depend only on the indices and are first needed by the FT
+            // gradient, so the sort overlaps the forward
+            if ((st = fork_side())) return st;
+            OccurrenceSortArgs os{};
+            os.idx_stm = p.stm;
+            os.idx_nstm = p.nstm;
+            os.nnz = p.nnz;
+            os.batch = b;
+            os.max_active = max_active;
+            os.cols = ft_in;
+            os.keys_in = occ_ki;
+            os.vals_in = occ_vi;
+            os.keys_out = occ_ko;
+            os.vals_out = occ_vo;
+            os.offsets = occ_off;
+            os.temp = occ_tmp;
+            os.temp_bytes = occ_tmp_bytes;
+            if ((st = launch_occurrence_sort(os, side))) return st;
+        }
         const int32_t* sched = nullptr;
         if (factorized) {
             if ((st = launch_king_block_keys(p.stm, p.nstm, p.nnz, sched_keys, b, max_active, ft_in, pi,
@@ -255,23 +276,6 @@ class SimpleTrainer final : public TrainerBase {
             bs.out = schedule;
             if ((st = launch_binsort(bs, stream))) return st;
             sched = schedule;
-        }
-        if (train) {
-            OccurrenceSortArgs os{};
-            os.idx_stm = p.stm;
-            os.idx_nstm = p.nstm;
-            os.nnz = p.nnz;
-            os.batch = b;
-            os.max_active = max_active;
-            os.cols = ft_in;
-            os.keys_in = occ_ki;
-            os.vals_in = occ_vi;
-            os.keys_out = occ_ko;
-            os.vals_out = occ_vo;
-            os.offsets = occ_off;
-            os.temp = occ_tmp;
-            os.temp_bytes = occ_tmp_bytes;
-            if ((st = launch_occurrence_sort(os, stream))) return st;
         }
         if (train && (st = prof_mark(1))) return st;
         FtForwardArgs fa{};
@@ -335,6 +339,7 @@ class SimpleTrainer final : public TrainerBase {
         fb.rows = ft_in;
         fb.apply_update = 1;
         fb.opt = scalars(0, lr, step_count);
+        if ((st = join_side())) return st;
         if ((st = launch_ft_grad_update(fb, stream))) return st;
         if ((st = prof_mark(5))) return st;
         if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;

@@ -287,6 +287,27 @@ class LayerStackTrainer final : public TrainerBase {
         const uint32_t b = p.b;
         padded = padded_sort_batch(b, nb);
         if (train && (st = prof_mark(0))) return st;
+        if (train) {
+            // occurrence lists for the FT backward, on the side stream: they
+            // depend only on the indices and are first needed by the FT
+            // gradient, so the sort overlaps the forward
+            if ((st = fork_side())) return st;
+            OccurrenceSortArgs os{};
+            os.idx_stm = p.stm;
+            os.idx_nstm = p.nstm;
+            os.nnz = p.nnz;
+            os.batch = b;
+            os.max_active = max_active;
+            os.cols = ft_in;
+            os.keys_in = occ_ki;
+            os.vals_in = occ_vi;
+            os.keys_out = occ_ko;
+            os.vals_out = occ_vo;
+            os.offsets = occ_off;
+            os.temp = occ_tmp;
+            os.temp_bytes = occ_tmp_bytes;
+            if ((st = launch_occurrence_sort(os, side))) return st;
+        }
         // king-block schedule for the gather
         const int32_t* sched = nullptr;
         if (factorized) {
@@ -323,23 +344,6 @@ class LayerStackTrainer final : public TrainerBase {
             bs.out_key = sorted_bin;
             bs.out_fill_len = padded;
             if ((st = launch_binsort(bs, stream))) return st;
-        }
-        if (train) {
-            OccurrenceSortArgs os{};
-            os.idx_stm = p.stm;
-            os.idx_nstm = p.nstm;
-            os.nnz = p.nnz;
-            os.batch = b;
-            os.max_active = max_active;
-            os.cols = ft_in;
-            os.keys_in = occ_ki;
-            os.vals_in = occ_vi;
-            os.keys_out = occ_ko;
-            os.vals_out = occ_vo;
-            os.offsets = occ_off;
-            os.temp = occ_tmp;
-            os.temp_bytes = occ_tmp_bytes;
-            if ((st = launch_occurrence_sort(os, stream))) return st;
         }
         if (train && (st = prof_mark(1))) return st;
         // FT gather + pairwise post
@@ -410,6 +414,7 @@ class LayerStackTrainer final : public TrainerBase {
         fb.rows = ft_in;
         fb.apply_update = 1;
         fb.opt = sf;
+        if ((st = join_side())) return st;
         if ((st = launch_ft_grad_update(fb, stream))) return st;
         if ((st = prof_mark(5))) return st;
         if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;

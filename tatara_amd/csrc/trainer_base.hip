@@ -19,13 +19,20 @@ TrainerBase::~TrainerBase() {
     for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
     for (auto& e : loss_ev)
         if (e) (void)hipEventDestroy(e);
+    if (side) (void)hipStreamSynchronize(side);
+    if (ev_fork) (void)hipEventDestroy(ev_fork);
+    if (ev_join) (void)hipEventDestroy(ev_join);
     if (pinned_loss) (void)hipHostFree(pinned_loss);
+    if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamDestroy(stream);
 }
 
 int32_t TrainerBase::init_runtime(int device) {
     TATARA_HIP(hipSetDevice(device), "hipSetDevice");
     TATARA_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    TATARA_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate (side)");
+    TATARA_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming), "hipEventCreate");
+    TATARA_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming), "hipEventCreate");
     TATARA_HIP(hipEventCreateWithFlags(&loss_ev[0], hipEventDisableTiming), "hipEventCreate");
     TATARA_HIP(hipEventCreateWithFlags(&loss_ev[1], hipEventDisableTiming), "hipEventCreate");
     TATARA_HIP(hipHostMalloc((void**)&pinned_loss, 2 * sizeof(double), hipHostMallocDefault),
@@ -203,6 +210,18 @@ int32_t TrainerBase::flush(double* out) {
         pending = -1;
     }
     if (out) *out = v;
+    return kOk;
+}
+
+int32_t TrainerBase::fork_side() {
+    TATARA_HIP(hipEventRecord(ev_fork, stream), "hipEventRecord (fork)");
+    TATARA_HIP(hipStreamWaitEvent(side, ev_fork, 0), "hipStreamWaitEvent (fork)");
+    return kOk;
+}
+
+int32_t TrainerBase::join_side() {
+    TATARA_HIP(hipEventRecord(ev_join, side), "hipEventRecord (join)");
+    TATARA_HIP(hipStreamWaitEvent(stream, ev_join, 0), "hipStreamWaitEvent (join)");
     return kOk;
 }
 

@@ -54,6 +54,9 @@ class TrainerBase {
 
     TataraTrainerConfig cfg{};
     hipStream_t stream = nullptr;
+    // second stream for work that only depends on the batch indices (the
+    // occurrence sort of the FT backward), overlapped with the forward
+    hipStream_t side = nullptr;
     DeviceArena arena;
     uint64_t step_count = 0;
     uint32_t last_b = 0;
@@ -87,6 +90,7 @@ class TrainerBase {
     int next_slot = 0;
     // phase profiling: kPhases + 1 events per profiled step
     std::vector<hipEvent_t> prof_events;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 
     int32_t init_runtime(int device);
     int32_t alloc_inputs(uint64_t max_b, uint32_t max_active);
@@ -102,6 +106,10 @@ class TrainerBase {
     // Queues this step's loss (device f64 at loss_dev[slot]) and returns the previous one.
     int32_t queue_loss(const double* loss_dev, int slot, double* lagged);
     int32_t prof_mark(int k);
+    // side waits for everything enqueued on stream so far
+    int32_t fork_side();
+    // stream waits for everything enqueued on side so far
+    int32_t join_side();
 };
 
 }  // namespace tatara
