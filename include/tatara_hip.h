@@ -108,6 +108,48 @@ TATARA_API int32_t tatara_op_ranger_lookahead_lerp(float* weights, float* slow, 
  * reference kernel used to calibrate HBM byte counters (FETCH_SIZE,
  * WRITE_SIZE).  bytes must be a multiple of 16.  No reference counterpart. */
 TATARA_API int32_t tatara_op_copy(void* dst, const void* src, uint64_t bytes);
+/* exp as the reference's CPU path evaluates it (Rust f32::exp = glibc expf on
+ * linux-gnu; used by ShogiProgressKPAbs::progress_board,
+ * crates/shogi-features/src/progress_kpabs.rs:140-150), elementwise on device
+ * arrays.  Equal to glibc's result for every non-NaN float. */
+TATARA_API int32_t tatara_op_expf(const float* x, float* y, uint64_t n);
+
+/* ------------------------------------------------------------------------ */
+/* Dataloader: PSV records -> batch (Batch::push_decoded + BucketMode)       */
+/* ------------------------------------------------------------------------ */
+
+/* FeatureSet (crates/shogi-features/src/feature_set.rs:55-185). */
+#define TATARA_FS_HALFKP 0
+#define TATARA_FS_HALFKA_SPLIT 1
+#define TATARA_FS_HALFKA_MERGED 2
+#define TATARA_FS_HALFKA_HM_SPLIT 3
+#define TATARA_FS_HALFKA_HM_MERGED 4
+/* BucketMode (crates/nnue-train/src/dataloader.rs:303-328); NONE gives bucket 0. */
+#define TATARA_BUCKET_NONE 0
+#define TATARA_BUCKET_KINGRANK9 1
+#define TATARA_BUCKET_PROGRESS_KPABS 2
+
+/* FeatureSetSpec::{king_buckets, piece_inputs, ft_in, max_active,
+ * feature_hash} (feature_set.rs:262-520).  Outputs may be NULL. */
+TATARA_API int32_t tatara_feature_set_info(int32_t feature_set, int32_t* king_buckets,
+                                           int32_t* piece_inputs, int32_t* ft_in,
+                                           int32_t* max_active, uint32_t* feature_hash);
+/* n PackedSfenValue records (40 bytes each, packed_sfen.rs:255-268) -> the
+ * arrays of Batch::push_decoded (dataloader.rs:444-497): index rows
+ * [n][max_active] in FeatureSetSpec::extract_active_features order
+ * (feature_set.rs:655-810), -1 past nnz; score = (float)i16 score; wdl 1 / 0.5 / 0
+ * for win / draw / loss; bucket_idx by BucketMode::bucket_board (kingrank9,
+ * kingrank9.rs:11-23, or KP-absolute progress with num_buckets in [1, 256] and
+ * the 81*1548 progress weights as f32, progress_kpabs.rs:106-170; f64 file
+ * values are rounded to nearest f32 as load_from_bin does).  All pointers are
+ * device memory; bucket_idx may be NULL.  Decoded on the GPU, one thread per
+ * record; synchronous. */
+TATARA_API int32_t tatara_psv_to_batch(const uint8_t* psv, int32_t n, int32_t feature_set,
+                                       int32_t bucket_mode, int32_t num_buckets,
+                                       const float* progress_weights, int32_t* stm_indices,
+                                       int32_t* nstm_indices, int32_t* nnz, int32_t* bucket_idx,
+                                       float* score, float* wdl);
+
 /* Host pre-compute of RAdam (crates/gpu-kernels/src/pointwise/radam_step.rs:75-97). */
 TATARA_API int32_t tatara_radam_step_size_denom(uint64_t step, float beta1, float beta2,
                                      float n_sma_threshold, float* step_size, int32_t* denom);

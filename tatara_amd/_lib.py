@@ -101,6 +101,12 @@ SIGNATURES = {
     ),
     "tatara_op_ranger_lookahead_lerp": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_float, C.c_uint64]),
     "tatara_op_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "tatara_op_expf": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "tatara_feature_set_info": (C.c_int32, [C.c_int32, c_i32p, c_i32p, c_i32p, c_i32p, C.POINTER(C.c_uint32)]),
+    "tatara_psv_to_batch": (
+        C.c_int32,
+        [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32] + [C.c_void_p] * 7,
+    ),
     "tatara_radam_step_size_denom": (
         C.c_int32,
         [C.c_uint64, C.c_float, C.c_float, C.c_float, c_f32p, c_i32p],

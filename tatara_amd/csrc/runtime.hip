@@ -15,6 +15,7 @@
 #include "binsort.hpp"
 #include "common.hpp"
 #include "ft_kernels.hpp"
+#include "psv_kernels.hpp"
 
 namespace tatara {
 
@@ -306,6 +307,58 @@ int32_t tatara_op_ranger_lookahead_lerp(float* weights, float* slow, float alpha
     int32_t st = launch_lerp(weights, slow, n, alpha, 0);
     if (st) return st;
     TATARA_HIP(hipDeviceSynchronize(), "ranger_lookahead_lerp");
+    return kOk;
+}
+
+int32_t tatara_op_expf(const float* x, float* y, uint64_t n) {
+    int32_t st = launch_expf(x, y, n, 0);
+    if (st) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "expf");
+    return kOk;
+}
+
+int32_t tatara_feature_set_info(int32_t feature_set, int32_t* king_buckets, int32_t* piece_inputs,
+                                int32_t* ft_in, int32_t* max_active, uint32_t* feature_hash) {
+    FeatureSetShape s;
+    int32_t st = feature_set_shape(feature_set, s);
+    if (st) return st;
+    if (king_buckets) *king_buckets = s.king_buckets;
+    if (piece_inputs) *piece_inputs = s.piece_inputs;
+    if (ft_in) *ft_in = s.king_buckets * s.piece_inputs;
+    if (max_active) *max_active = s.max_active;
+    if (feature_hash) *feature_hash = s.feature_hash;
+    return kOk;
+}
+
+int32_t tatara_psv_to_batch(const uint8_t* psv, int32_t n, int32_t feature_set, int32_t bucket_mode,
+                            int32_t num_buckets, const float* progress_weights, int32_t* stm_indices,
+                            int32_t* nstm_indices, int32_t* nnz, int32_t* bucket_idx, float* score,
+                            float* wdl) {
+    TATARA_REQUIRE(n >= 0, "n must be >= 0");
+    TATARA_REQUIRE(n == 0 || (psv && stm_indices && nstm_indices && nnz && score && wdl), "null argument");
+    FeatureSetShape s;
+    int32_t st = feature_set_shape(feature_set, s);
+    if (st) return st;
+    PsvArgs a{};
+    a.psv = psv;
+    a.n = (uint32_t)n;
+    a.piece_inputs = s.piece_inputs;
+    a.max_active = s.max_active;
+    a.emit_king = s.emit_king;
+    a.fold_enemy = s.fold_enemy;
+    a.mirror = s.mirror;
+    a.bucket_mode = bucket_mode;
+    a.num_buckets = num_buckets;
+    a.weights = progress_weights;
+    a.stm = stm_indices;
+    a.nstm = nstm_indices;
+    a.nnz = nnz;
+    a.bucket = bucket_idx;
+    a.score = score;
+    a.wdl = wdl;
+    a.progress = nullptr;
+    if ((st = launch_psv_to_batch(a, 0))) return st;
+    TATARA_HIP(hipDeviceSynchronize(), "psv_to_batch");
     return kOk;
 }
 
