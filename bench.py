@@ -39,19 +39,20 @@ WORKLOADS = {
     "ls1536": dict(
         metric="train pos/s @ batch 65536 (LayerStack ft-1536, 1 GPU); FT gather % HBM peak",
         arch="layerstack", spec="halfka-hm-merged", ft_out=1536, l1=16, l2=32, nb=8,
-        optimizer="ranger", lr=8.75e-4, ref=2.45e6, ref_src="README.md:41",
-        desc="LayerStack halfka-hm-merged ft-out 1536/16/32 fp32, batch 65536, 8 buckets, "
-             "Ranger, sigmoid loss 1/290, factorizer on (BASELINE configs[3])"),
+        bucket_mode="progress8kpabs", optimizer="ranger", lr=8.75e-4, ref=2.45e6, ref_src="README.md:41",
+        desc="LayerStack halfka-hm-merged ft-out 1536/16/32 fp32, batch 65536, progress8kpabs "
+             "(8 buckets, seeded progress weights ~ N(0, 0.01)), Ranger, sigmoid loss 1/290, "
+             "factorizer on (BASELINE configs[3])"),
     "ls768": dict(
         metric="train pos/s @ batch 65536 (LayerStack ft-768, 1 GPU); FT gather % HBM peak",
         arch="layerstack", spec="halfka-hm-merged", ft_out=768, l1=8, l2=32, nb=9,
-        optimizer="ranger", lr=8.75e-4, ref=4.24e6, ref_src="README.md:42",
-        desc="LayerStack halfka-hm-merged ft-out 768/8/32 fp32, batch 65536, 9 buckets, "
+        bucket_mode="kingrank9", optimizer="ranger", lr=8.75e-4, ref=4.24e6, ref_src="README.md:42",
+        desc="LayerStack halfka-hm-merged ft-out 768/8/32 fp32, batch 65536, kingrank9 (9 buckets), "
              "Ranger, sigmoid loss 1/290, factorizer on (BASELINE configs[2])"),
     "simple": dict(
         metric="train pos/s @ batch 65536 (Simple HalfKP 256x2-32-32, 1 GPU); FT gather % HBM peak",
         arch="simple", spec="halfkp", ft_out=256, l1=32, l2=32, nb=1,
-        optimizer="adamw", lr=1e-3, ref=11.29e6, ref_src="README.md:43",
+        bucket_mode="none", optimizer="adamw", lr=1e-3, ref=11.29e6, ref_src="README.md:43",
         desc="Simple HalfKP 256x2-32-32 fp32 crelu, batch 65536, AdamW lr 1e-3 wd 0.01, "
              "WRM with every scaling 290, factorizer on (BASELINE configs[1])"),
 }
@@ -80,7 +81,7 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(batches, ft_out, ft_in, max_active, lookahead_frac, out_rows):
+def algorithmic_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_rows):
     """Per-launch algorithmic bytes of the two FT kernels, averaged over the batches.
 
     ft_forward: gathered fp32 rows of both perspectives + the per-perspective
@@ -91,8 +92,8 @@ def algorithmic_bytes(batches, ft_out, ft_in, max_active, lookahead_frac, out_ro
     list + w, m, v read and written for every real row (+ slow on the
     lookahead step, 1 in 6) + the row gradient written for the virtual rows.
     """
-    nnz_total = np.mean([float(b.nnz.sum()) for b, _ in batches])
-    b = batches[0][0].n_positions
+    nnz_total = np.mean([float(h["nnz"].sum()) for h in host_batches])
+    b = host_batches[0]["nnz"].size
     gather = 2.0 * nnz_total * ft_out * 4
     fwd = gather + out_rows * b * ft_out * 4 + 2.0 * b * max_active * 4 + 4.0 * b
     rows = ft_in * ft_out * 4.0
@@ -106,14 +107,16 @@ WRM290 = {"kind": "wrm", "nnue2score": 290.0, "in_scaling": 290.0, "in_offset": 
 SIGMOID = {"kind": "sigmoid", "scale": 1.0 / 290.0}
 
 
-def cpu_baseline(w: dict, spec: dict, batch, bucket, threads: int) -> dict:
+def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:
     """Oracle (CPU restatement) step on this host, bounded sample of the same workload."""
     from oracle import ffi
 
     used = ffi.set_threads(threads)
     n = 16384 if w["arch"] == "layerstack" else 32768
-    bd = dict(stm=batch.stm_indices[:n], nstm=batch.nstm_indices[:n], nnz=batch.nnz[:n],
-              bucket=None if bucket is None else bucket[:n], score=batch.score[:n], wdl=batch.wdl[:n])
+    ma = spec["max_active"]
+    bd = dict(stm=hb["stm"].reshape(-1, ma)[:n], nstm=hb["nstm"].reshape(-1, ma)[:n], nnz=hb["nnz"][:n],
+              bucket=hb["bucket"][:n] if w["arch"] == "layerstack" else None, score=hb["score"][:n],
+              wdl=hb["wdl"][:n])
     if w["arch"] == "layerstack":
         from oracle import layerstack as ols
 
@@ -167,8 +170,10 @@ def main() -> int:
         return 2
 
     from tatara_amd import _lib
-    from tatara_amd.synthetic import HALFKA_HM_MERGED, HALFKP, structured_batch
-    from tatara_amd.trainer import (DeviceBatch, LayerStackConfig, LayerStackTrainer, Sigmoid,
+    from tatara_amd.dataloader import (ProgressWeights, device_batch_to_host, feature_set_info,
+                                       psv_to_device_batch)
+    from tatara_amd.psv import synthetic_progress_weights, synthetic_psv
+    from tatara_amd.trainer import (LayerStackConfig, LayerStackTrainer, Sigmoid,
                                     SimpleConfig, SimpleTrainer, Wrm)
 
     w = WORKLOADS[args.workload]
@@ -186,10 +191,20 @@ def main() -> int:
         _lib.check(lib.tatara_free(src.value))
         _lib.check(lib.tatara_free(dst.value))
         log(f"copied {args.copy_calibration_mb} MiB x3 (counter calibration)")
-    spec = HALFKA_HM_MERGED if w["spec"] == "halfka-hm-merged" else HALFKP
+    info = feature_set_info(w["spec"])
+    spec = dict(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"])
     b = args.batch
-    log(f"{args.workload}: generating {args.n_batches} synthetic batches of {b} positions")
-    batches = [structured_batch(b, spec, num_buckets=w["nb"], seed=1000 + i) for i in range(args.n_batches)]
+    log(f"{args.workload}: generating {args.n_batches} x {b} synthetic PSV positions")
+    records = [synthetic_psv(b, seed=1000 + i) for i in range(args.n_batches)]
+    pw = ProgressWeights(synthetic_progress_weights(seed=7)) if w["bucket_mode"] == "progress8kpabs" else None
+    # PSV -> feature indices + buckets on the GPU (the dataloader step)
+    t_dec = time.perf_counter()
+    dev = [psv_to_device_batch(r, w["spec"], w["bucket_mode"], w["nb"], pw) for r in records]
+    decode_ms = 1000.0 * (time.perf_counter() - t_dec) / len(dev)
+    host_batches = [device_batch_to_host(d) for d in dev]
+    log(f"decoded on the GPU: {decode_ms:.2f} ms per batch of {b} (incl. 40 B/pos upload); "
+        f"mean nnz {np.mean([h['nnz'].mean() for h in host_batches]):.1f}; bucket histogram "
+        f"{np.bincount(host_batches[0]['bucket'], minlength=w['nb']).tolist()}")
     lr = w["lr"]
     if w["arch"] == "layerstack":
         cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
@@ -208,7 +223,6 @@ def main() -> int:
                    target_scaling=290.0)
         step = lambda t, db: t.train_step(db, lr, 0.0, loss)  # noqa: E731
     with trainer as t:
-        dev = [DeviceBatch.upload(bt, bk if w["arch"] == "layerstack" else None) for bt, bk in batches]
         log(f"warm-up {args.warmup} steps")
         for i in range(args.warmup):
             step(t, dev[i % len(dev)])
@@ -237,7 +251,7 @@ def main() -> int:
     log("phases (ms/step): " + ", ".join(f"{k} {v:.3f}" for k, v in phase_avg.items()))
 
     la = 1.0 / 6.0 if w["optimizer"] == "ranger" else 0.0
-    fwd_bytes, grad_bytes = algorithmic_bytes(batches, w["ft_out"], spec["ft_in"], spec["max_active"],
+    fwd_bytes, grad_bytes = algorithmic_bytes(host_batches, w["ft_out"], spec["ft_in"], spec["max_active"],
                                               lookahead_frac=la,
                                               out_rows=3 if w["arch"] == "layerstack" else 4)
     kernels = {
@@ -273,8 +287,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle step)")
         try:
-            cpu = cpu_baseline(w, spec, batches[0][0], batches[0][1] if w["arch"] == "layerstack" else None,
-                               args.cpu_threads)
+            cpu = cpu_baseline(w, spec, host_batches[0], args.cpu_threads)
         except Exception as e:  # the baseline must not hide the GPU result
             cpu = {"value": None, "error": repr(e)}
 
@@ -290,7 +303,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": round(pos_s / w["ref"], 4),
         "dtype": "f32",
-        "data": f"synthetic (seeded king-blocked {w['spec']} index batches, resident in HBM)",
+        "data": f"synthetic: seeded PSV positions (40 pieces, 15% in hand, 10% promoted), decoded to "
+                f"{w['spec']} indices and {w['bucket_mode']} buckets on the GPU, resident in HBM",
         "config": {
             "workload": w["desc"],
             "global_batch": b,
@@ -302,6 +316,7 @@ def main() -> int:
         "roofline": roofline,
         "kernels": other,
         "phases_ms": {k: round(v, 4) for k, v in phase_avg.items()},
+        "psv_decode_ms_per_batch": round(decode_ms, 3),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -32,24 +32,22 @@ _UNPROMOTE = np.array([0, 1, 2, 3, 4, 5, 6, 7, 8, 1, 2, 3, 4, 5, 6], np.int64)
 HAND_TYPES = (1, 2, 3, 4, 7, 5, 6)  # pawn, lance, knight, silver, gold, bishop, rook
 
 
+_PAT = np.array([_HUFF[t][0] if t in _HUFF else 0 for t in range(9)], np.int64)
+_LEN = np.array([_HUFF[t][1] if t in _HUFF else 0 for t in range(9)], np.int64)
+
+
 def _board_code(ptype: np.ndarray, color: np.ndarray):
     """(value, length) of every square's board code; kings get length 0."""
     base = _UNPROMOTE[ptype]
-    pat = np.zeros_like(base)
-    ln = np.zeros_like(base)
-    for t, (p, l) in _HUFF.items():
-        pat[base == t] = p
-        ln[base == t] = l
-    prom = (ptype >= 9).astype(np.int64)
-    has_prom = (base != 7) & (base != 0)
-    val = pat.copy()
-    tot = ln.copy()
-    val = np.where(has_prom, val | (prom << tot), val)
+    val = _PAT[base]
+    tot = _LEN[base]
+    has_prom = ((base != 7) & (base != 0) & (base != 8)).astype(np.int64)
+    val = val | (((ptype >= 9).astype(np.int64) * has_prom) << tot)
     tot = tot + has_prom
-    occupied = base != 0
-    val = np.where(occupied, val | (color.astype(np.int64) << tot), val)
+    occupied = ((base != 0) & (base != 8)).astype(np.int64)
+    val = val | ((color.astype(np.int64) * occupied) << tot)
     tot = tot + occupied
-    is_king = ptype == 8
+    is_king = base == 8
     return np.where(is_king, 0, val), np.where(is_king, 0, tot)
 
 
@@ -105,12 +103,19 @@ def encode(ptype, color, hand, stm, score=None, result=None, ply=None) -> np.nda
     total = L.sum(1)
     if np.any(total > 256):
         raise ValueError("position does not fit 256 bits")
-    bits = np.zeros((n, 256), np.uint8)
-    for j in range(8):
-        m = L > j
-        r, c = np.nonzero(m)
-        bits[r, off[r, c] + j] = ((V[r, c] >> j) & 1).astype(np.uint8)
-    packed = np.packbits(bits, axis=1, bitorder="little")
+    # OR every field into four little-endian 64-bit words (fields are at most
+    # 8 bits long, so a field touches at most two words)
+    words = np.zeros((n, 6), np.uint64)
+    V = V.astype(np.uint64)
+    for j in range(V.shape[1]):
+        o = off[:, j].astype(np.uint64)
+        wi = (o >> np.uint64(6)).astype(np.int64)
+        sh = o & np.uint64(63)
+        lo = V[:, j] << sh
+        hi = np.where(sh > 0, V[:, j] >> (np.uint64(64) - np.maximum(sh, np.uint64(1))), np.uint64(0))
+        words[rows, wi] |= lo
+        words[rows, wi + 1] |= hi
+    packed = np.ascontiguousarray(words[:, :4].astype("<u8")).view(np.uint8).reshape(n, 32)
     out = np.zeros((n, RECORD_BYTES), np.uint8)
     out[:, :32] = packed
     sc = np.zeros(n, np.int16) if score is None else np.asarray(score, np.int16)
