@@ -19,6 +19,7 @@
 #include "dense_kernels.hpp"
 
 #include "common.hpp"
+#include "ft_kernels.hpp"
 
 namespace tatara {
 
@@ -473,7 +474,12 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
         const uint32_t persp = c0 < half ? 0 : 1;
         const uint32_t p0 = c0 - persp * half;
         const float* ft = persp ? a.ft_nstm : a.ft_stm;
-        float* dft = a.dft + persp * batch * ft_out;
+        // chunk-major dft: this thread's four columns c0..c0+3 and their pair
+        // partners each lie inside one 256-column chunk
+        const uint64_t cstride = 2 * batch * kDftChunk;
+        float* dft_a = a.dft + (uint64_t)(p0 / kDftChunk) * cstride + persp * batch * kDftChunk + p0 % kDftChunk;
+        float* dft_b = a.dft + (uint64_t)((p0 + half) / kDftChunk) * cstride + persp * batch * kDftChunk +
+                       (p0 + half) % kDftChunk;
         float ws[4][L1];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -549,9 +555,8 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                     ga[e] = (xa[e] > 0.0f && xa[e] < 1.0f) ? dyv[e] * yb * a.ft_post_scale : 0.0f;
                     gb[e] = (xb[e] > 0.0f && xb[e] < 1.0f) ? dyv[e] * ya * a.ft_post_scale : 0.0f;
                 }
-                float4* drow = reinterpret_cast<float4*>(dft + (uint64_t)orig * ft_out);
-                drow[p0 / 4] = make_float4(ga[0], ga[1], ga[2], ga[3]);
-                drow[(p0 + half) / 4] = make_float4(gb[0], gb[1], gb[2], gb[3]);
+                *reinterpret_cast<float4*>(dft_a + (uint64_t)orig * kDftChunk) = make_float4(ga[0], ga[1], ga[2], ga[3]);
+                *reinterpret_cast<float4*>(dft_b + (uint64_t)orig * kDftChunk) = make_float4(gb[0], gb[1], gb[2], gb[3]);
                 acc_a.x += ga[0];
                 acc_a.y += ga[1];
                 acc_a.z += ga[2];

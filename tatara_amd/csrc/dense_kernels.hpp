@@ -46,7 +46,7 @@ struct LsDenseArgs {
     float* l1_sorted;           // [padded_b][2*l1]  bucket part | shared part (biases added)
     float* dl1_sorted;          // [padded_b][l1]
     float* net_output;          // [batch]
-    float* dft;                 // [2][batch][ft_out]
+    float* dft;                 // chunk-major [ceil(ft_out/256)][2*batch][256]
     // inputs
     const float* score;
     const float* wdl;

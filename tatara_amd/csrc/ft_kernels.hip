@@ -281,7 +281,7 @@ __global__ void occurrence_offsets_kernel(const uint32_t* __restrict__ sorted_ke
 
 __device__ __forceinline__ float4 segment_sum(const float4* __restrict__ dft4, uint64_t row4,
                                               const uint32_t* __restrict__ vals, uint32_t s,
-                                              uint32_t e, uint32_t q) {
+                                              uint32_t e, uint64_t q) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     constexpr int U = 8;
     uint32_t i = s;
@@ -326,7 +326,7 @@ __device__ __forceinline__ void opt_update4(float* __restrict__ w, float* __rest
 }
 
 __global__ __launch_bounds__(256) void ft_grad_update_kernel(
-    const float* __restrict__ dft,  // [2][batch][ft_out]
+    const float* __restrict__ dft, uint64_t dft_row4, uint64_t dft_chunk4,
     const uint32_t* __restrict__ occ_vals, const uint32_t* __restrict__ occ_off,
     float* __restrict__ w, float* __restrict__ m, float* __restrict__ v, float* __restrict__ slow,
     float* __restrict__ grad_out,  // gradient per row (may be null without a factorizer)
@@ -343,7 +343,8 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(
     const uint32_t s0 = __builtin_amdgcn_readfirstlane(occ_off[2 * f]);
     const uint32_t s1 = __builtin_amdgcn_readfirstlane(occ_off[2 * f + 2]);
     if (q >= row4) return;
-    const float4 gr = segment_sum(reinterpret_cast<const float4*>(dft), row4, occ_vals, s0, s1, q);
+    const float4 gr = segment_sum(reinterpret_cast<const float4*>(dft), dft_row4, occ_vals, s0, s1,
+                                  (uint64_t)chunk * dft_chunk4 + lane);
     const uint64_t off4 = (uint64_t)f * row4 + q;
     if (grad_out) st_nt(reinterpret_cast<float4*>(grad_out) + off4, gr);
     if (apply_update) opt_update4(w, m, v, slow, off4, gr, s);
@@ -546,7 +547,9 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-    ft_grad_update_kernel<<<blocks, 256, 0, stream>>>(a.dft, a.occ_vals, a.occ_off, a.w, a.m, a.v,
+    TATARA_REQUIRE(a.dft_row_stride % 4 == 0 && a.dft_chunk_stride % 4 == 0, "dft strides");
+    ft_grad_update_kernel<<<blocks, 256, 0, stream>>>(a.dft, a.dft_row_stride / 4, a.dft_chunk_stride / 4,
+                                                      a.occ_vals, a.occ_off, a.w, a.m, a.v,
                                                       a.slow, a.grad, a.ft_out, a.rows, n_chunks,
                                                       a.apply_update, a.opt);
     TATARA_LAUNCHED("ft_grad_update");

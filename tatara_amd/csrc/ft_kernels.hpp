@@ -40,7 +40,12 @@ struct OccurrenceSortArgs {
 };
 
 struct FtGradArgs {
-    const float* dft;          // [2][batch][ft_out]
+    // dft rows: element (row r, column c) lives at
+    // dft[r * dft_row_stride + (c / 256) * dft_chunk_stride + c % 256], r = persp*batch + pos.
+    // Row-major [2][batch][ft_out]: (ft_out, 256); chunk-major
+    // [ceil(ft_out/256)][2*batch][256]: (256, 2*batch*256).
+    const float* dft;
+    uint64_t dft_row_stride, dft_chunk_stride;
     const uint32_t* occ_vals;  // sorted dft row ids
     const uint32_t* occ_off;   // offsets by key 2*f+p
     float *w, *m, *v, *slow;
@@ -50,6 +55,9 @@ struct FtGradArgs {
     int32_t apply_update;      // 0: only write gradients
     OptScalars opt;
 };
+
+// Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).
+constexpr uint32_t kDftChunk = 256;
 
 int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream);
 int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm, const int32_t* nnz,

@@ -266,6 +266,8 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
     if ((st = launch_occurrence_sort(os, 0))) return st;
     FtGradArgs g{};
     g.dft = dft;
+    g.dft_row_stride = ft_out;  // row-major [2][batch][ft_out]
+    g.dft_chunk_stride = kDftChunk;
     g.occ_vals = vo.as<uint32_t>();
     g.occ_off = off.as<uint32_t>();
     g.grad = grad;

@@ -18,6 +18,7 @@
 
 #include "common.hpp"
 #include "dense_kernels.hpp"
+#include "ft_kernels.hpp"
 
 namespace tatara {
 
@@ -293,11 +294,14 @@ __global__ __launch_bounds__(256) void simple_l1_input_post_kernel(SimpleDenseAr
         ws[o] = a.l1_w[(uint64_t)c * L1 + o];
         wn[o] = a.l1_w[(uint64_t)(ft_out + c) * L1 + o];
     }
-    float* dft_s = a.dft;
-    float* dft_n = a.dft + (uint64_t)batch * ft_out;
+    // chunk-major dft: column c of row r at (c / 256) * 2*batch*256 + r * 256 + c % 256
+    const uint64_t cbase = (uint64_t)(c / kDftChunk) * 2 * batch * kDftChunk + c % kDftChunk;
+    float* dft_s = a.dft + cbase;
+    float* dft_n = a.dft + cbase + (uint64_t)batch * kDftChunk;
     float acc = 0.0f;
     for (uint32_t r = 0; r < nr; ++r) {
         const uint64_t i = (uint64_t)(r0 + r) * ft_out + c;
+        const uint64_t di = (uint64_t)(r0 + r) * kDftChunk;
         float da = 0.0f, db = 0.0f;
 #pragma unroll
         for (int o = 0; o < L1; ++o) {
@@ -307,8 +311,8 @@ __global__ __launch_bounds__(256) void simple_l1_input_post_kernel(SimpleDenseAr
         const float xs = a.ft_stm[i], xn = a.ft_nstm[i];
         const float gs = (xs > 0.0f && xs < 1.0f) ? da : 0.0f;
         const float gn = (xn > 0.0f && xn < 1.0f) ? db : 0.0f;
-        dft_s[i] = gs;
-        dft_n[i] = gn;
+        dft_s[di] = gs;
+        dft_n[di] = gn;
         acc += gs + gn;
     }
     a.ftb_partial[(uint64_t)blockIdx.y * ft_out + c] = acc;

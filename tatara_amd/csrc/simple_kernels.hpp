@@ -34,7 +34,7 @@ struct SimpleDenseArgs {
     float* l1_pre;          // [batch][l1]
     float* dl1;             // [batch][l1] gradient at the L1 pre-activation
     float* net_output;      // [batch]
-    float* dft;             // [2][batch][ft_out]
+    float* dft;             // chunk-major [ceil(ft_out/256)][2*batch][256]
     const float* score;
     const float* wdl;
     float per_pos_norm, wdl_lambda;

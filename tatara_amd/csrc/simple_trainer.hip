@@ -148,7 +148,7 @@ class SimpleTrainer final : public TrainerBase {
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
         if ((st = arena.alloc(&ft_stm, B * ft_out, false)) || (st = arena.alloc(&ft_nstm, B * ft_out, false)) ||
-            (st = arena.alloc(&combined, B * K, false)) || (st = arena.alloc(&dft, 2 * B * ft_out, false)) ||
+            (st = arena.alloc(&combined, B * K, false)) || (st = arena.alloc(&dft, 2 * B * dft_chunks() * kDftChunk, false)) ||
             (st = arena.alloc(&l1_pre, B * l1)) || (st = arena.alloc(&dl1, B * l1)) ||
             (st = arena.alloc(&net_out, B)))
             return st;
@@ -181,13 +181,19 @@ class SimpleTrainer final : public TrainerBase {
         return nullptr;
     }
 
+    uint32_t dft_chunks() const { return ceil_div(ft_out, kDftChunk); }
+
+    int32_t copy_activation(const char* name, float* host, uint64_t n) override {
+        const bool s = !std::strcmp(name, "dft_stm"), ns = !std::strcmp(name, "dft_nstm");
+        if (!s && !ns) return TrainerBase::copy_activation(name, host, n);
+        return copy_chunk_major(dft, last_b, ft_out, ns ? 1 : 0, host, n);
+    }
+
     const float* activation(const char* name, uint64_t& cap) override {
         const uint64_t bf = (uint64_t)last_b * ft_out;
         cap = bf;
         if (!std::strcmp(name, "ft_stm_out")) return ft_stm;
         if (!std::strcmp(name, "ft_nstm_out")) return ft_nstm;
-        if (!std::strcmp(name, "dft_stm")) return dft;
-        if (!std::strcmp(name, "dft_nstm")) return dft + bf;
         cap = 2 * bf;
         if (!std::strcmp(name, "combined")) return combined;
         cap = (uint64_t)last_b * l1;
@@ -328,6 +334,8 @@ class SimpleTrainer final : public TrainerBase {
         step_count += 1;
         FtGradArgs fb{};
         fb.dft = dft;
+        fb.dft_row_stride = kDftChunk;  // chunk-major [chunk][2*b][256]
+        fb.dft_chunk_stride = 2ull * p.b * kDftChunk;
         fb.occ_vals = occ_vo;
         fb.occ_off = occ_off;
         fb.w = ft.w;

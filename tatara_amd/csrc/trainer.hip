@@ -191,7 +191,7 @@ class LayerStackTrainer final : public TrainerBase {
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
         if ((st = arena.alloc(&ft_stm, B * ft_out, false)) || (st = arena.alloc(&ft_nstm, B * ft_out, false)) ||
-            (st = arena.alloc(&combined, B * ft_out, false)) || (st = arena.alloc(&dft, 2 * B * ft_out, false)) ||
+            (st = arena.alloc(&combined, B * ft_out, false)) || (st = arena.alloc(&dft, 2 * B * dft_chunks() * kDftChunk, false)) ||
             (st = arena.alloc(&l1_sorted, P * 2 * l1)) || (st = arena.alloc(&dl1_sorted, P * l1)) ||
             (st = arena.alloc(&net_out, B)))
             return st;
@@ -403,6 +403,8 @@ class LayerStackTrainer final : public TrainerBase {
         const OptScalars sb = scalars(2, lr, step_count);
         FtGradArgs fb{};
         fb.dft = dft;
+        fb.dft_row_stride = kDftChunk;  // chunk-major [chunk][2*b][256]
+        fb.dft_chunk_stride = 2ull * p.b * kDftChunk;
         fb.occ_vals = occ_vo;
         fb.occ_off = occ_off;
         fb.w = ft.w;
@@ -464,14 +466,20 @@ class LayerStackTrainer final : public TrainerBase {
         return kOk;
     }
 
+    uint32_t dft_chunks() const { return ceil_div(ft_out, kDftChunk); }
+
+    int32_t copy_activation(const char* name, float* host, uint64_t n) override {
+        const bool s = !std::strcmp(name, "dft_stm"), ns = !std::strcmp(name, "dft_nstm");
+        if (!s && !ns) return TrainerBase::copy_activation(name, host, n);
+        return copy_chunk_major(dft, last_b, ft_out, ns ? 1 : 0, host, n);
+    }
+
     const float* activation(const char* name, uint64_t& cap) override {
         const uint64_t bf = (uint64_t)last_b * ft_out;
         cap = bf;
         if (!std::strcmp(name, "ft_stm_out")) return ft_stm;
         if (!std::strcmp(name, "ft_nstm_out")) return ft_nstm;
         if (!std::strcmp(name, "combined")) return combined;
-        if (!std::strcmp(name, "dft_stm")) return dft;
-        if (!std::strcmp(name, "dft_nstm")) return dft + bf;
         cap = last_b;
         if (!std::strcmp(name, "net_output")) return net_out;
         return nullptr;
@@ -590,14 +598,7 @@ int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int3
 int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const char* name, float* host,
                                       uint64_t n) {
     TATARA_REQUIRE(trainer && name && host, "null argument");
-    TrainerBase& t = *trainer->t;
-    uint64_t cap = 0;
-    const float* src = t.activation(name, cap);
-    TATARA_REQUIRE(src, std::string("unknown activation ") + name);
-    TATARA_REQUIRE(n <= cap, "activation request exceeds the last batch");
-    TATARA_HIP(hipStreamSynchronize(t.stream), "get_activation sync");
-    TATARA_HIP(hipMemcpy(host, src, n * sizeof(float), hipMemcpyDeviceToHost), "get_activation");
-    return kOk;
+    return trainer->t->copy_activation(name, host, n);
 }
 
 int32_t tatara_trainer_set_profiling(TataraTrainer* trainer, int32_t enable) {

@@ -3,6 +3,7 @@
 
 #include <cmath>
 #include <limits>
+#include <string>
 
 namespace tatara {
 
@@ -222,6 +223,32 @@ int32_t TrainerBase::fork_side() {
 int32_t TrainerBase::join_side() {
     TATARA_HIP(hipEventRecord(ev_join, side), "hipEventRecord (join)");
     TATARA_HIP(hipStreamWaitEvent(stream, ev_join, 0), "hipStreamWaitEvent (join)");
+    return kOk;
+}
+
+int32_t TrainerBase::copy_activation(const char* name, float* host, uint64_t n) {
+    uint64_t cap = 0;
+    const float* src = activation(name, cap);
+    TATARA_REQUIRE(src, std::string("unknown activation ") + name);
+    TATARA_REQUIRE(n <= cap, "activation request exceeds the last batch");
+    TATARA_HIP(hipStreamSynchronize(stream), "get_activation sync");
+    TATARA_HIP(hipMemcpy(host, src, n * sizeof(float), hipMemcpyDeviceToHost), "get_activation");
+    return kOk;
+}
+
+int32_t TrainerBase::copy_chunk_major(const float* dev, uint32_t b, uint32_t width, int persp,
+                                      float* host, uint64_t n) {
+    constexpr uint32_t kChunk = 256;
+    TATARA_REQUIRE(n <= (uint64_t)b * width, "activation request exceeds the last batch");
+    TATARA_HIP(hipStreamSynchronize(stream), "get_activation sync");
+    const uint32_t chunks = (width + kChunk - 1) / kChunk;
+    std::vector<float> all((uint64_t)chunks * 2 * b * kChunk);
+    TATARA_HIP(hipMemcpy(all.data(), dev, all.size() * sizeof(float), hipMemcpyDeviceToHost),
+               "get_activation");
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t r = i / width, c = i % width;
+        host[i] = all[((c / kChunk) * 2 * b + (uint64_t)persp * b + r) * kChunk + c % kChunk];
+    }
     return kOk;
 }
 

@@ -74,6 +74,8 @@ class TrainerBase {
     virtual int32_t sync_forward_weights() = 0;
     // Device activation of the last batch and its element capacity, or null.
     virtual const float* activation(const char* name, uint64_t& cap) = 0;
+    // Copies the first n elements of an activation to the host (row-major).
+    virtual int32_t copy_activation(const char* name, float* host, uint64_t n);
 
     int32_t flush(double* out);
     int32_t prof_collect();
@@ -106,6 +108,9 @@ class TrainerBase {
     // Queues this step's loss (device f64 at loss_dev[slot]) and returns the previous one.
     int32_t queue_loss(const double* loss_dev, int slot, double* lagged);
     int32_t prof_mark(int k);
+    // Row-major copy of perspective persp of a chunk-major [chunk][2*b][256] buffer.
+    int32_t copy_chunk_major(const float* dev, uint32_t b, uint32_t width, int persp, float* host,
+                             uint64_t n);
     // side waits for everything enqueued on stream so far
     int32_t fork_side();
     // stream waits for everything enqueued on side so far
