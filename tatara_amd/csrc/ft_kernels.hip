@@ -27,6 +27,11 @@ namespace {
 constexpr int kWave = 64;
 constexpr int kWavesPerBlock = 4;
 constexpr int kMaxActive = 64;  // one index per lane
+// Floats per lane in the FT gradient gather (a wave covers 64 * this columns).
+#ifndef TATARA_FT_GRAD_LANE_FLOATS
+#define TATARA_FT_GRAD_LANE_FLOATS 4
+#endif
+constexpr int kFtGradLaneFloats = TATARA_FT_GRAD_LANE_FLOATS;
 
 __device__ __forceinline__ float4 f4add(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
@@ -39,11 +44,6 @@ typedef float nt_f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void st_nt(float4* p, float4 v) {
     nt_f4 x = {v.x, v.y, v.z, v.w};
     __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(p));
-}
-
-__device__ __forceinline__ float4 ld_nt(const float4* p) {
-    const nt_f4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(p));
-    return make_float4(x.x, x.y, x.z, x.w);
 }
 
 // Loads the position's active indices into per-wave LDS in slot order,
@@ -275,62 +275,86 @@ __global__ void occurrence_offsets_kernel(const uint32_t* __restrict__ sorted_ke
 // then updated with RAdam (+ the Ranger lerp on lookahead steps) and its
 // gradient stored for the factorizer's virtual rows (phase B).
 // Tasks are chunk-major and swizzled so that an XCD walks consecutive rows of
-// one chunk: those rows share a king block, whose occurrences come from the
-// same few thousand positions, so the gathered dft rows stay in L2.
+// one column chunk: those rows share a king block, whose occurrences come from
+// the same few thousand (position, perspective) rows, so the gathered dft rows
+// stay in L2.  The chunk width bounds that working set: a full king block has
+// about 3.3k dft rows, i.e. 3.3 MB at 256 columns but 1.6 MB at 128, and an
+// XCD keeps one to two blocks in flight against a 4 MB L2.  A wave covers
+// kWave * V columns (V floats per lane).
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float4 segment_sum(const float4* __restrict__ dft4, uint64_t row4,
-                                              const uint32_t* __restrict__ vals, uint32_t s,
-                                              uint32_t e, uint64_t q) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    constexpr int U = 8;
+template <int V>
+using vecf = float __attribute__((ext_vector_type(V)));
+
+template <int V>
+__device__ __forceinline__ vecf<V> segment_sum(const vecf<V>* __restrict__ dft, uint64_t row_v,
+                                               const uint32_t* __restrict__ vals, uint32_t s,
+                                               uint32_t e, uint64_t q) {
+    vecf<V> acc = 0.0f;
+    constexpr int U = 32 / V;  // 8 (V=4) .. 32 (V=1) loads in flight per lane
     uint32_t i = s;
     for (; i + U <= e; i += U) {
-        float4 d[U];
+        vecf<V> d[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i + u]);
-            d[u] = dft4[r * row4 + q];
+            d[u] = dft[r * row_v + q];
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc = f4add(acc, d[u]);
+        for (int u = 0; u < U; ++u) acc += d[u];
     }
     for (; i < e; ++i) {
         const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i]);
-        acc = f4add(acc, dft4[r * row4 + q]);
+        acc += dft[r * row_v + q];
     }
     return acc;
 }
 
-__device__ __forceinline__ void opt_update4(float* __restrict__ w, float* __restrict__ m,
-                                            float* __restrict__ v, float* __restrict__ slow,
-                                            uint64_t off4, float4 g, const OptScalars& s) {
-    float4 W = ld_nt(reinterpret_cast<float4*>(w) + off4);
-    float4 M = ld_nt(reinterpret_cast<float4*>(m) + off4);
-    float4 V = ld_nt(reinterpret_cast<float4*>(v) + off4);
-    radam_elem(W.x, M.x, V.x, g.x, s);
-    radam_elem(W.y, M.y, V.y, g.y, s);
-    radam_elem(W.z, M.z, V.z, g.z, s);
-    radam_elem(W.w, M.w, V.w, g.w, s);
-    if (s.lookahead) {
-        float4 S = ld_nt(reinterpret_cast<float4*>(slow) + off4);
-        lerp_elem(W.x, S.x, s.alpha);
-        lerp_elem(W.y, S.y, s.alpha);
-        lerp_elem(W.z, S.z, s.alpha);
-        lerp_elem(W.w, S.w, s.alpha);
-        st_nt(reinterpret_cast<float4*>(slow) + off4, S);
+template <int V>
+__device__ __forceinline__ void opt_update(float* __restrict__ w, float* __restrict__ m,
+                                           float* __restrict__ v, float* __restrict__ slow,
+                                           uint64_t off, vecf<V> g, const OptScalars& s) {
+    vecf<V>* w_ = reinterpret_cast<vecf<V>*>(w) + off;
+    vecf<V>* m_ = reinterpret_cast<vecf<V>*>(m) + off;
+    vecf<V>* v_ = reinterpret_cast<vecf<V>*>(v) + off;
+    vecf<V> W = __builtin_nontemporal_load(w_);
+    vecf<V> M = __builtin_nontemporal_load(m_);
+    vecf<V> Q = __builtin_nontemporal_load(v_);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        float a = W[k], b = M[k], c = Q[k];
+        radam_elem(a, b, c, g[k], s);
+        W[k] = a;
+        M[k] = b;
+        Q[k] = c;
     }
-    st_nt(reinterpret_cast<float4*>(w) + off4, W);
-    st_nt(reinterpret_cast<float4*>(m) + off4, M);
-    st_nt(reinterpret_cast<float4*>(v) + off4, V);
+    if (s.lookahead) {
+        vecf<V>* s_ = reinterpret_cast<vecf<V>*>(slow) + off;
+        vecf<V> S = __builtin_nontemporal_load(s_);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            float a = W[k], b = S[k];
+            lerp_elem(a, b, s.alpha);
+            W[k] = a;
+            S[k] = b;
+        }
+        __builtin_nontemporal_store(S, s_);
+    }
+    __builtin_nontemporal_store(W, w_);
+    __builtin_nontemporal_store(M, m_);
+    __builtin_nontemporal_store(Q, v_);
 }
 
+// dft_row / dft_chunk: the dft strides in floats (chunk = kDftChunk columns).
+template <int V>
 __global__ __launch_bounds__(256) void ft_grad_update_kernel(
-    const float* __restrict__ dft, uint64_t dft_row4, uint64_t dft_chunk4,
+    const float* __restrict__ dft, uint64_t dft_row, uint64_t dft_chunk,
     const uint32_t* __restrict__ occ_vals, const uint32_t* __restrict__ occ_off,
     float* __restrict__ w, float* __restrict__ m, float* __restrict__ v, float* __restrict__ slow,
     float* __restrict__ grad_out,  // gradient per row (may be null without a factorizer)
     uint32_t ft_out, uint32_t rows, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
+    constexpr uint32_t kCols = kWave * V;
+    static_assert(kDftChunk % kCols == 0, "a wave's columns must lie in one dft chunk");
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -338,16 +362,16 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(
     if (task >= (uint64_t)rows * n_chunks) return;
     const uint32_t chunk = (uint32_t)(task / rows);
     const uint32_t f = (uint32_t)(task - (uint64_t)chunk * rows);
-    const uint32_t row4 = ft_out / 4;
-    const uint32_t q = chunk * kWave + lane;
+    const uint32_t col = chunk * kCols + lane * V;
     const uint32_t s0 = __builtin_amdgcn_readfirstlane(occ_off[2 * f]);
     const uint32_t s1 = __builtin_amdgcn_readfirstlane(occ_off[2 * f + 2]);
-    if (q >= row4) return;
-    const float4 gr = segment_sum(reinterpret_cast<const float4*>(dft), dft_row4, occ_vals, s0, s1,
-                                  (uint64_t)chunk * dft_chunk4 + lane);
-    const uint64_t off4 = (uint64_t)f * row4 + q;
-    if (grad_out) st_nt(reinterpret_cast<float4*>(grad_out) + off4, gr);
-    if (apply_update) opt_update4(w, m, v, slow, off4, gr, s);
+    if (col >= ft_out) return;
+    const uint64_t q = ((uint64_t)(col / kDftChunk) * dft_chunk + col % kDftChunk) / V;
+    const vecf<V> gr = segment_sum<V>(reinterpret_cast<const vecf<V>*>(dft), dft_row / V, occ_vals,
+                                      s0, s1, q);
+    const uint64_t off = ((uint64_t)f * ft_out + col) / V;
+    if (grad_out) __builtin_nontemporal_store(gr, reinterpret_cast<vecf<V>*>(grad_out) + off);
+    if (apply_update) opt_update<V>(w, m, v, slow, off, gr, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -387,7 +411,7 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(
     const uint64_t voff4 = (uint64_t)(ft_in + p) * row4 + q;
     reinterpret_cast<float4*>(grad)[voff4] = vsum;
     if (!apply_update) return;
-    opt_update4(w, m, v, slow, voff4, vsum, s);
+    opt_update<4>(w, m, v, slow, voff4, vecf<4>{vsum.x, vsum.y, vsum.z, vsum.w}, s);
     if (!comb) return;
     const float4 wv = reinterpret_cast<const float4*>(w)[voff4];
     for (j = 0; j + U <= count; j += U) {
@@ -542,16 +566,18 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) 
 }
 
 int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
+    constexpr int V = kFtGradLaneFloats;
+    constexpr uint32_t kCols = kWave * V;
     TATARA_REQUIRE(a.ft_out % 4 == 0, "ft_out must be a multiple of 4");
-    const uint32_t n_chunks = ceil_div(a.ft_out / 4, kWave);
+    TATARA_REQUIRE(a.dft_row_stride % 4 == 0 && a.dft_chunk_stride % 4 == 0, "dft strides");
+    const uint32_t n_chunks = ceil_div(a.ft_out, kCols);
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-    TATARA_REQUIRE(a.dft_row_stride % 4 == 0 && a.dft_chunk_stride % 4 == 0, "dft strides");
-    ft_grad_update_kernel<<<blocks, 256, 0, stream>>>(a.dft, a.dft_row_stride / 4, a.dft_chunk_stride / 4,
-                                                      a.occ_vals, a.occ_off, a.w, a.m, a.v,
-                                                      a.slow, a.grad, a.ft_out, a.rows, n_chunks,
-                                                      a.apply_update, a.opt);
+    ft_grad_update_kernel<V><<<blocks, 256, 0, stream>>>(a.dft, a.dft_row_stride, a.dft_chunk_stride,
+                                                         a.occ_vals, a.occ_off, a.w, a.m, a.v,
+                                                         a.slow, a.grad, a.ft_out, a.rows, n_chunks,
+                                                         a.apply_update, a.opt);
     TATARA_LAUNCHED("ft_grad_update");
     return kOk;
 }
