@@ -113,6 +113,21 @@ TATARA_API int32_t tatara_op_copy(void* dst, const void* src, uint64_t bytes);
  * crates/shogi-features/src/progress_kpabs.rs:140-150), elementwise on device
  * arrays.  Equal to glibc's result for every non-NaN float. */
 TATARA_API int32_t tatara_op_expf(const float* x, float* y, uint64_t n);
+/* FT-table quantisation of the quantised export.  Value i of the export-shape
+ * table [rows][cols] is v = w[i], plus, with piece_inputs > 0, the virtual row
+ * w[(rows + (i / cols) % piece_inputs) * cols + i % cols] added in f32
+ * (coalesce_ft_factorized, crates/nnue-format/src/layerstack_weights.rs:412-491);
+ * it is stored as saturate_i16(round(scale * (double)v)), rounding half away
+ * from zero, NaN -> 0 (layerstack_weights.rs:639-676,
+ * simple_weights.rs:596-603).  leb128 = 0: out receives rows*cols little-endian
+ * i16 (the SimpleWeights FT block); leb128 = 1: out receives the values'
+ * signed LEB128 bytes in order (encode_signed_leb128, layerstack_weights.rs:
+ * 120-138), without the magic and size prefix.  w and out are device memory;
+ * *out_bytes (host) receives the byte count, and out_capacity smaller than it
+ * is an error.  Synchronous. */
+TATARA_API int32_t tatara_op_quantise_ft(const float* w, uint64_t rows, uint32_t cols, uint32_t piece_inputs,
+                                         double scale, int32_t leb128, uint8_t* out, uint64_t out_capacity,
+                                         uint64_t* out_bytes);
 
 /* ------------------------------------------------------------------------ */
 /* Dataloader: PSV records -> batch (Batch::push_decoded + BucketMode)       */
@@ -226,6 +241,23 @@ TATARA_API int32_t tatara_trainer_flush_pending_loss(TataraTrainer* trainer, dou
 TATARA_API int32_t tatara_trainer_validate_step(TataraTrainer* trainer, const TataraBatch* batch,
                                      float wdl_lambda, const TataraLoss* loss, double* sum_sq_err,
                                      float* net_output);
+/* Quantised network export of the trainer's current weights to the file at
+ * `path` (GpuTrainer::save_checkpoint with OutputFormat::Tatara).
+ * LayerStack: LayerStackWeights::save_quantised (crates/nnue-format/src/
+ * layerstack_weights.rs:568-829) of to_layerstack_weights
+ * (bins/nnue_train/src/trainer_layerstack.rs:1351-1420): FT i16 = round(127 w)
+ * as signed LEB128, L1 bucket + shared merged to i8 = round(64 w) with i32
+ * biases = round(8128 b), L2 / L3 likewise, inputs padded to 32;
+ * has_fv_scale = 0 omits ",fv_scale=N" (fv_scale: Option<i32>; training.rs:
+ * 72-86 derives it).  Simple: SimpleWeights::save_quantised (simple_weights.rs:
+ * 374-429) of to_simple_weights (trainer_simple.rs:2680-2745) with the CReLU
+ * activation: raw i16 FT, fv_scale always written (has_fv_scale must be 1;
+ * simple_fv_scale, simple_weights.rs:90-95).  The factorizer's virtual rows
+ * are folded into the real rows (coalesce_ft_factorized).  feature_set
+ * (TATARA_FS_*) names the arch string and hashes and must match the trainer's
+ * ft_in (and piece_inputs with a factorizer).  Synchronous. */
+TATARA_API int32_t tatara_trainer_export_quantised(TataraTrainer* trainer, const char* path, int32_t feature_set,
+                                                   int32_t has_fv_scale, int32_t fv_scale);
 /* Number of optimizer steps taken. */
 TATARA_API int32_t tatara_trainer_step_count(TataraTrainer* trainer, uint64_t* steps);
 /* Parameter groups by reference name ("ft_w", "ft_b", "l1_w", "l1_b",

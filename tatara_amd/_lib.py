@@ -102,6 +102,10 @@ SIGNATURES = {
     "tatara_op_ranger_lookahead_lerp": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_float, C.c_uint64]),
     "tatara_op_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "tatara_op_expf": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "tatara_op_quantise_ft": (
+        C.c_int32,
+        [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_double, C.c_int32, C.c_void_p, C.c_uint64, c_u64p],
+    ),
     "tatara_feature_set_info": (C.c_int32, [C.c_int32, c_i32p, c_i32p, c_i32p, c_i32p, C.POINTER(C.c_uint32)]),
     "tatara_psv_to_batch": (
         C.c_int32,
@@ -128,6 +132,7 @@ SIGNATURES = {
     "tatara_trainer_set_tensor": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, c_f32p, C.c_uint64]),
     "tatara_trainer_get_activation": (C.c_int32, [C.c_void_p, C.c_char_p, c_f32p, C.c_uint64]),
     "tatara_trainer_sync_forward_weights": (C.c_int32, [C.c_void_p]),
+    "tatara_trainer_export_quantised": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int32]),
     "tatara_trainer_set_profiling": (C.c_int32, [C.c_void_p, C.c_int32]),
     "tatara_trainer_phase_times": (C.c_int32, [C.c_void_p, c_f64p, C.c_int32, c_u64p]),
 }

@@ -14,6 +14,7 @@
 #include "../../include/tatara_hip.h"
 #include "binsort.hpp"
 #include "common.hpp"
+#include "export.hpp"
 #include "ft_kernels.hpp"
 #include "psv_kernels.hpp"
 
@@ -316,6 +317,47 @@ int32_t tatara_op_expf(const float* x, float* y, uint64_t n) {
     int32_t st = launch_expf(x, y, n, 0);
     if (st) return st;
     TATARA_HIP(hipDeviceSynchronize(), "expf");
+    return kOk;
+}
+
+int32_t tatara_op_quantise_ft(const float* w, uint64_t rows, uint32_t cols, uint32_t piece_inputs,
+                              double scale, int32_t leb128, uint8_t* out, uint64_t out_capacity,
+                              uint64_t* out_bytes) {
+    TATARA_REQUIRE(out_bytes, "out_bytes is null");
+    TATARA_REQUIRE(rows == 0 || cols == 0 || (w && out), "null device pointer");
+    *out_bytes = 0;
+    const QuantSource src{w, rows, cols, piece_inputs};
+    const uint64_t n = rows * cols;
+    if (!leb128) {
+        TATARA_REQUIRE(out_capacity >= 2 * n, "out_capacity < 2 * rows * cols");
+        int32_t st = launch_quantise_i16(src, scale, reinterpret_cast<int16_t*>(out), 0);
+        if (st) return st;
+        TATARA_HIP(hipDeviceSynchronize(), "quantise_ft");
+        *out_bytes = 2 * n;
+        return kOk;
+    }
+    const uint64_t tiles = leb128_tiles(n);
+    uint32_t* tile_bytes = nullptr;
+    uint64_t* tile_off = nullptr;  // tile offsets, then the total in the last slot
+    TATARA_HIP(hipMalloc(&tile_bytes, (tiles + 1) * sizeof(uint32_t)), "hipMalloc quantise_ft");
+    hipError_t e = hipMalloc(&tile_off, (tiles + 1) * sizeof(uint64_t));
+    int32_t st = kOk;
+    uint64_t total = 0;
+    if (e == hipSuccess) st = launch_quantise_leb128(src, scale, tile_bytes, tile_off, tile_off + tiles, nullptr, 0);
+    if (e == hipSuccess && st == kOk)
+        e = hipMemcpy(&total, tile_off + tiles, sizeof total, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && st == kOk && total > out_capacity) {
+        set_error("invalid argument: out_capacity is smaller than the LEB128 stream");
+        st = kErrInvalid;
+    }
+    if (e == hipSuccess && st == kOk && total)
+        st = launch_quantise_leb128(src, scale, tile_bytes, tile_off, tile_off + tiles, out, 0);
+    if (e == hipSuccess && st == kOk) e = hipDeviceSynchronize();
+    (void)hipFree(tile_off);
+    (void)hipFree(tile_bytes);
+    if (st) return st;
+    TATARA_HIP(e, "quantise_ft");
+    *out_bytes = total;
     return kOk;
 }
 

@@ -23,6 +23,8 @@
 
 #include "binsort.hpp"
 #include "dense_kernels.hpp"
+#include "export.hpp"
+#include "psv_kernels.hpp"
 #include "ft_kernels.hpp"
 #include "init.hpp"
 #include "simple_kernels.hpp"
@@ -164,6 +166,30 @@ class SimpleTrainer final : public TrainerBase {
             return st;
         TATARA_HIP(hipDeviceSynchronize(), "trainer init");
         return sync_forward_weights();
+    }
+
+    // SimpleWeights::save_quantised of to_simple_weights() (trainer_simple.rs:
+    // 2680-2745): CReLU activation, the factorizer folded into the exported
+    // rows, dense weights transposed to out-major while writing.
+    int32_t export_quantised(const char* path, int32_t feature_set, int32_t has_fv, int32_t fv) override {
+        TATARA_REQUIRE(has_fv, "Simple export: the arch string always carries fv_scale");
+        ExportFeatureSet fs;
+        int32_t st = export_feature_set(feature_set, fs);
+        if (st) return st;
+        TATARA_REQUIRE(fs.ft_in == ft_in, "export: the feature set's ft_in differs from the trainer's");
+        if (factorized) {
+            FeatureSetShape sh;
+            if ((st = feature_set_shape(feature_set, sh))) return st;
+            TATARA_REQUIRE((uint32_t)sh.piece_inputs == pi,
+                           "export: the trainer's piece_inputs differ from the feature set's");
+        }
+        SimpleHost h;
+        std::vector<float>* dst[6] = {&h.l1_w, &h.l1_b, &h.l2_w, &h.l2_b, &h.l3_w, &h.l3_b};
+        for (int k = 0; k < 6; ++k)
+            if ((st = download(small[k + 1], *dst[k]))) return st;
+        QuantSource src{ft.w, ft_in, ft_out, factorized ? pi : 0u};
+        QuantSource bias{small[0].w, 1, ft_out, 0};
+        return write_simple_bin(path, fs, src, bias, l1, l2, h, fv, stream);
     }
 
     int32_t sync_forward_weights() override {

@@ -30,6 +30,8 @@
 #include "binsort.hpp"
 #include "common.hpp"
 #include "dense_kernels.hpp"
+#include "export.hpp"
+#include "psv_kernels.hpp"
 #include "ft_kernels.hpp"
 #include "init.hpp"
 #include "trainer_base.hpp"
@@ -211,6 +213,29 @@ class LayerStackTrainer final : public TrainerBase {
             return st;
         TATARA_HIP(hipDeviceSynchronize(), "trainer init");
         return sync_forward_weights();
+    }
+
+    // LayerStackWeights::save_quantised of to_layerstack_weights()
+    // (trainer_layerstack.rs:1351-1420): the factorizer is folded into the
+    // exported rows, L1 bucket + shared terms are merged per bucket.
+    int32_t export_quantised(const char* path, int32_t feature_set, int32_t has_fv, int32_t fv) override {
+        ExportFeatureSet fs;
+        int32_t st = export_feature_set(feature_set, fs);
+        if (st) return st;
+        TATARA_REQUIRE(fs.ft_in == ft_in, "export: the feature set's ft_in differs from the trainer's");
+        if (factorized) {
+            FeatureSetShape sh;
+            if ((st = feature_set_shape(feature_set, sh))) return st;
+            TATARA_REQUIRE((uint32_t)sh.piece_inputs == pi,
+                           "export: the trainer's piece_inputs differ from the feature set's");
+        }
+        LayerStackHost h;
+        std::vector<float>* dst[8] = {&h.l1_w, &h.l1_b, &h.l1s_w, &h.l1s_b, &h.l2_w, &h.l2_b, &h.l3_w, &h.l3_b};
+        for (int k = 0; k < 8; ++k)
+            if ((st = download(small[k + 1], *dst[k]))) return st;
+        QuantSource src{ft.w, ft_in, ft_out, factorized ? pi : 0u};
+        QuantSource bias{small[0].w, 1, ft_out, 0};
+        return write_layerstack_bin(path, fs, src, bias, l1, l2, nb, h, has_fv != 0, fv, stream);
     }
 
     int32_t sync_forward_weights() override {
@@ -626,6 +651,12 @@ int32_t tatara_trainer_phase_times(TataraTrainer* trainer, double* ms, int32_t n
 int32_t tatara_trainer_sync_forward_weights(TataraTrainer* trainer) {
     TATARA_REQUIRE(trainer, "trainer is null");
     return trainer->t->sync_forward_weights();
+}
+
+int32_t tatara_trainer_export_quantised(TataraTrainer* trainer, const char* path, int32_t feature_set,
+                                        int32_t has_fv_scale, int32_t fv_scale) {
+    TATARA_REQUIRE(trainer && path, "null argument");
+    return trainer->t->export_quantised(path, feature_set, has_fv_scale, fv_scale);
 }
 
 }  // extern "C"

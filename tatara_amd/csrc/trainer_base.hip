@@ -72,6 +72,15 @@ int32_t TrainerBase::upload(float* dst, const std::vector<float>& src) {
     return kOk;
 }
 
+int32_t TrainerBase::download(const ParamGroup& g, std::vector<float>& out) {
+    out.resize(g.n);
+    if (g.n == 0) return kOk;
+    TATARA_HIP(hipMemcpyAsync(out.data(), g.w, g.n * sizeof(float), hipMemcpyDeviceToHost, stream),
+               "download weights");
+    TATARA_HIP(hipStreamSynchronize(stream), "download weights");
+    return kOk;
+}
+
 int32_t TrainerBase::stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_bucket,
                                  uint32_t multiple, uint32_t max_b) {
     TATARA_REQUIRE(bt, "batch is null");

@@ -76,6 +76,10 @@ class TrainerBase {
     virtual const float* activation(const char* name, uint64_t& cap) = 0;
     // Copies the first n elements of an activation to the host (row-major).
     virtual int32_t copy_activation(const char* name, float* host, uint64_t n);
+    // Writes the quantised network of the current weights to `path`
+    // (feature_set: TATARA_FS_*).
+    virtual int32_t export_quantised(const char* path, int32_t feature_set, int32_t has_fv_scale,
+                                     int32_t fv_scale) = 0;
 
     int32_t flush(double* out);
     int32_t prof_collect();
@@ -99,6 +103,8 @@ class TrainerBase {
     int32_t alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx, int kind,
                         bool with_grad);
     int32_t upload(float* dst, const std::vector<float>& src);
+    // Synchronous copy of a group's weights to the host.
+    int32_t download(const ParamGroup& g, std::vector<float>& out);
     // need_bucket: bucket_idx is required; multiple: n_pos must be a multiple of it
     int32_t stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_bucket, uint32_t multiple,
                         uint32_t max_b);

@@ -12,6 +12,8 @@ only.  `Batch` mirrors crates/nnue-train/src/dataloader.rs:355-369 and
 from __future__ import annotations
 
 import ctypes as C
+import math
+import os
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -418,6 +420,36 @@ class _Trainer:
         return {g: {k: self.get(g, k) for k in ("w", "m", "v", "slow")} for g in self.GROUPS}
 
 
+    def _export(self, path, feature_set, fv_scale) -> None:
+        from .dataloader import FEATURE_SETS
+
+        fs = FEATURE_SETS[feature_set] if isinstance(feature_set, str) else int(feature_set)
+        check(self._lib.tatara_trainer_export_quantised(self._h, os.fsencode(path), fs,
+                                                        int(fv_scale is not None), int(fv_scale or 0)))
+
+
+def _round_half_away(x: float) -> int:
+    """Rust f32/f64 `round` of an exactly representable value."""
+    return int(math.floor(x + 0.5)) if x >= 0 else -int(math.floor(-x + 0.5))
+
+
+def simple_fv_scale(scale: float) -> int:
+    """simple_fv_scale (crates/nnue-format/src/simple_weights.rs:90-95):
+    round((127 * 64) as f32 / scale) in f32."""
+    return _round_half_away(float(np.float32(127 * 64) / np.float32(scale)))
+
+
+def layerstack_export_fv_scale(override, loss, score_scale: float):
+    """layerstack_export_fv_scale (bins/nnue_train/src/training.rs:72-86): the
+    override, else round(8128 / score_scale) in f32 for the sigmoid loss, else
+    None (WRM)."""
+    if override is not None:
+        return int(override)
+    if isinstance(loss, Sigmoid):
+        return _round_half_away(float(np.float32(127 * 64) / np.float32(score_scale)))
+    return None
+
+
 class LayerStackTrainer(_Trainer):
     """TrainerBackend for the LayerStack architecture on one MI355X."""
 
@@ -425,6 +457,11 @@ class LayerStackTrainer(_Trainer):
 
     def __init__(self, config: LayerStackConfig):
         super().__init__(config)
+
+    def save_quantised(self, path, feature_set, fv_scale=None) -> None:
+        """LayerStackWeights::save_quantised of the current weights (OutputFormat::Tatara);
+        fv_scale None omits the arch string's fv_scale token."""
+        self._export(path, feature_set, fv_scale)
 
 
 class SimpleTrainer(_Trainer):
@@ -440,3 +477,10 @@ class SimpleTrainer(_Trainer):
 
     def validate_step(self, batch, wdl_lambda: float = 0.0, loss=None):
         return super().validate_step(batch, None, wdl_lambda, Wrm() if loss is None else loss)
+
+    def save_quantised(self, path, feature_set, fv_scale: int) -> None:
+        """SimpleWeights::save_quantised (CReLU) of the current weights; fv_scale is
+        simple_fv_scale(scale) in the reference trainer."""
+        if fv_scale is None:
+            raise ValueError("the Simple format always carries fv_scale")
+        self._export(path, feature_set, int(fv_scale))
