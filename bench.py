@@ -148,6 +148,50 @@ def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:
     }
 
 
+def time_export(t, w: dict, spec: dict, args) -> dict:
+    """Times the quantised export (LayerStackWeights / SimpleWeights::save_quantised)
+    of the trainer's current weights to a temporary file: GPU quantisation, D2H of
+    the quantised stream and the file write, end to end.  With the CPU baseline,
+    the oracle exporter (one thread, from host f32 weights already downloaded)
+    writes the same file and the bytes are compared."""
+    import tempfile
+
+    fv = 28
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "net.bin")
+        times = []
+        for _ in range(args.export_reps):
+            t0 = time.perf_counter()
+            t.save_quantised(path, w["spec"], fv_scale=fv)
+            times.append(time.perf_counter() - t0)
+        with open(path, "rb") as f:
+            got = f.read()
+    out = {"ms_min": round(1e3 * min(times), 2), "ms_median": round(1e3 * float(np.median(times)), 2),
+           "bytes": len(got), "reps": args.export_reps, "format": w["arch"]}
+    if not args.no_cpu_baseline:
+        from oracle import export as ox
+
+        weights = {g: t.get(g) for g in t.GROUPS}
+        t0 = time.perf_counter()
+        weights["ft_w"] = ox.coalesce(weights["ft_w"], spec["ft_in"], spec["piece_inputs"], w["ft_out"])
+        from tatara_amd.dataloader import FEATURE_SETS, feature_set_info
+
+        fs = FEATURE_SETS[w["spec"]]
+        fh = feature_set_info(w["spec"])["feature_hash"]
+        if w["arch"] == "layerstack":
+            want = ox.ls_save_quantised(fs, fh, spec["ft_in"], w["ft_out"], w["l1"], w["l2"], w["nb"], weights,
+                                        fv_scale=fv)
+        else:
+            weights["l1_w"] = weights["l1_w"].reshape(2 * w["ft_out"], w["l1"]).T.copy()
+            weights["l2_w"] = weights["l2_w"].reshape(w["l1"], w["l2"]).T.copy()
+            want = ox.simple_save_quantised(fs, fh, spec["ft_in"], w["ft_out"], w["l1"], w["l2"], weights,
+                                            fv_scale=fv)
+        out["cpu_oracle_ms"] = round(1e3 * (time.perf_counter() - t0), 1)
+        out["cpu_oracle_threads"] = 1
+        out["identical_to_oracle"] = got == want
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +203,8 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
+    ap.add_argument("--export-reps", type=int, default=0,
+                    help="also time this many quantised exports (.bin) of the trained weights")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -247,6 +293,7 @@ def main() -> int:
         phases, nprof = t.phase_times()
         t.set_profiling(False)
         step_count = t.step_count
+        export = time_export(t, w, spec, args) if args.export_reps > 0 else None
     phase_avg = {k: v / max(nprof, 1) for k, v in phases.items()}
     log("phases (ms/step): " + ", ".join(f"{k} {v:.3f}" for k, v in phase_avg.items()))
 
@@ -319,6 +366,8 @@ def main() -> int:
         "psv_decode_ms_per_batch": round(decode_ms, 3),
         "cpu_baseline": cpu,
     }
+    if export is not None:
+        line["export"] = export
     print(json.dumps(line), flush=True)
     return 0
 

@@ -19,7 +19,9 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <limits>
 
 #include "common.hpp"
@@ -31,20 +33,77 @@ namespace tatara {
 namespace {
 
 constexpr int kQThreads = 256;
-constexpr int kQSteps = 16;
-constexpr uint64_t kQTile = (uint64_t)kQThreads * kQSteps;  // values per workgroup
+constexpr int kQVec = 4;    // consecutive values per thread per step (one float4)
+constexpr int kQSteps = 4;  // steps per tile
+constexpr uint64_t kQStep = (uint64_t)kQThreads * kQVec;           // values per step
+constexpr uint64_t kQTile = kQStep * kQSteps;                      // values per workgroup
 constexpr int kScanThreads = 1024;
+
+// Row, column and virtual-row index of cell i.  32-bit division whenever the
+// table has < 2^32 cells (every feature set at every supported width).
+__device__ __forceinline__ uint64_t virtual_offset(const QuantSource& s, uint64_t i) {
+    uint64_t c, p;
+    if (s.rows * s.cols < (1ull << 32)) {
+        const uint32_t i32 = (uint32_t)i;
+        const uint32_t r32 = i32 / s.cols;
+        c = i32 - r32 * s.cols;
+        p = r32 % s.piece_inputs;
+    } else {
+        const uint64_t r = i / s.cols;
+        c = i - r * s.cols;
+        p = r % s.piece_inputs;
+    }
+    return (s.rows + p) * s.cols + c;
+}
 
 // Cell i of the export-shape table: the real row's value plus, with a
 // factorizer, its piece's virtual row (an f32 add, as the fold does).
 __device__ __forceinline__ float source_value(const QuantSource& s, uint64_t i) {
     float v = s.w[i];
-    if (s.piece_inputs) {
-        const uint64_t r = i / s.cols;
-        const uint64_t c = i - r * s.cols;
-        v += s.w[(s.rows + r % s.piece_inputs) * s.cols + c];
-    }
+    if (s.piece_inputs) v += s.w[virtual_offset(s, i)];
     return v;
+}
+
+// The tile's values held by this thread: x[k][j] is cell
+// base + k * kQStep + kQVec * threadIdx.x + j; cells past n are 0 (and
+// counted as absent by the callers).  Full tiles of a 16-byte aligned table
+// with cols % 4 == 0 take the vector path: every load is issued before any
+// is used, and a float4 never straddles a row.
+__device__ __forceinline__ void load_tile(const QuantSource& s, uint64_t n, uint64_t base,
+                                          float (&x)[kQSteps][kQVec]) {
+    const uint64_t t0 = base + (uint64_t)kQVec * threadIdx.x;
+    const bool vec = base + kQTile <= n && s.cols % kQVec == 0 && ((uintptr_t)s.w & 15) == 0;
+    if (vec) {
+        float4 v[kQSteps];
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) v[k] = *reinterpret_cast<const float4*>(s.w + t0 + k * kQStep);
+        if (s.piece_inputs) {
+            float4 g[kQSteps];
+#pragma unroll
+            for (int k = 0; k < kQSteps; ++k)
+                g[k] = *reinterpret_cast<const float4*>(s.w + virtual_offset(s, t0 + k * kQStep));
+#pragma unroll
+            for (int k = 0; k < kQSteps; ++k) {
+                v[k].x += g[k].x;
+                v[k].y += g[k].y;
+                v[k].z += g[k].z;
+                v[k].w += g[k].w;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) {
+            x[k][0] = v[k].x;
+            x[k][1] = v[k].y;
+            x[k][2] = v[k].z;
+            x[k][3] = v[k].w;
+        }
+        return;
+    }
+    for (int k = 0; k < kQSteps; ++k)
+        for (int j = 0; j < kQVec; ++j) {
+            const uint64_t i = t0 + k * kQStep + j;
+            x[k][j] = i < n ? source_value(s, i) : 0.0f;
+        }
 }
 
 // saturate_i16(round(scale * v)) with NaN -> 0.
@@ -67,16 +126,19 @@ __global__ __launch_bounds__(256) void quantise_i16_kernel(QuantSource s, double
         out[i] = (int16_t)quant16(source_value(s, i), scale);
 }
 
-// Pass 1: bytes of each tile of kQTile values.  Value k*256 + t of a tile is
-// handled by thread t at step k, so every load is coalesced.
+// Pass 1: bytes of each tile of kQTile values.
 __global__ __launch_bounds__(kQThreads) void leb128_tile_bytes_kernel(QuantSource s, double scale, uint64_t n,
                                                                       uint32_t* __restrict__ tile_bytes) {
     const uint64_t base = (uint64_t)blockIdx.x * kQTile;
+    float x[kQSteps][kQVec];
+    load_tile(s, n, base, x);
+    const uint64_t t0 = base + (uint64_t)kQVec * threadIdx.x;
     uint32_t sum = 0;
-    for (int k = 0; k < kQSteps; ++k) {
-        const uint64_t i = base + (uint64_t)k * kQThreads + threadIdx.x;
-        if (i < n) sum += leb128_len(quant16(source_value(s, i), scale));
-    }
+#pragma unroll
+    for (int k = 0; k < kQSteps; ++k)
+#pragma unroll
+        for (int j = 0; j < kQVec; ++j)
+            if (t0 + k * kQStep + j < n) sum += leb128_len(quant16(x[k][j], scale));
     using Reduce = hipcub::BlockReduce<uint32_t, kQThreads>;
     __shared__ typename Reduce::TempStorage tmp;
     const uint32_t total = Reduce(tmp).Sum(sum);
@@ -105,35 +167,45 @@ __global__ __launch_bounds__(kScanThreads) void leb128_tile_scan_kernel(const ui
     if (threadIdx.x == 0) *total = agg;
 }
 
-// Pass 3: each tile re-quantises its values in order (step-major, as pass 1)
-// and writes their LEB128 bytes at the tile offset plus the in-tile prefix.
+// Pass 3: each tile re-quantises its values and writes their LEB128 bytes in
+// cell order: step by step, thread t's four cells follow threads 0..t-1's.
 __global__ __launch_bounds__(kQThreads) void leb128_scatter_kernel(QuantSource s, double scale, uint64_t n,
                                                                    const uint64_t* __restrict__ tile_off,
                                                                    uint8_t* __restrict__ out) {
     using Scan = hipcub::BlockScan<uint32_t, kQThreads>;
     __shared__ typename Scan::TempStorage tmp;
-    uint64_t off = tile_off[blockIdx.x];
     const uint64_t base = (uint64_t)blockIdx.x * kQTile;
+    float x[kQSteps][kQVec];
+    load_tile(s, n, base, x);
+    const uint64_t t0 = base + (uint64_t)kQVec * threadIdx.x;
+    uint64_t off = tile_off[blockIdx.x];
     for (int k = 0; k < kQSteps; ++k) {
-        const uint64_t i = base + (uint64_t)k * kQThreads + threadIdx.x;
-        int32_t q = 0;
+        int32_t q[kQVec];
         uint32_t len = 0;
-        if (i < n) {
-            q = quant16(source_value(s, i), scale);
-            len = leb128_len(q);
+#pragma unroll
+        for (int j = 0; j < kQVec; ++j) {
+            q[j] = quant16(x[k][j], scale);
+            if (t0 + k * kQStep + j < n) len += leb128_len(q[j]);
         }
         uint32_t excl, agg;
         Scan(tmp).ExclusiveSum(len, excl, agg);
         uint8_t* p = out + off + excl;
-        if (len == 1) {
-            p[0] = (uint8_t)(q & 0x7f);
-        } else if (len == 2) {
-            p[0] = (uint8_t)((q & 0x7f) | 0x80);
-            p[1] = (uint8_t)((q >> 7) & 0x7f);
-        } else if (len == 3) {
-            p[0] = (uint8_t)((q & 0x7f) | 0x80);
-            p[1] = (uint8_t)(((q >> 7) & 0x7f) | 0x80);
-            p[2] = (uint8_t)((q >> 14) & 0x7f);
+#pragma unroll
+        for (int j = 0; j < kQVec; ++j) {
+            if (t0 + k * kQStep + j >= n) break;
+            const int32_t v = q[j];
+            const uint32_t l = leb128_len(v);
+            if (l == 1) {
+                p[0] = (uint8_t)(v & 0x7f);
+            } else if (l == 2) {
+                p[0] = (uint8_t)((v & 0x7f) | 0x80);
+                p[1] = (uint8_t)((v >> 7) & 0x7f);
+            } else {
+                p[0] = (uint8_t)((v & 0x7f) | 0x80);
+                p[1] = (uint8_t)(((v >> 7) & 0x7f) | 0x80);
+                p[2] = (uint8_t)((v >> 14) & 0x7f);
+            }
+            p += l;
         }
         off += agg;
         __syncthreads();  // the scan's temp storage is reused by the next step
@@ -205,16 +277,23 @@ uint32_t layer_hash_chain(uint32_t slice, uint64_t out0, uint64_t out1) {
 
 std::string u(uint64_t v) { return std::to_string(v); }
 
-int32_t write_file(const char* path, const std::vector<uint8_t>& b) {
+struct Segment {
+    const void* p;
+    size_t n;
+};
+
+int32_t write_file(const char* path, std::initializer_list<Segment> parts) {
     TATARA_REQUIRE(path && *path, "export path is empty");
     FILE* f = std::fopen(path, "wb");
     if (!f) {
         set_error(std::string("export: cannot open ") + path + " for writing");
         return kErrInvalid;
     }
-    const size_t n = std::fwrite(b.data(), 1, b.size(), f);
-    const int closed = std::fclose(f);
-    if (n != b.size() || closed != 0) {
+    bool ok = true;
+    for (const Segment& g : parts)
+        if (g.n && std::fwrite(g.p, 1, g.n, f) != g.n) ok = false;
+    if (std::fclose(f) != 0) ok = false;
+    if (!ok) {
         set_error(std::string("export: write to ") + path + " failed");
         return kErrInvalid;
     }
@@ -252,15 +331,28 @@ int32_t launch_quantise_leb128(const QuantSource& s, double scale, uint32_t* til
     return kOk;
 }
 
-int32_t quantise_i16_to_host(const QuantSource& s, double scale, std::vector<int16_t>& out, hipStream_t stream) {
+HostBytes::~HostBytes() { std::free(p); }
+
+int32_t HostBytes::alloc(size_t bytes) {
+    std::free(p);
+    p = nullptr;
+    n = bytes;
+    if (bytes && !(p = static_cast<uint8_t*>(std::malloc(bytes)))) {
+        set_error("export: host allocation failed");
+        return kErrOutOfMemory;
+    }
+    return kOk;
+}
+
+int32_t quantise_i16_to_host(const QuantSource& s, double scale, HostBytes& out, hipStream_t stream) {
     const uint64_t n = s.rows * s.cols;
-    out.assign(n, 0);
-    if (n == 0) return kOk;
+    int32_t st = out.alloc(n * sizeof(int16_t));
+    if (st || n == 0) return st;
     int16_t* d = nullptr;
     TATARA_HIP(hipMalloc(&d, n * sizeof(int16_t)), "hipMalloc export i16");
-    int32_t st = launch_quantise_i16(s, scale, d, stream);
+    st = launch_quantise_i16(s, scale, d, stream);
     hipError_t e = hipSuccess;
-    if (st == kOk) e = hipMemcpyAsync(out.data(), d, n * sizeof(int16_t), hipMemcpyDeviceToHost, stream);
+    if (st == kOk) e = hipMemcpyAsync(out.p, d, n * sizeof(int16_t), hipMemcpyDeviceToHost, stream);
     if (st == kOk && e == hipSuccess) e = hipStreamSynchronize(stream);
     (void)hipFree(d);
     if (st) return st;
@@ -268,34 +360,29 @@ int32_t quantise_i16_to_host(const QuantSource& s, double scale, std::vector<int
     return kOk;
 }
 
-int32_t quantise_leb128_to_host(const QuantSource& s, double scale, std::vector<uint8_t>& out,
-                                hipStream_t stream) {
+int32_t quantise_leb128_to_host(const QuantSource& s, double scale, HostBytes& out, hipStream_t stream) {
     const uint64_t n = s.rows * s.cols;
     const uint64_t tiles = leb128_tiles(n);
     uint32_t* tile_bytes = nullptr;
-    uint64_t *tile_off = nullptr, *total = nullptr;
+    uint64_t* tile_off = nullptr;  // tile offsets, then the total in the last slot
     uint8_t* d = nullptr;
-    const size_t tb = (tiles ? tiles : 1) * sizeof(uint32_t), to = (tiles ? tiles : 1) * sizeof(uint64_t);
     int32_t st = kOk;
-    hipError_t e = hipMalloc(&tile_bytes, tb);
-    if (e == hipSuccess) e = hipMalloc(&tile_off, to);
-    if (e == hipSuccess) e = hipMalloc(&total, sizeof(uint64_t));
+    hipError_t e = hipMalloc(&tile_bytes, (tiles + 1) * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&tile_off, (tiles + 1) * sizeof(uint64_t));
     uint64_t bytes = 0;
-    if (e == hipSuccess) st = launch_quantise_leb128(s, scale, tile_bytes, tile_off, total, nullptr, stream);
-    if (e == hipSuccess && st == kOk) e = hipMemcpyAsync(&bytes, total, sizeof bytes, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) st = launch_quantise_leb128(s, scale, tile_bytes, tile_off, tile_off + tiles, nullptr, stream);
+    if (e == hipSuccess && st == kOk)
+        e = hipMemcpyAsync(&bytes, tile_off + tiles, sizeof bytes, hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess && st == kOk) e = hipStreamSynchronize(stream);
+    if (e == hipSuccess && st == kOk) st = out.alloc(bytes);
     if (e == hipSuccess && st == kOk && bytes) e = hipMalloc(&d, bytes);
     if (e == hipSuccess && st == kOk && bytes) {
         leb128_scatter_kernel<<<(uint32_t)tiles, kQThreads, 0, stream>>>(s, scale, n, tile_off, d);
         e = hipGetLastError();
-        out.resize(bytes);
-        if (e == hipSuccess) e = hipMemcpyAsync(out.data(), d, bytes, hipMemcpyDeviceToHost, stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(out.p, d, bytes, hipMemcpyDeviceToHost, stream);
         if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    } else {
-        out.clear();
     }
     (void)hipFree(d);
-    (void)hipFree(total);
     (void)hipFree(tile_off);
     (void)hipFree(tile_bytes);
     if (st) return st;
@@ -338,23 +425,25 @@ int32_t write_layerstack_bin(const char* path, const ExportFeatureSet& fs, const
                        ")])))))";
     if (has_fv) arch += ",fv_scale=" + std::to_string(fv);
 
-    std::vector<uint8_t> bias_stream, weight_stream;
+    HostBytes bias_stream, weight_stream;
     int32_t st;
     if ((st = quantise_leb128_to_host(ft_b, 127.0, bias_stream, stream))) return st;
     if ((st = quantise_leb128_to_host(ft, 127.0, weight_stream, stream))) return st;
 
-    Bytes w;
-    w.b.reserve(weight_stream.size() + 4096 + (size_t)nb * l1_out * (ft_out + 64));
-    w.u32(0x7AF32F21u);  // NNUE_VERSION
-    w.u32(fc_hash ^ ft_hash);
-    w.str(arch);
-    w.u32(nb);
-    w.u32(ft_hash);
-    for (const std::vector<uint8_t>* s : {&bias_stream, &weight_stream}) {
-        w.raw("COMPRESSED_LEB128", 17);
-        w.u32((uint32_t)s->size());
-        w.raw(s->data(), s->size());
-    }
+    // head: header, FT bias block, FT weight block prefix; the weight stream
+    // itself is written straight from its staging buffer
+    Bytes head, w;
+    head.u32(0x7AF32F21u);  // NNUE_VERSION
+    head.u32(fc_hash ^ ft_hash);
+    head.str(arch);
+    head.u32(nb);
+    head.u32(ft_hash);
+    head.raw("COMPRESSED_LEB128", 17);
+    head.u32((uint32_t)bias_stream.n);
+    head.raw(bias_stream.p, bias_stream.n);
+    head.raw("COMPRESSED_LEB128", 17);
+    head.u32((uint32_t)weight_stream.n);
+    w.b.reserve((size_t)nb * (l1_out * (ft_out + 64) + 4096));
     const uint64_t pin1 = (ft_out + 31) / 32 * 32, pin2 = (l2_in + 31) / 32 * 32, pin3 = (l2_out + 31) / 32 * 32;
     for (uint64_t b = 0; b < nb; ++b) {
         w.u32(fc_hash);
@@ -380,7 +469,7 @@ int32_t write_layerstack_bin(const char* path, const ExportFeatureSet& fs, const
         for (uint64_t i = 0; i < pin3; ++i)
             w.u8((uint8_t)(i < l2_out ? ls_i8(64.0 * (double)h.l3_w[b * l2_out + i]) : 0));
     }
-    return write_file(path, w.b);
+    return write_file(path, {{head.b.data(), head.b.size()}, {weight_stream.p, weight_stream.n}, {w.b.data(), w.b.size()}});
 }
 
 int32_t write_simple_bin(const char* path, const ExportFeatureSet& fs, const QuantSource& ft,
@@ -403,19 +492,17 @@ int32_t write_simple_bin(const char* path, const ExportFeatureSet& fs, const Qua
                              u(l1_out) + "](AffineTransformSparseInput[" + u(l1_out) + "<-" + L + "](InputSlice[" +
                              L + "(0:" + L + ")])))))" + ",fv_scale=" + std::to_string(fv);
 
-    std::vector<int16_t> qb, qw;
+    HostBytes qb, qw;
     int32_t st;
     if ((st = quantise_i16_to_host(ft_b, 127.0, qb, stream))) return st;
     if ((st = quantise_i16_to_host(ft, 127.0, qw, stream))) return st;
 
-    Bytes w;
-    w.b.reserve(2 * (qw.size() + qb.size()) + 8192 + l1_out * (l1_in + 32));
-    w.u32(0x7AF32F16u);  // NNUE_VERSION (YaneuraOu kVersion)
-    w.u32(fc_hash ^ ft_hash);
-    w.str(arch);
-    w.u32(ft_hash);
-    w.raw(qb.data(), qb.size() * sizeof(int16_t));  // little-endian host
-    w.raw(qw.data(), qw.size() * sizeof(int16_t));
+    Bytes head, w;
+    head.u32(0x7AF32F16u);  // NNUE_VERSION (YaneuraOu kVersion)
+    head.u32(fc_hash ^ ft_hash);
+    head.str(arch);
+    head.u32(ft_hash);
+    w.b.reserve(8192 + l1_out * (l1_in + 32));
     w.u32(fc_hash);
     const double bs = 127.0 * 64.0, ws = 64.0;
     auto pad = [](uint64_t x) { return (x + 31) / 32 * 32; };
@@ -431,7 +518,8 @@ int32_t write_simple_bin(const char* path, const ExportFeatureSet& fs, const Qua
     w.i32(simple_q<int32_t>(bs * (double)h.l3_b[0]));
     for (uint64_t i = 0; i < pad(l2_out); ++i)
         w.u8((uint8_t)(i < l2_out ? simple_q<int8_t>(ws * (double)h.l3_w[i]) : 0));
-    return write_file(path, w.b);
+    // the i16 blocks are little-endian host order, written from the staging buffers
+    return write_file(path, {{head.b.data(), head.b.size()}, {qb.p, qb.n}, {qw.p, qw.n}, {w.b.data(), w.b.size()}});
 }
 
 }  // namespace tatara

@@ -34,10 +34,25 @@ int32_t launch_quantise_i16(const QuantSource& s, double scale, int16_t* out, hi
 int32_t launch_quantise_leb128(const QuantSource& s, double scale, uint32_t* tile_bytes, uint64_t* tile_off,
                                uint64_t* d_total, uint8_t* out, hipStream_t stream);
 
-// Host-side wrappers used by the exporters (synchronous on `stream`).
-int32_t quantise_i16_to_host(const QuantSource& s, double scale, std::vector<int16_t>& out, hipStream_t stream);
-int32_t quantise_leb128_to_host(const QuantSource& s, double scale, std::vector<uint8_t>& out,
-                                hipStream_t stream);
+// Uninitialised host bytes, freed on destruction.  Ordinary pageable memory
+// on purpose: the file writer reads these bytes with the CPU, and CPU reads
+// of hipHostMalloc memory are uncached (an fwrite of 113 MB from it took
+// ~90 ms against ~20 ms from pageable memory, more than the faster D2H
+// saves).
+struct HostBytes {
+    uint8_t* p = nullptr;
+    size_t n = 0;
+    HostBytes() = default;
+    HostBytes(const HostBytes&) = delete;
+    HostBytes& operator=(const HostBytes&) = delete;
+    ~HostBytes();
+    int32_t alloc(size_t bytes);
+};
+
+// Host-side wrappers used by the exporters (synchronous on `stream`): the
+// quantised table as little-endian i16, or as its LEB128 stream.
+int32_t quantise_i16_to_host(const QuantSource& s, double scale, HostBytes& out, hipStream_t stream);
+int32_t quantise_leb128_to_host(const QuantSource& s, double scale, HostBytes& out, hipStream_t stream);
 
 // Export identity of a feature set (TATARA_FS_*): arch-string name, feature
 // hash and base FT input rows.
