@@ -43,6 +43,15 @@ WORKLOADS = {
         desc="LayerStack halfka-hm-merged ft-out 1536/16/32 fp32, batch 65536, progress8kpabs "
              "(8 buckets, seeded progress weights ~ N(0, 0.01)), Ranger, sigmoid loss 1/290, "
              "factorizer on (BASELINE configs[3])"),
+    "ls1536_mixed": dict(
+        metric="train pos/s @ batch 65536 (LayerStack ft-1536 --all-optim, 1 GPU); FT gather % HBM peak",
+        arch="layerstack", spec="halfka-hm-merged", ft_out=1536, l1=16, l2=32, nb=8,
+        bucket_mode="progress8kpabs", optimizer="ranger", lr=8.75e-4, ref=3.13e6, ref_src="README.md:41",
+        all_optim=True,
+        desc="LayerStack halfka-hm-merged ft-out 1536/16/32 in mixed precision (the --all-optim FT modes: "
+             "f16 forward table, f16 FT activations and gradients with loss scale 2^14*b, f16 ft_w moments; "
+             "f32 master weights and dense layers), batch 65536, progress8kpabs (8 buckets), Ranger, "
+             "sigmoid loss 1/290, factorizer on (BASELINE configs[4])"),
     "ls768": dict(
         metric="train pos/s @ batch 65536 (LayerStack ft-768, 1 GPU); FT gather % HBM peak",
         arch="layerstack", spec="halfka-hm-merged", ft_out=768, l1=8, l2=32, nb=9,
@@ -81,23 +90,28 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_rows):
+def algorithmic_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_rows, f16=False):
     """Per-launch algorithmic bytes of the two FT kernels, averaged over the batches.
 
-    ft_forward: gathered fp32 rows of both perspectives + the per-perspective
-    sums and combined written (out_rows rows of ft_out floats per position:
+    ft_forward: gathered rows of both perspectives + the per-perspective
+    sums and combined written (out_rows rows of ft_out values per position:
     3 for LayerStack, whose combined is ft_out wide; 4 for Simple, 2*ft_out)
     + index rows + nnz.
-    ft_grad_update: gathered fp32 dft rows (one per occurrence) + occurrence
+    ft_grad_update: gathered dft rows (one per occurrence) + occurrence
     list + w, m, v read and written for every real row (+ slow on the
     lookahead step, 1 in 6) + the row gradient written for the virtual rows.
+    f16 (the --all-optim modes): gathered rows, the two raw sums, the dft and
+    the moments are 2 bytes per value; w, slow, combined and the gradient stay 4.
     """
     nnz_total = np.mean([float(h["nnz"].sum()) for h in host_batches])
     b = host_batches[0]["nnz"].size
-    gather = 2.0 * nnz_total * ft_out * 4
-    fwd = gather + out_rows * b * ft_out * 4 + 2.0 * b * max_active * 4 + 4.0 * b
-    rows = ft_in * ft_out * 4.0
-    grad = gather + 2.0 * nnz_total * 4 + 6.0 * rows + lookahead_frac * 2.0 * rows + rows
+    s16 = 2.0 if f16 else 4.0
+    gather = 2.0 * nnz_total * ft_out * s16
+    outs = (2 * s16 + 4.0 * (out_rows - 2)) * b * ft_out
+    fwd = gather + outs + 2.0 * b * max_active * 4 + 4.0 * b
+    cells = float(ft_in) * ft_out
+    grad = (gather + 2.0 * nnz_total * 4 + cells * (2 * 4.0 + 4 * s16) + lookahead_frac * 2.0 * 4.0 * cells
+            + 4.0 * cells)
     return fwd, grad
 
 
@@ -107,7 +121,7 @@ WRM290 = {"kind": "wrm", "nnue2score": 290.0, "in_scaling": 290.0, "in_offset": 
 SIGMOID = {"kind": "sigmoid", "scale": 1.0 / 290.0}
 
 
-def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:
+def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:  # noqa: C901
     """Oracle (CPU restatement) step on this host, bounded sample of the same workload."""
     from oracle import ffi
 
@@ -122,10 +136,13 @@ def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:
 
         sh = ols.LsShape(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
                          ft_out=w["ft_out"], l1=w["l1"], l2=w["l2"], nb=w["nb"])
+        prec = ols.Precision.all_optim() if w.get("all_optim") else ols.Precision()
         st = ols.default_init(sh)
+        if prec.fp16_opt_state:
+            st = ols.to_f16_state(st)
         opt = ols.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
         t0 = time.perf_counter()
-        ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, 1)
+        ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, 1, prec)
         dt = time.perf_counter() - t0
     else:
         from oracle import simple as osi
@@ -145,6 +162,62 @@ def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:
         "kind": "port",
         "sample": f"1 full oracle step (fwd+bwd+{w['optimizer']} over all {n_ft / 1e6:.1f}M FT params) "
                   f"at b={n} of the same workload, {dt:.1f} s",
+    }
+
+
+def quantised_view(t) -> dict:
+    """The integer values save_quantised would write (layerstack_weights.rs:568-829),
+    computed from the trainer's f32 weights: FT i16 = round(127 w) with the
+    factorizer folded in, L1 (bucket + shared) i8 = round(64 w).  Rounding is
+    half away from zero, as Rust's f64::round."""
+    def rnd(x):
+        x = np.asarray(x, np.float64)
+        return np.sign(x) * np.floor(np.abs(x) + 0.5)
+
+    cfg = t.config
+    ft = t.get("ft_w").reshape(-1, cfg.ft_out)
+    real = ft[: cfg.ft_in].copy()
+    if cfg.piece_inputs:
+        real += np.tile(ft[cfg.ft_in:], (cfg.ft_in // cfg.piece_inputs, 1))
+    l1 = t.get("l1_w").reshape(cfg.num_buckets, cfg.l1_out, cfg.ft_out)
+    l1s = t.get("l1_shared_weight").reshape(cfg.ft_out, cfg.l1_out)
+    merged = (l1 + l1s.T[None]).astype(np.float32)
+    return {"ft_i16": np.clip(rnd(127.0 * real), -32768, 32767),
+            "l1_i8": np.clip(rnd(64.0 * merged), -128, 127)}
+
+
+def drift_report(w: dict, spec: dict, dev: list, b: int, steps_per_sb: int) -> dict:
+    """f32 vs mixed precision over 8 superbatches from the same initial weights and batches."""
+    from tatara_amd.trainer import LayerStackConfig, LayerStackTrainer, Sigmoid
+
+    base = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
+                            ft_out=w["ft_out"], l1_out=w["l1"], l2_out=w["l2"], num_buckets=w["nb"], max_batch=b,
+                            optimizer=w["optimizer"], weight_decay=0.01)
+    loss = Sigmoid(1.0 / 290.0)
+    curves, views = {}, {}
+    for name, cfg in (("f32", base), ("mixed", base.all_optim())):
+        with LayerStackTrainer(cfg) as t:
+            # train_step returns the previous step's loss; the flush returns the last
+            per_step = [t.train_step(dev[i % len(dev)], None, w["lr"], 0.0, loss) for i in range(8 * steps_per_sb)]
+            per_step = per_step[1:] + [t.flush_pending_loss()]
+            sb_loss = [float(np.sum(per_step[k * steps_per_sb:(k + 1) * steps_per_sb])) / (steps_per_sb * b)
+                       for k in range(8)]
+            views[name] = quantised_view(t)
+            if name == "mixed":
+                clamps, elems = t.fp16_clamp_count()
+        curves[name] = sb_loss
+    ft_diff = np.abs(views["f32"]["ft_i16"] - views["mixed"]["ft_i16"])
+    l1_diff = np.abs(views["f32"]["l1_i8"] - views["mixed"]["l1_i8"])
+    rel = [abs(m - f) / f for f, m in zip(curves["f32"], curves["mixed"]) if f]
+    return {
+        "superbatches": 8, "steps_per_superbatch": steps_per_sb, "positions_per_superbatch": steps_per_sb * b,
+        "loss_f32": [round(x, 6) for x in curves["f32"]], "loss_mixed": [round(x, 6) for x in curves["mixed"]],
+        "loss_rel_diff_max": round(max(rel), 6),
+        "ft_i16_differing_frac": float(np.count_nonzero(ft_diff)) / ft_diff.size,
+        "ft_i16_max_abs_diff": int(ft_diff.max()),
+        "l1_i8_differing_frac": float(np.count_nonzero(l1_diff)) / l1_diff.size,
+        "l1_i8_max_abs_diff": int(l1_diff.max()),
+        "dft_clamps": int(clamps), "dft_values_written": int(elems),
     }
 
 
@@ -203,6 +276,10 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
+    ap.add_argument("--drift", type=int, default=0, metavar="STEPS_PER_SUPERBATCH",
+                    help="mixed-precision workloads: train the f32 and the mixed trainer from the same "
+                         "initial weights over 8 superbatches of this many steps and report the loss "
+                         "curves and the drift of the quantised net")
     ap.add_argument("--export-reps", type=int, default=0,
                     help="also time this many quantised exports (.bin) of the trained weights")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -257,6 +334,8 @@ def main() -> int:
                                piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
                                l2_out=w["l2"], num_buckets=w["nb"], max_batch=b,
                                optimizer=w["optimizer"], weight_decay=0.01)
+        if w.get("all_optim"):
+            cfg = cfg.all_optim()
         trainer = LayerStackTrainer(cfg)
         loss = Sigmoid(1.0 / 290.0)
         step = lambda t, db: t.train_step(db, None, lr, 0.0, loss)  # noqa: E731
@@ -295,12 +374,17 @@ def main() -> int:
         step_count = t.step_count
         export = time_export(t, w, spec, args) if args.export_reps > 0 else None
     phase_avg = {k: v / max(nprof, 1) for k, v in phases.items()}
+    drift = None
+    if args.drift and w.get("all_optim"):
+        log(f"drift: f32 vs mixed, 8 superbatches of {args.drift} steps")
+        drift = drift_report(w, spec, dev, b, args.drift)
     log("phases (ms/step): " + ", ".join(f"{k} {v:.3f}" for k, v in phase_avg.items()))
 
     la = 1.0 / 6.0 if w["optimizer"] == "ranger" else 0.0
     fwd_bytes, grad_bytes = algorithmic_bytes(host_batches, w["ft_out"], spec["ft_in"], spec["max_active"],
                                               lookahead_frac=la,
-                                              out_rows=3 if w["arch"] == "layerstack" else 4)
+                                              out_rows=3 if w["arch"] == "layerstack" else 4,
+                                              f16=bool(w.get("all_optim")))
     kernels = {
         "ft_forward_kernel": (phase_avg["ft_forward"], fwd_bytes),
         "ft_grad_update_kernel": (phase_avg["ft_grad_update"], grad_bytes),
@@ -349,7 +433,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(pos_s / w["ref"], 4),
-        "dtype": "f32",
+        "dtype": "f16+f32" if w.get("all_optim") else "f32",
         "data": f"synthetic: seeded PSV positions (40 pieces, 15% in hand, 10% promoted), decoded to "
                 f"{w['spec']} indices and {w['bucket_mode']} buckets on the GPU, resident in HBM",
         "config": {
@@ -368,6 +452,8 @@ def main() -> int:
     }
     if export is not None:
         line["export"] = export
+    if drift is not None:
+        line["drift_vs_f32"] = drift
     print(json.dumps(line), flush=True)
     return 0
 

@@ -199,6 +199,15 @@ typedef struct TataraTrainerConfig {
     float ft_weight_decay, dense_weight_decay, bias_weight_decay;
     float ft_lr_mult, dense_lr_mult, bias_lr_mult;
     int32_t keep_grads;    /* debug: keep every gradient after the step */
+    /* Mixed precision, PrecisionFlags (bins/nnue_train/src/trainer_common.rs:
+     * 49-61; --all-optim sets all three).  LayerStack only; all 0 is the fp32
+     * path.  ft_fp16: the FT forward reads an f16 table (the factorized comb,
+     * or an f16 mirror of the weights), f32 accumulation.  ft_fp16_out (needs
+     * ft_fp16): FT raw sums stored f16, the FT activation gradient stored f16
+     * scaled by 2^14 * batch and clamped to +-65504 (clamps counted).
+     * fp16_opt_state: the ft_w moments stored f16, scaled by 2^28 (m) and
+     * 2^40 (v).  Master weights stay f32. */
+    int32_t ft_fp16, ft_fp16_out, fp16_opt_state;
 } TataraTrainerConfig;
 
 /* LossKind (crates/nnue-train/src/trainer.rs:89-135). */
@@ -258,6 +267,10 @@ TATARA_API int32_t tatara_trainer_validate_step(TataraTrainer* trainer, const Ta
  * ft_in (and piece_inputs with a factorizer).  Synchronous. */
 TATARA_API int32_t tatara_trainer_export_quantised(TataraTrainer* trainer, const char* path, int32_t feature_set,
                                                    int32_t has_fv_scale, int32_t fv_scale);
+/* TrainerBackend::read_fp16_clamp_count (crates/nnue-train/src/trainer.rs:
+ * 362-373): cumulative count of dft values clamped to +-65504 and of dft
+ * values written in the ft_fp16_out path (both 0 without it). */
+TATARA_API int32_t tatara_trainer_fp16_clamp_count(TataraTrainer* trainer, uint64_t* clamps, uint64_t* elems);
 /* Number of optimizer steps taken. */
 TATARA_API int32_t tatara_trainer_step_count(TataraTrainer* trainer, uint64_t* steps);
 /* Parameter groups by reference name ("ft_w", "ft_b", "l1_w", "l1_b",

@@ -88,6 +88,15 @@ def sparse_ft_backward_nnz(grad_out, indices, nnz, grad_weight, batch, rows, col
     return grad_weight
 
 
+def ft_grad_fp16(dft16, indices, nnz, grad_weight, batch, rows, cols, max_active, inv_scale, add):
+    """gather_and_sum_per_feature_{overwrite,add}_fp16 (in place on grad_weight)."""
+    g, idx, n = f32(dft16), i32(indices), i32(nnz)
+    assert grad_weight.dtype == np.float32 and grad_weight.flags.c_contiguous
+    lib().orc_ft_grad_fp16(P(g), P(idx), P(n), P(grad_weight), _I64(batch), _I64(rows), _I64(cols),
+                           _I64(max_active), C.c_float(inv_scale), C.c_int32(int(add)))
+    return grad_weight
+
+
 def ft_fold_virtual(w, ft_in, ft_out, piece_inputs):
     w = f32(w)
     comb = np.zeros(ft_in * ft_out, dtype=np.float32)

@@ -16,6 +16,21 @@ optimizer :4034-4489  RAdam on ft_w then the 9 uniform groups, lookahead
 
 Also provides the default LayerStack initialisation
 (crates/nnue-train/src/init.rs:252-266, trainer_layerstack.rs:844-870).
+
+Precision: the reference's PrecisionFlags (bins/nnue_train/src/
+trainer_common.rs:49-61) place f16 roundings at fixed points of the step; the
+f16 kernels (native_kernels.cu) compute in f32 between them, so the f32 CPU
+functions applied to f16-rounded inputs restate them (the reference's own
+fp16 kernel tests check them that way, gpu_cpu_equivalence_tests.rs:
+2489-2690):
+  ft_fp16         forward table = f16(comb) or f16(weights)
+                  (ft_fold_virtual_f16 / cast_f32_to_f16 / the f16 mirror)
+  ft_fp16_out     FT raw sums = f16(sum); dft = f16(clamp(g * 2^14 b,
+                  +-65504)) (ft_post_perspective_grad_fused_fp16, :2304-2352);
+                  FT weight gradient from the f16 dft x 1/(2^14 b)
+                  (gather_and_sum_per_feature_*_fp16, :1030-1100)
+  fp16_opt_state  ft_w moments stored f16(m 2^28), f16(v 2^40) and read back
+                  divided by the scale (radam_step_f16state, :1118-1170)
 """
 from __future__ import annotations
 
@@ -49,6 +64,40 @@ UNIFORM_GROUPS = (
     ("l3_w", "dense", True),
     ("l3_b", "bias", False),
 )
+
+
+F16_MAX = np.float32(65504.0)
+DFT_BASE_SCALE = np.float32(16384.0)       # FT_DFT_FP16_BASE_SCALE (arch.rs)
+M_SCALE = np.float32(2.0 ** 28)            # FT_OPT_M_SCALE
+V_SCALE = np.float32(2.0 ** 40)            # FT_OPT_V_SCALE
+
+
+@dataclass
+class Precision:
+    ft_fp16: bool = False
+    ft_fp16_out: bool = False
+    fp16_opt_state: bool = False
+
+    @classmethod
+    def all_optim(cls):
+        return cls(True, True, True)
+
+
+FP32 = Precision()
+
+
+def f16(x) -> np.ndarray:
+    """Round to f16 (nearest even, overflow to inf) and widen back to f32."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def to_f16_state(st: dict) -> dict:
+    """ft_w moments as stored with fp16_opt_state: f16(m 2^28), f16(v 2^40), as f32 values."""
+    ft = st["ft_w"]
+    ft["m16"] = f16(np.clip(ft["m"] * M_SCALE, -F16_MAX, F16_MAX))
+    ft["v16"] = f16(np.minimum(ft["v"] * V_SCALE, F16_MAX))
+    return st
 
 
 @dataclass
@@ -135,7 +184,7 @@ class OptConfig:
         return ffi.radam_step_size_denom(step, self.beta1, BETA2, N_SMA_THRESHOLD)
 
 
-def forward(sh: LsShape, st: dict, batch: dict, wdl_lambda: float, loss: dict):
+def forward(sh: LsShape, st: dict, batch: dict, wdl_lambda: float, loss: dict, prec: Precision = FP32):
     """Forward + loss.  Returns (intermediates, loss_acc)."""
     b = batch["stm"].shape[0]
     ma = sh.max_active
@@ -144,9 +193,13 @@ def forward(sh: LsShape, st: dict, batch: dict, wdl_lambda: float, loss: dict):
         w_fwd = ffi.ft_fold_virtual(ft_w, sh.ft_in, sh.ft_out, sh.piece_inputs)
     else:
         w_fwd = ft_w[: sh.ft_in * sh.ft_out]
+    if prec.ft_fp16:
+        w_fwd = f16(w_fwd)
     a = {}
     a["ft_stm"] = ffi.sparse_ft_forward(w_fwd, batch["stm"], batch["nnz"], b, sh.ft_out, sh.ft_in, ma)
     a["ft_nstm"] = ffi.sparse_ft_forward(w_fwd, batch["nstm"], batch["nnz"], b, sh.ft_out, sh.ft_in, ma)
+    if prec.ft_fp16_out:
+        a["ft_stm"], a["ft_nstm"] = f16(a["ft_stm"]), f16(a["ft_nstm"])
     a["combined"] = ffi.ft_post_perspective_fwd(a["ft_stm"], a["ft_nstm"], st["ft_b"]["w"], b,
                                                 sh.ft_out, FT_POST_SCALE)
     bk = batch["bucket"]
@@ -179,7 +232,7 @@ def forward(sh: LsShape, st: dict, batch: dict, wdl_lambda: float, loss: dict):
     return a, acc
 
 
-def backward(sh: LsShape, st: dict, batch: dict, a: dict) -> dict:
+def backward(sh: LsShape, st: dict, batch: dict, a: dict, prec: Precision = FP32) -> dict:
     """Gradients of every group (the reference grad buffers after backward)."""
     b = batch["stm"].shape[0]
     bk = batch["bucket"]
@@ -216,17 +269,32 @@ def backward(sh: LsShape, st: dict, batch: dict, a: dict) -> dict:
                                                  sh.ft_out, sh.ft_out // 2, sh.ft_out, FT_POST_SCALE)
     g["ft_b"] = ft_b_grad
     ft_grad = np.zeros(s["ft_w"], np.float32)
-    ffi.sparse_ft_backward_nnz(a["dft_stm"], batch["stm"], batch["nnz"], ft_grad, b, sh.ft_out,
-                               sh.ft_in, sh.max_active)
-    ffi.sparse_ft_backward_nnz(a["dft_nstm"], batch["nstm"], batch["nnz"], ft_grad, b, sh.ft_out,
-                               sh.ft_in, sh.max_active)
+    if prec.ft_fp16_out:
+        scale = DFT_BASE_SCALE * np.float32(b)
+        inv = np.float32(1.0) / scale
+        a["dft_scale"] = scale
+        a["clamps"] = 0
+        for k in ("dft_stm", "dft_nstm"):
+            scaled = a[k] * scale
+            a["clamps"] += int(np.count_nonzero(np.abs(scaled) > F16_MAX))
+            a[k + "16"] = f16(np.clip(scaled, -F16_MAX, F16_MAX))
+        ffi.ft_grad_fp16(a["dft_stm16"], batch["stm"], batch["nnz"], ft_grad, b, sh.ft_out, sh.ft_in,
+                         sh.max_active, inv, add=False)
+        ffi.ft_grad_fp16(a["dft_nstm16"], batch["nstm"], batch["nnz"], ft_grad, b, sh.ft_out, sh.ft_in,
+                         sh.max_active, inv, add=True)
+    else:
+        ffi.sparse_ft_backward_nnz(a["dft_stm"], batch["stm"], batch["nnz"], ft_grad, b, sh.ft_out,
+                                   sh.ft_in, sh.max_active)
+        ffi.sparse_ft_backward_nnz(a["dft_nstm"], batch["nstm"], batch["nnz"], ft_grad, b, sh.ft_out,
+                                   sh.ft_in, sh.max_active)
     if sh.piece_inputs:
         ffi.ft_reduce_virtual_grad(ft_grad, sh.ft_in, sh.ft_out, sh.piece_inputs)
     g["ft_w"] = ft_grad
     return g
 
 
-def optimizer_step(sh: LsShape, st: dict, grads: dict, opt: OptConfig, lr: float, step: int):
+def optimizer_step(sh: LsShape, st: dict, grads: dict, opt: OptConfig, lr: float, step: int,
+                   prec: Precision = FP32):
     """RAdam/Ranger/AdamW over every group (step is the new 1-based count)."""
     ss, denom = opt.step_size_denom(step)
     beta1 = opt.beta1
@@ -235,6 +303,17 @@ def optimizer_step(sh: LsShape, st: dict, grads: dict, opt: OptConfig, lr: float
         wd, lr_g = opt.group(kind, lr)
         lo, hi = (-float(QUANT), float(QUANT)) if quant else (F32_MIN, F32_MAX)
         grad = np.ascontiguousarray(grads[name], dtype=np.float32).copy()
+        if name == "ft_w" and prec.fp16_opt_state:
+            ft = st["ft_w"]
+            m = ft["m16"] / M_SCALE
+            v = ft["v16"] / V_SCALE
+            ffi.radam_step(ft["w"], m, v, grad, lr_g, ss, denom, wd, beta1, BETA2, EPS, lo, hi)
+            ft["m16"] = f16(np.clip(m * M_SCALE, -F16_MAX, F16_MAX))
+            with np.errstate(invalid="ignore"):
+                sv = v * V_SCALE
+            ft["v16"] = f16(np.where(sv > F16_MAX, F16_MAX, sv))  # a NaN stays NaN
+            ft["m"], ft["v"] = ft["m16"] / M_SCALE, ft["v16"] / V_SCALE
+            continue
         ffi.radam_step(st[name]["w"], st[name]["m"], st[name]["v"], grad, lr_g, ss, denom, wd, beta1,
                        BETA2, EPS, lo, hi)
     if opt.optimizer == "ranger" and step % RANGER_K == 0:
@@ -243,9 +322,10 @@ def optimizer_step(sh: LsShape, st: dict, grads: dict, opt: OptConfig, lr: float
 
 
 def train_step(sh: LsShape, st: dict, batch: dict, opt: OptConfig, lr: float, wdl_lambda: float,
-               loss: dict, step: int):
-    """Full step; mutates st.  Returns (loss_acc, intermediates, grads)."""
-    a, acc = forward(sh, st, batch, wdl_lambda, loss)
-    g = backward(sh, st, batch, a)
-    optimizer_step(sh, st, g, opt, lr, step)
+               loss: dict, step: int, prec: Precision = FP32):
+    """Full step; mutates st.  Returns (loss_acc, intermediates, grads).  With
+    fp16_opt_state, st["ft_w"] must carry "m16" / "v16" (to_f16_state)."""
+    a, acc = forward(sh, st, batch, wdl_lambda, loss, prec)
+    g = backward(sh, st, batch, a, prec)
+    optimizer_step(sh, st, g, opt, lr, step, prec)
     return acc, a, g

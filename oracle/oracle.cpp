@@ -102,6 +102,62 @@ void orc_sparse_ft_backward(const float* grad_out, const int32_t* indices, float
     }
 }
 
+// gather_and_sum_per_feature_{overwrite,add}_fp16
+// (crates/cuda-native-runtime/kernels/native_kernels.cu:1030-1100) on the
+// per-feature position lists of the trainer's backward (slots < nnz, indices
+// in [0, cols), one entry per occurrence).  The reference fills those lists
+// with atomics, so their order is unspecified; ascending position order is
+// used here.  dft16 holds the f16 activation gradients (scaled) as f32
+// values.  Per cell: four interleaved f32 partial sums, combined as
+// (s0 + s1) + (s2 + s3), times inv_scale; add = 0 overwrites every real
+// feature's cell, add = 1 adds the scaled sum when the sum is nonzero.
+void orc_ft_grad_fp16(const float* dft16, const int32_t* indices, const int32_t* nnz_arr,
+                      float* grad_weight, int64_t batch, int64_t rows, int64_t cols, int64_t max_active,
+                      float inv_scale, int32_t add) {
+    std::vector<int64_t> count(cols + 1, 0);
+    for (int64_t bi = 0; bi < batch; ++bi)
+        for (int64_t ni = 0; ni < nnz_arr[bi]; ++ni) {
+            const int32_t idx = indices[bi * max_active + ni];
+            if (idx >= 0 && (int64_t)idx < cols) ++count[idx + 1];
+        }
+    for (int64_t f = 0; f < cols; ++f) count[f + 1] += count[f];
+    std::vector<int64_t> fill(count.begin(), count.end() - 1);
+    std::vector<int64_t> pos(count[cols]);
+    for (int64_t bi = 0; bi < batch; ++bi)
+        for (int64_t ni = 0; ni < nnz_arr[bi]; ++ni) {
+            const int32_t idx = indices[bi * max_active + ni];
+            if (idx >= 0 && (int64_t)idx < cols) pos[fill[idx]++] = bi;
+        }
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int64_t f = 0; f < cols; ++f) {
+        const int64_t start = count[f], end = count[f + 1];
+        const int64_t unroll_end = end >= start + 3 ? end - 3 : start;
+        for (int64_t r = 0; r < rows; ++r) {
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+            int64_t i = start;
+            while (i < unroll_end) {
+                s0 += dft16[pos[i] * rows + r];
+                s1 += dft16[pos[i + 1] * rows + r];
+                s2 += dft16[pos[i + 2] * rows + r];
+                s3 += dft16[pos[i + 3] * rows + r];
+                i += 4;
+            }
+            while (i < end) {
+                s0 += dft16[pos[i] * rows + r];
+                ++i;
+            }
+            const float sum = (s0 + s1) + (s2 + s3);
+            const float scaled = sum * inv_scale;
+            float& g = grad_weight[f * rows + r];
+            if (add) {
+                if (sum != 0.0f) g += scaled;
+            } else {
+                g = scaled;
+            }
+        }
+    }
+}
+
 // The trainer-level variant of the backward: slots at or beyond nnz[bi] are
 // ignored, as build_feature_counts / scatter_positions do in the reference
 // trainer (crates/cuda-native-runtime/kernels/native_kernels.cu:1630-1765).

@@ -37,6 +37,9 @@ class TataraTrainerConfig(C.Structure):
         ("dense_lr_mult", C.c_float),
         ("bias_lr_mult", C.c_float),
         ("keep_grads", C.c_int32),
+        ("ft_fp16", C.c_int32),
+        ("ft_fp16_out", C.c_int32),
+        ("fp16_opt_state", C.c_int32),
     ]
 
 
@@ -132,6 +135,7 @@ SIGNATURES = {
     "tatara_trainer_set_tensor": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, c_f32p, C.c_uint64]),
     "tatara_trainer_get_activation": (C.c_int32, [C.c_void_p, C.c_char_p, c_f32p, C.c_uint64]),
     "tatara_trainer_sync_forward_weights": (C.c_int32, [C.c_void_p]),
+    "tatara_trainer_fp16_clamp_count": (C.c_int32, [C.c_void_p, c_u64p, c_u64p]),
     "tatara_trainer_export_quantised": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int32]),
     "tatara_trainer_set_profiling": (C.c_int32, [C.c_void_p, C.c_int32]),
     "tatara_trainer_phase_times": (C.c_int32, [C.c_void_p, c_f64p, C.c_int32, c_u64p]),

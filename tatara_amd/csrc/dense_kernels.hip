@@ -460,8 +460,36 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
 // (native_kernels.cu:2260-2302).  Grid (column block, row block): a thread
 // owns one float4 column group of kPostTiles sorted tiles and writes its ft_b
 // gradient partial per perspective for that row block.
+// H: f16 raw sums in, f16 dft out, scaled by dft_scale and clamped to
+// +-65504 with a count of every clamp (ft_post_perspective_grad_fused_fp16,
+// native_kernels.cu:2304-2352); the ft_b gradient stays unscaled f32.
 // ---------------------------------------------------------------------------
-template <int L1>
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <bool H>
+__device__ __forceinline__ float4 load_ft4(const float* ft, const _Float16* ft16, uint64_t elem) {
+    if constexpr (H) {
+        const f4v f = __builtin_convertvector(*reinterpret_cast<const h4*>(ft16 + elem), f4v);
+        return make_float4(f.x, f.y, f.z, f.w);
+    } else {
+        return *reinterpret_cast<const float4*>(ft + elem);
+    }
+}
+
+__device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
+    if (v > 65504.0f) {
+        ++clamps;
+        return 65504.0f;
+    }
+    if (v < -65504.0f) {
+        ++clamps;
+        return -65504.0f;
+    }
+    return v;
+}
+
+template <int L1, bool H>
 __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
     const uint32_t ft_out = a.ft_out, half = ft_out / 2, n4 = ft_out / 4;
     const uint64_t batch = a.batch;
@@ -474,12 +502,14 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
         const uint32_t persp = c0 < half ? 0 : 1;
         const uint32_t p0 = c0 - persp * half;
         const float* ft = persp ? a.ft_nstm : a.ft_stm;
+        const _Float16* ft16 = reinterpret_cast<const _Float16*>(persp ? a.ft_nstm16 : a.ft_stm16);
         // chunk-major dft: this thread's four columns c0..c0+3 and their pair
         // partners each lie inside one 256-column chunk
         const uint64_t cstride = 2 * batch * kDftChunk;
-        float* dft_a = a.dft + (uint64_t)(p0 / kDftChunk) * cstride + persp * batch * kDftChunk + p0 % kDftChunk;
-        float* dft_b = a.dft + (uint64_t)((p0 + half) / kDftChunk) * cstride + persp * batch * kDftChunk +
-                       (p0 + half) % kDftChunk;
+        const uint64_t off_a = (uint64_t)(p0 / kDftChunk) * cstride + persp * batch * kDftChunk + p0 % kDftChunk;
+        const uint64_t off_b = (uint64_t)((p0 + half) / kDftChunk) * cstride + persp * batch * kDftChunk +
+                               (p0 + half) % kDftChunk;
+        uint32_t clamps = 0;
         float ws[4][L1];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -509,9 +539,8 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
             int32_t orig_n = a.perm[tile * 16];
             float4 xa_n = zero4, xb_n = zero4;
             if (orig_n >= 0) {
-                const float4* src = reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out);
-                xa_n = src[p0 / 4];
-                xb_n = src[(p0 + half) / 4];
+                xa_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0);
+                xb_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0 + half);
             }
             for (uint32_t r = 0; r < 16; ++r) {
                 const uint64_t row = tile * 16 + r;
@@ -520,9 +549,8 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                 if (r + 1 < 16) {
                     orig_n = a.perm[row + 1];
                     if (orig_n >= 0) {
-                        const float4* src = reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out);
-                        xa_n = src[p0 / 4];
-                        xb_n = src[(p0 + half) / 4];
+                        xa_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0);
+                        xb_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0 + half);
                     }
                 }
                 if (orig < 0) continue;
@@ -555,8 +583,21 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                     ga[e] = (xa[e] > 0.0f && xa[e] < 1.0f) ? dyv[e] * yb * a.ft_post_scale : 0.0f;
                     gb[e] = (xb[e] > 0.0f && xb[e] < 1.0f) ? dyv[e] * ya * a.ft_post_scale : 0.0f;
                 }
-                *reinterpret_cast<float4*>(dft_a + (uint64_t)orig * kDftChunk) = make_float4(ga[0], ga[1], ga[2], ga[3]);
-                *reinterpret_cast<float4*>(dft_b + (uint64_t)orig * kDftChunk) = make_float4(gb[0], gb[1], gb[2], gb[3]);
+                if constexpr (H) {
+                    const float sc = a.dft_scale;
+                    const f4v sa = {clamp_f16_range(ga[0] * sc, clamps), clamp_f16_range(ga[1] * sc, clamps),
+                                    clamp_f16_range(ga[2] * sc, clamps), clamp_f16_range(ga[3] * sc, clamps)};
+                    const f4v sb = {clamp_f16_range(gb[0] * sc, clamps), clamp_f16_range(gb[1] * sc, clamps),
+                                    clamp_f16_range(gb[2] * sc, clamps), clamp_f16_range(gb[3] * sc, clamps)};
+                    _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
+                    *reinterpret_cast<h4*>(d16 + off_a + (uint64_t)orig * kDftChunk) = __builtin_convertvector(sa, h4);
+                    *reinterpret_cast<h4*>(d16 + off_b + (uint64_t)orig * kDftChunk) = __builtin_convertvector(sb, h4);
+                } else {
+                    *reinterpret_cast<float4*>(a.dft + off_a + (uint64_t)orig * kDftChunk) =
+                        make_float4(ga[0], ga[1], ga[2], ga[3]);
+                    *reinterpret_cast<float4*>(a.dft + off_b + (uint64_t)orig * kDftChunk) =
+                        make_float4(gb[0], gb[1], gb[2], gb[3]);
+                }
                 acc_a.x += ga[0];
                 acc_a.y += ga[1];
                 acc_a.z += ga[2];
@@ -570,6 +611,7 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
         float* pp = part + persp * ft_out;
         reinterpret_cast<float4*>(pp)[p0 / 4] = acc_a;
         reinterpret_cast<float4*>(pp)[(p0 + half) / 4] = acc_b;
+        if (H && clamps) atomicAdd(a.clamp_counter, (unsigned long long)clamps);
     }
 }
 
@@ -710,13 +752,21 @@ int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream) {
 }
 
 int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
+    TATARA_REQUIRE(!a.dft16 || (a.ft_stm16 && a.ft_nstm16 && a.clamp_counter),
+                   "an f16 dft needs the f16 raw sums and a clamp counter");
     const uint32_t rows = ls_post_workgroups(a.padded_b);
     if (rows == 0) return kOk;
     const dim3 grid(ceil_div(a.ft_out / 4, 128), rows);
     if (a.l1 == 16) {
-        ls_l1_input_post_kernel<16><<<grid, 128, 0, stream>>>(a);
+        if (a.dft16)
+            ls_l1_input_post_kernel<16, true><<<grid, 128, 0, stream>>>(a);
+        else
+            ls_l1_input_post_kernel<16, false><<<grid, 128, 0, stream>>>(a);
     } else if (a.l1 == 8) {
-        ls_l1_input_post_kernel<8><<<grid, 128, 0, stream>>>(a);
+        if (a.dft16)
+            ls_l1_input_post_kernel<8, true><<<grid, 128, 0, stream>>>(a);
+        else
+            ls_l1_input_post_kernel<8, false><<<grid, 128, 0, stream>>>(a);
     } else {
         TATARA_REQUIRE(false, "l1 must be 16 or 8");
     }

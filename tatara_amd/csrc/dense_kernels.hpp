@@ -47,6 +47,13 @@ struct LsDenseArgs {
     float* dl1_sorted;          // [padded_b][l1]
     float* net_output;          // [batch]
     float* dft;                 // chunk-major [ceil(ft_out/256)][2*batch][256]
+    // f16 FT activations (the reference's --ft-fp16-out): raw sums read as f16,
+    // dft written as f16(clamp(g * dft_scale, +-65504)) with every clamp counted
+    const uint16_t* ft_stm16;   // [batch][ft_out], used instead of ft_stm / ft_nstm when non-null
+    const uint16_t* ft_nstm16;
+    uint16_t* dft16;            // chunk-major like dft, written instead of dft when non-null
+    float dft_scale;
+    unsigned long long* clamp_counter;
     // inputs
     const float* score;
     const float* wdl;

@@ -46,6 +46,36 @@ __device__ __forceinline__ void st_nt(float4* p, float4 v) {
     __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(p));
 }
 
+// binary16 (f16) values: conversions to f16 round to nearest even
+// (__float2half_rn); f16 -> f32 is exact.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 h4_to_f4(h4 h) {
+    const nt_f4 f = __builtin_convertvector(h, nt_f4);
+    return make_float4(f.x, f.y, f.z, f.w);
+}
+
+__device__ __forceinline__ h4 f4_to_h4(float4 v) {
+    const nt_f4 f = {v.x, v.y, v.z, v.w};
+    return __builtin_convertvector(f, h4);
+}
+
+// Four consecutive values of a table at float4 index i4, as f32.
+template <typename T>
+struct Row4;
+template <>
+struct Row4<float> {
+    static __device__ __forceinline__ float4 load(const float* W, uint64_t i4) {
+        return reinterpret_cast<const float4*>(W)[i4];
+    }
+};
+template <>
+struct Row4<_Float16> {
+    static __device__ __forceinline__ float4 load(const _Float16* W, uint64_t i4) {
+        return h4_to_f4(reinterpret_cast<const h4*>(W)[i4]);
+    }
+};
+
 // Loads the position's active indices into per-wave LDS in slot order,
 // keeping only valid ones (slot < nnz and 0 <= idx < cols), and returns how
 // many there are.  Skipping invalid slots here matches the reference, which
@@ -65,16 +95,16 @@ __device__ __forceinline__ int compact_indices(const int32_t* __restrict__ idx_r
 }
 
 // Sums rows idx[0..nv) of W (row length ft_out) at float4 column q (and q2 if
-// TWO), in slot order, starting from +0.0.  Loads of UNROLL rows are issued
-// before their adds so that many 16-byte loads are in flight per lane.
-template <bool TWO, int UNROLL>
-__device__ __forceinline__ void gather_rows(const float* __restrict__ W, uint64_t ft_out,
+// TWO), in slot order, starting from +0.0, in f32 whatever the table's type.
+// Loads of UNROLL rows are issued before their adds so that many loads are in
+// flight per lane (16 bytes per row for f32 tables, 8 for f16).
+template <bool TWO, int UNROLL, typename T>
+__device__ __forceinline__ void gather_rows(const T* __restrict__ W, uint64_t ft_out,
                                             const int* s_idx, int nv, uint32_t q, uint32_t q2,
                                             bool active, float4& a0, float4& a1) {
     a0 = make_float4(0.f, 0.f, 0.f, 0.f);
     a1 = a0;
     if (!active) return;
-    const float4* __restrict__ W4 = reinterpret_cast<const float4*>(W);
     const uint64_t row4 = ft_out / 4;
     int k = 0;
     for (; k + UNROLL <= nv; k += UNROLL) {
@@ -82,8 +112,8 @@ __device__ __forceinline__ void gather_rows(const float* __restrict__ W, uint64_
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const uint64_t r = (uint32_t)__builtin_amdgcn_readfirstlane(s_idx[k + u]);
-            w0[u] = W4[r * row4 + q];
-            if (TWO) w1[u] = W4[r * row4 + q2];
+            w0[u] = Row4<T>::load(W, r * row4 + q);
+            if (TWO) w1[u] = Row4<T>::load(W, r * row4 + q2);
         }
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
@@ -93,10 +123,10 @@ __device__ __forceinline__ void gather_rows(const float* __restrict__ W, uint64_
     }
     for (; k < nv; ++k) {
         const uint64_t r = (uint32_t)__builtin_amdgcn_readfirstlane(s_idx[k]);
-        const float4 w0 = W4[r * row4 + q];
+        const float4 w0 = Row4<T>::load(W, r * row4 + q);
         a0 = f4add(a0, w0);
         if (TWO) {
-            const float4 w1 = W4[r * row4 + q2];
+            const float4 w1 = Row4<T>::load(W, r * row4 + q2);
             a1 = f4add(a1, w1);
         }
     }
@@ -114,16 +144,21 @@ __device__ __forceinline__ void gather_rows(const float* __restrict__ W, uint64_
 // grouped by king block, so concurrently running waves read rows of the same
 // king block (a few MB) and hit in L2; the XCD swizzle keeps neighbouring
 // tasks on one XCD.
+// T = _Float16 reads the f16 forward table (sparse_ft_forward_fp16,
+// native_kernels.cu:700-780: f16 rows, f32 accumulation); HOUT rounds the raw
+// sums to f16 before they are stored and before the pairwise post reads them
+// (sparse_ft_forward_fp16_out + ft_post_perspective_fwd_fp16, :762-857).
 // ---------------------------------------------------------------------------
 
 enum FwdMode : int { kRaw = 0, kPair = 1, kConcat = 2 };
 
-template <int MODE>
+template <int MODE, typename T, bool HOUT>
 __global__ __launch_bounds__(256) void ft_forward_kernel(
-    const float* __restrict__ W, const int32_t* __restrict__ idx_stm,
+    const T* __restrict__ W, const int32_t* __restrict__ idx_stm,
     const int32_t* __restrict__ idx_nstm, const int32_t* __restrict__ nnz,
     const int32_t* __restrict__ schedule,  // [n_persp][batch] position order, or null
     const float* __restrict__ bias, float* __restrict__ out_stm, float* __restrict__ out_nstm,
+    _Float16* __restrict__ out16_stm, _Float16* __restrict__ out16_nstm,
     float* __restrict__ combined, uint32_t batch, uint32_t ft_out, uint32_t cols,
     uint32_t max_active, uint32_t n_chunks, uint32_t n_persp, float scale) {
     __shared__ int s_idx_all[kWavesPerBlock][kMaxActive];
@@ -142,6 +177,7 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
 
     const int32_t* idx = persp == 0 ? idx_stm : idx_nstm;
     float* out = persp == 0 ? out_stm : out_nstm;
+    _Float16* out16 = persp == 0 ? out16_stm : out16_nstm;
     int* s_idx = s_idx_all[wave];
     const int nv = compact_indices(idx + (uint64_t)pos * max_active, nnz[pos], cols, max_active, s_idx);
 
@@ -153,7 +189,12 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
         const uint32_t qp = chunk * 32 + j;  // pair index
         const bool active = qp < half4;
         const uint32_t q = lane < 32 ? qp : qp + half4;
-        gather_rows<false, 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
+        gather_rows<false, sizeof(T) == 2 ? 16 : 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
+        h4 r16;
+        if (HOUT) {
+            r16 = f4_to_h4(a0);
+            a0 = h4_to_f4(r16);
+        }
         // first-half lanes receive their partner's sums from lane + 32
         float4 p;
         p.x = __shfl_xor(a0.x, 32);
@@ -161,8 +202,12 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
         p.z = __shfl_xor(a0.z, 32);
         p.w = __shfl_xor(a0.w, 32);
         if (!active) return;
-        float4* o4 = reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out);
-        st_nt(o4 + q, a0);
+        if (HOUT) {
+            __builtin_nontemporal_store(r16, reinterpret_cast<h4*>(out16 + (uint64_t)pos * ft_out) + q);
+        } else {
+            float4* o4 = reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out);
+            st_nt(o4 + q, a0);
+        }
         if (lane >= 32) return;
         const float4 b0 = reinterpret_cast<const float4*>(bias)[qp];
         const float4 b1 = reinterpret_cast<const float4*>(bias)[qp + half4];
@@ -175,7 +220,7 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
     } else {
         const uint32_t q = chunk * kWave + lane;
         const bool active = q < row4;
-        gather_rows<false, 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
+        gather_rows<false, sizeof(T) == 2 ? 16 : 8>(W, ft_out, s_idx, nv, q, 0, active, a0, a1);
         if (!active) return;
         if (MODE == kRaw) {
             reinterpret_cast<float4*>(out + (uint64_t)pos * ft_out)[q] = a0;
@@ -285,6 +330,8 @@ __global__ void occurrence_offsets_kernel(const uint32_t* __restrict__ sorted_ke
 
 template <int V>
 using vecf = float __attribute__((ext_vector_type(V)));
+template <int V>
+using vech = _Float16 __attribute__((ext_vector_type(V)));
 
 template <int V>
 __device__ __forceinline__ vecf<V> segment_sum(const vecf<V>* __restrict__ dft, uint64_t row_v,
@@ -310,10 +357,51 @@ __device__ __forceinline__ vecf<V> segment_sum(const vecf<V>* __restrict__ dft, 
     return acc;
 }
 
+// The same sequential sum over f16 dft rows (four values per lane), in f32.
+__device__ __forceinline__ vecf<4> segment_sum_f16(const vech<4>* __restrict__ dft, uint64_t row_v,
+                                                   const uint32_t* __restrict__ vals, uint32_t s,
+                                                   uint32_t e, uint64_t q) {
+    vecf<4> acc = 0.0f;
+    constexpr int U = 16;
+    uint32_t i = s;
+    for (; i + U <= e; i += U) {
+        vech<4> d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i + u]);
+            d[u] = dft[r * row_v + q];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += __builtin_convertvector(d[u], vecf<4>);
+    }
+    for (; i < e; ++i) {
+        const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i]);
+        acc += __builtin_convertvector(dft[r * row_v + q], vecf<4>);
+    }
+    return acc;
+}
+
 template <int V>
-__device__ __forceinline__ void opt_update(float* __restrict__ w, float* __restrict__ m,
-                                           float* __restrict__ v, float* __restrict__ slow,
-                                           uint64_t off, vecf<V> g, const OptScalars& s) {
+__device__ __forceinline__ void lookahead(vecf<V>& W, float* __restrict__ slow, uint64_t off,
+                                          const OptScalars& s) {
+    vecf<V>* s_ = reinterpret_cast<vecf<V>*>(slow) + off;
+    vecf<V> S = __builtin_nontemporal_load(s_);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        float a = W[k], b = S[k];
+        lerp_elem(a, b, s.alpha);
+        W[k] = a;
+        S[k] = b;
+    }
+    __builtin_nontemporal_store(S, s_);
+}
+
+// RAdam (+ Ranger lerp) on V consecutive cells with f32 moments; returns the
+// new weights.
+template <int V>
+__device__ __forceinline__ vecf<V> opt_update(float* __restrict__ w, float* __restrict__ m,
+                                              float* __restrict__ v, float* __restrict__ slow,
+                                              uint64_t off, vecf<V> g, const OptScalars& s) {
     vecf<V>* w_ = reinterpret_cast<vecf<V>*>(w) + off;
     vecf<V>* m_ = reinterpret_cast<vecf<V>*>(m) + off;
     vecf<V>* v_ = reinterpret_cast<vecf<V>*>(v) + off;
@@ -328,50 +416,97 @@ __device__ __forceinline__ void opt_update(float* __restrict__ w, float* __restr
         M[k] = b;
         Q[k] = c;
     }
-    if (s.lookahead) {
-        vecf<V>* s_ = reinterpret_cast<vecf<V>*>(slow) + off;
-        vecf<V> S = __builtin_nontemporal_load(s_);
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-            float a = W[k], b = S[k];
-            lerp_elem(a, b, s.alpha);
-            W[k] = a;
-            S[k] = b;
-        }
-        __builtin_nontemporal_store(S, s_);
-    }
+    if (s.lookahead) lookahead<V>(W, slow, off, s);
     __builtin_nontemporal_store(W, w_);
     __builtin_nontemporal_store(M, m_);
     __builtin_nontemporal_store(Q, v_);
+    return W;
 }
 
-// dft_row / dft_chunk: the dft strides in floats (chunk = kDftChunk columns).
+// The same with f16 moments stored scaled (radam_step_f16state,
+// native_kernels.cu:1118-1170): the previous moments are read back as
+// f16 / scale, the step runs in f32 on them, and the new moments are stored
+// as f16(m * m_scale) clamped to +-65504 and f16(v * v_scale) clamped above
+// at 65504 (a NaN stays NaN).
 template <int V>
-__global__ __launch_bounds__(256) void ft_grad_update_kernel(
-    const float* __restrict__ dft, uint64_t dft_row, uint64_t dft_chunk,
-    const uint32_t* __restrict__ occ_vals, const uint32_t* __restrict__ occ_off,
-    float* __restrict__ w, float* __restrict__ m, float* __restrict__ v, float* __restrict__ slow,
-    float* __restrict__ grad_out,  // gradient per row (may be null without a factorizer)
-    uint32_t ft_out, uint32_t rows, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
+__device__ __forceinline__ vecf<V> opt_update_f16(float* __restrict__ w, _Float16* __restrict__ m16,
+                                                  _Float16* __restrict__ v16, float* __restrict__ slow,
+                                                  uint64_t off, vecf<V> g, const OptScalars& s, float ms,
+                                                  float vs) {
+    vecf<V>* w_ = reinterpret_cast<vecf<V>*>(w) + off;
+    vech<V>* m_ = reinterpret_cast<vech<V>*>(m16) + off;
+    vech<V>* v_ = reinterpret_cast<vech<V>*>(v16) + off;
+    vecf<V> W = __builtin_nontemporal_load(w_);
+    vech<V> M = __builtin_nontemporal_load(m_);
+    vech<V> Q = __builtin_nontemporal_load(v_);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        float a = W[k], b = (float)M[k] / ms, c = (float)Q[k] / vs;
+        radam_elem(a, b, c, g[k], s);
+        W[k] = a;
+        float sm = b * ms;
+        sm = sm > 65504.0f ? 65504.0f : (sm < -65504.0f ? -65504.0f : sm);
+        float sv = c * vs;
+        sv = sv > 65504.0f ? 65504.0f : sv;
+        M[k] = (_Float16)sm;
+        Q[k] = (_Float16)sv;
+    }
+    if (s.lookahead) lookahead<V>(W, slow, off, s);
+    __builtin_nontemporal_store(W, w_);
+    __builtin_nontemporal_store(M, m_);
+    __builtin_nontemporal_store(Q, v_);
+    return W;
+}
+
+// One cell group's update in the moment format the trainer uses, plus the f16
+// mirror of the new weights when the forward reads one.
+template <int V, bool HSTATE>
+__device__ __forceinline__ void update_cells(const FtGradArgs& a, uint64_t off, vecf<V> g) {
+    vecf<V> W;
+    if constexpr (HSTATE)
+        W = opt_update_f16<V>(a.w, reinterpret_cast<_Float16*>(a.m16), reinterpret_cast<_Float16*>(a.v16), a.slow,
+                              off, g, a.opt, a.m_scale, a.v_scale);
+    else
+        W = opt_update<V>(a.w, a.m, a.v, a.slow, off, g, a.opt);
+    if (a.mirror16)
+        __builtin_nontemporal_store(__builtin_convertvector(W, vech<V>),
+                                    reinterpret_cast<vech<V>*>(a.mirror16) + off);
+}
+
+// dft_row_stride / dft_chunk_stride: the dft strides in elements (chunk =
+// kDftChunk columns).  HDFT: the dft is f16 and each row sum is multiplied by
+// dft_inv_scale (gather_and_sum_per_feature_*_fp16, native_kernels.cu:
+// 1030-1100).
+template <int V, bool HDFT, bool HSTATE>
+__global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint32_t n_chunks) {
     constexpr uint32_t kCols = kWave * V;
     static_assert(kDftChunk % kCols == 0, "a wave's columns must lie in one dft chunk");
+    static_assert(!HDFT || V == 4, "the f16 dft gather reads four values per lane");
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
-    if (task >= (uint64_t)rows * n_chunks) return;
-    const uint32_t chunk = (uint32_t)(task / rows);
-    const uint32_t f = (uint32_t)(task - (uint64_t)chunk * rows);
+    if (task >= (uint64_t)a.rows * n_chunks) return;
+    const uint32_t chunk = (uint32_t)(task / a.rows);
+    const uint32_t f = (uint32_t)(task - (uint64_t)chunk * a.rows);
     const uint32_t col = chunk * kCols + lane * V;
-    const uint32_t s0 = __builtin_amdgcn_readfirstlane(occ_off[2 * f]);
-    const uint32_t s1 = __builtin_amdgcn_readfirstlane(occ_off[2 * f + 2]);
-    if (col >= ft_out) return;
-    const uint64_t q = ((uint64_t)(col / kDftChunk) * dft_chunk + col % kDftChunk) / V;
-    const vecf<V> gr = segment_sum<V>(reinterpret_cast<const vecf<V>*>(dft), dft_row / V, occ_vals,
-                                      s0, s1, q);
-    const uint64_t off = ((uint64_t)f * ft_out + col) / V;
-    if (grad_out) __builtin_nontemporal_store(gr, reinterpret_cast<vecf<V>*>(grad_out) + off);
-    if (apply_update) opt_update<V>(w, m, v, slow, off, gr, s);
+    const uint32_t s0 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f]);
+    const uint32_t s1 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f + 2]);
+    if (col >= a.ft_out) return;
+    const uint64_t q =
+        ((uint64_t)(col / kDftChunk) * a.dft_chunk_stride + col % kDftChunk) / V;
+    vecf<V> gr;
+    if constexpr (HDFT) {
+        gr = segment_sum_f16(reinterpret_cast<const vech<4>*>(a.dft16), a.dft_row_stride / 4, a.occ_vals, s0,
+                             s1, q);
+        gr *= a.dft_inv_scale;
+    } else {
+        gr = segment_sum<V>(reinterpret_cast<const vecf<V>*>(a.dft), a.dft_row_stride / V, a.occ_vals, s0, s1,
+                            q);
+    }
+    const uint64_t off = ((uint64_t)f * a.ft_out + col) / V;
+    if (a.grad) __builtin_nontemporal_store(gr, reinterpret_cast<vecf<V>*>(a.grad) + off);
+    if (a.apply_update) update_cells<V, HSTATE>(a, off, gr);
 }
 
 // ---------------------------------------------------------------------------
@@ -382,21 +517,22 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(
 // comb = w + w_virtual is rewritten for the piece's rows (ft_fold_virtual).
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void ft_virtual_fold_kernel(
-    float* __restrict__ grad, float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
-    float* __restrict__ slow, float* __restrict__ comb, uint32_t ft_out, uint32_t ft_in,
-    uint32_t piece_inputs, uint32_t n_chunks, int32_t apply_update, OptScalars s) {
+template <bool HSTATE, bool HCOMB>
+__global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint32_t piece_inputs,
+                                                              uint32_t n_chunks, float* __restrict__ comb,
+                                                              _Float16* __restrict__ comb16) {
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint64_t task = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
     if (task >= (uint64_t)piece_inputs * n_chunks) return;
     const uint32_t chunk = (uint32_t)(task / piece_inputs);
     const uint32_t p = (uint32_t)(task - (uint64_t)chunk * piece_inputs);
+    const uint32_t ft_out = a.ft_out, ft_in = a.rows;
     const uint32_t row4 = ft_out / 4;
     const uint32_t q = chunk * kWave + lane;
     if (q >= row4) return;
     const uint32_t count = ft_in / piece_inputs;
-    const float4* g4 = reinterpret_cast<const float4*>(grad);
+    const float4* g4 = reinterpret_cast<const float4*>(a.grad);
     float4 vsum = make_float4(0.f, 0.f, 0.f, 0.f);
     constexpr int U = 8;
     uint32_t j = 0;
@@ -409,28 +545,44 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(
     }
     for (; j < count; ++j) vsum = f4add(vsum, g4[(uint64_t)(p + j * piece_inputs) * row4 + q]);
     const uint64_t voff4 = (uint64_t)(ft_in + p) * row4 + q;
-    reinterpret_cast<float4*>(grad)[voff4] = vsum;
-    if (!apply_update) return;
-    opt_update<4>(w, m, v, slow, voff4, vecf<4>{vsum.x, vsum.y, vsum.z, vsum.w}, s);
-    if (!comb) return;
-    const float4 wv = reinterpret_cast<const float4*>(w)[voff4];
+    reinterpret_cast<float4*>(a.grad)[voff4] = vsum;
+    if (!a.apply_update) return;
+    const vecf<4> g = {vsum.x, vsum.y, vsum.z, vsum.w};
+    if constexpr (HSTATE)
+        opt_update_f16<4>(a.w, reinterpret_cast<_Float16*>(a.m16), reinterpret_cast<_Float16*>(a.v16), a.slow,
+                          voff4, g, a.opt, a.m_scale, a.v_scale);
+    else
+        opt_update<4>(a.w, a.m, a.v, a.slow, voff4, g, a.opt);
+    if (!comb && !comb16) return;
+    // the forward rows of this piece: comb = w + w_virtual (f32 add), rounded
+    // to f16 for an f16 forward table (ft_fold_virtual_f16, native_kernels.cu:262-300)
+    const float4 wv = reinterpret_cast<const float4*>(a.w)[voff4];
+    auto put = [&](uint64_t off4, float4 wr) {
+        const float4 c = f4add(wr, wv);
+        if constexpr (HCOMB)
+            reinterpret_cast<h4*>(comb16)[off4] = f4_to_h4(c);
+        else
+            reinterpret_cast<float4*>(comb)[off4] = c;
+    };
     for (j = 0; j + U <= count; j += U) {
         float4 wr[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) wr[u] = reinterpret_cast<const float4*>(w)[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q];
-#pragma unroll
         for (int u = 0; u < U; ++u)
-            reinterpret_cast<float4*>(comb)[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q] = f4add(wr[u], wv);
+            wr[u] = reinterpret_cast<const float4*>(a.w)[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q];
+#pragma unroll
+        for (int u = 0; u < U; ++u) put((uint64_t)(p + (j + u) * piece_inputs) * row4 + q, wr[u]);
     }
     for (; j < count; ++j) {
         const uint64_t off4 = (uint64_t)(p + j * piece_inputs) * row4 + q;
-        reinterpret_cast<float4*>(comb)[off4] = f4add(reinterpret_cast<const float4*>(w)[off4], wv);
+        put(off4, reinterpret_cast<const float4*>(a.w)[off4]);
     }
 }
 
 // Standalone fold / reduce (Base mode), used when they are not fused.
+template <bool HCOMB>
 __global__ void ft_fold_kernel(const float* __restrict__ w, float* __restrict__ comb,
-                               uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs) {
+                               _Float16* __restrict__ comb16, uint32_t ft_in, uint32_t ft_out,
+                               uint32_t piece_inputs) {
     const uint64_t n4 = (uint64_t)ft_in * ft_out / 4;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n4) return;
@@ -438,8 +590,18 @@ __global__ void ft_fold_kernel(const float* __restrict__ w, float* __restrict__ 
     const uint64_t f = i / row4;
     const uint32_t c = (uint32_t)(i - f * row4);
     const uint64_t vrow = ft_in + f % piece_inputs;
-    reinterpret_cast<float4*>(comb)[i] =
+    const float4 x =
         f4add(reinterpret_cast<const float4*>(w)[i], reinterpret_cast<const float4*>(w)[vrow * row4 + c]);
+    if constexpr (HCOMB)
+        reinterpret_cast<h4*>(comb16)[i] = f4_to_h4(x);
+    else
+        reinterpret_cast<float4*>(comb)[i] = x;
+}
+
+__global__ void cast_f16_kernel(const float* __restrict__ src, _Float16* __restrict__ dst, uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = (_Float16)src[i];
 }
 
 __global__ void ft_reduce_kernel(float* __restrict__ grad, uint32_t ft_in, uint32_t ft_out,
@@ -492,29 +654,39 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.max_active <= (uint32_t)kMaxActive, "max_active must be <= 64");
     TATARA_REQUIRE(a.ft_out % 8 == 0, "ft_out must be a multiple of 8");
     TATARA_REQUIRE(a.n_persp == 1 || a.n_persp == 2, "n_persp must be 1 or 2");
+    const bool h_out = a.out_stm16 != nullptr;
+    TATARA_REQUIRE(!h_out || (a.mode == kPair && a.W16), "f16 raw sums need the pairwise mode and an f16 table");
+    TATARA_REQUIRE(!a.W16 || a.mode == kPair, "an f16 table is read by the pairwise mode only");
     if (a.batch == 0) return kOk;
     const uint32_t n_chunks = a.mode == kPair ? ceil_div(a.ft_out / 8, 32) : ceil_div(a.ft_out / 4, kWave);
     const uint64_t tasks = (uint64_t)a.n_persp * n_chunks * a.batch;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+    _Float16* o16s = reinterpret_cast<_Float16*>(a.out_stm16);
+    _Float16* o16n = reinterpret_cast<_Float16*>(a.out_nstm16);
+    const _Float16* W16 = reinterpret_cast<const _Float16*>(a.W16);
+#define TATARA_FWD(MODE, T, HOUT, WPTR)                                                                      \
+    ft_forward_kernel<MODE, T, HOUT><<<blocks, 256, 0, stream>>>(                                          \
+        WPTR, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm, o16s, o16n, a.combined, \
+        a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale)
     switch (a.mode) {
         case kRaw:
-            ft_forward_kernel<kRaw><<<blocks, 256, 0, stream>>>(
-                a.W, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm,
-                a.combined, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale);
+            TATARA_FWD(kRaw, float, false, a.W);
             break;
         case kPair:
-            ft_forward_kernel<kPair><<<blocks, 256, 0, stream>>>(
-                a.W, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm,
-                a.combined, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale);
+            if (h_out)
+                TATARA_FWD(kPair, _Float16, true, W16);
+            else if (W16)
+                TATARA_FWD(kPair, _Float16, false, W16);
+            else
+                TATARA_FWD(kPair, float, false, a.W);
             break;
         case kConcat:
-            ft_forward_kernel<kConcat><<<blocks, 256, 0, stream>>>(
-                a.W, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm,
-                a.combined, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale);
+            TATARA_FWD(kConcat, float, false, a.W);
             break;
         default:
             TATARA_REQUIRE(false, "unknown forward mode");
     }
+#undef TATARA_FWD
     TATARA_LAUNCHED("ft_forward");
     return kOk;
 }
@@ -570,40 +742,70 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     constexpr uint32_t kCols = kWave * V;
     TATARA_REQUIRE(a.ft_out % 4 == 0, "ft_out must be a multiple of 4");
     TATARA_REQUIRE(a.dft_row_stride % 4 == 0 && a.dft_chunk_stride % 4 == 0, "dft strides");
+    const bool hdft = a.dft16 != nullptr, hstate = a.m16 != nullptr;
+    TATARA_REQUIRE(!hstate || a.v16, "f16 moments need both m16 and v16");
     const uint32_t n_chunks = ceil_div(a.ft_out, kCols);
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-    ft_grad_update_kernel<V><<<blocks, 256, 0, stream>>>(a.dft, a.dft_row_stride, a.dft_chunk_stride,
-                                                         a.occ_vals, a.occ_off, a.w, a.m, a.v,
-                                                         a.slow, a.grad, a.ft_out, a.rows, n_chunks,
-                                                         a.apply_update, a.opt);
+    if (hdft && hstate)
+        ft_grad_update_kernel<4, true, true><<<blocks, 256, 0, stream>>>(a, ceil_div(a.ft_out, kWave * 4));
+    else if (hdft)
+        ft_grad_update_kernel<4, true, false><<<blocks, 256, 0, stream>>>(a, ceil_div(a.ft_out, kWave * 4));
+    else if (hstate)
+        ft_grad_update_kernel<V, false, true><<<blocks, 256, 0, stream>>>(a, n_chunks);
+    else
+        ft_grad_update_kernel<V, false, false><<<blocks, 256, 0, stream>>>(a, n_chunks);
     TATARA_LAUNCHED("ft_grad_update");
     return kOk;
 }
 
-int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb,
+int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
                                hipStream_t stream) {
     TATARA_REQUIRE(piece_inputs > 0 && a.rows % piece_inputs == 0,
                    "virtual fold: rows must be a multiple of piece_inputs");
     TATARA_REQUIRE(a.grad, "virtual fold needs the real-row gradients");
+    TATARA_REQUIRE(!(comb && comb16), "virtual fold writes one forward table");
     const uint32_t n_chunks = ceil_div(a.ft_out / 4, kWave);
     const uint64_t tasks = (uint64_t)piece_inputs * n_chunks;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-    ft_virtual_fold_kernel<<<blocks, 256, 0, stream>>>(a.grad, a.w, a.m, a.v, a.slow, comb, a.ft_out,
-                                                       a.rows, piece_inputs, n_chunks,
-                                                       a.apply_update, a.opt);
+    _Float16* c16 = reinterpret_cast<_Float16*>(comb16);
+    if (a.m16) {
+        if (comb16)
+            ft_virtual_fold_kernel<true, true><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+        else
+            ft_virtual_fold_kernel<true, false><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+    } else {
+        if (comb16)
+            ft_virtual_fold_kernel<false, true><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+        else
+            ft_virtual_fold_kernel<false, false><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+    }
     TATARA_LAUNCHED("ft_virtual_fold");
     return kOk;
 }
 
-int32_t launch_ft_fold(const float* w, float* comb, uint32_t ft_in, uint32_t ft_out,
+int32_t launch_ft_fold(const float* w, float* comb, uint16_t* comb16, uint32_t ft_in, uint32_t ft_out,
                        uint32_t piece_inputs, hipStream_t stream) {
     TATARA_REQUIRE(ft_out % 4 == 0 && piece_inputs > 0, "fold: ft_out%4==0, piece_inputs>0");
+    TATARA_REQUIRE((comb != nullptr) != (comb16 != nullptr), "fold: exactly one of comb / comb16");
     const uint64_t n4 = (uint64_t)ft_in * ft_out / 4;
     if (n4 == 0) return kOk;
-    ft_fold_kernel<<<ceil_div(n4, 256), 256, 0, stream>>>(w, comb, ft_in, ft_out, piece_inputs);
+    if (comb16)
+        ft_fold_kernel<true><<<ceil_div(n4, 256), 256, 0, stream>>>(
+            w, nullptr, reinterpret_cast<_Float16*>(comb16), ft_in, ft_out, piece_inputs);
+    else
+        ft_fold_kernel<false><<<ceil_div(n4, 256), 256, 0, stream>>>(w, comb, nullptr, ft_in, ft_out,
+                                                                      piece_inputs);
     TATARA_LAUNCHED("ft_fold");
+    return kOk;
+}
+
+int32_t launch_cast_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    const uint32_t blocks = ceil_div(n, 256) < 65536u ? ceil_div(n, 256) : 65536u;
+    cast_f16_kernel<<<blocks, 256, 0, stream>>>(src, reinterpret_cast<_Float16*>(dst), n);
+    TATARA_LAUNCHED("cast_f32_to_f16");
     return kOk;
 }
 

@@ -10,9 +10,14 @@
 
 namespace tatara {
 
+// 16-bit tables and activations are IEEE binary16 values held as uint16_t
+// (the --ft-fp16 / --ft-fp16-out / --fp16-opt-state modes of the reference,
+// bins/nnue_train/src/trainer_common.rs:49-61).
+
 struct FtForwardArgs {
     int mode;  // 0 raw sum, 1 LayerStack pairwise post, 2 Simple concat post
     const float* W;
+    const uint16_t* W16;  // f16 forward table, read instead of W when non-null
     const int32_t* idx_stm;
     const int32_t* idx_nstm;
     const int32_t* nnz;
@@ -20,6 +25,8 @@ struct FtForwardArgs {
     const float* bias;
     float* out_stm;
     float* out_nstm;
+    uint16_t* out_stm16;  // pairwise mode: f16 raw sums, written instead of out_* when non-null
+    uint16_t* out_nstm16;
     float* combined;
     uint32_t batch, ft_out, cols, max_active, n_persp;
     float scale;
@@ -45,10 +52,15 @@ struct FtGradArgs {
     // Row-major [2][batch][ft_out]: (ft_out, 256); chunk-major
     // [ceil(ft_out/256)][2*batch][256]: (256, 2*batch*256).
     const float* dft;
+    const uint16_t* dft16;     // f16 dft (values scaled by 1 / dft_inv_scale), read instead of dft
+    float dft_inv_scale;
     uint64_t dft_row_stride, dft_chunk_stride;
     const uint32_t* occ_vals;  // sorted dft row ids
     const uint32_t* occ_off;   // offsets by key 2*f+p
     float *w, *m, *v, *slow;
+    uint16_t *m16, *v16;       // f16 moments stored x m_scale / x v_scale, used instead of m / v
+    float m_scale, v_scale;
+    uint16_t* mirror16;        // f16 copy of every updated real row (unfactorized f16 forward), or null
     float* grad;               // gradient per row (required with a factorizer)
     uint32_t ft_out;
     uint32_t rows;             // real FT rows (ft_in)
@@ -67,10 +79,14 @@ uint32_t occurrence_key_bits(uint32_t cols);
 size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols);
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream);
 int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream);
-int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb,
+// comb or comb16 (f16) receives the rewritten forward rows; both may be null.
+int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
                                hipStream_t stream);
-int32_t launch_ft_fold(const float* w, float* comb, uint32_t ft_in, uint32_t ft_out,
+// comb = w + w_virtual (f32), or comb16 = f16(w + w_virtual) when comb is null.
+int32_t launch_ft_fold(const float* w, float* comb, uint16_t* comb16, uint32_t ft_in, uint32_t ft_out,
                        uint32_t piece_inputs, hipStream_t stream);
+// dst[i] = f16(src[i]), round to nearest even (cast_f32_to_f16).
+int32_t launch_cast_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream);
 int32_t launch_ft_reduce(float* grad, uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs,
                          hipStream_t stream);
 int32_t launch_radam(float* w, float* m, float* v, float* g, float* slow, uint64_t n,

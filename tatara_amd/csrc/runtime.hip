@@ -282,7 +282,7 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
 
 int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,
                                   uint32_t ft_out, uint32_t piece_inputs) {
-    int32_t st = launch_ft_fold(weight, comb, ft_in, ft_out, piece_inputs, 0);
+    int32_t st = launch_ft_fold(weight, comb, nullptr, ft_in, ft_out, piece_inputs, 0);
     if (st) return st;
     TATARA_HIP(hipDeviceSynchronize(), "ft_fold_virtual");
     return kOk;

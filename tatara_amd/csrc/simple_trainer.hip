@@ -73,6 +73,8 @@ class SimpleTrainer final : public TrainerBase {
                        "Simple (l1, l2) must be (32, 32) or (16, 32)");
         TATARA_REQUIRE(c.optimizer >= 0 && c.optimizer <= 2, "unknown optimizer");
         TATARA_REQUIRE(c.piece_inputs >= 0, "piece_inputs >= 0");
+        TATARA_REQUIRE(!c.ft_fp16 && !c.ft_fp16_out && !c.fp16_opt_state,
+                       "the f16 modes are built for the LayerStack architecture only");
         if (c.piece_inputs > 0)
             TATARA_REQUIRE(c.ft_in % c.piece_inputs == 0, "ft_in must be a multiple of piece_inputs");
         int32_t st;
@@ -194,7 +196,7 @@ class SimpleTrainer final : public TrainerBase {
 
     int32_t sync_forward_weights() override {
         if (!factorized) return kOk;
-        int32_t st = launch_ft_fold(ft.w, comb, ft_in, ft_out, pi, stream);
+        int32_t st = launch_ft_fold(ft.w, comb, nullptr, ft_in, ft_out, pi, stream);
         if (st) return st;
         TATARA_HIP(hipStreamSynchronize(stream), "sync_forward_weights");
         return kOk;
@@ -212,7 +214,7 @@ class SimpleTrainer final : public TrainerBase {
     int32_t copy_activation(const char* name, float* host, uint64_t n) override {
         const bool s = !std::strcmp(name, "dft_stm"), ns = !std::strcmp(name, "dft_nstm");
         if (!s && !ns) return TrainerBase::copy_activation(name, host, n);
-        return copy_chunk_major(dft, last_b, ft_out, ns ? 1 : 0, host, n);
+        return copy_chunk_major(dft, false, last_b, ft_out, ns ? 1 : 0, host, n);
     }
 
     const float* activation(const char* name, uint64_t& cap) override {
@@ -376,7 +378,7 @@ class SimpleTrainer final : public TrainerBase {
         if ((st = join_side())) return st;
         if ((st = launch_ft_grad_update(fb, stream))) return st;
         if ((st = prof_mark(5))) return st;
-        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;
+        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, nullptr, stream))) return st;
         if ((st = prof_mark(6))) return st;
         SimpleDenseGroup groups[7];
         for (int k = 0; k < 7; ++k) {

@@ -45,6 +45,11 @@ namespace {
 constexpr float kFtPostScale = 127.0f / 128.0f;  // arch.rs FT_POST_SCALE
 constexpr float kL1SqrScale = 127.0f / 128.0f;   // arch.rs L1_SQR_SCALE
 constexpr float kQuantClamp = 127.0f / 64.0f;    // i8::MAX / QB
+// f16 modes (bins/nnue_train/src/trainer_common.rs:134-166): dft loss scale
+// base (x batch), ft_w moment scales
+constexpr float kDftF16BaseScale = 16384.0f;              // FT_DFT_FP16_BASE_SCALE = 2^14
+constexpr float kMomentF16Scale = 268435456.0f;           // FT_OPT_M_SCALE = 2^28
+constexpr float kVelocityF16Scale = 1099511627776.0f;     // FT_OPT_V_SCALE = 2^40
 
 __global__ void bucket_keys_kernel(const int32_t* __restrict__ bucket, uint8_t* __restrict__ keys,
                                    uint32_t n, uint32_t nb) {
@@ -70,6 +75,13 @@ class LayerStackTrainer final : public TrainerBase {
     ParamGroup ft;          // ft_w
     ParamGroup small[9];    // uniform_optim_group_layout order
     float* comb = nullptr;  // factorized forward table [ft_in][ft_out]
+    // mixed precision (PrecisionFlags): f16 forward table, f16 FT activations
+    // and dft, f16 ft_w moments
+    bool h_fwd = false, h_out = false, h_state = false;
+    uint16_t* fwd16 = nullptr;  // [ft_in][ft_out] f16 comb (factorizer) or mirror of the real rows
+    uint16_t *ft_stm16 = nullptr, *ft_nstm16 = nullptr, *dft16 = nullptr;
+    unsigned long long* clamp_ctr = nullptr;  // cumulative dft clamps
+    uint64_t clamp_elems = 0;                 // cumulative dft values written
 
     // schedule
     uint32_t n_king_bins = 1;
@@ -110,9 +122,14 @@ class LayerStackTrainer final : public TrainerBase {
         TATARA_REQUIRE(c.piece_inputs >= 0, "piece_inputs >= 0");
         if (c.piece_inputs > 0)
             TATARA_REQUIRE(c.ft_in % c.piece_inputs == 0, "ft_in must be a multiple of piece_inputs");
+        // trainer_layerstack.rs:801-805
+        TATARA_REQUIRE(!c.ft_fp16_out || c.ft_fp16, "ft_fp16_out requires ft_fp16");
         int32_t st;
         if ((st = init_runtime(c.device))) return st;
 
+        h_fwd = c.ft_fp16 != 0;
+        h_out = c.ft_fp16_out != 0;
+        h_state = c.fp16_opt_state != 0;
         ft_in = c.ft_in;
         pi = c.piece_inputs;
         factorized = pi > 0;
@@ -130,8 +147,10 @@ class LayerStackTrainer final : public TrainerBase {
         const uint32_t l2_in = 2 * (l1 - 1);
 
         if ((st = alloc_group(ft, "ft_w", (uint64_t)train_ft_in * ft_out, fmin, fmax, 0,
-                              keep || c.piece_inputs > 0)))
+                              keep || c.piece_inputs > 0, h_state)))
             return st;
+        ft.m_scale = kMomentF16Scale;
+        ft.v_scale = kVelocityF16Scale;
         const struct {
             const char* name;
             uint64_t n;
@@ -154,7 +173,12 @@ class LayerStackTrainer final : public TrainerBase {
             if ((st = alloc_group(small[k], layout[k].name, layout[k].n, mn, mx, layout[k].kind, true)))
                 return st;
         }
-        if (factorized && (st = arena.alloc(&comb, (uint64_t)ft_in * ft_out))) return st;
+        if (h_fwd) {
+            if ((st = arena.alloc(&fwd16, (uint64_t)ft_in * ft_out))) return st;
+        } else if (factorized && (st = arena.alloc(&comb, (uint64_t)ft_in * ft_out))) {
+            return st;
+        }
+        if ((st = arena.alloc(&clamp_ctr, 1))) return st;
 
         // initial weights: LayerStackInit::default_uniform; FT real block sampled
         // with the base fan-in, factorizer rows appended as zeros (:844-870)
@@ -192,10 +216,17 @@ class LayerStackTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
-        if ((st = arena.alloc(&ft_stm, B * ft_out, false)) || (st = arena.alloc(&ft_nstm, B * ft_out, false)) ||
-            (st = arena.alloc(&combined, B * ft_out, false)) || (st = arena.alloc(&dft, 2 * B * dft_chunks() * kDftChunk, false)) ||
-            (st = arena.alloc(&l1_sorted, P * 2 * l1)) || (st = arena.alloc(&dl1_sorted, P * l1)) ||
-            (st = arena.alloc(&net_out, B)))
+        const uint64_t dft_n = 2 * B * dft_chunks() * kDftChunk;
+        if (h_out) {
+            if ((st = arena.alloc(&ft_stm16, B * ft_out, false)) || (st = arena.alloc(&ft_nstm16, B * ft_out, false)) ||
+                (st = arena.alloc(&dft16, dft_n, false)))
+                return st;
+        } else if ((st = arena.alloc(&ft_stm, B * ft_out, false)) ||
+                   (st = arena.alloc(&ft_nstm, B * ft_out, false)) || (st = arena.alloc(&dft, dft_n, false))) {
+            return st;
+        }
+        if ((st = arena.alloc(&combined, B * ft_out, false)) || (st = arena.alloc(&l1_sorted, P * 2 * l1)) ||
+            (st = arena.alloc(&dl1_sorted, P * l1)) || (st = arena.alloc(&net_out, B)))
             return st;
         const TailDims td{l1, l2, nb};
         const uint64_t n_tail = ls_tail_workgroups(max_p), n_post = ls_post_workgroups(max_p);
@@ -238,9 +269,28 @@ class LayerStackTrainer final : public TrainerBase {
         return write_layerstack_bin(path, fs, src, bias, l1, l2, nb, h, has_fv != 0, fv, stream);
     }
 
+    int32_t fp16_clamp_count(uint64_t* clamps, uint64_t* elems) override {
+        unsigned long long c = 0;
+        TATARA_HIP(hipMemcpyAsync(&c, clamp_ctr, sizeof c, hipMemcpyDeviceToHost, stream), "clamp count");
+        TATARA_HIP(hipStreamSynchronize(stream), "clamp count");
+        *clamps = c;
+        *elems = clamp_elems;
+        return kOk;
+    }
+
+    // Rebuilds the forward table from the master weights: f32 comb, f16 comb
+    // (ft_fold_virtual_f16) or the f16 mirror (cast_f32_to_f16,
+    // trainer_layerstack.rs:1782-1835).
     int32_t sync_forward_weights() override {
-        if (!factorized) return kOk;
-        int32_t st = launch_ft_fold(ft.w, comb, ft_in, ft_out, pi, stream);
+        int32_t st = kOk;
+        if (h_fwd && factorized)
+            st = launch_ft_fold(ft.w, nullptr, fwd16, ft_in, ft_out, pi, stream);
+        else if (h_fwd)
+            st = launch_cast_f16(ft.w, fwd16, (uint64_t)ft_in * ft_out, stream);
+        else if (factorized)
+            st = launch_ft_fold(ft.w, comb, nullptr, ft_in, ft_out, pi, stream);
+        else
+            return kOk;
         if (st) return st;
         TATARA_HIP(hipStreamSynchronize(stream), "sync_forward_weights");
         return kOk;
@@ -275,6 +325,11 @@ class LayerStackTrainer final : public TrainerBase {
         a.dl1_sorted = dl1_sorted;
         a.net_output = net_out;
         a.dft = dft;
+        a.ft_stm16 = ft_stm16;
+        a.ft_nstm16 = ft_nstm16;
+        a.dft16 = dft16;
+        a.dft_scale = kDftF16BaseScale * (float)p.b;
+        a.clamp_counter = clamp_ctr;
         a.score = p.score;
         a.wdl = p.wdl;
         a.per_pos_norm = p.b ? 1.0f / (float)p.b : 0.0f;
@@ -375,6 +430,9 @@ class LayerStackTrainer final : public TrainerBase {
         FtForwardArgs fa{};
         fa.mode = 1;
         fa.W = factorized ? comb : ft.w;
+        fa.W16 = h_fwd ? fwd16 : nullptr;
+        fa.out_stm16 = ft_stm16;
+        fa.out_nstm16 = ft_nstm16;
         fa.idx_stm = p.stm;
         fa.idx_nstm = p.nstm;
         fa.nnz = p.nnz;
@@ -428,6 +486,8 @@ class LayerStackTrainer final : public TrainerBase {
         const OptScalars sb = scalars(2, lr, step_count);
         FtGradArgs fb{};
         fb.dft = dft;
+        fb.dft16 = dft16;
+        fb.dft_inv_scale = 1.0f / da.dft_scale;
         fb.dft_row_stride = kDftChunk;  // chunk-major [chunk][2*b][256]
         fb.dft_chunk_stride = 2ull * p.b * kDftChunk;
         fb.occ_vals = occ_vo;
@@ -435,6 +495,11 @@ class LayerStackTrainer final : public TrainerBase {
         fb.w = ft.w;
         fb.m = ft.m;
         fb.v = ft.v;
+        fb.m16 = ft.m16;
+        fb.v16 = ft.v16;
+        fb.m_scale = ft.m_scale;
+        fb.v_scale = ft.v_scale;
+        fb.mirror16 = (h_fwd && !factorized) ? fwd16 : nullptr;
         fb.slow = ft.slow;
         fb.grad = ft.grad;
         fb.ft_out = ft_out;
@@ -444,7 +509,8 @@ class LayerStackTrainer final : public TrainerBase {
         if ((st = join_side())) return st;
         if ((st = launch_ft_grad_update(fb, stream))) return st;
         if ((st = prof_mark(5))) return st;
-        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, stream))) return st;
+        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, h_fwd ? fwd16 : nullptr, stream))) return st;
+        if (h_out) clamp_elems += 2ull * p.b * ft_out;
         if ((st = prof_mark(6))) return st;
         LsDenseGroup groups[9];
         for (int k = 0; k < 9; ++k) {
@@ -494,9 +560,17 @@ class LayerStackTrainer final : public TrainerBase {
     uint32_t dft_chunks() const { return ceil_div(ft_out, kDftChunk); }
 
     int32_t copy_activation(const char* name, float* host, uint64_t n) override {
+        // f16 activations are returned as the f32 values of what is stored
+        // (the dft scaled by 2^14 * batch)
         const bool s = !std::strcmp(name, "dft_stm"), ns = !std::strcmp(name, "dft_nstm");
-        if (!s && !ns) return TrainerBase::copy_activation(name, host, n);
-        return copy_chunk_major(dft, last_b, ft_out, ns ? 1 : 0, host, n);
+        if (s || ns)
+            return copy_chunk_major(h_out ? (const void*)dft16 : (const void*)dft, h_out, last_b, ft_out, ns ? 1 : 0,
+                                    host, n);
+        if (h_out && (!std::strcmp(name, "ft_stm_out") || !std::strcmp(name, "ft_nstm_out"))) {
+            TATARA_REQUIRE(n <= (uint64_t)last_b * ft_out, "activation request exceeds the last batch");
+            return copy_f16(!std::strcmp(name, "ft_stm_out") ? ft_stm16 : ft_nstm16, host, n);
+        }
+        return TrainerBase::copy_activation(name, host, n);
     }
 
     const float* activation(const char* name, uint64_t& cap) override {
@@ -585,6 +659,23 @@ static float* group_ptr(ParamGroup* g, int32_t which) {
     }
 }
 
+// f16 moments (MomentBuf::F16): which 1 / 2 are read back as f16 * (1 / scale)
+// (MomentBuf::to_host_f32) and written as f16(clamp(x * scale, +-65504))
+// (MomentBuf::from_host_f32), trainer_common.rs:78-132.
+static bool f16_moment(ParamGroup* g, int32_t which, uint16_t*& dev, float& scale) {
+    if (which == 1 && g->m16) {
+        dev = g->m16;
+        scale = g->m_scale;
+        return true;
+    }
+    if (which == 2 && g->v16) {
+        dev = g->v16;
+        scale = g->v_scale;
+        return true;
+    }
+    return false;
+}
+
 int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int32_t which,
                                   float* host, uint64_t n) {
     TATARA_REQUIRE(trainer && name && host, "null argument");
@@ -594,6 +685,15 @@ int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int3
     TATARA_REQUIRE(which >= 0 && which <= 4, "which must be 0..4");
     TATARA_REQUIRE(n == g->n, "element count mismatch");
     TATARA_HIP(hipStreamSynchronize(t.stream), "get_tensor sync");
+    uint16_t* dev16 = nullptr;
+    float scale = 1.0f;
+    if (f16_moment(g, which, dev16, scale)) {
+        std::vector<_Float16> h(n);
+        TATARA_HIP(hipMemcpy(h.data(), dev16, n * 2, hipMemcpyDeviceToHost), "get_tensor");
+        const float inv = 1.0f / scale;
+        for (uint64_t i = 0; i < n; ++i) host[i] = (float)h[i] * inv;
+        return kOk;
+    }
     float* src = group_ptr(g, which);
     if (which == 4 && !t.cfg.keep_grads) src = nullptr;
     if (!src) {
@@ -612,12 +712,29 @@ int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int3
     ParamGroup* g = t.find(name);
     TATARA_REQUIRE(g, std::string("unknown tensor ") + name);
     TATARA_REQUIRE(n == g->n, "element count mismatch");
+    TATARA_HIP(hipStreamSynchronize(t.stream), "set_tensor sync");
+    uint16_t* dev16 = nullptr;
+    float scale = 1.0f;
+    if (f16_moment(g, which, dev16, scale)) {
+        std::vector<_Float16> h(n);
+        for (uint64_t i = 0; i < n; ++i) {
+            float x = host[i] * scale;
+            x = x < -65504.0f ? -65504.0f : (x > 65504.0f ? 65504.0f : x);
+            h[i] = (_Float16)x;
+        }
+        TATARA_HIP(hipMemcpy(dev16, h.data(), n * 2, hipMemcpyHostToDevice), "set_tensor");
+        return kOk;
+    }
     float* dst = group_ptr(g, which);
     TATARA_REQUIRE(dst, "tensor not allocated (which)");
-    TATARA_HIP(hipStreamSynchronize(t.stream), "set_tensor sync");
     TATARA_HIP(hipMemcpy(dst, host, n * sizeof(float), hipMemcpyHostToDevice), "set_tensor");
     if (!std::strcmp(name, "ft_w") && which == 0) return t.sync_forward_weights();
     return kOk;
+}
+
+int32_t tatara_trainer_fp16_clamp_count(TataraTrainer* trainer, uint64_t* clamps, uint64_t* elems) {
+    TATARA_REQUIRE(trainer && clamps && elems, "null argument");
+    return trainer->t->fp16_clamp_count(clamps, elems);
 }
 
 int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const char* name, float* host,

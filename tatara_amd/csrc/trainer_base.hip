@@ -52,16 +52,19 @@ int32_t TrainerBase::alloc_inputs(uint64_t B, uint32_t max_active) {
 }
 
 int32_t TrainerBase::alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx,
-                                 int kind, bool with_grad) {
+                                 int kind, bool with_grad, bool f16_moments) {
     g.name = name;
     g.n = n;
     g.min_w = mn;
     g.max_w = mx;
     g.kind = kind;
     int32_t st;
-    if ((st = arena.alloc(&g.w, n)) || (st = arena.alloc(&g.m, n)) || (st = arena.alloc(&g.v, n)) ||
-        (st = arena.alloc(&g.slow, n)))
+    if ((st = arena.alloc(&g.w, n)) || (st = arena.alloc(&g.slow, n))) return st;
+    if (f16_moments) {
+        if ((st = arena.alloc(&g.m16, n)) || (st = arena.alloc(&g.v16, n))) return st;
+    } else if ((st = arena.alloc(&g.m, n)) || (st = arena.alloc(&g.v, n))) {
         return st;
+    }
     if (with_grad && (st = arena.alloc(&g.grad, n))) return st;
     return kOk;
 }
@@ -245,19 +248,33 @@ int32_t TrainerBase::copy_activation(const char* name, float* host, uint64_t n) 
     return kOk;
 }
 
-int32_t TrainerBase::copy_chunk_major(const float* dev, uint32_t b, uint32_t width, int persp,
+int32_t TrainerBase::copy_chunk_major(const void* dev, bool f16, uint32_t b, uint32_t width, int persp,
                                       float* host, uint64_t n) {
     constexpr uint32_t kChunk = 256;
     TATARA_REQUIRE(n <= (uint64_t)b * width, "activation request exceeds the last batch");
     TATARA_HIP(hipStreamSynchronize(stream), "get_activation sync");
     const uint32_t chunks = (width + kChunk - 1) / kChunk;
-    std::vector<float> all((uint64_t)chunks * 2 * b * kChunk);
-    TATARA_HIP(hipMemcpy(all.data(), dev, all.size() * sizeof(float), hipMemcpyDeviceToHost),
-               "get_activation");
+    const uint64_t total = (uint64_t)chunks * 2 * b * kChunk;
+    std::vector<float> all(total);
+    if (f16) {
+        std::vector<_Float16> h(total);
+        TATARA_HIP(hipMemcpy(h.data(), dev, total * 2, hipMemcpyDeviceToHost), "get_activation");
+        for (uint64_t i = 0; i < total; ++i) all[i] = (float)h[i];
+    } else {
+        TATARA_HIP(hipMemcpy(all.data(), dev, total * sizeof(float), hipMemcpyDeviceToHost), "get_activation");
+    }
     for (uint64_t i = 0; i < n; ++i) {
         const uint64_t r = i / width, c = i % width;
         host[i] = all[((c / kChunk) * 2 * b + (uint64_t)persp * b + r) * kChunk + c % kChunk];
     }
+    return kOk;
+}
+
+int32_t TrainerBase::copy_f16(const uint16_t* dev, float* host, uint64_t n) {
+    TATARA_HIP(hipStreamSynchronize(stream), "get_activation sync");
+    std::vector<_Float16> h(n);
+    TATARA_HIP(hipMemcpy(h.data(), dev, n * 2, hipMemcpyDeviceToHost), "get_activation");
+    for (uint64_t i = 0; i < n; ++i) host[i] = (float)h[i];
     return kOk;
 }
 

@@ -36,6 +36,10 @@ struct DeviceArena {
 struct ParamGroup {
     const char* name = "";
     float *w = nullptr, *m = nullptr, *v = nullptr, *slow = nullptr, *grad = nullptr;
+    // f16 moments stored x m_scale / x v_scale, allocated instead of m / v
+    // (MomentBuf::F16, bins/nnue_train/src/trainer_common.rs:63-132)
+    uint16_t *m16 = nullptr, *v16 = nullptr;
+    float m_scale = 1.0f, v_scale = 1.0f;
     uint64_t n = 0;
     float min_w = 0.f, max_w = 0.f;
     int32_t kind = 0;  // 0 ft, 1 dense, 2 bias
@@ -80,6 +84,12 @@ class TrainerBase {
     // (feature_set: TATARA_FS_*).
     virtual int32_t export_quantised(const char* path, int32_t feature_set, int32_t has_fv_scale,
                                      int32_t fv_scale) = 0;
+    // Cumulative dft clamps and dft values written in the f16 activation path.
+    virtual int32_t fp16_clamp_count(uint64_t* clamps, uint64_t* elems) {
+        *clamps = 0;
+        *elems = 0;
+        return kOk;
+    }
 
     int32_t flush(double* out);
     int32_t prof_collect();
@@ -101,7 +111,7 @@ class TrainerBase {
     int32_t init_runtime(int device);
     int32_t alloc_inputs(uint64_t max_b, uint32_t max_active);
     int32_t alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx, int kind,
-                        bool with_grad);
+                        bool with_grad, bool f16_moments = false);
     int32_t upload(float* dst, const std::vector<float>& src);
     // Synchronous copy of a group's weights to the host.
     int32_t download(const ParamGroup& g, std::vector<float>& out);
@@ -114,9 +124,12 @@ class TrainerBase {
     // Queues this step's loss (device f64 at loss_dev[slot]) and returns the previous one.
     int32_t queue_loss(const double* loss_dev, int slot, double* lagged);
     int32_t prof_mark(int k);
-    // Row-major copy of perspective persp of a chunk-major [chunk][2*b][256] buffer.
-    int32_t copy_chunk_major(const float* dev, uint32_t b, uint32_t width, int persp, float* host,
+    // Row-major copy of perspective persp of a chunk-major [chunk][2*b][256]
+    // buffer of f32, or (f16 = true) of f16 values returned as f32.
+    int32_t copy_chunk_major(const void* dev, bool f16, uint32_t b, uint32_t width, int persp, float* host,
                              uint64_t n);
+    // The first n f16 values of a device buffer, as f32.
+    int32_t copy_f16(const uint16_t* dev, float* host, uint64_t n);
     // side waits for everything enqueued on stream so far
     int32_t fork_side();
     // stream waits for everything enqueued on side so far

@@ -229,6 +229,16 @@ class LayerStackConfig:
     bias_lr_mult: float = 1.0
     device: int = 0
     keep_grads: bool = False
+    # PrecisionFlags (trainer_common.rs:49-61); all_optim() sets the three
+    ft_fp16: bool = False
+    ft_fp16_out: bool = False
+    fp16_opt_state: bool = False
+
+    def all_optim(self) -> "LayerStackConfig":
+        """The --all-optim precision flags (cli.rs:627-638) on a copy of this config."""
+        import dataclasses
+
+        return dataclasses.replace(self, ft_fp16=True, ft_fp16_out=True, fp16_opt_state=True)
 
     def to_c(self) -> TataraTrainerConfig:
         wd = self.weight_decay
@@ -251,6 +261,9 @@ class LayerStackConfig:
             dense_lr_mult=self.dense_lr_mult,
             bias_lr_mult=self.bias_lr_mult,
             keep_grads=1 if self.keep_grads else 0,
+            ft_fp16=int(self.ft_fp16),
+            ft_fp16_out=int(self.ft_fp16_out),
+            fp16_opt_state=int(self.fp16_opt_state),
         )
 
     @property
@@ -457,6 +470,12 @@ class LayerStackTrainer(_Trainer):
 
     def __init__(self, config: LayerStackConfig):
         super().__init__(config)
+
+    def fp16_clamp_count(self) -> tuple[int, int]:
+        """read_fp16_clamp_count: cumulative (dft values clamped, dft values written)."""
+        c, e = C.c_uint64(), C.c_uint64()
+        check(self._lib.tatara_trainer_fp16_clamp_count(self._h, C.byref(c), C.byref(e)))
+        return c.value, e.value
 
     def save_quantised(self, path, feature_set, fv_scale=None) -> None:
         """LayerStackWeights::save_quantised of the current weights (OutputFormat::Tatara);

@@ -27,10 +27,13 @@ def close(got, exp, rtol, atol_frac=0.0, atol=0.0, what=""):
     tol = atol + atol_frac * scale + rtol * np.abs(exp)
     err = np.abs(got - exp)
     bad = err > tol
-    assert not bad.any(), (
-        f"{what}: {bad.sum()} / {bad.size} outside tolerance; worst abs err {err.max():.3e} "
-        f"at {int(err.argmax())} (got {got.ravel()[err.argmax()]:.9g}, exp {exp.ravel()[err.argmax()]:.9g})"
-    )
+    if bad.any():
+        ratio = np.where(tol > 0, err / np.where(tol > 0, tol, 1.0), np.inf)
+        i = int(np.argmax(np.where(bad, ratio, -1.0)))
+        raise AssertionError(
+            f"{what}: {bad.sum()} / {bad.size} outside tolerance; worst at {i}: got {got.ravel()[i]:.9g}, "
+            f"exp {exp.ravel()[i]:.9g}, err {err.ravel()[i]:.3e} > tol {tol.ravel()[i]:.3e} "
+            f"(largest abs err {err.max():.3e})")
 
 
 def make(nb=8, ft_out=256, l1=16, optimizer="ranger", b=256, keep=True, factorize=True):
