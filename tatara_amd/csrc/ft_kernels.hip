@@ -240,6 +240,96 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Forward gather from an f16 table, pairwise post (LayerStack).  As the
+// kPair mode above, but every lane owns eight columns (one 16-byte f16 load
+// per gathered row, half the load instructions of four-column lanes): lane
+// j < 32 of chunk c owns columns 8(32c + j) .. +7 of the first half and lane
+// j + 32 their partners in the second half.  Sums are f32 in slot order;
+// HOUT rounds them to f16 before they are stored and before the post reads
+// them.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f8v __attribute__((ext_vector_type(8)));
+
+template <bool HOUT>
+__global__ __launch_bounds__(256) void ft_forward_pair16_kernel(
+    const _Float16* __restrict__ W, const int32_t* __restrict__ idx_stm, const int32_t* __restrict__ idx_nstm,
+    const int32_t* __restrict__ nnz, const int32_t* __restrict__ schedule, const float* __restrict__ bias,
+    float* __restrict__ out_stm, float* __restrict__ out_nstm, _Float16* __restrict__ out16_stm,
+    _Float16* __restrict__ out16_nstm, float* __restrict__ combined, uint32_t batch, uint32_t ft_out,
+    uint32_t cols, uint32_t max_active, uint32_t n_chunks, uint32_t n_persp, float scale) {
+    __shared__ int s_idx_all[kWavesPerBlock][kMaxActive];
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
+    const uint64_t per_persp = (uint64_t)n_chunks * batch;
+    if (task >= per_persp * n_persp) return;
+    const uint32_t persp = (uint32_t)(task / per_persp);
+    const uint64_t rem = task - (uint64_t)persp * per_persp;
+    const uint32_t chunk = (uint32_t)(rem / batch);
+    const uint32_t slot = (uint32_t)(rem - (uint64_t)chunk * batch);
+    const uint32_t pos = schedule ? (uint32_t)schedule[(uint64_t)persp * batch + slot] : slot;
+    if (pos >= batch) return;
+
+    const int32_t* idx = persp == 0 ? idx_stm : idx_nstm;
+    int* s_idx = s_idx_all[wave];
+    const int nv = compact_indices(idx + (uint64_t)pos * max_active, nnz[pos], cols, max_active, s_idx);
+
+    const uint32_t half8 = ft_out / 16;  // 8-column groups per half
+    const uint32_t row8 = ft_out / 8;
+    const uint32_t j = lane & 31u;
+    const uint32_t qp = chunk * 32 + j;  // group index within the first half
+    const bool active = qp < half8;
+    const uint32_t q = lane < 32 ? qp : qp + half8;
+    const h8* __restrict__ W8 = reinterpret_cast<const h8*>(W);
+    f8v acc = 0.0f;
+    if (active) {
+        constexpr int U = 8;
+        int k = 0;
+        for (; k + U <= nv; k += U) {
+            h8 w[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint64_t r = (uint32_t)__builtin_amdgcn_readfirstlane(s_idx[k + u]);
+                w[u] = W8[r * row8 + q];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc += __builtin_convertvector(w[u], f8v);
+        }
+        for (; k < nv; ++k) {
+            const uint64_t r = (uint32_t)__builtin_amdgcn_readfirstlane(s_idx[k]);
+            acc += __builtin_convertvector(W8[r * row8 + q], f8v);
+        }
+    }
+    h8 r16;
+    if (HOUT) {
+        r16 = __builtin_convertvector(acc, h8);
+        acc = __builtin_convertvector(r16, f8v);
+    }
+    f8v p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(acc[e], 32);
+    if (!active) return;
+    if (HOUT) {
+        _Float16* o = persp == 0 ? out16_stm : out16_nstm;
+        __builtin_nontemporal_store(r16, reinterpret_cast<h8*>(o + (uint64_t)pos * ft_out) + q);
+    } else {
+        float* o = persp == 0 ? out_stm : out_nstm;
+        __builtin_nontemporal_store(acc, reinterpret_cast<f8v*>(o + (uint64_t)pos * ft_out) + q);
+    }
+    if (lane >= 32) return;
+    const f8v b0 = reinterpret_cast<const f8v*>(bias)[qp];
+    const f8v b1 = reinterpret_cast<const f8v*>(bias)[qp + half8];
+    f8v c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c[e] = crelu01(acc[e] + b0[e]) * crelu01(p[e] + b1[e]) * scale;
+    __builtin_nontemporal_store(
+        c, reinterpret_cast<f8v*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2)) + qp);
+}
+
+// ---------------------------------------------------------------------------
 // Forward schedule keys: item p*batch + b gets key p*n_bins + (king block of
 // position b in perspective p), where the king block is the first valid
 // index divided by piece_inputs.  A stable bin sort of these keys yields,
@@ -357,26 +447,27 @@ __device__ __forceinline__ vecf<V> segment_sum(const vecf<V>* __restrict__ dft, 
     return acc;
 }
 
-// The same sequential sum over f16 dft rows (four values per lane), in f32.
-__device__ __forceinline__ vecf<4> segment_sum_f16(const vech<4>* __restrict__ dft, uint64_t row_v,
+// The same sequential sum over f16 dft rows (V values per lane), in f32.
+template <int V>
+__device__ __forceinline__ vecf<V> segment_sum_f16(const vech<V>* __restrict__ dft, uint64_t row_v,
                                                    const uint32_t* __restrict__ vals, uint32_t s,
                                                    uint32_t e, uint64_t q) {
-    vecf<4> acc = 0.0f;
-    constexpr int U = 16;
+    vecf<V> acc = 0.0f;
+    constexpr int U = 64 / V;
     uint32_t i = s;
     for (; i + U <= e; i += U) {
-        vech<4> d[U];
+        vech<V> d[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i + u]);
             d[u] = dft[r * row_v + q];
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc += __builtin_convertvector(d[u], vecf<4>);
+        for (int u = 0; u < U; ++u) acc += __builtin_convertvector(d[u], vecf<V>);
     }
     for (; i < e; ++i) {
         const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i]);
-        acc += __builtin_convertvector(dft[r * row_v + q], vecf<4>);
+        acc += __builtin_convertvector(dft[r * row_v + q], vecf<V>);
     }
     return acc;
 }
@@ -480,8 +571,8 @@ __device__ __forceinline__ void update_cells(const FtGradArgs& a, uint64_t off, 
 template <int V, bool HDFT, bool HSTATE>
 __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint32_t n_chunks) {
     constexpr uint32_t kCols = kWave * V;
-    static_assert(kDftChunk % kCols == 0, "a wave's columns must lie in one dft chunk");
-    static_assert(!HDFT || V == 4, "the f16 dft gather reads four values per lane");
+    static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
+                  "a lane's values must lie in one dft chunk");
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -497,8 +588,8 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
         ((uint64_t)(col / kDftChunk) * a.dft_chunk_stride + col % kDftChunk) / V;
     vecf<V> gr;
     if constexpr (HDFT) {
-        gr = segment_sum_f16(reinterpret_cast<const vech<4>*>(a.dft16), a.dft_row_stride / 4, a.occ_vals, s0,
-                             s1, q);
+        gr = segment_sum_f16<V>(reinterpret_cast<const vech<V>*>(a.dft16), a.dft_row_stride / V, a.occ_vals, s0,
+                                s1, q);
         gr *= a.dft_inv_scale;
     } else {
         gr = segment_sum<V>(reinterpret_cast<const vecf<V>*>(a.dft), a.dft_row_stride / V, a.occ_vals, s0, s1,
@@ -673,12 +764,23 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
             TATARA_FWD(kRaw, float, false, a.W);
             break;
         case kPair:
-            if (h_out)
-                TATARA_FWD(kPair, _Float16, true, W16);
-            else if (W16)
-                TATARA_FWD(kPair, _Float16, false, W16);
-            else
+            if (W16) {
+                // eight columns per lane: a chunk covers 256 pairs
+                TATARA_REQUIRE(a.ft_out % 16 == 0, "an f16 table needs ft_out % 16 == 0");
+                const uint32_t c16 = ceil_div(a.ft_out / 16, 32);
+                const uint64_t t16 = (uint64_t)a.n_persp * c16 * a.batch;
+                const uint32_t b16 = (uint32_t)((t16 + kWavesPerBlock - 1) / kWavesPerBlock);
+                if (h_out)
+                    ft_forward_pair16_kernel<true><<<b16, 256, 0, stream>>>(
+                        W16, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm, o16s, o16n,
+                        a.combined, a.batch, a.ft_out, a.cols, a.max_active, c16, a.n_persp, a.scale);
+                else
+                    ft_forward_pair16_kernel<false><<<b16, 256, 0, stream>>>(
+                        W16, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm, o16s, o16n,
+                        a.combined, a.batch, a.ft_out, a.cols, a.max_active, c16, a.n_persp, a.scale);
+            } else {
                 TATARA_FWD(kPair, float, false, a.W);
+            }
             break;
         case kConcat:
             TATARA_FWD(kConcat, float, false, a.W);
@@ -748,11 +850,17 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-    if (hdft && hstate)
-        ft_grad_update_kernel<4, true, true><<<blocks, 256, 0, stream>>>(a, ceil_div(a.ft_out, kWave * 4));
-    else if (hdft)
-        ft_grad_update_kernel<4, true, false><<<blocks, 256, 0, stream>>>(a, ceil_div(a.ft_out, kWave * 4));
-    else if (hstate)
+    if (hdft) {
+        // four f16 values per lane: a wave's rows are 512 bytes, so a king
+        // block's dft working set stays half the f32 one (eight values per
+        // lane halve the loads but double that working set, and measure slower)
+        const uint32_t c4 = ceil_div(a.ft_out, kWave * 4);
+        const uint32_t b4 = (uint32_t)(((uint64_t)a.rows * c4 + kWavesPerBlock - 1) / kWavesPerBlock);
+        if (hstate)
+            ft_grad_update_kernel<4, true, true><<<b4, 256, 0, stream>>>(a, c4);
+        else
+            ft_grad_update_kernel<4, true, false><<<b4, 256, 0, stream>>>(a, c4);
+    } else if (hstate)
         ft_grad_update_kernel<V, false, true><<<blocks, 256, 0, stream>>>(a, n_chunks);
     else
         ft_grad_update_kernel<V, false, false><<<blocks, 256, 0, stream>>>(a, n_chunks);
