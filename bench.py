@@ -121,7 +121,8 @@ WRM290 = {"kind": "wrm", "nnue2score": 290.0, "in_scaling": 290.0, "in_offset": 
 SIGMOID = {"kind": "sigmoid", "scale": 1.0 / 290.0}
 
 
-def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:  # noqa: C901
+def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int, min_seconds: float = 12.0,
+                 max_steps: int = 40) -> dict:  # noqa: C901
     """Oracle (CPU restatement) step on this host, bounded sample of the same workload."""
     from oracle import ffi
 
@@ -141,9 +142,8 @@ def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:  # noqa: 
         if prec.fp16_opt_state:
             st = ols.to_f16_state(st)
         opt = ols.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
-        t0 = time.perf_counter()
-        ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, 1, prec)
-        dt = time.perf_counter() - t0
+        def one(step):
+            ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, step, prec)
     else:
         from oracle import simple as osi
 
@@ -151,17 +151,25 @@ def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int) -> dict:  # noqa: 
                              piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1=w["l1"], l2=w["l2"])
         st = osi.default_init(sh)
         opt = osi.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
-        t0 = time.perf_counter()
-        osi.train_step(sh, st, bd, opt, w["lr"], 0.0, WRM290, 1)
+        def one(step):
+            osi.train_step(sh, st, bd, opt, w["lr"], 0.0, WRM290, step)
+    # consecutive training steps on the same batch until the sample holds
+    # about min_seconds of CPU work (at least two steps, at most max_steps)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        steps += 1
+        one(steps)
         dt = time.perf_counter() - t0
+        if steps >= max_steps or (steps >= 2 and dt >= min_seconds):
+            break
     n_ft = (spec["ft_in"] + spec["piece_inputs"]) * w["ft_out"]
     return {
-        "value": round(n / dt, 1),
+        "value": round(steps * n / dt, 1),
         "unit": "pos/s",
         "cores": used,
         "kind": "port",
-        "sample": f"1 full oracle step (fwd+bwd+{w['optimizer']} over all {n_ft / 1e6:.1f}M FT params) "
-                  f"at b={n} of the same workload, {dt:.1f} s",
+        "sample": f"{steps} consecutive full oracle steps (fwd+bwd+{w['optimizer']} over all {n_ft / 1e6:.1f}M "
+                  f"FT params) at b={n} of the same workload, {dt:.1f} s",
     }
 
 
