@@ -32,11 +32,6 @@ constexpr int kMaxActive = 64;  // one index per lane
 #define TATARA_FT_GRAD_LANE_FLOATS 4
 #endif
 constexpr int kFtGradLaneFloats = TATARA_FT_GRAD_LANE_FLOATS;
-// f32 dft rows gathered per unrolled group (loads in flight per lane).
-#ifndef TATARA_FT_GRAD_UNROLL
-#define TATARA_FT_GRAD_UNROLL 8
-#endif
-constexpr int kFtGradUnroll = TATARA_FT_GRAD_UNROLL;
 // Split the FT backward into an stm pass and an nstm pass (needs the
 // gradient buffer for the running sums).
 #ifndef TATARA_FT_GRAD_SPLIT
@@ -434,33 +429,52 @@ using vecf = float __attribute__((ext_vector_type(V)));
 template <int V>
 using vech = _Float16 __attribute__((ext_vector_type(V)));
 
-// Sequential sum, from acc, of the dft rows vals[s..e) at vector column q,
-// in f32 whatever the dft's element type RAW (V values per lane).  The row
-// ids are read 64 at a time with one coalesced load and broadcast with
-// readlane, so a row's address is a scalar base plus the lane's column and
-// the U gathers of an unrolled group issue back to back.
-template <typename RAW, int V, int U>
-__device__ __forceinline__ vecf<V> segment_sum(const RAW* __restrict__ dft, uint64_t row_v,
+// Sequential sums, from acc, of the dft rows vals[s..e) at vector column q,
+// in f32 (V values per lane).  The row ids are wave-uniform, so a row's
+// address is a scalar base plus the lane's column.
+template <int V>
+__device__ __forceinline__ vecf<V> segment_sum(const vecf<V>* __restrict__ dft, uint64_t row_v,
                                                const uint32_t* __restrict__ vals, uint32_t s,
                                                uint32_t e, uint64_t q, vecf<V> acc) {
-    const uint32_t lane = __lane_id();
-    for (uint32_t k = s; k < e; k += kWave) {
-        const uint32_t cnt = e - k < (uint32_t)kWave ? e - k : (uint32_t)kWave;
-        const int32_t my = lane < cnt ? (int32_t)vals[k + lane] : 0;
-        for (uint32_t j = 0; j < cnt; j += U) {
-            // a last, partial group re-reads the block's last row in its
-            // spare slots (in bounds, already cached) and does not add them
-            RAW d[U];
+    constexpr int U = 32 / V;  // 8 (V=4) .. 32 (V=1) loads in flight per lane
+    uint32_t i = s;
+    for (; i + U <= e; i += U) {
+        vecf<V> d[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t t = j + u < cnt ? j + u : cnt - 1;
-                const uint64_t r = (uint32_t)__builtin_amdgcn_readlane(my, t);
-                d[u] = dft[r * row_v + q];
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (u == 0 || j + u < cnt) acc += __builtin_convertvector(d[u], vecf<V>);  // j < cnt
+        for (int u = 0; u < U; ++u) {
+            const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i + u]);
+            d[u] = dft[r * row_v + q];
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += d[u];
+    }
+    for (; i < e; ++i) {
+        const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i]);
+        acc += dft[r * row_v + q];
+    }
+    return acc;
+}
+
+// The same sequential sum over f16 dft rows (V values per lane), in f32.
+template <int V>
+__device__ __forceinline__ vecf<V> segment_sum_f16(const vech<V>* __restrict__ dft, uint64_t row_v,
+                                                   const uint32_t* __restrict__ vals, uint32_t s,
+                                                   uint32_t e, uint64_t q, vecf<V> acc) {
+    constexpr int U = 64 / V;
+    uint32_t i = s;
+    for (; i + U <= e; i += U) {
+        vech<V> d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i + u]);
+            d[u] = dft[r * row_v + q];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += __builtin_convertvector(d[u], vecf<V>);
+    }
+    for (; i < e; ++i) {
+        const uint64_t r = __builtin_amdgcn_readfirstlane(vals[i]);
+        acc += __builtin_convertvector(dft[r * row_v + q], vecf<V>);
     }
     return acc;
 }
@@ -571,7 +585,7 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
     constexpr uint32_t kCols = kWave * V;
     static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
                   "a lane's values must lie in one dft chunk");
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
@@ -581,22 +595,18 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
     const uint32_t col = chunk * kCols + lane * V;
     const uint32_t s0 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f + (PHASE == 2 ? 1 : 0)]);
     const uint32_t s1 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f + (PHASE == 1 ? 1 : 2)]);
-    // lanes past the last column gather the last vector (in bounds) and
-    // store nothing: every lane takes part in the row-id loads
-    const bool active = col < a.ft_out;
-    const uint32_t cq = active ? col : a.ft_out - V;
-    const uint64_t q = ((uint64_t)(cq / kDftChunk) * a.dft_chunk_stride + cq % kDftChunk) / V;
-    const uint64_t off = ((uint64_t)f * a.ft_out + cq) / V;
+    if (col >= a.ft_out) return;
+    const uint64_t q = ((uint64_t)(col / kDftChunk) * a.dft_chunk_stride + col % kDftChunk) / V;
+    const uint64_t off = ((uint64_t)f * a.ft_out + col) / V;
     vecf<V>* grad = reinterpret_cast<vecf<V>*>(a.grad);
     vecf<V> gr = 0.0f;
     if constexpr (PHASE == 2) gr = __builtin_nontemporal_load(grad + off);
     if constexpr (HDFT)
-        gr = segment_sum<vech<V>, V, 64 / V>(reinterpret_cast<const vech<V>*>(a.dft16), a.dft_row_stride / V,
-                                             a.occ_vals, s0, s1, q, gr);
+        gr = segment_sum_f16<V>(reinterpret_cast<const vech<V>*>(a.dft16), a.dft_row_stride / V, a.occ_vals, s0,
+                                s1, q, gr);
     else
-        gr = segment_sum<vecf<V>, V, kFtGradUnroll>(reinterpret_cast<const vecf<V>*>(a.dft), a.dft_row_stride / V,
-                                                    a.occ_vals, s0, s1, q, gr);
-    if (!active) return;
+        gr = segment_sum<V>(reinterpret_cast<const vecf<V>*>(a.dft), a.dft_row_stride / V, a.occ_vals, s0, s1, q,
+                            gr);
     if constexpr (PHASE == 1) {
         __builtin_nontemporal_store(gr, grad + off);  // the running (unscaled) sum
         return;
