@@ -301,6 +301,70 @@ TATARA_API int32_t tatara_trainer_phase_times(TataraTrainer* trainer, double* ms
  * ft_w (sync_ft_forward_weights, trainer_layerstack.rs:1787). */
 TATARA_API int32_t tatara_trainer_sync_forward_weights(TataraTrainer* trainer);
 
+/* ------------------------------------------------------------------------ */
+/* Raw resume checkpoints (RNRC version 8, bins/nnue_train/src/ckpt.rs)      */
+/* ------------------------------------------------------------------------ */
+
+/* RawCkptArch (ckpt.rs:213-226): the identity a header records.  The feature
+ * set gives the canonical name, feature hash, train ft_in (+ its piece inputs
+ * with ft_factorize) and max_active; LayerStack records bucket_mode
+ * (TATARA_BUCKET_KINGRANK9 "kingrank9" or TATARA_BUCKET_PROGRESS_KPABS
+ * "progress8kpabs") and topology [ft_out, l1_out, l2_out, num_buckets]
+ * (layerstack_topology, ckpt.rs:186-199); Simple records no bucket mode
+ * (TATARA_BUCKET_NONE) and [ft_out, l1_out, l2_out]. */
+typedef struct TataraCkptArch {
+    int32_t feature_set;   /* TATARA_FS_* */
+    int32_t ft_factorize;
+    int32_t arch;          /* TATARA_ARCH_* */
+    int32_t bucket_mode;   /* TATARA_BUCKET_* */
+    uint64_t ft_out, l1_out, l2_out, num_buckets;
+} TataraCkptArch;
+
+/* RawCkptHeader (ckpt.rs:247-265).  lr_horizon 0 and run_id "" mean none;
+ * header_bytes is the offset of the first group. */
+typedef struct TataraCkptHeader {
+    uint32_t version;
+    uint64_t superbatch, step_count, lr_horizon, num_groups, header_bytes;
+    char run_id[257];
+} TataraCkptHeader;
+
+/* write_raw_ckpt_header (ckpt.rs:269-312): the version-8 header into out
+ * (*out_bytes receives its size; capacity smaller than it is an error).  A
+ * run id longer than 256 bytes is omitted.  Host only. */
+TATARA_API int32_t tatara_ckpt_write_header(const TataraCkptArch* arch, const char* run_id, uint64_t superbatch,
+                                            uint64_t step_count, uint64_t lr_horizon, uint64_t num_groups,
+                                            uint8_t* out, uint64_t capacity, uint64_t* out_bytes);
+/* read_raw_ckpt_header (ckpt.rs:322-612): parses a version 1..8 header from
+ * memory and checks it against expected with the reference's rules (feature
+ * set, factorizer flag, feature hash, ft_in, ft_out, max_active - twice the
+ * base accepted when factorized -, arch kind, bucket mode - progress8kpabs
+ * for LayerStack files before version 8 -, topology).  Malformed or
+ * mismatching input returns TATARA_ERR_INVALID with the reference's message
+ * ("... truncated while reading ...", "... arch kind mismatch ...").  Host
+ * only. */
+TATARA_API int32_t tatara_ckpt_read_header(const uint8_t* data, uint64_t n, const TataraCkptArch* expected,
+                                           TataraCkptHeader* out);
+/* GpuTrainer / SimpleGpuTrainer::save_raw_checkpoint (trainer_layerstack.rs:
+ * 1577-1610, trainer_simple.rs:2870-2905; file by save_raw_checkpoint_file,
+ * ckpt.rs:614-699): header, then per parameter group in the reference order
+ * (LayerStack ft_w, ft_b, l1_w, l1_b, l1_shared_weight, l1_shared_bias, l2_w,
+ * l2_b, l3_w, l3_b; Simple ft_w, ft_b, l1_w, l1_b, l2_w, l2_b, l3_w, l3_b) u64
+ * len and f32 w, m, v, slow (f16 moments as their true f32 values).  Written
+ * to "<path>.tmp" and renamed over path.  feature_set must match the
+ * trainer's ft_in (and piece inputs with a factorizer).  Synchronous. */
+TATARA_API int32_t tatara_trainer_save_resume(TataraTrainer* trainer, const char* path, int32_t feature_set,
+                                              int32_t bucket_mode, uint64_t superbatch, const char* run_id,
+                                              uint64_t lr_horizon);
+/* load_raw_checkpoint (trainer_layerstack.rs:1631-1726, trainer_simple.rs:
+ * 2907-2970; load_raw_checkpoint_file, ckpt.rs:705-754): checks the header,
+ * the group count and every group length against the trainer and that the
+ * file holds all group data, before changing any state; then uploads every
+ * group (f16 moments re-quantised: f16(clamp(x * scale, +-65504))), restores
+ * the step counter and rebuilds the forward table.  header may be NULL.
+ * Synchronous. */
+TATARA_API int32_t tatara_trainer_load_resume(TataraTrainer* trainer, const char* path, int32_t feature_set,
+                                              int32_t bucket_mode, TataraCkptHeader* header);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,31 @@ class TataraBatch(C.Structure):
     ]
 
 
+class TataraCkptArch(C.Structure):
+    _fields_ = [
+        ("feature_set", C.c_int32),
+        ("ft_factorize", C.c_int32),
+        ("arch", C.c_int32),
+        ("bucket_mode", C.c_int32),
+        ("ft_out", C.c_uint64),
+        ("l1_out", C.c_uint64),
+        ("l2_out", C.c_uint64),
+        ("num_buckets", C.c_uint64),
+    ]
+
+
+class TataraCkptHeader(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("superbatch", C.c_uint64),
+        ("step_count", C.c_uint64),
+        ("lr_horizon", C.c_uint64),
+        ("num_groups", C.c_uint64),
+        ("header_bytes", C.c_uint64),
+        ("run_id", C.c_char * 257),
+    ]
+
+
 # name -> (restype, argtypes); every entry point returns an int32 status
 # except the two string getters.
 SIGNATURES = {
@@ -138,6 +163,23 @@ SIGNATURES = {
     "tatara_trainer_fp16_clamp_count": (C.c_int32, [C.c_void_p, c_u64p, c_u64p]),
     "tatara_trainer_export_quantised": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int32]),
     "tatara_trainer_set_profiling": (C.c_int32, [C.c_void_p, C.c_int32]),
+    "tatara_ckpt_write_header": (
+        C.c_int32,
+        [C.POINTER(TataraCkptArch), C.c_char_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_void_p,
+         C.c_uint64, c_u64p],
+    ),
+    "tatara_ckpt_read_header": (
+        C.c_int32,
+        [C.c_void_p, C.c_uint64, C.POINTER(TataraCkptArch), C.POINTER(TataraCkptHeader)],
+    ),
+    "tatara_trainer_save_resume": (
+        C.c_int32,
+        [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_uint64, C.c_char_p, C.c_uint64],
+    ),
+    "tatara_trainer_load_resume": (
+        C.c_int32,
+        [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.POINTER(TataraCkptHeader)],
+    ),
     "tatara_trainer_phase_times": (C.c_int32, [C.c_void_p, c_f64p, C.c_int32, c_u64p]),
 }
 

@@ -202,6 +202,12 @@ class SimpleTrainer final : public TrainerBase {
         return kOk;
     }
 
+    std::vector<const char*> group_names() const override {
+        std::vector<const char*> names{"ft_w"};
+        for (const auto& g : small) names.push_back(g.name);
+        return names;
+    }
+
     ParamGroup* find(const char* name) override {
         if (!std::strcmp(name, "ft_w")) return &ft;
         for (auto& g : small)

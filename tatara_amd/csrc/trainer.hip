@@ -34,6 +34,7 @@
 #include "psv_kernels.hpp"
 #include "ft_kernels.hpp"
 #include "init.hpp"
+#include "checkpoint.hpp"
 #include "trainer_base.hpp"
 
 namespace tatara {
@@ -294,6 +295,12 @@ class LayerStackTrainer final : public TrainerBase {
         if (st) return st;
         TATARA_HIP(hipStreamSynchronize(stream), "sync_forward_weights");
         return kOk;
+    }
+
+    std::vector<const char*> group_names() const override {
+        std::vector<const char*> names{"ft_w"};
+        for (const auto& g : small) names.push_back(g.name);
+        return names;
     }
 
     ParamGroup* find(const char* name) override {
@@ -648,34 +655,6 @@ int32_t tatara_trainer_tensor_size(TataraTrainer* trainer, const char* name, uin
     return kOk;
 }
 
-static float* group_ptr(ParamGroup* g, int32_t which) {
-    switch (which) {
-        case 0: return g->w;
-        case 1: return g->m;
-        case 2: return g->v;
-        case 3: return g->slow;
-        case 4: return g->grad;
-        default: return nullptr;
-    }
-}
-
-// f16 moments (MomentBuf::F16): which 1 / 2 are read back as f16 * (1 / scale)
-// (MomentBuf::to_host_f32) and written as f16(clamp(x * scale, +-65504))
-// (MomentBuf::from_host_f32), trainer_common.rs:78-132.
-static bool f16_moment(ParamGroup* g, int32_t which, uint16_t*& dev, float& scale) {
-    if (which == 1 && g->m16) {
-        dev = g->m16;
-        scale = g->m_scale;
-        return true;
-    }
-    if (which == 2 && g->v16) {
-        dev = g->v16;
-        scale = g->v_scale;
-        return true;
-    }
-    return false;
-}
-
 int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int32_t which,
                                   float* host, uint64_t n) {
     TATARA_REQUIRE(trainer && name && host, "null argument");
@@ -684,25 +663,7 @@ int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char* name, int3
     TATARA_REQUIRE(g, std::string("unknown tensor ") + name);
     TATARA_REQUIRE(which >= 0 && which <= 4, "which must be 0..4");
     TATARA_REQUIRE(n == g->n, "element count mismatch");
-    TATARA_HIP(hipStreamSynchronize(t.stream), "get_tensor sync");
-    uint16_t* dev16 = nullptr;
-    float scale = 1.0f;
-    if (f16_moment(g, which, dev16, scale)) {
-        std::vector<_Float16> h(n);
-        TATARA_HIP(hipMemcpy(h.data(), dev16, n * 2, hipMemcpyDeviceToHost), "get_tensor");
-        const float inv = 1.0f / scale;
-        for (uint64_t i = 0; i < n; ++i) host[i] = (float)h[i] * inv;
-        return kOk;
-    }
-    float* src = group_ptr(g, which);
-    if (which == 4 && !t.cfg.keep_grads) src = nullptr;
-    if (!src) {
-        // the optimizer leaves zero gradients; without keep_grads none are kept
-        std::memset(host, 0, n * sizeof(float));
-        return kOk;
-    }
-    TATARA_HIP(hipMemcpy(host, src, n * sizeof(float), hipMemcpyDeviceToHost), "get_tensor");
-    return kOk;
+    return t.read_group(*g, which, host);
 }
 
 int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int32_t which,
@@ -712,22 +673,8 @@ int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int3
     ParamGroup* g = t.find(name);
     TATARA_REQUIRE(g, std::string("unknown tensor ") + name);
     TATARA_REQUIRE(n == g->n, "element count mismatch");
-    TATARA_HIP(hipStreamSynchronize(t.stream), "set_tensor sync");
-    uint16_t* dev16 = nullptr;
-    float scale = 1.0f;
-    if (f16_moment(g, which, dev16, scale)) {
-        std::vector<_Float16> h(n);
-        for (uint64_t i = 0; i < n; ++i) {
-            float x = host[i] * scale;
-            x = x < -65504.0f ? -65504.0f : (x > 65504.0f ? 65504.0f : x);
-            h[i] = (_Float16)x;
-        }
-        TATARA_HIP(hipMemcpy(dev16, h.data(), n * 2, hipMemcpyHostToDevice), "set_tensor");
-        return kOk;
-    }
-    float* dst = group_ptr(g, which);
-    TATARA_REQUIRE(dst, "tensor not allocated (which)");
-    TATARA_HIP(hipMemcpy(dst, host, n * sizeof(float), hipMemcpyHostToDevice), "set_tensor");
+    int32_t st = t.write_group(*g, which, host);
+    if (st) return st;
     if (!std::strcmp(name, "ft_w") && which == 0) return t.sync_forward_weights();
     return kOk;
 }
@@ -768,6 +715,50 @@ int32_t tatara_trainer_phase_times(TataraTrainer* trainer, double* ms, int32_t n
 int32_t tatara_trainer_sync_forward_weights(TataraTrainer* trainer) {
     TATARA_REQUIRE(trainer, "trainer is null");
     return trainer->t->sync_forward_weights();
+}
+
+// The checkpoint identity of a trainer: the feature set (TATARA_FS_*) must
+// have the trainer's base ft_in and, with a factorizer, its piece inputs.
+static int32_t trainer_ckpt_arch(const TrainerBase& t, int32_t feature_set, int32_t bucket_mode, CkptArch& a) {
+    FeatureSetShape s{};
+    int32_t st = feature_set_shape(feature_set, s);
+    if (st) return st;
+    const TataraTrainerConfig& c = t.cfg;
+    TATARA_REQUIRE((int64_t)s.king_buckets * s.piece_inputs == c.ft_in,
+                   "the feature set's ft_in differs from the trainer's");
+    TATARA_REQUIRE(c.piece_inputs == 0 || c.piece_inputs == s.piece_inputs,
+                   "the feature set's piece inputs differ from the trainer's factorizer");
+    TataraCkptArch ca{};
+    ca.feature_set = feature_set;
+    ca.ft_factorize = c.piece_inputs > 0;
+    ca.arch = c.arch;
+    ca.bucket_mode = bucket_mode;
+    ca.ft_out = (uint64_t)c.ft_out;
+    ca.l1_out = (uint64_t)c.l1_out;
+    ca.l2_out = (uint64_t)c.l2_out;
+    ca.num_buckets = c.arch == TATARA_ARCH_LAYERSTACK ? (uint64_t)c.num_buckets : 0;
+    return ckpt_arch_from_c(ca, a);
+}
+
+int32_t tatara_trainer_save_resume(TataraTrainer* trainer, const char* path, int32_t feature_set,
+                                   int32_t bucket_mode, uint64_t superbatch, const char* run_id,
+                                   uint64_t lr_horizon) {
+    TATARA_REQUIRE(trainer && path, "null argument");
+    TrainerBase& t = *trainer->t;
+    CkptArch a;
+    int32_t st = trainer_ckpt_arch(t, feature_set, bucket_mode, a);
+    if (st) return st;
+    return save_resume_checkpoint(t, path, a, t.group_names(), superbatch, run_id, lr_horizon);
+}
+
+int32_t tatara_trainer_load_resume(TataraTrainer* trainer, const char* path, int32_t feature_set,
+                                   int32_t bucket_mode, TataraCkptHeader* header) {
+    TATARA_REQUIRE(trainer && path, "null argument");
+    TrainerBase& t = *trainer->t;
+    CkptArch a;
+    int32_t st = trainer_ckpt_arch(t, feature_set, bucket_mode, a);
+    if (st) return st;
+    return load_resume_checkpoint(t, path, a, t.group_names(), header);
 }
 
 int32_t tatara_trainer_export_quantised(TataraTrainer* trainer, const char* path, int32_t feature_set,

@@ -1,6 +1,8 @@
 // Shared trainer services (see trainer_base.hpp).
 #include "trainer_base.hpp"
 
+#include <cstring>
+
 #include <cmath>
 #include <limits>
 #include <string>
@@ -267,6 +269,82 @@ int32_t TrainerBase::copy_chunk_major(const void* dev, bool f16, uint32_t b, uin
         const uint64_t r = i / width, c = i % width;
         host[i] = all[((c / kChunk) * 2 * b + (uint64_t)persp * b + r) * kChunk + c % kChunk];
     }
+    return kOk;
+}
+
+namespace {
+
+float* group_ptr(const ParamGroup& g, int32_t which) {
+    switch (which) {
+        case 0: return g.w;
+        case 1: return g.m;
+        case 2: return g.v;
+        case 3: return g.slow;
+        case 4: return g.grad;
+        default: return nullptr;
+    }
+}
+
+// The f16 array and scale of an f16 moment (MomentBuf::F16), or false.
+bool f16_moment(const ParamGroup& g, int32_t which, uint16_t*& dev, float& scale) {
+    if (which == 1 && g.m16) {
+        dev = g.m16;
+        scale = g.m_scale;
+        return true;
+    }
+    if (which == 2 && g.v16) {
+        dev = g.v16;
+        scale = g.v_scale;
+        return true;
+    }
+    return false;
+}
+
+}  // namespace
+
+int32_t TrainerBase::read_group(const ParamGroup& g, int32_t which, float* host) {
+    TATARA_REQUIRE(which >= 0 && which <= 4, "which must be 0..4");
+    const uint64_t n = g.n;
+    TATARA_HIP(hipStreamSynchronize(stream), "read_group sync");
+    uint16_t* dev16 = nullptr;
+    float scale = 1.0f;
+    if (f16_moment(g, which, dev16, scale)) {
+        std::vector<_Float16> h(n);
+        TATARA_HIP(hipMemcpy(h.data(), dev16, n * 2, hipMemcpyDeviceToHost), "read_group");
+        const float inv = 1.0f / scale;
+        for (uint64_t i = 0; i < n; ++i) host[i] = (float)h[i] * inv;
+        return kOk;
+    }
+    const float* src = group_ptr(g, which);
+    if (which == 4 && !cfg.keep_grads) src = nullptr;
+    if (!src) {
+        // the optimizer leaves zero gradients; without keep_grads none are kept
+        std::memset(host, 0, n * sizeof(float));
+        return kOk;
+    }
+    TATARA_HIP(hipMemcpy(host, src, n * sizeof(float), hipMemcpyDeviceToHost), "read_group");
+    return kOk;
+}
+
+int32_t TrainerBase::write_group(ParamGroup& g, int32_t which, const float* host) {
+    TATARA_REQUIRE(which >= 0 && which <= 4, "which must be 0..4");
+    const uint64_t n = g.n;
+    TATARA_HIP(hipStreamSynchronize(stream), "write_group sync");
+    uint16_t* dev16 = nullptr;
+    float scale = 1.0f;
+    if (f16_moment(g, which, dev16, scale)) {
+        std::vector<_Float16> h(n);
+        for (uint64_t i = 0; i < n; ++i) {
+            float x = host[i] * scale;
+            x = x < -65504.0f ? -65504.0f : (x > 65504.0f ? 65504.0f : x);
+            h[i] = (_Float16)x;
+        }
+        TATARA_HIP(hipMemcpy(dev16, h.data(), n * 2, hipMemcpyHostToDevice), "write_group");
+        return kOk;
+    }
+    float* dst = group_ptr(g, which);
+    TATARA_REQUIRE(dst, "tensor not allocated (which)");
+    TATARA_HIP(hipMemcpy(dst, host, n * sizeof(float), hipMemcpyHostToDevice), "write_group");
     return kOk;
 }
 

@@ -94,6 +94,17 @@ class TrainerBase {
     int32_t flush(double* out);
     int32_t prof_collect();
 
+    // Host copies of one array of a group (which: 0 w, 1 m, 2 v, 3 slow,
+    // 4 grad), n = g.n values.  f16 moments are read as f16 * (1 / scale)
+    // and written as f16(clamp(x * scale, +-65504)) (MomentBuf::to_host_f32 /
+    // from_host_f32, bins/nnue_train/src/trainer_common.rs:89-126).  An
+    // unallocated gradient reads as zeros.  Synchronous; write_group does not
+    // rebuild the forward table.
+    int32_t read_group(const ParamGroup& g, int32_t which, float* host);
+    int32_t write_group(ParamGroup& g, int32_t which, const float* host);
+    // Reference names of the parameter groups in checkpoint order.
+    virtual std::vector<const char*> group_names() const = 0;
+
    protected:
     // device copies of host batches
     int32_t *in_stm = nullptr, *in_nstm = nullptr, *in_nnz = nullptr, *in_bucket = nullptr;

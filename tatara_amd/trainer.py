@@ -433,6 +433,30 @@ class _Trainer:
         return {g: {k: self.get(g, k) for k in ("w", "m", "v", "slow")} for g in self.GROUPS}
 
 
+    def save_resume_checkpoint(self, path, feature_set, bucket_mode, superbatch: int, run_id: str = "",
+                               lr_horizon=None) -> None:
+        """save_raw_checkpoint (RNRC v8, bins/nnue_train/src/ckpt.rs:614-699): every
+        group's w, m, v, slow and the step counter, written atomically.
+        bucket_mode: "kingrank9" / "progress8kpabs" for LayerStack, None for Simple."""
+        from .checkpoint import BUCKET_MODES, FEATURE_SETS
+
+        fs = FEATURE_SETS[feature_set] if isinstance(feature_set, str) else int(feature_set)
+        check(self._lib.tatara_trainer_save_resume(self._h, os.fsencode(path), fs, BUCKET_MODES[bucket_mode],
+                                                   int(superbatch), run_id.encode(), int(lr_horizon or 0)))
+
+    def load_resume_checkpoint(self, path, feature_set, bucket_mode):
+        """load_raw_checkpoint: restores every group and the step counter and
+        rebuilds the forward table; returns (superbatch, producer run id or
+        None, LR horizon or None) as RawCkptResumeState (ckpt.rs:134-137)."""
+        from ._lib import TataraCkptHeader
+        from .checkpoint import BUCKET_MODES, FEATURE_SETS
+
+        fs = FEATURE_SETS[feature_set] if isinstance(feature_set, str) else int(feature_set)
+        h = TataraCkptHeader()
+        check(self._lib.tatara_trainer_load_resume(self._h, os.fsencode(path), fs, BUCKET_MODES[bucket_mode],
+                                                   C.byref(h)))
+        return h.superbatch, (h.run_id.decode() or None), (h.lr_horizon or None)
+
     def _export(self, path, feature_set, fv_scale) -> None:
         from .dataloader import FEATURE_SETS
 
