@@ -457,26 +457,17 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
 // dcombined[c] = sum_o dl1[o] * l1_w[g][o][c]  +  sum_o dl1[o] * l1s_w[c][o]
 // (the reference's two input-gradient kernels, added as in
 // ft_post_perspective_grad_fused), then the pairwise CReLU gradient into dft
-// (native_kernels.cu:2260-2302).  Grid (column block, row block): a thread
-// owns one float4 column group of kPostTiles sorted tiles and writes its ft_b
-// gradient partial per perspective for that row block.
-// H: f16 raw sums in, f16 dft out, scaled by dft_scale and clamped to
-// +-65504 with a count of every clamp (ft_post_perspective_grad_fused_fp16,
-// native_kernels.cu:2304-2352); the ft_b gradient stays unscaled f32.
+// (native_kernels.cu:2260-2302).  Grid (column block, row block): a lane owns
+// its columns of the combined output over kPostTiles sorted tiles (the L1
+// gradient row is wave-uniform, the weights stay in registers) and writes
+// its ft_b gradient partials per perspective for that row block.  The f16
+// variant reads f16 raw sums and writes the f16 dft, scaled by dft_scale and
+// clamped to +-65504 with a count of every clamp
+// (ft_post_perspective_grad_fused_fp16, native_kernels.cu:2304-2352); the
+// ft_b gradient stays unscaled f32.  Measured on MI355X: four columns per
+// lane suit the f32 dft (2 KB of each raw-sum row half per block), one
+// column per lane (86 VGPRs, five waves per SIMD) the f16 one.
 // ---------------------------------------------------------------------------
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-
-template <bool H>
-__device__ __forceinline__ float4 load_ft4(const float* ft, const _Float16* ft16, uint64_t elem) {
-    if constexpr (H) {
-        const f4v f = __builtin_convertvector(*reinterpret_cast<const h4*>(ft16 + elem), f4v);
-        return make_float4(f.x, f.y, f.z, f.w);
-    } else {
-        return *reinterpret_cast<const float4*>(ft + elem);
-    }
-}
-
 __device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
     if (v > 65504.0f) {
         ++clamps;
@@ -489,8 +480,92 @@ __device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
     return v;
 }
 
-template <int L1, bool H>
-__global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
+// f16 dft (and raw sums): one lane per combined column c; a wave covers 64
+// consecutive columns of one perspective's half (ft_out % 128 == 0).  The
+// tile's 16 raw-sum pairs are loaded before any of its rows is computed.
+template <int L1>
+__global__ __launch_bounds__(128) void ls_l1_input_post_h_kernel(LsDenseArgs a) {
+    const uint32_t ft_out = a.ft_out, half = ft_out / 2;
+    const uint64_t batch = a.batch;
+    const uint32_t c = blockIdx.x * 128 + threadIdx.x;
+    if (c >= ft_out) return;
+    const uint32_t persp = c < half ? 0 : 1;
+    const uint32_t p = c - persp * half;
+    const _Float16* ft16 = reinterpret_cast<const _Float16*>(persp ? a.ft_nstm16 : a.ft_stm16);
+    const uint64_t cstride = 2 * batch * kDftChunk;
+    const uint64_t off_a = (uint64_t)(p / kDftChunk) * cstride + persp * batch * kDftChunk + p % kDftChunk;
+    const uint64_t off_b =
+        (uint64_t)((p + half) / kDftChunk) * cstride + persp * batch * kDftChunk + (p + half) % kDftChunk;
+    float ws[L1];
+#pragma unroll
+    for (int o = 0; o < L1; ++o) ws[o] = a.l1s_w[(uint64_t)c * L1 + o];
+    const float ba = a.ft_b[p], bb = a.ft_b[p + half];
+    float w1[L1];
+    int32_t cur_bin = -2;
+    bool bvalid = false;
+    float acc_a = 0.0f, acc_b = 0.0f;
+    uint32_t clamps = 0;
+    const uint32_t tile0 = blockIdx.y * kPostTiles;
+    for (uint32_t tt = 0; tt < kPostTiles; ++tt) {
+        const uint64_t tile = tile0 + tt;
+        if (tile * 16 >= a.padded_b) break;
+        const int32_t bin = a.sorted_bin[tile * 16];
+        if (bin < 0) continue;
+        if (bin != cur_bin) {
+            cur_bin = bin;
+            bvalid = (uint32_t)bin < a.nb;
+#pragma unroll
+            for (int o = 0; o < L1; ++o) w1[o] = bvalid ? a.l1_w[((uint64_t)bin * L1 + o) * ft_out + c] : 0.0f;
+        }
+        int32_t orig[16];
+        float xr[16], yr[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            orig[r] = a.perm[tile * 16 + r];
+            xr[r] = 0.0f;
+            yr[r] = 0.0f;
+            if (orig[r] >= 0) {
+                const uint64_t base = (uint64_t)orig[r] * ft_out + p;
+                xr[r] = (float)ft16[base];
+                yr[r] = (float)ft16[base + half];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (orig[r] < 0) continue;
+            const float* d = a.dl1_sorted + (tile * 16 + r) * L1;
+            float da = 0.0f;
+            if (bvalid) {
+#pragma unroll
+                for (int o = 0; o < L1; ++o) da += d[o] * w1[o];
+            }
+            float db = 0.0f;
+#pragma unroll
+            for (int o = 0; o < L1; ++o) db += d[o] * ws[o];
+            const float dy = da + db;
+            const float xa = xr[r] + ba, xb = yr[r] + bb;
+            const float ya = crelu01(xa), yb = crelu01(xb);
+            const float ga = (xa > 0.0f && xa < 1.0f) ? dy * yb * a.ft_post_scale : 0.0f;
+            const float gb = (xb > 0.0f && xb < 1.0f) ? dy * ya * a.ft_post_scale : 0.0f;
+            const uint64_t row = (uint64_t)orig[r] * kDftChunk;
+            const float sc = a.dft_scale;
+            _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
+            d16[off_a + row] = (_Float16)clamp_f16_range(ga * sc, clamps);
+            d16[off_b + row] = (_Float16)clamp_f16_range(gb * sc, clamps);
+            acc_a += ga;
+            acc_b += gb;
+        }
+    }
+    float* pp = a.ftb_partial + ((uint64_t)blockIdx.y * 2 + persp) * ft_out;
+    pp[p] = acc_a;
+    pp[p + half] = acc_b;
+    if (clamps) atomicAdd(a.clamp_counter, (unsigned long long)clamps);
+}
+
+// f32 dft: a lane owns one float4 column group (four columns and their four
+// pair partners), so a 128-lane block covers 2 KB of each raw-sum row half.
+template <int L1>
+__global__ __launch_bounds__(128) void ls_l1_input_post_f4_kernel(LsDenseArgs a) {
     const uint32_t ft_out = a.ft_out, half = ft_out / 2, n4 = ft_out / 4;
     const uint64_t batch = a.batch;
     const uint32_t tile0 = blockIdx.y * kPostTiles;
@@ -502,14 +577,12 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
         const uint32_t persp = c0 < half ? 0 : 1;
         const uint32_t p0 = c0 - persp * half;
         const float* ft = persp ? a.ft_nstm : a.ft_stm;
-        const _Float16* ft16 = reinterpret_cast<const _Float16*>(persp ? a.ft_nstm16 : a.ft_stm16);
         // chunk-major dft: this thread's four columns c0..c0+3 and their pair
         // partners each lie inside one 256-column chunk
         const uint64_t cstride = 2 * batch * kDftChunk;
         const uint64_t off_a = (uint64_t)(p0 / kDftChunk) * cstride + persp * batch * kDftChunk + p0 % kDftChunk;
         const uint64_t off_b = (uint64_t)((p0 + half) / kDftChunk) * cstride + persp * batch * kDftChunk +
                                (p0 + half) % kDftChunk;
-        uint32_t clamps = 0;
         float ws[4][L1];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -539,8 +612,8 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
             int32_t orig_n = a.perm[tile * 16];
             float4 xa_n = zero4, xb_n = zero4;
             if (orig_n >= 0) {
-                xa_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0);
-                xb_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0 + half);
+                xa_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0);
+                xb_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0 + half);
             }
             for (uint32_t r = 0; r < 16; ++r) {
                 const uint64_t row = tile * 16 + r;
@@ -549,8 +622,8 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                 if (r + 1 < 16) {
                     orig_n = a.perm[row + 1];
                     if (orig_n >= 0) {
-                        xa_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0);
-                        xb_n = load_ft4<H>(ft, ft16, (uint64_t)orig_n * ft_out + p0 + half);
+                        xa_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0);
+                        xb_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0 + half);
                     }
                 }
                 if (orig < 0) continue;
@@ -583,21 +656,10 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
                     ga[e] = (xa[e] > 0.0f && xa[e] < 1.0f) ? dyv[e] * yb * a.ft_post_scale : 0.0f;
                     gb[e] = (xb[e] > 0.0f && xb[e] < 1.0f) ? dyv[e] * ya * a.ft_post_scale : 0.0f;
                 }
-                if constexpr (H) {
-                    const float sc = a.dft_scale;
-                    const f4v sa = {clamp_f16_range(ga[0] * sc, clamps), clamp_f16_range(ga[1] * sc, clamps),
-                                    clamp_f16_range(ga[2] * sc, clamps), clamp_f16_range(ga[3] * sc, clamps)};
-                    const f4v sb = {clamp_f16_range(gb[0] * sc, clamps), clamp_f16_range(gb[1] * sc, clamps),
-                                    clamp_f16_range(gb[2] * sc, clamps), clamp_f16_range(gb[3] * sc, clamps)};
-                    _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
-                    *reinterpret_cast<h4*>(d16 + off_a + (uint64_t)orig * kDftChunk) = __builtin_convertvector(sa, h4);
-                    *reinterpret_cast<h4*>(d16 + off_b + (uint64_t)orig * kDftChunk) = __builtin_convertvector(sb, h4);
-                } else {
-                    *reinterpret_cast<float4*>(a.dft + off_a + (uint64_t)orig * kDftChunk) =
-                        make_float4(ga[0], ga[1], ga[2], ga[3]);
-                    *reinterpret_cast<float4*>(a.dft + off_b + (uint64_t)orig * kDftChunk) =
-                        make_float4(gb[0], gb[1], gb[2], gb[3]);
-                }
+                *reinterpret_cast<float4*>(a.dft + off_a + (uint64_t)orig * kDftChunk) =
+                    make_float4(ga[0], ga[1], ga[2], ga[3]);
+                *reinterpret_cast<float4*>(a.dft + off_b + (uint64_t)orig * kDftChunk) =
+                    make_float4(gb[0], gb[1], gb[2], gb[3]);
                 acc_a.x += ga[0];
                 acc_a.y += ga[1];
                 acc_a.z += ga[2];
@@ -611,7 +673,6 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_kernel(LsDenseArgs a) {
         float* pp = part + persp * ft_out;
         reinterpret_cast<float4*>(pp)[p0 / 4] = acc_a;
         reinterpret_cast<float4*>(pp)[(p0 + half) / 4] = acc_b;
-        if (H && clamps) atomicAdd(a.clamp_counter, (unsigned long long)clamps);
     }
 }
 
@@ -756,17 +817,18 @@ int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
                    "an f16 dft needs the f16 raw sums and a clamp counter");
     const uint32_t rows = ls_post_workgroups(a.padded_b);
     if (rows == 0) return kOk;
-    const dim3 grid(ceil_div(a.ft_out / 4, 128), rows);
+    TATARA_REQUIRE(a.ft_out % 128 == 0, "ft_out must be a multiple of 128");
+    const dim3 grid_h(a.ft_out / 128, rows), grid_f(ceil_div(a.ft_out / 4, 128), rows);
     if (a.l1 == 16) {
         if (a.dft16)
-            ls_l1_input_post_kernel<16, true><<<grid, 128, 0, stream>>>(a);
+            ls_l1_input_post_h_kernel<16><<<grid_h, 128, 0, stream>>>(a);
         else
-            ls_l1_input_post_kernel<16, false><<<grid, 128, 0, stream>>>(a);
+            ls_l1_input_post_f4_kernel<16><<<grid_f, 128, 0, stream>>>(a);
     } else if (a.l1 == 8) {
         if (a.dft16)
-            ls_l1_input_post_kernel<8, true><<<grid, 128, 0, stream>>>(a);
+            ls_l1_input_post_h_kernel<8><<<grid_h, 128, 0, stream>>>(a);
         else
-            ls_l1_input_post_kernel<8, false><<<grid, 128, 0, stream>>>(a);
+            ls_l1_input_post_f4_kernel<8><<<grid_f, 128, 0, stream>>>(a);
     } else {
         TATARA_REQUIRE(false, "l1 must be 16 or 8");
     }
