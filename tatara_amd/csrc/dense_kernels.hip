@@ -147,43 +147,62 @@ __global__ __launch_bounds__(256) void sum_partials_f64_kernel(const double* __r
 }
 
 // ---------------------------------------------------------------------------
-// Tail: one thread per sorted row.
+// Tail: one 64-lane workgroup per sorted 16-row tile (one bucket, the tile's
+// rows being bucket-sorted and 16-aligned).  Lane l serves row r = l % 16 with
+// quarter q = l / 16: its eight L2 outputs o = 8q..8q+7 in the forward, the
+// L2 inputs k = q, q+4, .. in the backward, the L1 outputs k = q, q+4, .. of
+// the L1-tail gradient.  The bucket's L2/L3 weights are staged in LDS.  Every
+// per-row sum keeps the reference order (k ascending for L2, o ascending for
+// L3 and for the L2 input gradient); the gradient partials are per tile, rows
+// in order, and are reduced per bucket over the bucket's tiles.
 // ---------------------------------------------------------------------------
 template <int L1, int L2>
-__global__ __launch_bounds__(kTailRows) void ls_tail_kernel(LsDenseArgs a, int32_t train) {
+__global__ __launch_bounds__(64) void ls_tail_kernel(LsDenseArgs a, int32_t train) {
     constexpr int LE = L1 - 1;
     constexpr int LIN = 2 * LE;
-    constexpr int R = kTailRows;
-    __shared__ float s_l2in[R][LIN + 1];
-    __shared__ float s_dl2o[R][L2 + 1];
-    __shared__ float s_l2a[R][L2 + 1];
-    __shared__ float s_dl1[R][L1 + 1];
-    __shared__ float s_dy[R];
-    __shared__ int32_t s_bin[R];
-    __shared__ double s_loss[R];
-    __shared__ uint32_t s_lo[16], s_hi[16];
+    constexpr int OQ = L2 / 4;             // L2 outputs per lane
+    constexpr int KQ = (LIN + 3) / 4;      // L2 inputs per lane (backward)
+    constexpr int JQ = L1 / 4;             // L1 outputs per lane (backward)
+    static_assert(L2 % 4 == 0 && L1 % 4 == 0, "quarters");
+    __shared__ float sW2[L2 * LIN];
+    __shared__ float sB2[L2], sW3[L2];
+    __shared__ float s_l2in[16][LIN + 1];
+    __shared__ float s_l2a[16][L2 + 1];
+    __shared__ float s_dl2o[16][L2 + 1];
+    __shared__ float s_dl2pre[16][LIN + 1];
+    __shared__ float s_dl1[16][L1 + 1];
+    __shared__ float s_dy[16];
+    __shared__ double s_loss[16];
+    __shared__ int32_t s_real[16];
 
-    const uint32_t t = threadIdx.x;
-    const uint64_t row = (uint64_t)blockIdx.x * R + t;
-    const uint32_t nb = a.nb;
-    int32_t bin = -1, orig = -1;
-    if (row < a.padded_b) {
-        bin = a.sorted_bin[row];
-        orig = a.perm[row];
-    }
-    const bool real = orig >= 0;
-    const bool bvalid = real && (uint32_t)bin < nb;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t r = lane % 16, q = lane / 16;
+    const uint64_t tile = blockIdx.x;
+    const uint64_t row = tile * 16 + r;
+    // the tile's bucket: its first row is real unless the tile is all padding
+    const int32_t orig0 = a.perm[tile * 16];
+    const int32_t bin = orig0 >= 0 ? a.sorted_bin[tile * 16] : -1;
+    const bool bvalid = bin >= 0 && (uint32_t)bin < a.nb;
     const int g = bvalid ? bin : 0;
+    if (bvalid) {
+        const float* W2 = a.l2_w + (uint64_t)g * L2 * LIN;
+        for (uint32_t i = lane; i < (uint32_t)(L2 * LIN); i += 64) sW2[i] = W2[i];
+        if (lane < (uint32_t)L2) {
+            sB2[lane] = a.l2_b[g * L2 + lane];
+            sW3[lane] = a.l3_w[g * L2 + lane];
+        }
+    }
+    const float b3 = bvalid ? a.l3_b[g] : 0.0f;
+    const int32_t orig = a.perm[row];
+    const bool real = orig >= 0;
 
-    float l1t[L1];
-    float l2pre[LIN], l2in[LIN], l2o[L2], l2a[L2];
-    float net = 0.0f, dy = 0.0f;
-    double loss_c = 0.0;
+    float l1t[L1], l2pre[LIN], l2in[LIN];
+    float skip = 0.0f;
     if (real) {
         const float* l1v = a.l1_sorted + row * 2 * L1;
 #pragma unroll
         for (int o = 0; o < L1; ++o) l1t[o] = l1v[o] + l1v[L1 + o];  // elementwise_add
-        const float skip = l1t[L1 - 1];                                // slice_extract_2d
+        skip = l1t[L1 - 1];                                          // slice_extract_2d
 #pragma unroll
         for (int k = 0; k < LE; ++k) {
             const float mk = l1t[k];
@@ -192,147 +211,140 @@ __global__ __launch_bounds__(kTailRows) void ls_tail_kernel(LsDenseArgs a, int32
         }
 #pragma unroll
         for (int k = 0; k < LIN; ++k) l2in[k] = crelu01(l2pre[k]);
-        const float* W2 = a.l2_w + (uint64_t)g * L2 * LIN;
-#pragma unroll
-        for (int o = 0; o < L2; ++o) {
-            float acc = bvalid ? a.l2_b[g * L2 + o] : 0.0f;
-            if (bvalid) {
-#pragma unroll
-                for (int k = 0; k < LIN; ++k) acc += l2in[k] * W2[o * LIN + k];
-            }
-            l2o[o] = bvalid ? acc : 0.0f;
-            l2a[o] = crelu01(l2o[o]);
-        }
-        float l3 = 0.0f;
-        if (bvalid) {
-            l3 = a.l3_b[g];
-#pragma unroll
-            for (int o = 0; o < L2; ++o) l3 += l2a[o] * a.l3_w[g * L2 + o];
-        }
-        net = l3 + skip;
-        a.net_output[orig] = net;
-        // loss (loss_wdl / loss_wrm)
-        loss_c = position_loss(net, a.score[orig], a.wdl[orig], a.wdl_lambda, a.loss, a.per_pos_norm,
-                               a.weight_sum, a.batch, dy);
-    }
-    s_loss[t] = loss_c;
-    if (!train) {
-        __syncthreads();
-        if (t == 0) {
-            double acc = 0.0;
-            for (int k = 0; k < R; ++k) acc += s_loss[k];
-            a.loss_partial[blockIdx.x] = acc;
-        }
-        return;
-    }
-
-    // backward through L3, L2 and the L1 tail
-    float dl1[L1];
-#pragma unroll
-    for (int o = 0; o < L1; ++o) dl1[o] = 0.0f;
-    float dl2o[L2];
-    if (real) {
-        float dl2a[L2];
-#pragma unroll
-        for (int o = 0; o < L2; ++o) {
-            float acc = 0.0f;  // dense_mm_bwd_input_bucket, out_dim 1
-            if (bvalid) acc += dy * a.l3_w[g * L2 + o];
-            dl2a[o] = acc;
-            dl2o[o] = (l2o[o] > 0.0f && l2o[o] < 1.0f) ? dl2a[o] : 0.0f;  // crelu_grad
-        }
-        const float* W2 = a.l2_w + (uint64_t)g * L2 * LIN;
-        float dl2pre[LIN];
-#pragma unroll
-        for (int k = 0; k < LIN; ++k) {
-            float acc = 0.0f;
-            if (bvalid) {
-#pragma unroll
-                for (int o = 0; o < L2; ++o) acc += dl2o[o] * W2[o * LIN + k];
-            }
-            dl2pre[k] = (l2pre[k] > 0.0f && l2pre[k] < 1.0f) ? acc : 0.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < LE; ++k) {
-            const float from_sqr = 2.0f * l1t[k] * a.l1_sqr_scale * dl2pre[k];  // abs_pow2_scale_grad
-            dl1[k] = dl2pre[LE + k] + from_sqr;                                  // elementwise_add
-        }
-        dl1[L1 - 1] = dy;  // slice_scatter_2d of the skip gradient
     } else {
 #pragma unroll
-        for (int o = 0; o < L2; ++o) dl2o[o] = 0.0f;
+        for (int o = 0; o < L1; ++o) l1t[o] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < LIN; ++k) l2pre[k] = l2in[k] = 0.0f;
     }
-    if (row < a.padded_b) {
-        float* d = a.dl1_sorted + row * L1;
+    __syncthreads();  // staged weights visible
+    // L2 (dense_mm_fwd_bucket: the sum starts at the bias, k ascending) + CReLU
+    float l2o[OQ];
 #pragma unroll
-        for (int o = 0; o < L1; ++o) d[o] = dl1[o];
-    }
+    for (int j = 0; j < OQ; ++j) {
+        const int o = OQ * q + j;
+        float acc = bvalid ? sB2[o] : 0.0f;
+        if (bvalid) {
 #pragma unroll
-    for (int k = 0; k < LIN; ++k) s_l2in[t][k] = real ? l2in[k] : 0.0f;
-#pragma unroll
-    for (int o = 0; o < L2; ++o) {
-        s_dl2o[t][o] = dl2o[o];
-        s_l2a[t][o] = real ? l2a[o] : 0.0f;
-    }
-#pragma unroll
-    for (int o = 0; o < L1; ++o) s_dl1[t][o] = dl1[o];
-    s_dy[t] = dy;
-    s_bin[t] = bvalid ? bin : -1;
-    __syncthreads();
-
-    if (t == 0) {
-        double acc = 0.0;
-        for (int k = 0; k < R; ++k) acc += s_loss[k];
-        a.loss_partial[blockIdx.x] = acc;
-        for (uint32_t gg = 0; gg < nb; ++gg) {
-            s_lo[gg] = R;
-            s_hi[gg] = 0;
+            for (int k = 0; k < LIN; ++k) acc += l2in[k] * sW2[o * LIN + k];
         }
-        for (int k = 0; k < R; ++k) {
-            const int32_t bk = s_bin[k];
-            if (bk >= 0) {
-                if ((uint32_t)k < s_lo[bk]) s_lo[bk] = k;
-                s_hi[bk] = k + 1;
+        l2o[j] = bvalid ? acc : 0.0f;
+        s_l2a[r][o] = real ? crelu01(l2o[j]) : 0.0f;
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int k = 0; k < LIN; ++k) s_l2in[r][k] = l2in[k];
+        s_real[r] = real ? 1 : 0;
+    }
+    __syncthreads();
+    if (q == 0) {
+        // L3 (o ascending from the bias), net = l3 + skip, loss
+        double loss_c = 0.0;
+        float dy = 0.0f;
+        if (real) {
+            float l3 = 0.0f;
+            if (bvalid) {
+                l3 = b3;
+#pragma unroll
+                for (int o = 0; o < L2; ++o) l3 += s_l2a[r][o] * sW3[o];
+            }
+            const float net = l3 + skip;
+            a.net_output[orig] = net;
+            loss_c = position_loss(net, a.score[orig], a.wdl[orig], a.wdl_lambda, a.loss, a.per_pos_norm,
+                                   a.weight_sum, a.batch, dy);
+        }
+        s_dy[r] = dy;
+        s_loss[r] = loss_c;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        double acc = 0.0;
+        for (int k = 0; k < 16; ++k) acc += s_loss[k];
+        a.loss_partial[tile] = acc;
+    }
+    if (!train) return;
+
+    // backward: L3 input gradient and the L2 CReLU mask for this lane's outputs
+    const float dy = s_dy[r];
+#pragma unroll
+    for (int j = 0; j < OQ; ++j) {
+        const int o = OQ * q + j;
+        float acc = 0.0f;  // dense_mm_bwd_input_bucket, out_dim 1
+        if (bvalid) acc += dy * sW3[o];
+        const float d = (l2o[j] > 0.0f && l2o[j] < 1.0f) ? acc : 0.0f;  // crelu_grad
+        s_dl2o[r][o] = real ? d : 0.0f;
+    }
+    __syncthreads();
+    // L2 input gradient for this lane's inputs (o ascending), masked by the L1-tail CReLU
+#pragma unroll
+    for (int i = 0; i < KQ; ++i) {
+        const int k = (int)q + 4 * i;
+        if (k >= LIN) break;
+        float acc = 0.0f;
+        if (bvalid) {
+#pragma unroll
+            for (int o = 0; o < L2; ++o) acc += s_dl2o[r][o] * sW2[o * LIN + k];
+        }
+        s_dl2pre[r][k] = (l2pre[k] > 0.0f && l2pre[k] < 1.0f) ? acc : 0.0f;
+    }
+    __syncthreads();
+    // L1-tail gradient for this lane's L1 outputs
+#pragma unroll
+    for (int i = 0; i < JQ; ++i) {
+        const int k = (int)q + 4 * i;
+        float d = 0.0f;
+        if (real) {
+            if (k < LE) {
+                const float from_sqr = 2.0f * l1t[k] * a.l1_sqr_scale * s_dl2pre[r][k];  // abs_pow2_scale_grad
+                d = s_dl2pre[r][LE + k] + from_sqr;                                        // elementwise_add
+            } else {
+                d = dy;  // slice_scatter_2d of the skip gradient
             }
         }
+        a.dl1_sorted[row * L1 + k] = d;
+        s_dl1[r][k] = d;
     }
     __syncthreads();
 
-    const TailDims td{(uint32_t)L1, (uint32_t)L2, nb};
-    const uint32_t cells = td.cells();
-    float* part = a.tail_partial + (uint64_t)blockIdx.x * nb * cells;
-    for (uint32_t c = t; c < cells; c += R) {
-        for (uint32_t gg = 0; gg < nb; ++gg) {
-            const uint32_t lo = s_lo[gg], hi = s_hi[gg];
+    // per-tile gradient partials, rows in order (real rows only)
+    if (bvalid) {
+        const TailDims td{(uint32_t)L1, (uint32_t)L2, a.nb};
+        const uint32_t cells = td.cells();
+        float* part = a.tail_partial + tile * cells;
+        for (uint32_t c = lane; c < cells; c += 64) {
             float acc = 0.0f;
             if (c < td.off_b2()) {
                 const uint32_t o = c / LIN, k = c % LIN;
-                for (uint32_t r = lo; r < hi; ++r)
-                    if (s_bin[r] == (int32_t)gg) acc += s_l2in[r][k] * s_dl2o[r][o];
+                for (int rr = 0; rr < 16; ++rr)
+                    if (s_real[rr]) acc += s_l2in[rr][k] * s_dl2o[rr][o];
             } else if (c < td.off_w3()) {
                 const uint32_t o = c - td.off_b2();
-                for (uint32_t r = lo; r < hi; ++r)
-                    if (s_bin[r] == (int32_t)gg) acc += s_dl2o[r][o];
+                for (int rr = 0; rr < 16; ++rr)
+                    if (s_real[rr]) acc += s_dl2o[rr][o];
             } else if (c < td.off_b3()) {
                 const uint32_t o = c - td.off_w3();
-                for (uint32_t r = lo; r < hi; ++r)
-                    if (s_bin[r] == (int32_t)gg) acc += s_l2a[r][o] * s_dy[r];
+                for (int rr = 0; rr < 16; ++rr)
+                    if (s_real[rr]) acc += s_l2a[rr][o] * s_dy[rr];
             } else if (c < td.off_b1()) {
-                for (uint32_t r = lo; r < hi; ++r)
-                    if (s_bin[r] == (int32_t)gg) acc += s_dy[r];
+                for (int rr = 0; rr < 16; ++rr)
+                    if (s_real[rr]) acc += s_dy[rr];
             } else {
                 const uint32_t o = c - td.off_b1();
-                for (uint32_t r = lo; r < hi; ++r)
-                    if (s_bin[r] == (int32_t)gg) acc += s_dl1[r][o];
+                for (int rr = 0; rr < 16; ++rr)
+                    if (s_real[rr]) acc += s_dl1[rr][o];
             }
-            part[(uint64_t)gg * cells + c] = acc;
+            part[c] = acc;
         }
     }
     // shared L1 bias: every real row, including rows of an invalid bucket
-    if (t < (uint32_t)L1) {
+    if (lane < (uint32_t)L1) {
         float acc = 0.0f;
-        for (int r = 0; r < R; ++r) acc += s_dl1[r][t];
-        a.b1s_partial[(uint64_t)blockIdx.x * L1 + t] = acc;
+        for (int rr = 0; rr < 16; ++rr)
+            if (s_real[rr]) acc += s_dl1[rr][lane];
+        a.b1s_partial[tile * L1 + lane] = acc;
     }
+    // the bucket segments of the tile partials (first tile of each bin)
+    if (tile == 0 && lane <= a.nb) a.tail_seg[lane] = a.bin_start[lane] / 16;
 }
 
 // ---------------------------------------------------------------------------
@@ -364,33 +376,47 @@ __global__ void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
 // ---------------------------------------------------------------------------
 // Deterministic column sums of a partial matrix P[rows][n_cols]:
 // out[seg][c] = sum over the segment's rows of P[r][c].  Thread (c, phase)
-// sums rows phase, phase + 16, ... sequentially; the 16 phase sums are then
+// sums rows phase, phase + PH, ... sequentially; the PH phase sums are then
 // combined by a fixed pairwise tree.  Segment s covers rows
 // [seg_rows[s], seg_rows[s+1]) when seg_rows is given, else all rows.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kReducePhases = 16;
 
-__global__ __launch_bounds__(64 * kReducePhases) void reduce_rows_kernel(
-    const float* __restrict__ P, uint32_t n_rows, uint32_t n_cols, const uint32_t* __restrict__ seg_rows,
-    float* __restrict__ out) {
-    __shared__ float part[kReducePhases][64];
-    const uint32_t lane = threadIdx.x % 64, phase = threadIdx.x / 64;
-    const uint32_t c = blockIdx.x * 64 + lane;
+// COLS columns per workgroup and 1024 / COLS phases: 64 columns (16 phases)
+// for wide matrices, 16 columns (64 phases) for tall narrow ones.
+template <uint32_t COLS>
+__global__ __launch_bounds__(1024) void reduce_rows_kernel(const float* __restrict__ P, uint32_t n_rows,
+                                                           uint32_t n_cols, const uint32_t* __restrict__ seg_rows,
+                                                           float* __restrict__ out) {
+    constexpr uint32_t PH = 1024 / COLS;
+    __shared__ float part[PH][COLS];
+    const uint32_t lane = threadIdx.x % COLS, phase = threadIdx.x / COLS;
+    const uint32_t c = blockIdx.x * COLS + lane;
     const uint32_t seg = blockIdx.y;
     const uint32_t r0 = seg_rows ? seg_rows[seg] : 0;
     const uint32_t r1 = seg_rows ? seg_rows[seg + 1] : n_rows;
     float acc = 0.0f;
     if (c < n_cols) {
 #pragma unroll 8
-        for (uint32_t r = r0 + phase; r < r1; r += kReducePhases) acc += P[(uint64_t)r * n_cols + c];
+        for (uint32_t r = r0 + phase; r < r1; r += PH) acc += P[(uint64_t)r * n_cols + c];
     }
     part[phase][lane] = acc;
     __syncthreads();
-    for (uint32_t w = kReducePhases / 2; w > 0; w >>= 1) {
+    for (uint32_t w = PH / 2; w > 0; w >>= 1) {
         if (phase < w) part[phase][lane] = part[phase][lane] + part[phase + w][lane];
         __syncthreads();
     }
     if (phase == 0 && c < n_cols) out[(uint64_t)seg * n_cols + c] = part[0][lane];
+}
+
+// The reduce_rows_kernel shape for a matrix n_cols wide.
+void reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols, const uint32_t* seg_rows, uint32_t n_seg,
+                 float* out, hipStream_t stream) {
+    if (n_cols <= 16)
+        reduce_rows_kernel<16><<<dim3(ceil_div(n_cols, 16), n_seg), 1024, 0, stream>>>(P, n_rows, n_cols, seg_rows,
+                                                                                      out);
+    else
+        reduce_rows_kernel<64><<<dim3(ceil_div(n_cols, 64), n_seg), 1024, 0, stream>>>(P, n_rows, n_cols, seg_rows,
+                                                                                      out);
 }
 
 // ---------------------------------------------------------------------------
@@ -759,7 +785,7 @@ __global__ __launch_bounds__(256) void ls_dense_finalize_kernel(LsDenseArgs a, G
 
 }  // namespace
 
-uint32_t ls_tail_workgroups(uint32_t padded_b) { return ceil_div(padded_b, kTailRows); }
+uint32_t ls_tail_workgroups(uint32_t padded_b) { return ceil_div(padded_b, 16); }
 uint32_t ls_post_workgroups(uint32_t padded_b) { return ceil_div(padded_b / 16, kPostTiles); }
 uint32_t ls_max_chunks(uint32_t padded_b, uint32_t nb) {
     return ceil_div(padded_b / 16, kChunkTiles) + nb + 1;
@@ -789,12 +815,13 @@ int32_t launch_wrm_weight_sum(const float* score, uint32_t n, const LossParams& 
 
 int32_t launch_ls_tail(const LsDenseArgs& a, int32_t train, hipStream_t stream) {
     TATARA_REQUIRE(a.nb <= 16, "num_buckets must be <= 16");
+    TATARA_REQUIRE(a.padded_b % 16 == 0, "the sorted batch is whole 16-row tiles");
     const uint32_t blocks = ls_tail_workgroups(a.padded_b);
     if (blocks == 0) return kOk;
     if (a.l1 == 16 && a.l2 == 32) {
-        ls_tail_kernel<16, 32><<<blocks, kTailRows, 0, stream>>>(a, train);
+        ls_tail_kernel<16, 32><<<blocks, 64, 0, stream>>>(a, train);
     } else if (a.l1 == 8 && a.l2 == 32) {
-        ls_tail_kernel<8, 32><<<blocks, kTailRows, 0, stream>>>(a, train);
+        ls_tail_kernel<8, 32><<<blocks, 64, 0, stream>>>(a, train);
     } else {
         TATARA_REQUIRE(false, "LayerStack (l1, l2) must be (16, 32) or (8, 32)");
     }
@@ -849,15 +876,11 @@ int32_t launch_ls_dense_finalize(const LsDenseArgs& a, LsDenseGroup* groups,
     const TailDims td{a.l1, a.l2, a.nb};
     const uint32_t n_tail = ls_tail_workgroups(a.padded_b);
     const uint32_t n_post = ls_post_workgroups(a.padded_b);
-    const uint32_t tail_cols = a.nb * td.cells();
-    reduce_rows_kernel<<<dim3(ceil_div(tail_cols, 64), 1), 64 * kReducePhases, 0, stream>>>(
-        a.tail_partial, n_tail, tail_cols, nullptr, a.tail_sum);
-    reduce_rows_kernel<<<dim3(ceil_div(a.l1, 64), 1), 64 * kReducePhases, 0, stream>>>(a.b1s_partial, n_tail, a.l1,
-                                                                        nullptr, a.b1s_sum);
-    reduce_rows_kernel<<<dim3(ceil_div(2 * a.ft_out, 64), 1), 64 * kReducePhases, 0, stream>>>(
-        a.ftb_partial, n_post, 2 * a.ft_out, nullptr, a.ftb_sum);
-    reduce_rows_kernel<<<dim3(ceil_div(a.l1 * a.ft_out, 64), a.nb + 1), 64 * kReducePhases, 0, stream>>>(
-        a.w1_partial, 0, a.l1 * a.ft_out, a.chunk_info + 3 * a.max_chunks + 1, a.w1_seg);
+    // bucket g's tile partials are the rows [tail_seg[g], tail_seg[g + 1])
+    reduce_rows(a.tail_partial, n_tail, td.cells(), a.tail_seg, a.nb, a.tail_sum, stream);
+    reduce_rows(a.b1s_partial, n_tail, a.l1, nullptr, 1, a.b1s_sum, stream);
+    reduce_rows(a.ftb_partial, n_post, 2 * a.ft_out, nullptr, 1, a.ftb_sum, stream);
+    reduce_rows(a.w1_partial, 0, a.l1 * a.ft_out, a.chunk_info + 3 * a.max_chunks + 1, a.nb + 1, a.w1_seg, stream);
     TATARA_LAUNCHED("reduce_rows");
     ls_dense_finalize_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(a, gt, dense, bias, apply_update,
                                                                     keep_grads);
@@ -873,8 +896,7 @@ int32_t launch_reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols,
                            const uint32_t* seg_rows, uint32_t n_seg, float* out, hipStream_t stream) {
     TATARA_REQUIRE(seg_rows || n_seg == 1, "reduce_rows: n_seg must be 1 without segments");
     if (n_cols == 0 || n_seg == 0) return kOk;
-    reduce_rows_kernel<<<dim3(ceil_div(n_cols, 64), n_seg), 64 * kReducePhases, 0, stream>>>(P, n_rows, n_cols,
-                                                                               seg_rows, out);
+    reduce_rows(P, n_rows, n_cols, seg_rows, n_seg, out, stream);
     TATARA_LAUNCHED("reduce_rows");
     return kOk;
 }

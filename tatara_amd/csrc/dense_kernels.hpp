@@ -23,7 +23,6 @@ struct TailDims {
     __host__ __device__ uint32_t off_b1() const { return off_b3() + 1; }
 };
 
-constexpr uint32_t kTailRows = 128;      // sorted rows per tail workgroup
 constexpr uint32_t kChunkTiles = 16;     // 16-row tiles per L1 weight-gradient chunk
 constexpr uint32_t kPostTiles = 4;       // 16-row tiles per L1-input/FT-post row block
 
@@ -73,9 +72,10 @@ struct LsDenseArgs {
     const float* l3_b;          // [nb]
     float ft_post_scale, l1_sqr_scale;
     // partials
-    float* tail_partial;        // [n_tail_wg][nb][cells]
-    float* b1s_partial;         // [n_tail_wg][l1]
-    double* loss_partial;       // [n_tail_wg]
+    float* tail_partial;        // [n_tiles][cells], written for tiles of a valid bucket
+    uint32_t* tail_seg;         // [nb + 1] first tile of each bin (bin nb: end of the last bucket)
+    float* b1s_partial;         // [n_tiles][l1]
+    double* loss_partial;       // [n_tiles]
     float* w1_partial;          // [max_chunks][l1][ft_out]
     float* ftb_partial;         // [n_post_wg][2][ft_out]
     double* loss_out;           // [1] reduced loss

@@ -102,6 +102,7 @@ class LayerStackTrainer final : public TrainerBase {
     float *ft_stm = nullptr, *ft_nstm = nullptr, *combined = nullptr, *dft = nullptr;
     float *l1_sorted = nullptr, *dl1_sorted = nullptr, *net_out = nullptr;
     // partials
+    uint32_t* tail_seg = nullptr;
     float *tail_partial = nullptr, *b1s_partial = nullptr, *w1_partial = nullptr,
           *ftb_partial = nullptr;
     double* loss_partial = nullptr;
@@ -232,7 +233,7 @@ class LayerStackTrainer final : public TrainerBase {
         const TailDims td{l1, l2, nb};
         const uint64_t n_tail = ls_tail_workgroups(max_p), n_post = ls_post_workgroups(max_p);
         max_chunks = ls_max_chunks(max_p, nb);
-        if ((st = arena.alloc(&tail_partial, n_tail * nb * td.cells())) ||
+        if ((st = arena.alloc(&tail_partial, n_tail * td.cells())) || (st = arena.alloc(&tail_seg, nb + 1)) ||
             (st = arena.alloc(&b1s_partial, n_tail * l1)) || (st = arena.alloc(&loss_partial, n_tail)) ||
             (st = arena.alloc(&w1_partial, (uint64_t)max_chunks * l1 * ft_out)) ||
             (st = arena.alloc(&ftb_partial, n_post * 2 * ft_out)) ||
@@ -355,6 +356,7 @@ class LayerStackTrainer final : public TrainerBase {
         a.ft_post_scale = kFtPostScale;
         a.l1_sqr_scale = kL1SqrScale;
         a.tail_partial = tail_partial;
+        a.tail_seg = tail_seg;
         a.b1s_partial = b1s_partial;
         a.loss_partial = loss_partial;
         a.w1_partial = w1_partial;
