@@ -12,7 +12,7 @@
 //
 // MFMA (v_mfma_f32_16x16x4_f32) carries the two FT->L1 contractions (the L1
 // forward, K = 2*ft_out, and the L1 weight gradient, K = rows); the tiny L2/L3
-// layers run one row per thread.  Batch reductions go through per-workgroup
+// layers run one 64-lane workgroup per 16-row tile, four lanes per row.  Batch reductions go through per-workgroup
 // partials summed in a fixed order: no float atomics, bit-reproducible steps.
 #include "simple_kernels.hpp"
 
@@ -98,118 +98,132 @@ __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Output kernel: one thread per row.  CReLU, L2, CReLU, L3, loss; with train
-// the backward to dl1 and this workgroup's gradient partials (rows in order).
+// Tail: one 64-lane workgroup per 16-row tile.  Lane l serves row r = l % 16
+// with quarter q = l / 16: L2 outputs o = 8q..8q+7 in the forward, L1 inputs
+// k = q, q+4, .. in the backward.  The weights are staged in LDS.  Every
+// per-row sum keeps the reference order (k ascending for L2, o ascending for
+// L3 and the L2 input gradient); the gradient partials are per tile, rows in
+// order.
 // ---------------------------------------------------------------------------
 template <int L1, int L2>
-__global__ __launch_bounds__(kSimpleTailRows) void simple_tail_kernel(SimpleDenseArgs a,
-                                                                      int32_t train) {
-    constexpr int R = kSimpleTailRows;
-    __shared__ float s_l1a[R][L1 + 1];
-    __shared__ float s_dl2[R][L2 + 1];
-    __shared__ float s_l2a[R][L2 + 1];
-    __shared__ float s_dl1[R][L1 + 1];
-    __shared__ float s_dy[R];
-    __shared__ double s_loss[R];
+__global__ __launch_bounds__(64) void simple_tail_kernel(SimpleDenseArgs a, int32_t train) {
+    constexpr int OQ = L2 / 4;  // L2 outputs per lane
+    constexpr int KQ = L1 / 4;  // L1 inputs per lane (backward)
+    static_assert(L1 % 4 == 0 && L2 % 4 == 0, "quarters");
+    __shared__ float sW2[L1 * L2];
+    __shared__ float sB2[L2], sW3[L2];
+    __shared__ float s_l1p[16][L1 + 1];
+    __shared__ float s_l1a[16][L1 + 1];
+    __shared__ float s_l2a[16][L2 + 1];
+    __shared__ float s_dl2[16][L2 + 1];
+    __shared__ float s_dl1[16][L1 + 1];
+    __shared__ float s_dy[16];
+    __shared__ double s_loss[16];
 
-    const uint32_t t = threadIdx.x;
-    const uint32_t row = blockIdx.x * R + t;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t r = lane % 16, q = lane / 16;
+    const uint64_t tile = blockIdx.x;
+    const uint64_t row = tile * 16 + r;
     const bool real = row < a.batch;
-    float l1p[L1], l1a[L1], l2p[L2], l2a[L2];
-    float dy = 0.0f;
-    double loss_c = 0.0;
-    if (real) {
-        const float* src = a.l1_pre + (uint64_t)row * L1;
-#pragma unroll
-        for (int k = 0; k < L1; ++k) {
-            l1p[k] = src[k];
-            l1a[k] = crelu01(l1p[k]);
-        }
-#pragma unroll
-        for (int o = 0; o < L2; ++o) {
-            float acc = a.l2_b[o];
-#pragma unroll
-            for (int k = 0; k < L1; ++k) acc += l1a[k] * a.l2_w[k * L2 + o];
-            l2p[o] = acc;
-            l2a[o] = crelu01(acc);
-        }
-        float net = a.l3_b[0];
-#pragma unroll
-        for (int k = 0; k < L2; ++k) net += l2a[k] * a.l3_w[k];
-        a.net_output[row] = net;
-        loss_c = position_loss(net, a.score[row], a.wdl[row], a.wdl_lambda, a.loss, a.per_pos_norm,
-                               a.weight_sum, a.batch, dy);
+    for (uint32_t i = lane; i < (uint32_t)(L1 * L2); i += 64) sW2[i] = a.l2_w[i];
+    if (lane < (uint32_t)L2) {
+        sB2[lane] = a.l2_b[lane];
+        sW3[lane] = a.l3_w[lane];
     }
-    s_loss[t] = loss_c;
-    if (!train) {
-        __syncthreads();
-        if (t == 0) {
-            double acc = 0.0;
-            for (int k = 0; k < R; ++k) acc += s_loss[k];
-            a.loss_partial[blockIdx.x] = acc;
-        }
-        return;
+    // the tile's L1 pre-activations, read once and coalesced; padding rows are zero
+    const float* src = a.l1_pre + tile * 16 * L1;
+    for (uint32_t i = lane; i < (uint32_t)(16 * L1); i += 64) {
+        const uint32_t rr = i / L1, k = i % L1;
+        const float v = tile * 16 + rr < a.batch ? src[i] : 0.0f;
+        s_l1p[rr][k] = v;
+        s_l1a[rr][k] = crelu01(v);
     }
-
-    float dl2[L2], dl1[L1];
-    if (real) {
+    __syncthreads();  // staged weights and activations visible
+    // k outermost: every output's sum still adds k in ascending order
+    float l2p[OQ];
 #pragma unroll
-        for (int o = 0; o < L2; ++o) {
-            const float g = dy * a.l3_w[o];                    // x . W^T with out_dim 1
-            dl2[o] = (l2p[o] > 0.0f && l2p[o] < 1.0f) ? g : 0.0f;  // crelu_grad
-        }
-#pragma unroll
-        for (int k = 0; k < L1; ++k) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int o = 0; o < L2; ++o) acc += dl2[o] * a.l2_w[k * L2 + o];
-            dl1[k] = (l1p[k] > 0.0f && l1p[k] < 1.0f) ? acc : 0.0f;
-        }
-        float* d = a.dl1 + (uint64_t)row * L1;
-#pragma unroll
-        for (int k = 0; k < L1; ++k) d[k] = dl1[k];
-    } else {
-#pragma unroll
-        for (int o = 0; o < L2; ++o) dl2[o] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < L1; ++k) dl1[k] = 0.0f;
-    }
-#pragma unroll
+    for (int j = 0; j < OQ; ++j) l2p[j] = sB2[OQ * q + j];
+#pragma unroll 4
     for (int k = 0; k < L1; ++k) {
-        s_l1a[t][k] = real ? l1a[k] : 0.0f;
-        s_dl1[t][k] = dl1[k];
+        const float x = s_l1a[r][k];
+        const float* w = sW2 + k * L2 + OQ * q;
+#pragma unroll
+        for (int j = 0; j < OQ; ++j) l2p[j] += x * w[j];
     }
 #pragma unroll
-    for (int o = 0; o < L2; ++o) {
-        s_dl2[t][o] = dl2[o];
-        s_l2a[t][o] = real ? l2a[o] : 0.0f;
-    }
-    s_dy[t] = dy;
+    for (int j = 0; j < OQ; ++j) s_l2a[r][OQ * q + j] = real ? crelu01(l2p[j]) : 0.0f;
     __syncthreads();
-    if (t == 0) {
-        double acc = 0.0;
-        for (int k = 0; k < R; ++k) acc += s_loss[k];
-        a.loss_partial[blockIdx.x] = acc;
+    if (q == 0) {
+        double loss_c = 0.0;
+        float dy = 0.0f;
+        if (real) {
+            float net = a.l3_b[0];
+#pragma unroll
+            for (int k = 0; k < L2; ++k) net += s_l2a[r][k] * sW3[k];
+            a.net_output[row] = net;
+            loss_c = position_loss(net, a.score[row], a.wdl[row], a.wdl_lambda, a.loss, a.per_pos_norm,
+                                   a.weight_sum, a.batch, dy);
+        }
+        s_dy[r] = dy;
+        s_loss[r] = loss_c;
     }
+    __syncthreads();
+    if (lane == 0) {
+        double acc = 0.0;
+        for (int k = 0; k < 16; ++k) acc += s_loss[k];
+        a.loss_partial[tile] = acc;
+    }
+    if (!train) return;
+
+    const float dy = s_dy[r];
+#pragma unroll
+    for (int j = 0; j < OQ; ++j) {
+        const int o = OQ * q + j;
+        const float g = dy * sW3[o];                                  // x . W^T with out_dim 1
+        const float d = (l2p[j] > 0.0f && l2p[j] < 1.0f) ? g : 0.0f;  // crelu_grad
+        s_dl2[r][o] = real ? d : 0.0f;
+    }
+    __syncthreads();
+    // o outermost: every input's sum still adds o in ascending order
+    float g1[KQ];
+#pragma unroll
+    for (int i = 0; i < KQ; ++i) g1[i] = 0.0f;
+#pragma unroll 4
+    for (int o = 0; o < L2; ++o) {
+        const float d = s_dl2[r][o];
+#pragma unroll
+        for (int i = 0; i < KQ; ++i) g1[i] += d * sW2[((int)q + 4 * i) * L2 + o];
+    }
+#pragma unroll
+    for (int i = 0; i < KQ; ++i) {
+        const int k = (int)q + 4 * i;
+        const float p = s_l1p[r][k];
+        const float d = (real && p > 0.0f && p < 1.0f) ? g1[i] : 0.0f;
+        if (real) a.dl1[row * L1 + k] = d;
+        s_dl1[r][k] = d;
+    }
+    __syncthreads();
+
     const SimpleTailDims td{(uint32_t)L1, (uint32_t)L2};
     const uint32_t cells = td.cells();
-    float* part = a.tail_partial + (uint64_t)blockIdx.x * cells;
-    for (uint32_t c = t; c < cells; c += R) {
+    const int nreal = a.batch - tile * 16 < 16 ? (int)(a.batch - tile * 16) : 16;  // real rows come first
+    float* part = a.tail_partial + tile * cells;
+    for (uint32_t c = lane; c < cells; c += 64) {
         float acc = 0.0f;
         if (c < td.off_b2()) {
             const uint32_t k = c / L2, o = c % L2;
-            for (int r = 0; r < R; ++r) acc += s_l1a[r][k] * s_dl2[r][o];
+            for (int rr = 0; rr < nreal; ++rr) acc += s_l1a[rr][k] * s_dl2[rr][o];
         } else if (c < td.off_w3()) {
             const uint32_t o = c - td.off_b2();
-            for (int r = 0; r < R; ++r) acc += s_dl2[r][o];
+            for (int rr = 0; rr < nreal; ++rr) acc += s_dl2[rr][o];
         } else if (c < td.off_b3()) {
             const uint32_t o = c - td.off_w3();
-            for (int r = 0; r < R; ++r) acc += s_l2a[r][o] * s_dy[r];
+            for (int rr = 0; rr < nreal; ++rr) acc += s_l2a[rr][o] * s_dy[rr];
         } else if (c < td.off_b1()) {
-            for (int r = 0; r < R; ++r) acc += s_dy[r];
+            for (int rr = 0; rr < nreal; ++rr) acc += s_dy[rr];
         } else {
             const uint32_t k = c - td.off_b1();
-            for (int r = 0; r < R; ++r) acc += s_dl1[r][k];
+            for (int rr = 0; rr < nreal; ++rr) acc += s_dl1[rr][k];
         }
         part[c] = acc;
     }
@@ -367,7 +381,7 @@ __global__ __launch_bounds__(256) void simple_dense_finalize_kernel(SimpleDenseA
 
 }  // namespace
 
-uint32_t simple_tail_workgroups(uint32_t batch) { return ceil_div(batch, kSimpleTailRows); }
+uint32_t simple_tail_workgroups(uint32_t batch) { return ceil_div(batch, 16); }
 uint32_t simple_chunks(uint32_t batch) { return ceil_div(batch, kSimpleChunkRows); }
 uint32_t simple_post_workgroups(uint32_t batch) { return ceil_div(batch, kSimplePostRows); }
 
@@ -397,9 +411,9 @@ int32_t launch_simple_tail(const SimpleDenseArgs& a, int32_t train, hipStream_t 
     const uint32_t blocks = simple_tail_workgroups(a.batch);
     if (blocks == 0) return kOk;
     if (a.l1 == 32)
-        simple_tail_kernel<32, 32><<<blocks, kSimpleTailRows, 0, stream>>>(a, train);
+        simple_tail_kernel<32, 32><<<blocks, 64, 0, stream>>>(a, train);
     else
-        simple_tail_kernel<16, 32><<<blocks, kSimpleTailRows, 0, stream>>>(a, train);
+        simple_tail_kernel<16, 32><<<blocks, 64, 0, stream>>>(a, train);
     TATARA_LAUNCHED("simple_tail");
     return kOk;
 }

@@ -22,7 +22,6 @@ struct SimpleTailDims {
     __host__ __device__ uint32_t cells() const { return off_b1() + l1; }
 };
 
-constexpr uint32_t kSimpleTailRows = 64;     // rows per output workgroup (one wave)
 constexpr uint32_t kSimpleChunkRows = 256;   // rows per L1 weight-gradient chunk
 constexpr uint32_t kSimplePostRows = 128;    // rows per L1-input/FT-post workgroup
 
