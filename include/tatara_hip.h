@@ -94,6 +94,19 @@ TATARA_API int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm
                                  const int32_t* nstm_idx, const int32_t* nnz, float* grad,
                                  uint32_t batch, uint32_t ft_out, uint32_t cols,
                                  uint32_t max_active);
+/* The same gradient computed the way the trainers compute it for a
+ * factorized (king-bucketed) feature set: the rows of each king block are
+ * walked once in (perspective, position) order and added to the features of
+ * the block that occur in them, so every cell is the same sequential sum as
+ * sparse_ft_backward.rs:247-267 (stm then nstm).  A batch with a row whose
+ * features lie in two king blocks (piece_inputs rows each) is computed from
+ * occurrence lists instead; *used_block_scan (optional) reports which path
+ * ran.  Overwrites grad rows [0, cols).  Synchronises. */
+TATARA_API int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_idx,
+                                         const int32_t* nstm_idx, const int32_t* nnz, float* grad,
+                                         uint32_t batch, uint32_t ft_out, uint32_t cols,
+                                         uint32_t max_active, uint32_t piece_inputs,
+                                         uint32_t* used_block_scan);
 /* ft_fold_virtual / ft_reduce_virtual_grad, Base mode (native_kernels.cu:204-406). */
 TATARA_API int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,
                                   uint32_t ft_out, uint32_t piece_inputs);

@@ -16,7 +16,9 @@
 #include "ft_kernels.hpp"
 
 #include <hipcub/hipcub.hpp>
+#include <type_traits>
 
+#include "binsort.hpp"
 #include "common.hpp"
 #include "optim.hpp"
 
@@ -494,81 +496,95 @@ __device__ __forceinline__ void lookahead(vecf<V>& W, float* __restrict__ slow, 
     __builtin_nontemporal_store(S, s_);
 }
 
-// RAdam (+ Ranger lerp) on V consecutive cells with f32 moments; returns the
-// new weights.
-template <int V>
-__device__ __forceinline__ vecf<V> opt_update(float* __restrict__ w, float* __restrict__ m,
-                                              float* __restrict__ v, float* __restrict__ slow,
-                                              uint64_t off, vecf<V> g, const OptScalars& s) {
-    vecf<V>* w_ = reinterpret_cast<vecf<V>*>(w) + off;
-    vecf<V>* m_ = reinterpret_cast<vecf<V>*>(m) + off;
-    vecf<V>* v_ = reinterpret_cast<vecf<V>*>(v) + off;
-    vecf<V> W = __builtin_nontemporal_load(w_);
-    vecf<V> M = __builtin_nontemporal_load(m_);
-    vecf<V> Q = __builtin_nontemporal_load(v_);
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-        float a = W[k], b = M[k], c = Q[k];
-        radam_elem(a, b, c, g[k], s);
-        W[k] = a;
-        M[k] = b;
-        Q[k] = c;
-    }
-    if (s.lookahead) lookahead<V>(W, slow, off, s);
-    __builtin_nontemporal_store(W, w_);
-    __builtin_nontemporal_store(M, m_);
-    __builtin_nontemporal_store(Q, v_);
-    return W;
-}
-
-// The same with f16 moments stored scaled (radam_step_f16state,
-// native_kernels.cu:1118-1170): the previous moments are read back as
-// f16 / scale, the step runs in f32 on them, and the new moments are stored
-// as f16(m * m_scale) clamped to +-65504 and f16(v * v_scale) clamped above
-// at 65504 (a NaN stays NaN).
-template <int V>
-__device__ __forceinline__ vecf<V> opt_update_f16(float* __restrict__ w, _Float16* __restrict__ m16,
-                                                  _Float16* __restrict__ v16, float* __restrict__ slow,
-                                                  uint64_t off, vecf<V> g, const OptScalars& s, float ms,
-                                                  float vs) {
-    vecf<V>* w_ = reinterpret_cast<vecf<V>*>(w) + off;
-    vech<V>* m_ = reinterpret_cast<vech<V>*>(m16) + off;
-    vech<V>* v_ = reinterpret_cast<vech<V>*>(v16) + off;
-    vecf<V> W = __builtin_nontemporal_load(w_);
-    vech<V> M = __builtin_nontemporal_load(m_);
-    vech<V> Q = __builtin_nontemporal_load(v_);
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-        float a = W[k], b = (float)M[k] / ms, c = (float)Q[k] / vs;
-        radam_elem(a, b, c, g[k], s);
-        W[k] = a;
-        float sm = b * ms;
-        sm = sm > 65504.0f ? 65504.0f : (sm < -65504.0f ? -65504.0f : sm);
-        float sv = c * vs;
-        sv = sv > 65504.0f ? 65504.0f : sv;
-        M[k] = (_Float16)sm;
-        Q[k] = (_Float16)sv;
-    }
-    if (s.lookahead) lookahead<V>(W, slow, off, s);
-    __builtin_nontemporal_store(W, w_);
-    __builtin_nontemporal_store(M, m_);
-    __builtin_nontemporal_store(Q, v_);
-    return W;
-}
-
-// One cell group's update in the moment format the trainer uses, plus the f16
-// mirror of the new weights when the forward reads one.
+// The optimizer state of V consecutive cells (f32 weights; f32 moments, or
+// f16 moments stored scaled when HSTATE), loaded with non-temporal loads.
 template <int V, bool HSTATE>
-__device__ __forceinline__ void update_cells(const FtGradArgs& a, uint64_t off, vecf<V> g) {
-    vecf<V> W;
-    if constexpr (HSTATE)
-        W = opt_update_f16<V>(a.w, reinterpret_cast<_Float16*>(a.m16), reinterpret_cast<_Float16*>(a.v16), a.slow,
-                              off, g, a.opt, a.m_scale, a.v_scale);
-    else
-        W = opt_update<V>(a.w, a.m, a.v, a.slow, off, g, a.opt);
+struct CellState {
+    using Mom = typename std::conditional<HSTATE, vech<V>, vecf<V>>::type;
+    vecf<V> w;
+    Mom m, v;
+};
+
+template <int V, bool HSTATE>
+__device__ __forceinline__ CellState<V, HSTATE> load_cells(const FtGradArgs& a, uint64_t off) {
+    using Mom = typename CellState<V, HSTATE>::Mom;
+    CellState<V, HSTATE> c;
+    c.w = __builtin_nontemporal_load(reinterpret_cast<vecf<V>*>(a.w) + off);
+    if constexpr (HSTATE) {
+        c.m = __builtin_nontemporal_load(reinterpret_cast<Mom*>(a.m16) + off);
+        c.v = __builtin_nontemporal_load(reinterpret_cast<Mom*>(a.v16) + off);
+    } else {
+        c.m = __builtin_nontemporal_load(reinterpret_cast<Mom*>(a.m) + off);
+        c.v = __builtin_nontemporal_load(reinterpret_cast<Mom*>(a.v) + off);
+    }
+    return c;
+}
+
+// RAdam (+ Ranger lerp every lookahead step) of the loaded cells with
+// gradient g, and the stores: weights, moments (f16 moments as
+// radam_step_f16state, native_kernels.cu:1118-1170: read back as f16 / scale,
+// stored as f16(m * m_scale) clamped to +-65504 and f16(v * v_scale) clamped
+// above at 65504, a NaN staying NaN), and the f16 mirror of the new weights
+// when the forward reads one.
+template <int V, bool HSTATE>
+__device__ __forceinline__ void apply_cells(const FtGradArgs& a, uint64_t off, vecf<V> g,
+                                            CellState<V, HSTATE> c) {
+    const OptScalars& s = a.opt;
+    vecf<V> W = c.w;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        float w = W[k], m, v;
+        if constexpr (HSTATE) {
+            m = (float)c.m[k] / a.m_scale;
+            v = (float)c.v[k] / a.v_scale;
+        } else {
+            m = c.m[k];
+            v = c.v[k];
+        }
+        radam_elem(w, m, v, g[k], s);
+        W[k] = w;
+        if constexpr (HSTATE) {
+            float sm = m * a.m_scale;
+            sm = sm > 65504.0f ? 65504.0f : (sm < -65504.0f ? -65504.0f : sm);
+            float sv = v * a.v_scale;
+            sv = sv > 65504.0f ? 65504.0f : sv;
+            c.m[k] = (_Float16)sm;
+            c.v[k] = (_Float16)sv;
+        } else {
+            c.m[k] = m;
+            c.v[k] = v;
+        }
+    }
+    if (s.lookahead) {
+        vecf<V>* s_ = reinterpret_cast<vecf<V>*>(a.slow) + off;
+        vecf<V> S = __builtin_nontemporal_load(s_);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            float x = W[k], y = S[k];
+            lerp_elem(x, y, s.alpha);
+            W[k] = x;
+            S[k] = y;
+        }
+        __builtin_nontemporal_store(S, s_);
+    }
+    using Mom = typename CellState<V, HSTATE>::Mom;
+    __builtin_nontemporal_store(W, reinterpret_cast<vecf<V>*>(a.w) + off);
+    if constexpr (HSTATE) {
+        __builtin_nontemporal_store(c.m, reinterpret_cast<Mom*>(a.m16) + off);
+        __builtin_nontemporal_store(c.v, reinterpret_cast<Mom*>(a.v16) + off);
+    } else {
+        __builtin_nontemporal_store(c.m, reinterpret_cast<Mom*>(a.m) + off);
+        __builtin_nontemporal_store(c.v, reinterpret_cast<Mom*>(a.v) + off);
+    }
     if (a.mirror16)
         __builtin_nontemporal_store(__builtin_convertvector(W, vech<V>),
                                     reinterpret_cast<vech<V>*>(a.mirror16) + off);
+}
+
+// One cell group's update in the moment format the trainer uses.
+template <int V, bool HSTATE>
+__device__ __forceinline__ void update_cells(const FtGradArgs& a, uint64_t off, vecf<V> g) {
+    apply_cells<V, HSTATE>(a, off, g, load_cells<V, HSTATE>(a, off));
 }
 
 // dft_row_stride / dft_chunk_stride: the dft strides in elements (chunk =
@@ -585,6 +601,7 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
     constexpr uint32_t kCols = kWave * V;
     static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
                   "a lane's values must lie in one dft chunk");
+    if (a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0u) return;
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -614,6 +631,267 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
     if constexpr (HDFT) gr *= a.dft_inv_scale;
     if (a.grad) __builtin_nontemporal_store(gr, grad + off);
     if (a.apply_update) update_cells<V, HSTATE>(a, off, gr);
+}
+
+// ---------------------------------------------------------------------------
+// FT backward by block scan.
+//
+// In a king-bucketed feature set every active feature of a perspective lies
+// in that perspective's king block [K*PI, (K+1)*PI), so the dft rows that
+// contribute to block K's features are exactly the rows the forward schedule
+// files under block K: the stm rows of its bin (positions ascending), then
+// the nstm rows of its bin.  That is the order in which the reference CPU
+// backward visits them (stm pass over positions, then nstm), so walking the
+// list once and adding each row to the features that occur in it gives every
+// feature the sequential sum of the occurrence-list kernel above, bit for
+// bit.
+//
+// A workgroup owns one 256-column chunk and a group of GS features of one
+// block (wave w: features g*GS + 32w .. +31 of the block, accumulated in
+// registers, four columns per lane).  It stages each row's chunk in LDS once
+// (a dft row is read once per group instead of once per occurrence) and
+// every wave adds it to those of its features whose bit is set in the row's
+// hit mask.  Per stage of 32 rows a wave turns its 32 row masks into 32
+// feature masks (one ballot each), so feature k's accumulator is a fixed
+// register and its rows are added in list order.  The optimizer update of
+// the group's cells follows the scan in the same workgroup.
+//
+// Hit masks (ft_scan_masks_kernel): for schedule entry e (a row) and word
+// q = g*W + w, bit k of masks[q][e] is set when block feature g*GS + 32w + k
+// occurs in the row.  A row with a feature outside its own block, or with
+// one feature in two slots, sets *multi; the scan then leaves the step to
+// the occurrence-list kernel, which runs only in that case.
+// ---------------------------------------------------------------------------
+
+#ifndef TATARA_FT_SCAN_WAVES
+#define TATARA_FT_SCAN_WAVES 8
+#endif
+constexpr int kScanWaves = TATARA_FT_SCAN_WAVES;
+#ifndef TATARA_FT_SCAN_FEAT
+#define TATARA_FT_SCAN_FEAT 16
+#endif
+constexpr int kScanFeat = TATARA_FT_SCAN_FEAT;  // features per wave (low bits of a mask word)
+static_assert(kScanFeat <= 32, "a mask word per wave");
+constexpr int kScanStage = 32;  // rows per LDS stage
+
+constexpr int kScanMaxWords = 128;  // mask words per row
+
+struct ScanGeom {
+    uint32_t n_groups, group_size, words;
+};
+
+__host__ __device__ inline ScanGeom scan_geom(uint32_t piece_inputs) {
+    const uint32_t cap = (uint32_t)(kScanWaves * kScanFeat);
+    ScanGeom g;
+    g.n_groups = (piece_inputs + cap - 1) / cap;
+    g.group_size = g.n_groups ? (piece_inputs + g.n_groups - 1) / g.n_groups : 0;
+    g.words = g.n_groups * kScanWaves;
+    return g;
+}
+
+// One wave per schedule entry; lane = slot.
+__global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanGeom geom) {
+    __shared__ uint32_t s_m[4][kScanMaxWords];
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint64_t e = (uint64_t)blockIdx.x * 4 + wave;
+    const uint64_t two_b = 2ull * s.batch;
+    if (e >= two_b) return;
+    for (uint32_t q = lane; q < (uint32_t)kScanMaxWords; q += 64) s_m[wave][q] = 0u;
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t persp = e >= s.batch ? 1u : 0u;
+    const uint32_t pos = (uint32_t)s.schedule[e];
+    const int32_t* row = (persp ? s.idx_nstm : s.idx_stm) + (uint64_t)pos * s.max_active;
+    const int nn = s.nnz[pos] < (int)s.max_active ? s.nnz[pos] : (int)s.max_active;
+    int v = -1;
+    if (lane < (uint32_t)nn) v = row[lane];
+    const bool ok = lane < (uint32_t)nn && v >= 0 && (uint32_t)v < s.cols;
+    // the row's block: that of its first valid feature, as king_block_keys
+    const uint64_t okm = __ballot(ok);
+    uint32_t blk = 0;
+    if (okm) {
+        const int first = __builtin_ctzll(okm);
+        blk = (uint32_t)__shfl(v, first) / s.piece_inputs;
+        if (blk >= s.n_blocks) blk = s.n_blocks - 1;
+    }
+    bool dup = false;
+    if (ok) {
+        const int64_t local = (int64_t)v - (int64_t)blk * s.piece_inputs;
+        if (local < 0 || local >= (int64_t)s.piece_inputs) {
+            atomicOr(s.multi, 1u);
+        } else {
+            const uint32_t g = (uint32_t)local / geom.group_size;
+            const uint32_t r = (uint32_t)local - g * geom.group_size;
+            const uint32_t q = g * kScanWaves + r / kScanFeat;
+            const uint32_t bit = 1u << (r % kScanFeat);
+            const uint32_t old = atomicOr(&s_m[wave][q], bit);
+            dup = (old & bit) != 0u;
+        }
+    }
+    if (dup) atomicOr(s.multi, 1u);
+    __builtin_amdgcn_wave_barrier();
+    for (uint32_t q = lane; q < geom.words; q += 64) s.masks[(uint64_t)q * two_b + e] = s_m[wave][q];
+}
+
+template <bool HSTATE>
+__global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArgs a, FtBlockScan s,
+                                                                       ScanGeom geom) {
+    constexpr int R = kScanStage, RPW = kScanStage / kScanWaves;
+    static_assert(R == 32 && (RPW == 2 || RPW == 4), "32 rows per stage, two or four per wave");
+    if (__builtin_amdgcn_readfirstlane(*s.multi)) return;  // the occurrence-list kernel runs instead
+    // row R of each buffer stays zero: a feature without a row to add in a
+    // step of the paired loop below adds +0.0, which leaves any sum that
+    // started at +0.0 unchanged (such a sum is never -0.0)
+    __shared__ float4 s_rows[2][R + 1][64];
+    s_rows[0][R][threadIdx.x % 64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    s_rows[1][R][threadIdx.x % 64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t g = bid % geom.n_groups;
+    const uint32_t t2 = bid / geom.n_groups;
+    const uint32_t K = t2 % s.n_blocks;
+    const uint32_t chunk = t2 / s.n_blocks;
+    const uint32_t PI = s.piece_inputs;
+    const uint32_t blk_lo = K * PI;
+    const uint32_t blk_n = s.cols > blk_lo ? (s.cols - blk_lo < PI ? s.cols - blk_lo : PI) : 0u;
+    const uint32_t lo = g * geom.group_size + wave * kScanFeat;
+    const uint32_t g_hi = (g + 1) * geom.group_size < blk_n ? (g + 1) * geom.group_size : blk_n;
+    const uint32_t nf = g_hi > lo ? (g_hi - lo < (uint32_t)kScanFeat ? g_hi - lo : (uint32_t)kScanFeat) : 0u;
+    const uint32_t f0 = blk_lo + lo;
+    // the block's rows: its stm bin, then its nstm bin, as schedule entries
+    const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
+    const uint32_t b0 = s.sched_start[s.n_blocks + K];
+    const uint32_t n = na + (s.sched_start[s.n_blocks + K + 1] - b0);
+    const uint32_t* mrow = s.masks + (uint64_t)(g * kScanWaves + wave) * (2ull * s.batch);
+    const float4* dft4 = reinterpret_cast<const float4*>(a.dft + (uint64_t)chunk * a.dft_chunk_stride) + lane;
+    auto entry = [&](uint32_t j) -> uint32_t {
+        j = j < n ? j : n - 1;  // stage slots past the list repeat its last row (never used)
+        return j < na ? a0 + j : b0 + (j - na);
+    };
+    // Lane l < 32 loads the position of row 32T + l (its dft row adds the
+    // perspective offset where it is used) and its mask word (lanes 32..63
+    // and rows past the list count as 0 where it is used), so no load is
+    // waited for before its stage needs it.
+    auto positions = [&](uint32_t T) -> uint32_t { return (uint32_t)s.schedule[entry(T * R + (lane & 31u))]; };
+    auto masks = [&](uint32_t T) -> uint32_t { return mrow[entry(T * R + (lane & 31u))]; };
+    auto dft_row = [&](uint32_t pos_lanes, uint32_t j) -> const float4* {
+        const uint32_t e = entry(j);
+        const uint64_t r = (e >= s.batch ? (uint64_t)s.batch : 0ull) +
+                           (uint32_t)__builtin_amdgcn_readlane(pos_lanes, j % R);
+        return dft4 + r * (kDftChunk / 4);
+    };
+
+    float4 acc[kScanFeat];
+#pragma unroll
+    for (int k = 0; k < kScanFeat; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t n_stages = (n + R - 1) / R;
+    // Stage T = rows 32T .. 32T+31 of the list; wave w stages rows 32T + 4w
+    // .. +3 in LDS buffer T % 2.  Register sets A / B belong to even / odd
+    // stages.  While stage T is summed, the rows of stage T+2 are in flight
+    // (issued with row ids loaded a stage earlier, no scalar-load chain), the
+    // rows of stage T+1 wait in registers, and loads past the list repeat
+    // its last row.
+    float4 sA0, sA1, sA2, sA3, sB0, sB1, sB2, sB3;
+    uint32_t ridA = 0, ridB = 0, mA = 0, mB = 0;
+#define TATARA_LOAD_ROWS(S, RID, T)                          \
+    do {                                                     \
+        const uint32_t jb = (T) * R + wave * RPW;            \
+        S##0 = *dft_row(RID, jb + 0);                        \
+        S##1 = *dft_row(RID, jb + 1);                        \
+        if constexpr (RPW == 4) {                            \
+            S##2 = *dft_row(RID, jb + 2);                    \
+            S##3 = *dft_row(RID, jb + 3);                    \
+        }                                                    \
+    } while (0)
+#define TATARA_STORE_ROWS(BUF, S)                            \
+    do {                                                     \
+        s_rows[(BUF)][wave * RPW + 0][lane] = S##0;          \
+        s_rows[(BUF)][wave * RPW + 1][lane] = S##1;          \
+        if constexpr (RPW == 4) {                            \
+            s_rows[(BUF)][wave * RPW + 2][lane] = S##2;      \
+            s_rows[(BUF)][wave * RPW + 3][lane] = S##3;      \
+        }                                                    \
+    } while (0)
+#define TATARA_SUM_STAGE(BUF, M, T)                                       \
+    do {                                                                  \
+        const uint32_t mm = (lane < (uint32_t)R && (T) * R + lane < n) ? (M) : 0u; \
+        if (nf) {                                                         \
+            _Pragma("unroll") for (int k = 0; k < kScanFeat; k += 2) {    \
+                /* the stage's rows that hold features k and k+1, in      \
+                   ascending order; both rows are read before either add */ \
+                uint32_t r0 = (uint32_t)__ballot((mm >> k) & 1u);         \
+                uint32_t r1 = (uint32_t)__ballot((mm >> (k + 1)) & 1u);   \
+                while (r0 | r1) {                                         \
+                    const uint32_t j0 = r0 ? __builtin_ctz(r0) : (uint32_t)R; \
+                    const uint32_t j1 = r1 ? __builtin_ctz(r1) : (uint32_t)R; \
+                    r0 &= r0 - 1u;                                        \
+                    r1 &= r1 - 1u;                                        \
+                    const float4 x0 = s_rows[(BUF)][j0][lane];            \
+                    const float4 x1 = s_rows[(BUF)][j1][lane];            \
+                    acc[k] = f4add(acc[k], x0);                           \
+                    acc[k + 1] = f4add(acc[k + 1], x1);                   \
+                }                                                         \
+            }                                                             \
+        }                                                                 \
+    } while (0)
+#define TATARA_STAGE(T, X, Y, BUF)                \
+    do {                                          \
+        rid##Y = positions((T) + 3);              \
+        TATARA_LOAD_ROWS(s##X, rid##X, (T) + 2);  \
+        TATARA_SUM_STAGE(BUF, m##X, T);           \
+        m##X = masks((T) + 2);                    \
+        TATARA_STORE_ROWS((BUF) ^ 1, s##Y);       \
+        __syncthreads();                          \
+    } while (0)
+    if (n_stages > 0) {
+        // the same issue order as a stage (positions, rows, masks), so the
+        // loop is entered with the loads in flight that it expects
+        ridA = positions(0);
+        ridB = positions(1);
+        TATARA_LOAD_ROWS(sA, ridA, 0u);
+        mA = masks(0);
+        ridA = positions(2);
+        TATARA_LOAD_ROWS(sB, ridB, 1u);
+        mB = masks(1);
+        TATARA_STORE_ROWS(0, sA);
+    }
+    __syncthreads();
+    for (uint32_t t = 0; t < n_stages; t += 2) {
+        TATARA_STAGE(t, A, B, 0);
+        if (t + 1 >= n_stages) break;
+        TATARA_STAGE(t + 1, B, A, 1);
+    }
+#undef TATARA_LOAD_ROWS
+#undef TATARA_STORE_ROWS
+#undef TATARA_SUM_STAGE
+#undef TATARA_STAGE
+
+    const uint32_t col = chunk * kDftChunk + lane * 4;
+    if (col >= a.ft_out) return;
+    vecf<4>* grad = reinterpret_cast<vecf<4>*>(a.grad);
+    const uint64_t off0 = ((uint64_t)f0 * a.ft_out + col) / 4, row4 = a.ft_out / 4;
+    // the state of two features is loaded before either is updated
+    constexpr int kB = 2;
+    static_assert(kScanFeat % kB == 0, "feature batches");
+#pragma unroll
+    for (int kb = 0; kb < kScanFeat; kb += kB) {
+        CellState<4, HSTATE> cs[kB];
+        if (a.apply_update) {
+#pragma unroll
+            for (int u = 0; u < kB; ++u)
+                if ((uint32_t)(kb + u) < nf) cs[u] = load_cells<4, HSTATE>(a, off0 + (kb + u) * row4);
+        }
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            const int k = kb + u;
+            if ((uint32_t)k < nf) {
+                const uint64_t off = off0 + k * row4;
+                const vecf<4> gr = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
+                if (a.grad) __builtin_nontemporal_store(gr, grad + off);
+                if (a.apply_update) apply_cells<4, HSTATE>(a, off, gr, cs[u]);
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -655,11 +933,7 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint
     reinterpret_cast<float4*>(a.grad)[voff4] = vsum;
     if (!a.apply_update) return;
     const vecf<4> g = {vsum.x, vsum.y, vsum.z, vsum.w};
-    if constexpr (HSTATE)
-        opt_update_f16<4>(a.w, reinterpret_cast<_Float16*>(a.m16), reinterpret_cast<_Float16*>(a.v16), a.slow,
-                          voff4, g, a.opt, a.m_scale, a.v_scale);
-    else
-        opt_update<4>(a.w, a.m, a.v, a.slow, voff4, g, a.opt);
+    update_cells<4, HSTATE>(a, voff4, g);  // a factorizer has no f16 mirror
     if (!comb && !comb16) return;
     // the forward rows of this piece: comb = w + w_virtual (f32 add), rounded
     // to f16 for an f16 forward table (ft_fold_virtual_f16, native_kernels.cu:262-300)
@@ -891,6 +1165,43 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     }
 #undef TATARA_GRAD
     return kOk;
+}
+
+uint32_t ft_scan_mask_words(uint32_t piece_inputs) {
+    const ScanGeom g = scan_geom(piece_inputs);
+    return piece_inputs > 0 && g.words <= (uint32_t)kScanMaxWords ? g.words : 0u;
+}
+
+int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream) {
+    TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
+    TATARA_REQUIRE(s.max_active <= (uint32_t)kMaxActive, "max_active must be <= 64");
+    TATARA_REQUIRE(s.n_blocks >= 1, "block scan: n_blocks >= 1");
+    int32_t st = launch_fill_i32(reinterpret_cast<int32_t*>(s.multi), 1, 0, stream);
+    if (st) return st;
+    if (s.batch == 0) return kOk;
+    ft_scan_masks_kernel<<<ceil_div(2ull * s.batch, 4), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
+    TATARA_LAUNCHED("ft_scan_masks");
+    return kOk;
+}
+
+int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream) {
+    TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
+    TATARA_REQUIRE(a.dft && !a.dft16, "block scan: f32 dft");
+    TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
+                   "block scan: chunk-major dft");
+    TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "block scan: shapes");
+    const ScanGeom geom = scan_geom(s.piece_inputs);
+    const uint64_t grid = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks * geom.n_groups;
+    if (grid > 0) {
+        if (a.m16)
+            ft_grad_scan_kernel<true><<<(uint32_t)grid, kScanWaves * 64, 0, stream>>>(a, s, geom);
+        else
+            ft_grad_scan_kernel<false><<<(uint32_t)grid, kScanWaves * 64, 0, stream>>>(a, s, geom);
+        TATARA_LAUNCHED("ft_grad_scan");
+    }
+    FtGradArgs fallback = a;
+    fallback.run_if = s.multi;
+    return launch_ft_grad_update(fallback, stream);
 }
 
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,

@@ -66,10 +66,32 @@ struct FtGradArgs {
     uint32_t rows;             // real FT rows (ft_in)
     int32_t apply_update;      // 0: only write gradients
     OptScalars opt;
+    const uint32_t* run_if;    // when non-null the kernel does nothing unless *run_if != 0
+};
+
+// The block-scan FT backward (ft_grad_scan_kernel): the forward's king-block
+// schedule, per-row hit masks and the flag that hands a step to the
+// occurrence-list kernel.
+struct FtBlockScan {
+    const int32_t* idx_stm;
+    const int32_t* idx_nstm;
+    const int32_t* nnz;
+    const int32_t* schedule;      // [2*batch] positions grouped by (perspective, block), ascending
+    const uint32_t* sched_start;  // [2*n_blocks + 1] first entry of each (perspective, block) bin
+    uint32_t* masks;              // [ft_scan_mask_words(piece_inputs)][2*batch]
+    uint32_t* multi;              // [1] set when a row has features of two blocks, or one twice
+    uint32_t batch, max_active, cols, piece_inputs, n_blocks;
 };
 
 // Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).
 constexpr uint32_t kDftChunk = 256;
+
+// The trainers' FT backward for factorized feature sets with an f32 dft:
+// block scan (1) or occurrence lists only (0).
+#ifndef TATARA_FT_SCAN
+#define TATARA_FT_SCAN 1
+#endif
+constexpr bool kUseFtScan = TATARA_FT_SCAN != 0;
 
 int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream);
 int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm, const int32_t* nnz,
@@ -79,6 +101,13 @@ uint32_t occurrence_key_bits(uint32_t cols);
 size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols);
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream);
 int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream);
+// Mask words per schedule entry (0 when the block scan cannot serve piece_inputs).
+uint32_t ft_scan_mask_words(uint32_t piece_inputs);
+// Hit masks and the multi flag of a batch (after its schedule).
+int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream);
+// FT gradient + update by block scan (f32 chunk-major dft), with the
+// occurrence-list kernel as the fallback when *s.multi is set.
+int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream);
 // comb or comb16 (f16) receives the rewritten forward rows; both may be null.
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
                                hipStream_t stream);

@@ -52,6 +52,16 @@ struct DevScratch {
     }
 };
 
+// row-major [rows][ft_out] -> chunk-major [ceil(ft_out/256)][rows][256]
+__global__ void to_chunk_major_kernel(const float* __restrict__ src, float* __restrict__ dst, uint64_t rows,
+                                      uint32_t ft_out) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * ft_out) return;
+    const uint64_t r = i / ft_out;
+    const uint32_t c = (uint32_t)(i - r * ft_out);
+    dst[(uint64_t)(c / kDftChunk) * rows * kDftChunk + r * kDftChunk + c % kDftChunk] = src[i];
+}
+
 __global__ void copy_f4_kernel(const float4* __restrict__ src, float4* __restrict__ dst, uint64_t n4) {
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
@@ -277,6 +287,99 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
     g.apply_update = 0;
     if ((st = launch_ft_grad_update(g, 0))) return st;
     TATARA_HIP(hipDeviceSynchronize(), "ft_weight_grad");
+    return kOk;
+}
+
+int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_idx, const int32_t* nstm_idx,
+                                         const int32_t* nnz, float* grad, uint32_t batch, uint32_t ft_out,
+                                         uint32_t cols, uint32_t max_active, uint32_t piece_inputs,
+                                         uint32_t* used_block_scan) {
+    TATARA_REQUIRE(ft_out % 4 == 0, "ft_out must be a multiple of 4");
+    TATARA_REQUIRE(max_active <= 64, "max_active must be <= 64");
+    TATARA_REQUIRE(ft_scan_mask_words(piece_inputs) > 0, "piece_inputs out of range for the block scan");
+    int32_t st;
+    uint32_t n_blocks = ceil_div(cols, piece_inputs);
+    if (n_blocks > 128) n_blocks = 128;
+    const uint64_t two_b = 2ull * batch;
+    const uint32_t chunks = ceil_div(ft_out, kDftChunk);
+    // king-block schedule, as the trainer builds it for the forward
+    DevScratch keys, sched, hist, start, count, cm, masks, multi;
+    if ((st = keys.alloc(two_b)) || (st = sched.alloc(4 * two_b)) ||
+        (st = hist.alloc(4ull * 2 * n_blocks * binsort_tiles((uint32_t)two_b))) ||
+        (st = start.alloc(4ull * (2 * n_blocks + 1))) || (st = count.alloc(4ull * 2 * n_blocks)) ||
+        (st = cm.alloc(4ull * chunks * two_b * kDftChunk)) ||
+        (st = masks.alloc(4ull * ft_scan_mask_words(piece_inputs) * two_b)) ||
+        (st = multi.alloc(4)))
+        return st;
+    if ((st = launch_king_block_keys(stm_idx, nstm_idx, nnz, keys.as<uint8_t>(), batch, max_active, cols,
+                                     piece_inputs, n_blocks, 0)))
+        return st;
+    BinSortArgs bs{};
+    bs.keys = keys.as<uint8_t>();
+    bs.n_items = (uint32_t)two_b;
+    bs.n_bins = 2 * n_blocks;
+    bs.align = 1;
+    bs.value_mod = batch;
+    bs.hist = hist.as<uint32_t>();
+    bs.bin_start = start.as<uint32_t>();
+    bs.bin_count = count.as<uint32_t>();
+    bs.out = sched.as<int32_t>();
+    if ((st = launch_binsort(bs, 0))) return st;
+    if (two_b * ft_out > 0) {
+        to_chunk_major_kernel<<<ceil_div(two_b * ft_out, 256), 256>>>(dft, cm.as<float>(), two_b, ft_out);
+        TATARA_LAUNCHED("to_chunk_major");
+    }
+    FtBlockScan sc{};
+    sc.idx_stm = stm_idx;
+    sc.idx_nstm = nstm_idx;
+    sc.nnz = nnz;
+    sc.schedule = sched.as<int32_t>();
+    sc.sched_start = start.as<uint32_t>();
+    sc.masks = masks.as<uint32_t>();
+    sc.multi = multi.as<uint32_t>();
+    sc.batch = batch;
+    sc.max_active = max_active;
+    sc.cols = cols;
+    sc.piece_inputs = piece_inputs;
+    sc.n_blocks = n_blocks;
+    if ((st = launch_ft_scan_masks(sc, 0))) return st;
+    // occurrence lists for the fallback (a row with features of two blocks)
+    const uint64_t n_items = two_b * max_active;
+    const uint32_t n_keys = 2 * cols + 1;
+    DevScratch ki, vi, ko, vo, off, tmp;
+    const size_t tb = occurrence_sort_temp_bytes(n_items, cols);
+    if ((st = ki.alloc(4 * n_items)) || (st = vi.alloc(4 * n_items)) || (st = ko.alloc(4 * n_items)) ||
+        (st = vo.alloc(4 * n_items)) || (st = off.alloc(4ull * (n_keys + 1))) || (st = tmp.alloc(tb)))
+        return st;
+    OccurrenceSortArgs os{};
+    os.idx_stm = stm_idx;
+    os.idx_nstm = nstm_idx;
+    os.nnz = nnz;
+    os.batch = batch;
+    os.max_active = max_active;
+    os.cols = cols;
+    os.keys_in = ki.as<uint32_t>();
+    os.vals_in = vi.as<uint32_t>();
+    os.keys_out = ko.as<uint32_t>();
+    os.vals_out = vo.as<uint32_t>();
+    os.offsets = off.as<uint32_t>();
+    os.temp = tmp.p;
+    os.temp_bytes = tb;
+    if ((st = launch_occurrence_sort(os, 0))) return st;
+    FtGradArgs g{};
+    g.dft = cm.as<float>();
+    g.dft_row_stride = kDftChunk;
+    g.dft_chunk_stride = two_b * kDftChunk;
+    g.occ_vals = vo.as<uint32_t>();
+    g.occ_off = off.as<uint32_t>();
+    g.grad = grad;
+    g.ft_out = ft_out;
+    g.rows = cols;
+    g.apply_update = 0;
+    if ((st = launch_ft_grad_scan(g, sc, 0))) return st;
+    uint32_t m = 0;
+    TATARA_HIP(hipMemcpy(&m, multi.p, 4, hipMemcpyDeviceToHost), "ft_weight_grad_blocked");
+    if (used_block_scan) *used_block_scan = m ? 0u : 1u;
     return kOk;
 }
 

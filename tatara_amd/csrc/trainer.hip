@@ -98,6 +98,9 @@ class LayerStackTrainer final : public TrainerBase {
     uint32_t* occ_off = nullptr;
     void* occ_tmp = nullptr;
     size_t occ_tmp_bytes = 0;
+    // block-scan FT backward (f32 dft, factorized feature sets)
+    bool use_scan = false;
+    uint32_t *scan_masks = nullptr, *scan_multi = nullptr;
     // activations
     float *ft_stm = nullptr, *ft_nstm = nullptr, *combined = nullptr, *dft = nullptr;
     float *l1_sorted = nullptr, *dl1_sorted = nullptr, *net_out = nullptr;
@@ -217,6 +220,10 @@ class LayerStackTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_ko, n_items, false)) || (st = arena.alloc(&occ_vo, n_items, false)) ||
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
+            return st;
+        use_scan = kUseFtScan && factorized && !h_out && ft_scan_mask_words(pi) > 0;
+        if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
+                         (st = arena.alloc(&scan_multi, 1))))
             return st;
         const uint64_t dft_n = 2 * B * dft_chunks() * kDftChunk;
         if (h_out) {
@@ -369,6 +376,23 @@ class LayerStackTrainer final : public TrainerBase {
         return a;
     }
 
+    FtBlockScan block_scan(const BatchPtrs& p) const {
+        FtBlockScan sc{};
+        sc.idx_stm = p.stm;
+        sc.idx_nstm = p.nstm;
+        sc.nnz = p.nnz;
+        sc.schedule = schedule;
+        sc.sched_start = sched_start;
+        sc.masks = scan_masks;
+        sc.multi = scan_multi;
+        sc.batch = p.b;
+        sc.max_active = max_active;
+        sc.cols = ft_in;
+        sc.piece_inputs = pi;
+        sc.n_blocks = n_king_bins;
+        return sc;
+    }
+
     // prep + forward (+ loss); shared by train and validate
     int32_t forward(const BatchPtrs& p, float wdl_lambda, const LossParams& lp, int32_t train,
                     int slot, uint32_t& padded) {
@@ -415,6 +439,11 @@ class LayerStackTrainer final : public TrainerBase {
             bs.out = schedule;
             if ((st = launch_binsort(bs, stream))) return st;
             sched = schedule;
+            if (train && use_scan) {
+                // hit masks of the block-scan backward, beside the forward
+                if ((st = fork_side())) return st;
+                if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
+            }
         }
         // bucket sort (16-aligned, invalid buckets in bin nb)
         bucket_keys_kernel<<<ceil_div(b, 256), 256, 0, stream>>>(p.bucket, bkt_keys, b, nb);
@@ -516,7 +545,8 @@ class LayerStackTrainer final : public TrainerBase {
         fb.apply_update = 1;
         fb.opt = sf;
         if ((st = join_side())) return st;
-        if ((st = launch_ft_grad_update(fb, stream))) return st;
+        if ((st = use_scan ? launch_ft_grad_scan(fb, block_scan(p), stream) : launch_ft_grad_update(fb, stream)))
+            return st;
         if ((st = prof_mark(5))) return st;
         if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, h_fwd ? fwd16 : nullptr, stream))) return st;
         if (h_out) clamp_elems += 2ull * p.b * ft_out;

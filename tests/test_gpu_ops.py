@@ -108,6 +108,84 @@ def test_ft_weight_grad_bit_exact(gpu, b, ma, cols, ft_out):
     assert np.array_equal(g.to_host(), exp)
 
 
+def _blocked_grad(gpu, dft, si, ni, nnz, b, ft_out, cols, ma, pi):
+    D, S, Nn, N = dev(dft), dev(si), dev(ni), dev(nnz)
+    g = DeviceArray(np.full(cols * ft_out, 7.0, np.float32))
+    used = C.c_uint32(99)
+    check(gpu.tatara_op_ft_weight_grad_blocked(D.ptr, S.ptr, Nn.ptr, N.ptr, g.ptr, b, ft_out, cols, ma, pi,
+                                               C.byref(used)))
+    return g.to_host(), used.value
+
+
+def _oracle_grad(dft, si, ni, nnz, b, ft_out, cols, ma):
+    exp = np.zeros(cols * ft_out, np.float32)
+    ffi.sparse_ft_backward_nnz(dft[0].ravel(), si, nnz, exp, b, ft_out, cols, ma)
+    ffi.sparse_ft_backward_nnz(dft[1].ravel(), ni, nnz, exp, b, ft_out, cols, ma)
+    return exp
+
+
+@pytest.mark.parametrize("kb,pi,ma,b,ft_out", [(10, 64, 40, 256, 256), (45, 1629, 40, 1024, 512),
+                                               (81, 1548, 38, 512, 256), (7, 300, 12, 48, 200),
+                                               (3, 40, 8, 16, 64)])
+def test_ft_weight_grad_block_scan_bit_exact(gpu, kb, pi, ma, b, ft_out):
+    """King-bucketed rows: the block scan runs and every cell equals the
+    oracle's sequential stm-then-nstm sum."""
+    from tatara_amd.synthetic import small_spec, structured_batch, HALFKA_HM_MERGED, HALFKP
+    spec = {1629: HALFKA_HM_MERGED, 1548: HALFKP}.get(pi) or small_spec(king_buckets=kb, piece_inputs=pi,
+                                                                        max_active=ma)
+    batch, _ = structured_batch(b, spec, num_buckets=1, seed=pi + b, nnz_min=ma // 2)
+    cols = spec["ft_in"]
+    rng = np.random.default_rng(b)
+    dft = rng.standard_normal((2, b, ft_out)).astype(np.float32)
+    got, used = _blocked_grad(gpu, dft, batch.stm_indices, batch.nstm_indices, batch.nnz, b, ft_out, cols, ma,
+                              spec["piece_inputs"])
+    assert used == 1
+    exp = _oracle_grad(dft, batch.stm_indices, batch.nstm_indices, batch.nnz, b, ft_out, cols, ma)
+    assert np.array_equal(got, exp)
+
+
+def test_ft_weight_grad_block_scan_duplicates_and_ragged(gpu):
+    """A feature twice (or three times) in one row hands the batch to the
+    occurrence-list path; invalid and out-of-range slots and empty rows do
+    not.  Bit-exact either way."""
+    from tatara_amd.synthetic import small_spec, structured_batch
+    spec = small_spec(king_buckets=6, piece_inputs=96, max_active=24)
+    b, ma, ft_out = 96, 24, 256
+    batch, _ = structured_batch(b, spec, num_buckets=1, seed=5, nnz_min=4)
+    si, ni, nnz = batch.stm_indices.copy(), batch.nstm_indices.copy(), batch.nnz.copy()
+    nnz[:8] = ma
+    si[0, 5] = si[0, 0]               # twice
+    si[1, 3] = si[1, 9] = si[1, 2]    # three times
+    ni[2, 7] = ni[2, 1]
+    si[3, 4] = -1                     # skipped slot inside nnz
+    ni[4, 6] = spec["ft_in"] + 5      # out of range: skipped
+    nnz[5] = 0                        # empty row
+    cols = spec["ft_in"]
+    rng = np.random.default_rng(11)
+    dft = rng.standard_normal((2, b, ft_out)).astype(np.float32)
+    got, used = _blocked_grad(gpu, dft, si, ni, nnz, b, ft_out, cols, ma, spec["piece_inputs"])
+    assert used == 0
+    assert np.array_equal(got, _oracle_grad(dft, si, ni, nnz, b, ft_out, cols, ma))
+    # without the repeated features: the block scan
+    si[0, 5], si[1, 3], si[1, 9], ni[2, 7] = -1, -1, -1, -1
+    got, used = _blocked_grad(gpu, dft, si, ni, nnz, b, ft_out, cols, ma, spec["piece_inputs"])
+    assert used == 1
+    assert np.array_equal(got, _oracle_grad(dft, si, ni, nnz, b, ft_out, cols, ma))
+
+
+def test_ft_weight_grad_block_scan_falls_back(gpu):
+    """Rows whose features span king blocks take the occurrence-list path,
+    with the same bit-exact result."""
+    rng = np.random.default_rng(3)
+    b, ma, cols, ft_out, pi = 64, 20, 640, 256, 64
+    si, nnz = ragged_indices(rng, b, ma, cols)
+    ni, _ = ragged_indices(rng, b, ma, cols)
+    dft = rng.standard_normal((2, b, ft_out)).astype(np.float32)
+    got, used = _blocked_grad(gpu, dft, si, ni, nnz, b, ft_out, cols, ma, pi)
+    assert used == 0
+    assert np.array_equal(got, _oracle_grad(dft, si, ni, nnz, b, ft_out, cols, ma))
+
+
 def test_fold_reduce_bit_exact(gpu):
     rng = np.random.default_rng(9)
     ft_in, ft_out, pi = 45 * 12, 256, 12
