@@ -689,47 +689,53 @@ __host__ __device__ inline ScanGeom scan_geom(uint32_t piece_inputs) {
     return g;
 }
 
-// One wave per schedule entry; lane = slot.
+// 64 schedule entries per workgroup: a wave builds the masks of one entry at
+// a time (lane = slot) in LDS, then every mask plane's 64 words are written
+// as one coalesced segment.
 __global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanGeom geom) {
-    __shared__ uint32_t s_m[4][kScanMaxWords];
+    __shared__ uint32_t s_m[kScanMaxWords][65];  // [word][entry], padded against bank conflicts
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const uint64_t e = (uint64_t)blockIdx.x * 4 + wave;
+    const uint64_t e0 = (uint64_t)blockIdx.x * 64;
     const uint64_t two_b = 2ull * s.batch;
-    if (e >= two_b) return;
-    for (uint32_t q = lane; q < (uint32_t)kScanMaxWords; q += 64) s_m[wave][q] = 0u;
-    __builtin_amdgcn_wave_barrier();
-    const uint32_t persp = e >= s.batch ? 1u : 0u;
-    const uint32_t pos = (uint32_t)s.schedule[e];
-    const int32_t* row = (persp ? s.idx_nstm : s.idx_stm) + (uint64_t)pos * s.max_active;
-    const int nn = s.nnz[pos] < (int)s.max_active ? s.nnz[pos] : (int)s.max_active;
-    int v = -1;
-    if (lane < (uint32_t)nn) v = row[lane];
-    const bool ok = lane < (uint32_t)nn && v >= 0 && (uint32_t)v < s.cols;
-    // the row's block: that of its first valid feature, as king_block_keys
-    const uint64_t okm = __ballot(ok);
-    uint32_t blk = 0;
-    if (okm) {
-        const int first = __builtin_ctzll(okm);
-        blk = (uint32_t)__shfl(v, first) / s.piece_inputs;
-        if (blk >= s.n_blocks) blk = s.n_blocks - 1;
-    }
-    bool dup = false;
-    if (ok) {
-        const int64_t local = (int64_t)v - (int64_t)blk * s.piece_inputs;
-        if (local < 0 || local >= (int64_t)s.piece_inputs) {
-            atomicOr(s.multi, 1u);
-        } else {
-            const uint32_t g = (uint32_t)local / geom.group_size;
-            const uint32_t r = (uint32_t)local - g * geom.group_size;
-            const uint32_t q = g * kScanWaves + r / kScanFeat;
-            const uint32_t bit = 1u << (r % kScanFeat);
-            const uint32_t old = atomicOr(&s_m[wave][q], bit);
-            dup = (old & bit) != 0u;
+    for (uint32_t i = threadIdx.x; i < geom.words * 64; i += 256) s_m[i / 64][i % 64] = 0u;
+    __syncthreads();
+    bool multi = false;
+    for (uint32_t r = wave; r < 64 && e0 + r < two_b; r += 4) {
+        const uint64_t e = e0 + r;
+        const uint32_t persp = e >= s.batch ? 1u : 0u;
+        const uint32_t pos = (uint32_t)s.schedule[e];
+        const int32_t* row = (persp ? s.idx_nstm : s.idx_stm) + (uint64_t)pos * s.max_active;
+        const int nn = s.nnz[pos] < (int)s.max_active ? s.nnz[pos] : (int)s.max_active;
+        int v = -1;
+        if (lane < (uint32_t)nn) v = row[lane];
+        const bool ok = lane < (uint32_t)nn && v >= 0 && (uint32_t)v < s.cols;
+        // the row's block: that of its first valid feature, as king_block_keys
+        const uint64_t okm = __ballot(ok);
+        uint32_t blk = 0;
+        if (okm) {
+            blk = (uint32_t)__shfl(v, (int)__builtin_ctzll(okm)) / s.piece_inputs;
+            if (blk >= s.n_blocks) blk = s.n_blocks - 1;
+        }
+        if (ok) {
+            const int64_t local = (int64_t)v - (int64_t)blk * s.piece_inputs;
+            if (local < 0 || local >= (int64_t)s.piece_inputs) {
+                multi = true;  // a feature outside the row's block
+            } else {
+                const uint32_t g = (uint32_t)local / geom.group_size;
+                const uint32_t rr = (uint32_t)local - g * geom.group_size;
+                const uint32_t q = g * kScanWaves + rr / kScanFeat;
+                const uint32_t bit = 1u << (rr % kScanFeat);
+                const uint32_t old = atomicOr(&s_m[q][r], bit);
+                if (old & bit) multi = true;  // the feature is in the row twice
+            }
         }
     }
-    if (dup) atomicOr(s.multi, 1u);
-    __builtin_amdgcn_wave_barrier();
-    for (uint32_t q = lane; q < geom.words; q += 64) s.masks[(uint64_t)q * two_b + e] = s_m[wave][q];
+    if (multi) atomicOr(s.multi, 1u);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < geom.words * 64; i += 256) {
+        const uint32_t q = i / 64, r = i % 64;
+        if (e0 + r < two_b) s.masks[(uint64_t)q * two_b + e0 + r] = s_m[q][r];
+    }
 }
 
 template <bool HSTATE>
@@ -1179,7 +1185,7 @@ int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream) {
     int32_t st = launch_fill_i32(reinterpret_cast<int32_t*>(s.multi), 1, 0, stream);
     if (st) return st;
     if (s.batch == 0) return kOk;
-    ft_scan_masks_kernel<<<ceil_div(2ull * s.batch, 4), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
+    ft_scan_masks_kernel<<<ceil_div(2ull * s.batch, 64), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
     TATARA_LAUNCHED("ft_scan_masks");
     return kOk;
 }

@@ -86,8 +86,10 @@ struct FtBlockScan {
 // Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).
 constexpr uint32_t kDftChunk = 256;
 
-// The trainers' FT backward for factorized feature sets with an f32 dft:
-// block scan (1) or occurrence lists only (0).
+// The trainers' FT backward for factorized feature sets with an f32 dft and
+// ft_out of two 256-column chunks or more (with one chunk a batch gives too
+// few workgroups for the scan to pay): block scan (1) or occurrence lists
+// only (0).
 #ifndef TATARA_FT_SCAN
 #define TATARA_FT_SCAN 1
 #endif

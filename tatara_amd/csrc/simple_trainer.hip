@@ -56,6 +56,9 @@ class SimpleTrainer final : public TrainerBase {
     uint32_t* occ_off = nullptr;
     void* occ_tmp = nullptr;
     size_t occ_tmp_bytes = 0;
+    // block-scan FT backward (factorized feature sets)
+    bool use_scan = false;
+    uint32_t *scan_masks = nullptr, *scan_multi = nullptr;
     // activations
     float *ft_stm = nullptr, *ft_nstm = nullptr, *combined = nullptr, *dft = nullptr;
     float *l1_pre = nullptr, *dl1 = nullptr, *net_out = nullptr;
@@ -150,6 +153,10 @@ class SimpleTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_ko, n_items, false)) || (st = arena.alloc(&occ_vo, n_items, false)) ||
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
+            return st;
+        use_scan = kUseFtScan && factorized && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
+        if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
+                         (st = arena.alloc(&scan_multi, 1))))
             return st;
         if ((st = arena.alloc(&ft_stm, B * ft_out, false)) || (st = arena.alloc(&ft_nstm, B * ft_out, false)) ||
             (st = arena.alloc(&combined, B * K, false)) || (st = arena.alloc(&dft, 2 * B * dft_chunks() * kDftChunk, false)) ||
@@ -274,6 +281,23 @@ class SimpleTrainer final : public TrainerBase {
         return a;
     }
 
+    FtBlockScan block_scan(const BatchPtrs& p) const {
+        FtBlockScan sc{};
+        sc.idx_stm = p.stm;
+        sc.idx_nstm = p.nstm;
+        sc.nnz = p.nnz;
+        sc.schedule = schedule;
+        sc.sched_start = sched_start;
+        sc.masks = scan_masks;
+        sc.multi = scan_multi;
+        sc.batch = p.b;
+        sc.max_active = max_active;
+        sc.cols = ft_in;
+        sc.piece_inputs = pi;
+        sc.n_blocks = n_king_bins;
+        return sc;
+    }
+
     int32_t forward(const BatchPtrs& p, float wdl_lambda, const LossParams& lp, int32_t train, int slot) {
         int32_t st;
         const uint32_t b = p.b;
@@ -316,6 +340,11 @@ class SimpleTrainer final : public TrainerBase {
             bs.out = schedule;
             if ((st = launch_binsort(bs, stream))) return st;
             sched = schedule;
+            if (train && use_scan) {
+                // hit masks of the block-scan backward, beside the forward
+                if ((st = fork_side())) return st;
+                if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
+            }
         }
         if (train && (st = prof_mark(1))) return st;
         FtForwardArgs fa{};
@@ -382,7 +411,8 @@ class SimpleTrainer final : public TrainerBase {
         fb.apply_update = 1;
         fb.opt = scalars(0, lr, step_count);
         if ((st = join_side())) return st;
-        if ((st = launch_ft_grad_update(fb, stream))) return st;
+        if ((st = use_scan ? launch_ft_grad_scan(fb, block_scan(p), stream) : launch_ft_grad_update(fb, stream)))
+            return st;
         if ((st = prof_mark(5))) return st;
         if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, nullptr, stream))) return st;
         if ((st = prof_mark(6))) return st;

@@ -112,8 +112,36 @@ def test_one_step_matches_oracle(gpu, loss, optimizer):
         assert t.step_count == 1
 
 
-def test_multi_step_ranger_with_lookahead(gpu):
-    sh, cfg = make(optimizer="ranger")
+def test_rows_across_king_blocks_and_repeated_features(gpu):
+    """Index rows that are not king-bucketed (features of several blocks in
+    one row) or repeat a feature: the step takes the occurrence-list FT
+    backward and still matches the oracle; the next king-bucketed batch
+    takes the block scan again (ft_out of two 256-column chunks)."""
+    from tatara_amd.trainer import Batch
+    sh, cfg = make(optimizer="ranger", ft_out=512)
+    b = cfg.max_batch
+    rng = np.random.default_rng(21)
+    batch, bucket = batch_for(2, b, sh.nb)
+    stm = batch.stm_indices.copy()
+    stm[:, 0] = rng.integers(0, sh.ft_in, b)  # first slot from any block
+    nstm = batch.nstm_indices.copy()
+    nstm[5, 3] = nstm[5, 2]                   # a repeated feature
+    mixed = Batch(stm, nstm, batch.nnz, batch.score, batch.wdl)
+    st = ols.default_init(sh)
+    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+    with LayerStackTrainer(cfg) as t:
+        for step, (bt, bk) in enumerate([(mixed, bucket), batch_for(3, b, sh.nb)], start=1):
+            t.train_step(bt, bk, 1e-3, 0.0, Sigmoid())
+            ols.train_step(sh, st, as_dict(bt, bk), opt, 1e-3, 0.0, loss_dict(Sigmoid()), step)
+            for name in ("ft_w", "ft_b"):
+                for k in ("w", "m", "v"):
+                    close(t.get(name, k), st[name][k], 1e-5, atol=1e-6 if k == "w" else 0.0,
+                          atol_frac=1e-5 if k != "w" else 0.0, what=f"step {step} {name}.{k}")
+
+
+@pytest.mark.parametrize("ft_out", [256, 512], ids=["occurrence_lists", "block_scan"])
+def test_multi_step_ranger_with_lookahead(gpu, ft_out):
+    sh, cfg = make(optimizer="ranger", ft_out=ft_out)
     b = cfg.max_batch
     st = ols.default_init(sh)
     opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
