@@ -97,9 +97,10 @@ def algorithmic_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, o
     sums and combined written (out_rows rows of ft_out values per position:
     3 for LayerStack, whose combined is ft_out wide; 4 for Simple, 2*ft_out)
     + index rows + nnz.
-    ft_grad_update: gathered dft rows (one per occurrence) + occurrence
-    list + w, m, v read and written for every real row (+ slow on the
-    lookahead step, 1 in 6) + the row gradient written for the virtual rows.
+    FT gradient + update (ft_grad_scan_kernel or ft_grad_update_kernel, the
+    reference's formula whichever kernel runs): gathered dft rows (one per
+    occurrence) + occurrence list + w, m, v read and written for every real
+    row (+ slow on the lookahead step, 1 in 6) + the row gradient written.
     f16 (the --all-optim modes): gathered rows, the two raw sums, the dft and
     the moments are 2 bytes per value; w, slow, combined and the gradient stay 4.
     """
@@ -427,11 +428,16 @@ def main() -> int:
                                               lookahead_frac=la,
                                               out_rows=3 if w["arch"] == "layerstack" else 4,
                                               f16=bool(w.get("all_optim")))
-    # the f16 forward table is gathered by the eight-column pair kernel
+    # the f16 forward table is gathered by the eight-column pair kernel; the
+    # trainers run the FT gradient as a block scan for an f32 dft of two
+    # 256-column chunks or more (factorized feature sets), else from
+    # occurrence lists
     fwd_kernel = "ft_forward_pair16_kernel" if w.get("all_optim") else "ft_forward_kernel"
+    grad_kernel = ("ft_grad_scan_kernel" if not w.get("all_optim") and w["ft_out"] >= 512
+                   else "ft_grad_update_kernel")
     kernels = {
         fwd_kernel: (phase_avg["ft_forward"], fwd_bytes),
-        "ft_grad_update_kernel": (phase_avg["ft_grad_update"], grad_bytes),
+        grad_kernel: (phase_avg["ft_grad_update"], grad_bytes),
     }
     dom = max(kernels, key=lambda k: kernels[k][0])
     ms, byts = kernels[dom]

@@ -597,16 +597,8 @@ __device__ __forceinline__ void update_cells(const FtGradArgs& a, uint64_t off, 
 // their order are those of PHASE 0; a split pass gathers from half the dft
 // rows of a king block at a time.
 template <int V, bool HDFT, bool HSTATE, int PHASE>
-__global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint32_t n_chunks) {
+__device__ __forceinline__ void grad_update_task(const FtGradArgs& a, uint64_t task, uint32_t lane) {
     constexpr uint32_t kCols = kWave * V;
-    static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
-                  "a lane's values must lie in one dft chunk");
-    if (a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0u) return;
-    const uint32_t wave = threadIdx.x / kWave;
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
-    if (task >= (uint64_t)a.rows * n_chunks) return;
     const uint32_t chunk = (uint32_t)(task / a.rows);
     const uint32_t f = (uint32_t)(task - (uint64_t)chunk * a.rows);
     const uint32_t col = chunk * kCols + lane * V;
@@ -631,6 +623,24 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
     if constexpr (HDFT) gr *= a.dft_inv_scale;
     if (a.grad) __builtin_nontemporal_store(gr, grad + off);
     if (a.apply_update) update_cells<V, HSTATE>(a, off, gr);
+}
+
+// One wave per task (feature row, column chunk), tasks strided over the
+// grid (a gated launch uses a bounded grid, so it costs little when *run_if
+// is 0).
+template <int V, bool HDFT, bool HSTATE, int PHASE>
+__global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint32_t n_chunks) {
+    constexpr uint32_t kCols = kWave * V;
+    static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
+                  "a lane's values must lie in one dft chunk");
+    if (a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0u) return;
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint64_t total = (uint64_t)a.rows * n_chunks;
+    const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock;
+    for (uint64_t task = (uint64_t)bid * kWavesPerBlock + wave; task < total; task += stride)
+        grad_update_task<V, HDFT, HSTATE, PHASE>(a, task, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1145,12 +1155,16 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     const uint32_t n_chunks = ceil_div(a.ft_out, kCols);
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
-    const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+    // a gated launch (the block scan's fallback) strides over a bounded grid
+    const uint32_t cap = a.run_if ? 8192u : 0xFFFFFFFFu;
+    uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+    blocks = blocks < cap ? blocks : cap;
     // four f16 values per lane: a wave's rows are 512 bytes, so a king
     // block's dft working set stays half the f32 one (eight values per lane
     // halve the loads but double that working set, and measure slower)
     const uint32_t c4 = ceil_div(a.ft_out, kWave * 4);
-    const uint32_t b4 = (uint32_t)(((uint64_t)a.rows * c4 + kWavesPerBlock - 1) / kWavesPerBlock);
+    uint32_t b4 = (uint32_t)(((uint64_t)a.rows * c4 + kWavesPerBlock - 1) / kWavesPerBlock);
+    b4 = b4 < cap ? b4 : cap;
 #define TATARA_GRAD(PH)                                                                           \
     do {                                                                                          \
         if (hdft && hstate)                                                                       \
@@ -1190,7 +1204,7 @@ int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream) {
     return kOk;
 }
 
-int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream) {
+int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
     TATARA_REQUIRE(a.dft && !a.dft16, "block scan: f32 dft");
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
@@ -1205,9 +1219,10 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
             ft_grad_scan_kernel<false><<<(uint32_t)grid, kScanWaves * 64, 0, stream>>>(a, s, geom);
         TATARA_LAUNCHED("ft_grad_scan");
     }
-    FtGradArgs fallback = a;
-    fallback.run_if = s.multi;
-    return launch_ft_grad_update(fallback, stream);
+    if (!fallback) return kOk;
+    FtGradArgs gated = a;
+    gated.run_if = s.multi;
+    return launch_ft_grad_update(gated, stream);
 }
 
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,

@@ -107,9 +107,10 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream);
 uint32_t ft_scan_mask_words(uint32_t piece_inputs);
 // Hit masks and the multi flag of a batch (after its schedule).
 int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream);
-// FT gradient + update by block scan (f32 chunk-major dft), with the
-// occurrence-list kernel as the fallback when *s.multi is set.
-int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream);
+// FT gradient + update by block scan (f32 chunk-major dft); the kernel does
+// nothing when *s.multi is set.  With fallback, the occurrence-list kernel
+// (its lists already sorted) is queued behind it and runs only in that case.
+int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback = true);
 // comb or comb16 (f16) receives the rewritten forward rows; both may be null.
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
                                hipStream_t stream);

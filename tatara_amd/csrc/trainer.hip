@@ -376,6 +376,40 @@ class LayerStackTrainer final : public TrainerBase {
         return a;
     }
 
+    // Occurrence lists of the batch (key 2*feature + perspective).
+    int32_t sort_occurrences(const BatchPtrs& p, hipStream_t s) {
+        OccurrenceSortArgs os{};
+        os.idx_stm = p.stm;
+        os.idx_nstm = p.nstm;
+        os.nnz = p.nnz;
+        os.batch = p.b;
+        os.max_active = max_active;
+        os.cols = ft_in;
+        os.keys_in = occ_ki;
+        os.vals_in = occ_vi;
+        os.keys_out = occ_ko;
+        os.vals_out = occ_vo;
+        os.offsets = occ_off;
+        os.temp = occ_tmp;
+        os.temp_bytes = occ_tmp_bytes;
+        return launch_occurrence_sort(os, s);
+    }
+
+    // FT gradient + update: the block scan, or occurrence lists when the
+    // trainer does not scan or the batch has a row the scan cannot take
+    // (the flag posted beside the forward; reading it waits only for the
+    // hit-mask pass, which runs early in the step).
+    int32_t ft_gradient(const BatchPtrs& p, const FtGradArgs& fb) {
+        int32_t st;
+        if (use_scan) {
+            uint32_t multi = 0;
+            if ((st = read_flag(multi))) return st;
+            if (!multi) return launch_ft_grad_scan(fb, block_scan(p), stream, false);
+            if ((st = sort_occurrences(p, stream))) return st;
+        }
+        return launch_ft_grad_update(fb, stream);
+    }
+
     FtBlockScan block_scan(const BatchPtrs& p) const {
         FtBlockScan sc{};
         sc.idx_stm = p.stm;
@@ -400,26 +434,12 @@ class LayerStackTrainer final : public TrainerBase {
         const uint32_t b = p.b;
         padded = padded_sort_batch(b, nb);
         if (train && (st = prof_mark(0))) return st;
-        if (train) {
+        if (train && !use_scan) {
             // occurrence lists for the FT backward, on the side stream: they
             // depend only on the indices and are first needed by the FT
             // gradient, so the sort overlaps the forward
             if ((st = fork_side())) return st;
-            OccurrenceSortArgs os{};
-            os.idx_stm = p.stm;
-            os.idx_nstm = p.nstm;
-            os.nnz = p.nnz;
-            os.batch = b;
-            os.max_active = max_active;
-            os.cols = ft_in;
-            os.keys_in = occ_ki;
-            os.vals_in = occ_vi;
-            os.keys_out = occ_ko;
-            os.vals_out = occ_vo;
-            os.offsets = occ_off;
-            os.temp = occ_tmp;
-            os.temp_bytes = occ_tmp_bytes;
-            if ((st = launch_occurrence_sort(os, side))) return st;
+            if ((st = sort_occurrences(p, side))) return st;
         }
         // king-block schedule for the gather
         const int32_t* sched = nullptr;
@@ -440,9 +460,11 @@ class LayerStackTrainer final : public TrainerBase {
             if ((st = launch_binsort(bs, stream))) return st;
             sched = schedule;
             if (train && use_scan) {
-                // hit masks of the block-scan backward, beside the forward
+                // hit masks of the block-scan backward, beside the forward;
+                // the host learns whether the batch needs occurrence lists
                 if ((st = fork_side())) return st;
                 if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
+                if ((st = post_flag(scan_multi, side))) return st;
             }
         }
         // bucket sort (16-aligned, invalid buckets in bin nb)
@@ -545,8 +567,7 @@ class LayerStackTrainer final : public TrainerBase {
         fb.apply_update = 1;
         fb.opt = sf;
         if ((st = join_side())) return st;
-        if ((st = use_scan ? launch_ft_grad_scan(fb, block_scan(p), stream) : launch_ft_grad_update(fb, stream)))
-            return st;
+        if ((st = ft_gradient(p, fb))) return st;
         if ((st = prof_mark(5))) return st;
         if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, h_fwd ? fwd16 : nullptr, stream))) return st;
         if (h_out) clamp_elems += 2ull * p.b * ft_out;
