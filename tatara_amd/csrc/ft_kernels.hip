@@ -625,22 +625,28 @@ __device__ __forceinline__ void grad_update_task(const FtGradArgs& a, uint64_t t
     if (a.apply_update) update_cells<V, HSTATE>(a, off, gr);
 }
 
-// One wave per task (feature row, column chunk), tasks strided over the
-// grid (a gated launch uses a bounded grid, so it costs little when *run_if
-// is 0).
-template <int V, bool HDFT, bool HSTATE, int PHASE>
+// One wave per task (feature row, column chunk).  GATED: the launch does
+// nothing unless *run_if != 0 and strides its tasks over a bounded grid, so
+// it costs little when skipped (the block scan's fallback); otherwise one
+// task per wave, which keeps the gather loop's code tight.
+template <int V, bool HDFT, bool HSTATE, int PHASE, bool GATED>
 __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint32_t n_chunks) {
     constexpr uint32_t kCols = kWave * V;
     static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
                   "a lane's values must lie in one dft chunk");
-    if (a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0u) return;
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint64_t total = (uint64_t)a.rows * n_chunks;
-    const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock;
-    for (uint64_t task = (uint64_t)bid * kWavesPerBlock + wave; task < total; task += stride)
-        grad_update_task<V, HDFT, HSTATE, PHASE>(a, task, lane);
+    if constexpr (GATED) {
+        if (__builtin_amdgcn_readfirstlane(*a.run_if) == 0u) return;
+        const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock;
+        for (uint64_t task = (uint64_t)bid * kWavesPerBlock + wave; task < total; task += stride)
+            grad_update_task<V, HDFT, HSTATE, PHASE>(a, task, lane);
+    } else {
+        const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
+        if (task < total) grad_update_task<V, HDFT, HSTATE, PHASE>(a, task, lane);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1165,17 +1171,24 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     const uint32_t c4 = ceil_div(a.ft_out, kWave * 4);
     uint32_t b4 = (uint32_t)(((uint64_t)a.rows * c4 + kWavesPerBlock - 1) / kWavesPerBlock);
     b4 = b4 < cap ? b4 : cap;
-#define TATARA_GRAD(PH)                                                                           \
-    do {                                                                                          \
-        if (hdft && hstate)                                                                       \
-            ft_grad_update_kernel<4, true, true, PH><<<b4, 256, 0, stream>>>(a, c4);              \
-        else if (hdft)                                                                            \
-            ft_grad_update_kernel<4, true, false, PH><<<b4, 256, 0, stream>>>(a, c4);             \
-        else if (hstate)                                                                          \
-            ft_grad_update_kernel<V, false, true, PH><<<blocks, 256, 0, stream>>>(a, n_chunks);   \
-        else                                                                                      \
-            ft_grad_update_kernel<V, false, false, PH><<<blocks, 256, 0, stream>>>(a, n_chunks);  \
-        TATARA_LAUNCHED("ft_grad_update");                                                       \
+#define TATARA_GRAD_G(PH, G)                                                                         \
+    do {                                                                                             \
+        if (hdft && hstate)                                                                          \
+            ft_grad_update_kernel<4, true, true, PH, G><<<b4, 256, 0, stream>>>(a, c4);              \
+        else if (hdft)                                                                               \
+            ft_grad_update_kernel<4, true, false, PH, G><<<b4, 256, 0, stream>>>(a, c4);             \
+        else if (hstate)                                                                             \
+            ft_grad_update_kernel<V, false, true, PH, G><<<blocks, 256, 0, stream>>>(a, n_chunks);   \
+        else                                                                                         \
+            ft_grad_update_kernel<V, false, false, PH, G><<<blocks, 256, 0, stream>>>(a, n_chunks);  \
+        TATARA_LAUNCHED("ft_grad_update");                                                          \
+    } while (0)
+#define TATARA_GRAD(PH)              \
+    do {                             \
+        if (a.run_if)                \
+            TATARA_GRAD_G(PH, true);  \
+        else                         \
+            TATARA_GRAD_G(PH, false); \
     } while (0)
     if (kFtGradSplit && a.grad) {
         TATARA_GRAD(1);
@@ -1184,6 +1197,7 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
         TATARA_GRAD(0);
     }
 #undef TATARA_GRAD
+#undef TATARA_GRAD_G
     return kOk;
 }
 
