@@ -760,12 +760,7 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     constexpr int R = kScanStage, RPW = kScanStage / kScanWaves;
     static_assert(R == 32 && (RPW == 2 || RPW == 4), "32 rows per stage, two or four per wave");
     if (__builtin_amdgcn_readfirstlane(*s.multi)) return;  // the occurrence-list kernel runs instead
-    // row R of each buffer stays zero: a feature without a row to add in a
-    // step of the paired loop below adds +0.0, which leaves any sum that
-    // started at +0.0 unchanged (such a sum is never -0.0)
-    __shared__ float4 s_rows[2][R + 1][64];
-    s_rows[0][R][threadIdx.x % 64] = make_float4(0.f, 0.f, 0.f, 0.f);
-    s_rows[1][R][threadIdx.x % 64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    __shared__ float4 s_rows[2][R][64];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -838,20 +833,13 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     do {                                                                  \
         const uint32_t mm = (lane < (uint32_t)R && (T) * R + lane < n) ? (M) : 0u; \
         if (nf) {                                                         \
-            _Pragma("unroll") for (int k = 0; k < kScanFeat; k += 2) {    \
-                /* the stage's rows that hold features k and k+1, in      \
-                   ascending order; both rows are read before either add */ \
-                uint32_t r0 = (uint32_t)__ballot((mm >> k) & 1u);         \
-                uint32_t r1 = (uint32_t)__ballot((mm >> (k + 1)) & 1u);   \
-                while (r0 | r1) {                                         \
-                    const uint32_t j0 = r0 ? __builtin_ctz(r0) : (uint32_t)R; \
-                    const uint32_t j1 = r1 ? __builtin_ctz(r1) : (uint32_t)R; \
-                    r0 &= r0 - 1u;                                        \
-                    r1 &= r1 - 1u;                                        \
-                    const float4 x0 = s_rows[(BUF)][j0][lane];            \
-                    const float4 x1 = s_rows[(BUF)][j1][lane];            \
-                    acc[k] = f4add(acc[k], x0);                           \
-                    acc[k + 1] = f4add(acc[k + 1], x1);                   \
+            _Pragma("unroll") for (int k = 0; k < kScanFeat; ++k) {       \
+                /* the stage's rows that hold feature k, ascending */     \
+                uint32_t rows = (uint32_t)__ballot((mm >> k) & 1u);       \
+                while (rows) {                                            \
+                    const uint32_t jj = __builtin_ctz(rows);              \
+                    rows &= rows - 1u;                                    \
+                    acc[k] = f4add(acc[k], s_rows[(BUF)][jj][lane]);      \
                 }                                                         \
             }                                                             \
         }                                                                 \
