@@ -490,9 +490,11 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
 // variant reads f16 raw sums and writes the f16 dft, scaled by dft_scale and
 // clamped to +-65504 with a count of every clamp
 // (ft_post_perspective_grad_fused_fp16, native_kernels.cu:2304-2352); the
-// ft_b gradient stays unscaled f32.  Measured on MI355X: four columns per
-// lane suit the f32 dft (2 KB of each raw-sum row half per block), one
-// column per lane (86 VGPRs, five waves per SIMD) the f16 one.
+// ft_b gradient stays unscaled f32.  One column per lane (86-97 VGPRs, four
+// or five waves per SIMD) measured faster than four columns per lane (193
+// VGPRs) for the f32 dft as well.  The two 16-term input-gradient sums use
+// fused multiply-adds (these layers are checked within tolerance, and their
+// reference GPU kernels contract too).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
     if (v > 65504.0f) {
@@ -506,11 +508,11 @@ __device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
     return v;
 }
 
-// f16 dft (and raw sums): one lane per combined column c; a wave covers 64
-// consecutive columns of one perspective's half (ft_out % 128 == 0).  The
-// tile's 16 raw-sum pairs are loaded before any of its rows is computed.
-template <int L1>
-__global__ __launch_bounds__(128) void ls_l1_input_post_h_kernel(LsDenseArgs a) {
+// One lane per combined column c; a wave covers 64 consecutive columns of
+// one perspective's half (ft_out % 128 == 0).  The tile's 16 raw-sum pairs
+// are loaded before any of its rows is computed.  H16: f16 raw sums and dft.
+template <int L1, bool H16>
+__global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) {
     const uint32_t ft_out = a.ft_out, half = ft_out / 2;
     const uint64_t batch = a.batch;
     const uint32_t c = blockIdx.x * 128 + threadIdx.x;
@@ -518,6 +520,7 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_h_kernel(LsDenseArgs a) 
     const uint32_t persp = c < half ? 0 : 1;
     const uint32_t p = c - persp * half;
     const _Float16* ft16 = reinterpret_cast<const _Float16*>(persp ? a.ft_nstm16 : a.ft_stm16);
+    const float* ft32 = persp ? a.ft_nstm : a.ft_stm;
     const uint64_t cstride = 2 * batch * kDftChunk;
     const uint64_t off_a = (uint64_t)(p / kDftChunk) * cstride + persp * batch * kDftChunk + p % kDftChunk;
     const uint64_t off_b =
@@ -552,8 +555,13 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_h_kernel(LsDenseArgs a) 
             yr[r] = 0.0f;
             if (orig[r] >= 0) {
                 const uint64_t base = (uint64_t)orig[r] * ft_out + p;
-                xr[r] = (float)ft16[base];
-                yr[r] = (float)ft16[base + half];
+                if constexpr (H16) {
+                    xr[r] = (float)ft16[base];
+                    yr[r] = (float)ft16[base + half];
+                } else {
+                    xr[r] = ft32[base];
+                    yr[r] = ft32[base + half];
+                }
             }
         }
 #pragma unroll
@@ -563,21 +571,26 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_h_kernel(LsDenseArgs a) 
             float da = 0.0f;
             if (bvalid) {
 #pragma unroll
-                for (int o = 0; o < L1; ++o) da += d[o] * w1[o];
+                for (int o = 0; o < L1; ++o) da = __builtin_fmaf(d[o], w1[o], da);
             }
             float db = 0.0f;
 #pragma unroll
-            for (int o = 0; o < L1; ++o) db += d[o] * ws[o];
+            for (int o = 0; o < L1; ++o) db = __builtin_fmaf(d[o], ws[o], db);
             const float dy = da + db;
             const float xa = xr[r] + ba, xb = yr[r] + bb;
             const float ya = crelu01(xa), yb = crelu01(xb);
             const float ga = (xa > 0.0f && xa < 1.0f) ? dy * yb * a.ft_post_scale : 0.0f;
             const float gb = (xb > 0.0f && xb < 1.0f) ? dy * ya * a.ft_post_scale : 0.0f;
             const uint64_t row = (uint64_t)orig[r] * kDftChunk;
-            const float sc = a.dft_scale;
-            _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
-            d16[off_a + row] = (_Float16)clamp_f16_range(ga * sc, clamps);
-            d16[off_b + row] = (_Float16)clamp_f16_range(gb * sc, clamps);
+            if constexpr (H16) {
+                const float sc = a.dft_scale;
+                _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
+                d16[off_a + row] = (_Float16)clamp_f16_range(ga * sc, clamps);
+                d16[off_b + row] = (_Float16)clamp_f16_range(gb * sc, clamps);
+            } else {
+                a.dft[off_a + row] = ga;
+                a.dft[off_b + row] = gb;
+            }
             acc_a += ga;
             acc_b += gb;
         }
@@ -585,123 +598,11 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_h_kernel(LsDenseArgs a) 
     float* pp = a.ftb_partial + ((uint64_t)blockIdx.y * 2 + persp) * ft_out;
     pp[p] = acc_a;
     pp[p + half] = acc_b;
-    if (clamps) atomicAdd(a.clamp_counter, (unsigned long long)clamps);
+    if (H16 && clamps) atomicAdd(a.clamp_counter, (unsigned long long)clamps);
 }
 
 // f32 dft: a lane owns one float4 column group (four columns and their four
 // pair partners), so a 128-lane block covers 2 KB of each raw-sum row half.
-template <int L1>
-__global__ __launch_bounds__(128) void ls_l1_input_post_f4_kernel(LsDenseArgs a) {
-    const uint32_t ft_out = a.ft_out, half = ft_out / 2, n4 = ft_out / 4;
-    const uint64_t batch = a.batch;
-    const uint32_t tile0 = blockIdx.y * kPostTiles;
-    float* part = a.ftb_partial + (uint64_t)blockIdx.y * 2 * ft_out;
-    {
-        const uint32_t qq = blockIdx.x * 128 + threadIdx.x;
-        if (qq >= n4) return;
-        const uint32_t c0 = 4 * qq;
-        const uint32_t persp = c0 < half ? 0 : 1;
-        const uint32_t p0 = c0 - persp * half;
-        const float* ft = persp ? a.ft_nstm : a.ft_stm;
-        // chunk-major dft: this thread's four columns c0..c0+3 and their pair
-        // partners each lie inside one 256-column chunk
-        const uint64_t cstride = 2 * batch * kDftChunk;
-        const uint64_t off_a = (uint64_t)(p0 / kDftChunk) * cstride + persp * batch * kDftChunk + p0 % kDftChunk;
-        const uint64_t off_b = (uint64_t)((p0 + half) / kDftChunk) * cstride + persp * batch * kDftChunk +
-                               (p0 + half) % kDftChunk;
-        float ws[4][L1];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int o = 0; o < L1; ++o) ws[e][o] = a.l1s_w[(uint64_t)(c0 + e) * L1 + o];
-        const float4 ba = reinterpret_cast<const float4*>(a.ft_b)[p0 / 4];
-        const float4 bb = reinterpret_cast<const float4*>(a.ft_b)[(p0 + half) / 4];
-        float4 w1[L1];
-        int32_t cur_bin = -2;
-        float4 acc_a = make_float4(0.f, 0.f, 0.f, 0.f), acc_b = acc_a;
-        for (uint32_t tt = 0; tt < kPostTiles; ++tt) {
-            const uint64_t tile = tile0 + tt;
-            if (tile * 16 >= a.padded_b) break;
-            const int32_t bin = a.sorted_bin[tile * 16];
-            if (bin < 0) continue;
-            const bool bvalid = (uint32_t)bin < a.nb;
-            if (bin != cur_bin) {
-                cur_bin = bin;
-#pragma unroll
-                for (int o = 0; o < L1; ++o)
-                    w1[o] = bvalid ? reinterpret_cast<const float4*>(
-                                         a.l1_w + ((uint64_t)bin * L1 + o) * ft_out)[qq]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            // the FT sums of row r + 1 are loaded before row r is computed
-            const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            int32_t orig_n = a.perm[tile * 16];
-            float4 xa_n = zero4, xb_n = zero4;
-            if (orig_n >= 0) {
-                xa_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0);
-                xb_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0 + half);
-            }
-            for (uint32_t r = 0; r < 16; ++r) {
-                const uint64_t row = tile * 16 + r;
-                const int32_t orig = orig_n;
-                const float4 xa4 = xa_n, xb4 = xb_n;
-                if (r + 1 < 16) {
-                    orig_n = a.perm[row + 1];
-                    if (orig_n >= 0) {
-                        xa_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0);
-                        xb_n = *reinterpret_cast<const float4*>(ft + (uint64_t)orig_n * ft_out + p0 + half);
-                    }
-                }
-                if (orig < 0) continue;
-                float d[L1];
-                const float* dsrc = a.dl1_sorted + row * L1;
-#pragma unroll
-                for (int o = 0; o < L1; ++o) d[o] = dsrc[o];
-                float dyv[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float da = 0.0f;
-                    if (bvalid) {
-#pragma unroll
-                        for (int o = 0; o < L1; ++o) {
-                            const float wv = e == 0 ? w1[o].x : e == 1 ? w1[o].y : e == 2 ? w1[o].z : w1[o].w;
-                            da += d[o] * wv;
-                        }
-                    }
-                    float db = 0.0f;
-#pragma unroll
-                    for (int o = 0; o < L1; ++o) db += d[o] * ws[e][o];
-                    dyv[e] = da + db;
-                }
-                const float xa[4] = {xa4.x + ba.x, xa4.y + ba.y, xa4.z + ba.z, xa4.w + ba.w};
-                const float xb[4] = {xb4.x + bb.x, xb4.y + bb.y, xb4.z + bb.z, xb4.w + bb.w};
-                float ga[4], gb[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float ya = crelu01(xa[e]), yb = crelu01(xb[e]);
-                    ga[e] = (xa[e] > 0.0f && xa[e] < 1.0f) ? dyv[e] * yb * a.ft_post_scale : 0.0f;
-                    gb[e] = (xb[e] > 0.0f && xb[e] < 1.0f) ? dyv[e] * ya * a.ft_post_scale : 0.0f;
-                }
-                *reinterpret_cast<float4*>(a.dft + off_a + (uint64_t)orig * kDftChunk) =
-                    make_float4(ga[0], ga[1], ga[2], ga[3]);
-                *reinterpret_cast<float4*>(a.dft + off_b + (uint64_t)orig * kDftChunk) =
-                    make_float4(gb[0], gb[1], gb[2], gb[3]);
-                acc_a.x += ga[0];
-                acc_a.y += ga[1];
-                acc_a.z += ga[2];
-                acc_a.w += ga[3];
-                acc_b.x += gb[0];
-                acc_b.y += gb[1];
-                acc_b.z += gb[2];
-                acc_b.w += gb[3];
-            }
-        }
-        float* pp = part + persp * ft_out;
-        reinterpret_cast<float4*>(pp)[p0 / 4] = acc_a;
-        reinterpret_cast<float4*>(pp)[(p0 + half) / 4] = acc_b;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Dense gradient finalize + optimizer: one thread per parameter element of
 // the nine non-FT groups (uniform_optim_group_layout order,
@@ -845,17 +746,17 @@ int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
     const uint32_t rows = ls_post_workgroups(a.padded_b);
     if (rows == 0) return kOk;
     TATARA_REQUIRE(a.ft_out % 128 == 0, "ft_out must be a multiple of 128");
-    const dim3 grid_h(a.ft_out / 128, rows), grid_f(ceil_div(a.ft_out / 4, 128), rows);
+    const dim3 grid(a.ft_out / 128, rows);
     if (a.l1 == 16) {
         if (a.dft16)
-            ls_l1_input_post_h_kernel<16><<<grid_h, 128, 0, stream>>>(a);
+            ls_l1_input_post_c_kernel<16, true><<<grid, 128, 0, stream>>>(a);
         else
-            ls_l1_input_post_f4_kernel<16><<<grid_f, 128, 0, stream>>>(a);
+            ls_l1_input_post_c_kernel<16, false><<<grid, 128, 0, stream>>>(a);
     } else if (a.l1 == 8) {
         if (a.dft16)
-            ls_l1_input_post_h_kernel<8><<<grid_h, 128, 0, stream>>>(a);
+            ls_l1_input_post_c_kernel<8, true><<<grid, 128, 0, stream>>>(a);
         else
-            ls_l1_input_post_f4_kernel<8><<<grid_f, 128, 0, stream>>>(a);
+            ls_l1_input_post_c_kernel<8, false><<<grid, 128, 0, stream>>>(a);
     } else {
         TATARA_REQUIRE(false, "l1 must be 16 or 8");
     }
