@@ -107,6 +107,15 @@ TATARA_API int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int3
                                          uint32_t batch, uint32_t ft_out, uint32_t cols,
                                          uint32_t max_active, uint32_t piece_inputs,
                                          uint32_t* used_block_scan);
+/* The same from an f16 dft (the --ft-fp16-out mode,
+ * gather_and_sum_per_feature_*_fp16, native_kernels.cu:1030-1100): each
+ * cell is the sequential f32 sum of the f16 values (converted exactly), in
+ * the same order, times dft_inv_scale. */
+TATARA_API int32_t tatara_op_ft_weight_grad_blocked_f16(const uint16_t* dft16, float dft_inv_scale,
+                                             const int32_t* stm_idx, const int32_t* nstm_idx,
+                                             const int32_t* nnz, float* grad, uint32_t batch,
+                                             uint32_t ft_out, uint32_t cols, uint32_t max_active,
+                                             uint32_t piece_inputs, uint32_t* used_block_scan);
 /* ft_fold_virtual / ft_reduce_virtual_grad, Base mode (native_kernels.cu:204-406). */
 TATARA_API int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,
                                   uint32_t ft_out, uint32_t piece_inputs);

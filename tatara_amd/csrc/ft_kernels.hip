@@ -63,6 +63,9 @@ __device__ __forceinline__ float4 h4_to_f4(h4 h) {
     return make_float4(f.x, f.y, f.z, f.w);
 }
 
+__device__ __forceinline__ float4 as_f4(float4 v) { return v; }
+__device__ __forceinline__ float4 as_f4(h4 v) { return h4_to_f4(v); }
+
 __device__ __forceinline__ h4 f4_to_h4(float4 v) {
     const nt_f4 f = {v.x, v.y, v.z, v.w};
     return __builtin_convertvector(f, h4);
@@ -754,13 +757,18 @@ __global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanG
     }
 }
 
-template <bool HSTATE>
+// HDFT: the dft is f16 (the --ft-fp16-out mode): rows are staged as f16
+// (512 bytes per 256-column chunk), each added value is converted to f32,
+// and the sum is multiplied by dft_inv_scale at the end, as the
+// occurrence-list kernel does.
+template <bool HDFT, bool HSTATE>
 __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArgs a, FtBlockScan s,
                                                                        ScanGeom geom) {
     constexpr int R = kScanStage, RPW = kScanStage / kScanWaves;
     static_assert(R == 32 && (RPW == 2 || RPW == 4), "32 rows per stage, two or four per wave");
     if (__builtin_amdgcn_readfirstlane(*s.multi)) return;  // the occurrence-list kernel runs instead
-    __shared__ float4 s_rows[2][R][64];
+    using Row4 = typename std::conditional<HDFT, h4, float4>::type;  // a lane's four columns
+    __shared__ Row4 s_rows[2][R][64];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -780,7 +788,10 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     const uint32_t b0 = s.sched_start[s.n_blocks + K];
     const uint32_t n = na + (s.sched_start[s.n_blocks + K + 1] - b0);
     const uint32_t* mrow = s.masks + (uint64_t)(g * kScanWaves + wave) * (2ull * s.batch);
-    const float4* dft4 = reinterpret_cast<const float4*>(a.dft + (uint64_t)chunk * a.dft_chunk_stride) + lane;
+    const Row4* dft4 =
+        HDFT ? reinterpret_cast<const Row4*>(reinterpret_cast<const _Float16*>(a.dft16) + (uint64_t)chunk * a.dft_chunk_stride) +
+                   lane
+             : reinterpret_cast<const Row4*>(a.dft + (uint64_t)chunk * a.dft_chunk_stride) + lane;
     auto entry = [&](uint32_t j) -> uint32_t {
         j = j < n ? j : n - 1;  // stage slots past the list repeat its last row (never used)
         return j < na ? a0 + j : b0 + (j - na);
@@ -791,7 +802,7 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     // waited for before its stage needs it.
     auto positions = [&](uint32_t T) -> uint32_t { return (uint32_t)s.schedule[entry(T * R + (lane & 31u))]; };
     auto masks = [&](uint32_t T) -> uint32_t { return mrow[entry(T * R + (lane & 31u))]; };
-    auto dft_row = [&](uint32_t pos_lanes, uint32_t j) -> const float4* {
+    auto dft_row = [&](uint32_t pos_lanes, uint32_t j) -> const Row4* {
         const uint32_t e = entry(j);
         const uint64_t r = (e >= s.batch ? (uint64_t)s.batch : 0ull) +
                            (uint32_t)__builtin_amdgcn_readlane(pos_lanes, j % R);
@@ -808,7 +819,7 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     // (issued with row ids loaded a stage earlier, no scalar-load chain), the
     // rows of stage T+1 wait in registers, and loads past the list repeat
     // its last row.
-    float4 sA0, sA1, sA2, sA3, sB0, sB1, sB2, sB3;
+    Row4 sA0, sA1, sA2, sA3, sB0, sB1, sB2, sB3;
     uint32_t ridA = 0, ridB = 0, mA = 0, mB = 0;
 #define TATARA_LOAD_ROWS(S, RID, T)                          \
     do {                                                     \
@@ -839,7 +850,7 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
                 while (rows) {                                            \
                     const uint32_t jj = __builtin_ctz(rows);              \
                     rows &= rows - 1u;                                    \
-                    acc[k] = f4add(acc[k], s_rows[(BUF)][jj][lane]);      \
+                    acc[k] = f4add(acc[k], as_f4(s_rows[(BUF)][jj][lane])); \
                 }                                                         \
             }                                                             \
         }                                                                 \
@@ -896,7 +907,8 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
             const int k = kb + u;
             if ((uint32_t)k < nf) {
                 const uint64_t off = off0 + k * row4;
-                const vecf<4> gr = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
+                vecf<4> gr = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
+            if constexpr (HDFT) gr *= a.dft_inv_scale;
                 if (a.grad) __builtin_nontemporal_store(gr, grad + off);
                 if (a.apply_update) apply_cells<4, HSTATE>(a, off, gr, cs[u]);
             }
@@ -1208,17 +1220,22 @@ int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream) {
 
 int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
-    TATARA_REQUIRE(a.dft && !a.dft16, "block scan: f32 dft");
+    TATARA_REQUIRE((a.dft != nullptr) != (a.dft16 != nullptr), "block scan: one dft (f32 or f16)");
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
                    "block scan: chunk-major dft");
     TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "block scan: shapes");
     const ScanGeom geom = scan_geom(s.piece_inputs);
     const uint64_t grid = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks * geom.n_groups;
     if (grid > 0) {
-        if (a.m16)
-            ft_grad_scan_kernel<true><<<(uint32_t)grid, kScanWaves * 64, 0, stream>>>(a, s, geom);
+        const uint32_t g = (uint32_t)grid, t = kScanWaves * 64;
+        if (a.dft16 && a.m16)
+            ft_grad_scan_kernel<true, true><<<g, t, 0, stream>>>(a, s, geom);
+        else if (a.dft16)
+            ft_grad_scan_kernel<true, false><<<g, t, 0, stream>>>(a, s, geom);
+        else if (a.m16)
+            ft_grad_scan_kernel<false, true><<<g, t, 0, stream>>>(a, s, geom);
         else
-            ft_grad_scan_kernel<false><<<(uint32_t)grid, kScanWaves * 64, 0, stream>>>(a, s, geom);
+            ft_grad_scan_kernel<false, false><<<g, t, 0, stream>>>(a, s, geom);
         TATARA_LAUNCHED("ft_grad_scan");
     }
     if (!fallback) return kOk;

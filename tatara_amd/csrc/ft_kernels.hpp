@@ -86,8 +86,9 @@ struct FtBlockScan {
 // Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).
 constexpr uint32_t kDftChunk = 256;
 
-// The trainers' FT backward for factorized feature sets with an f32 dft and
-// ft_out of two 256-column chunks or more (with one chunk a batch gives too
+// The trainers' FT backward for factorized feature sets with an f32 dft
+// (with an f16 dft the occurrence lists measure faster) and ft_out of two
+// 256-column chunks or more (with one chunk a batch gives too
 // few workgroups for the scan to pay): block scan (1) or occurrence lists
 // only (0).
 #ifndef TATARA_FT_SCAN
@@ -107,7 +108,7 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream);
 uint32_t ft_scan_mask_words(uint32_t piece_inputs);
 // Hit masks and the multi flag of a batch (after its schedule).
 int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream);
-// FT gradient + update by block scan (f32 chunk-major dft); the kernel does
+// FT gradient + update by block scan (chunk-major dft, f32 or f16); the kernel does
 // nothing when *s.multi is set.  With fallback, the occurrence-list kernel
 // (its lists already sorted) is queued behind it and runs only in that case.
 int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback = true);

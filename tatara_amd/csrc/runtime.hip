@@ -53,7 +53,8 @@ struct DevScratch {
 };
 
 // row-major [rows][ft_out] -> chunk-major [ceil(ft_out/256)][rows][256]
-__global__ void to_chunk_major_kernel(const float* __restrict__ src, float* __restrict__ dst, uint64_t rows,
+template <typename T>
+__global__ void to_chunk_major_kernel(const T* __restrict__ src, T* __restrict__ dst, uint64_t rows,
                                       uint32_t ft_out) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * ft_out) return;
@@ -290,10 +291,10 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
     return kOk;
 }
 
-int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_idx, const int32_t* nstm_idx,
-                                         const int32_t* nnz, float* grad, uint32_t batch, uint32_t ft_out,
-                                         uint32_t cols, uint32_t max_active, uint32_t piece_inputs,
-                                         uint32_t* used_block_scan) {
+static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, float inv_scale,
+                                      const int32_t* stm_idx, const int32_t* nstm_idx, const int32_t* nnz,
+                                      float* grad, uint32_t batch, uint32_t ft_out, uint32_t cols,
+                                      uint32_t max_active, uint32_t piece_inputs, uint32_t* used_block_scan) {
     TATARA_REQUIRE(ft_out % 4 == 0, "ft_out must be a multiple of 4");
     TATARA_REQUIRE(max_active <= 64, "max_active must be <= 64");
     TATARA_REQUIRE(ft_scan_mask_words(piece_inputs) > 0, "piece_inputs out of range for the block scan");
@@ -326,7 +327,10 @@ int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_id
     bs.out = sched.as<int32_t>();
     if ((st = launch_binsort(bs, 0))) return st;
     if (two_b * ft_out > 0) {
-        to_chunk_major_kernel<<<ceil_div(two_b * ft_out, 256), 256>>>(dft, cm.as<float>(), two_b, ft_out);
+        if (dft16)
+            to_chunk_major_kernel<<<ceil_div(two_b * ft_out, 256), 256>>>(dft16, cm.as<uint16_t>(), two_b, ft_out);
+        else
+            to_chunk_major_kernel<<<ceil_div(two_b * ft_out, 256), 256>>>(dft, cm.as<float>(), two_b, ft_out);
         TATARA_LAUNCHED("to_chunk_major");
     }
     FtBlockScan sc{};
@@ -367,7 +371,12 @@ int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_id
     os.temp_bytes = tb;
     if ((st = launch_occurrence_sort(os, 0))) return st;
     FtGradArgs g{};
-    g.dft = cm.as<float>();
+    if (dft16) {
+        g.dft16 = cm.as<uint16_t>();
+        g.dft_inv_scale = inv_scale;
+    } else {
+        g.dft = cm.as<float>();
+    }
     g.dft_row_stride = kDftChunk;
     g.dft_chunk_stride = two_b * kDftChunk;
     g.occ_vals = vo.as<uint32_t>();
@@ -381,6 +390,23 @@ int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_id
     TATARA_HIP(hipMemcpy(&m, multi.p, 4, hipMemcpyDeviceToHost), "ft_weight_grad_blocked");
     if (used_block_scan) *used_block_scan = m ? 0u : 1u;
     return kOk;
+}
+
+int32_t tatara_op_ft_weight_grad_blocked(const float* dft, const int32_t* stm_idx, const int32_t* nstm_idx,
+                                         const int32_t* nnz, float* grad, uint32_t batch, uint32_t ft_out,
+                                         uint32_t cols, uint32_t max_active, uint32_t piece_inputs,
+                                         uint32_t* used_block_scan) {
+    return ft_weight_grad_blocked(dft, nullptr, 1.0f, stm_idx, nstm_idx, nnz, grad, batch, ft_out, cols,
+                                  max_active, piece_inputs, used_block_scan);
+}
+
+int32_t tatara_op_ft_weight_grad_blocked_f16(const uint16_t* dft16, float dft_inv_scale, const int32_t* stm_idx,
+                                             const int32_t* nstm_idx, const int32_t* nnz, float* grad,
+                                             uint32_t batch, uint32_t ft_out, uint32_t cols,
+                                             uint32_t max_active, uint32_t piece_inputs,
+                                             uint32_t* used_block_scan) {
+    return ft_weight_grad_blocked(nullptr, dft16, dft_inv_scale, stm_idx, nstm_idx, nnz, grad, batch, ft_out,
+                                  cols, max_active, piece_inputs, used_block_scan);
 }
 
 int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,

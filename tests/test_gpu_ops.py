@@ -186,6 +186,33 @@ def test_ft_weight_grad_block_scan_falls_back(gpu):
     assert np.array_equal(got, _oracle_grad(dft, si, ni, nnz, b, ft_out, cols, ma))
 
 
+@pytest.mark.parametrize("bucketed", [True, False], ids=["block_scan", "occurrence_lists"])
+def test_ft_weight_grad_blocked_f16_bit_exact(gpu, bucketed):
+    """f16 dft: each cell is the sequential f32 sum of the f16 values
+    (converted exactly, so the f32 oracle of the converted values gives the
+    sum bit for bit), times the inverse scale."""
+    from tatara_amd.synthetic import small_spec, structured_batch
+    spec = small_spec(king_buckets=8, piece_inputs=200, max_active=30)
+    b, ma, ft_out, cols = 128, 30, 512, spec["ft_in"]
+    rng = np.random.default_rng(17)
+    if bucketed:
+        batch, _ = structured_batch(b, spec, num_buckets=1, seed=4, nnz_min=10)
+        si, ni, nnz = batch.stm_indices, batch.nstm_indices, batch.nnz
+    else:
+        si, nnz = ragged_indices(rng, b, ma, cols)
+        ni, _ = ragged_indices(rng, b, ma, cols)
+    dft16 = (rng.standard_normal((2, b, ft_out)) * 3000.0).astype(np.float16)
+    inv = np.float32(1.0 / (16384.0 * b))
+    D, S, Nn, N = dev(dft16.view(np.uint16)), dev(si), dev(ni), dev(nnz)
+    g = DeviceArray(np.full(cols * ft_out, 7.0, np.float32))
+    used = C.c_uint32(99)
+    check(gpu.tatara_op_ft_weight_grad_blocked_f16(D.ptr, C.c_float(inv), S.ptr, Nn.ptr, N.ptr, g.ptr, b, ft_out,
+                                                   cols, ma, spec["piece_inputs"], C.byref(used)))
+    assert used.value == (1 if bucketed else 0)
+    exp = _oracle_grad(dft16.astype(np.float32), si, ni, nnz, b, ft_out, cols, ma) * inv
+    assert np.array_equal(g.to_host(), exp.astype(np.float32))
+
+
 def test_fold_reduce_bit_exact(gpu):
     rng = np.random.default_rng(9)
     ft_in, ft_out, pi = 45 * 12, 256, 12
