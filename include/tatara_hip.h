@@ -197,6 +197,62 @@ TATARA_API int32_t tatara_radam_step_size_denom(uint64_t step, float beta1, floa
 
 typedef struct TataraTrainer TataraTrainer;
 
+/* ------------------------------------------------------------------------ */
+/* Schedules (crates/nnue-train/src/schedule.rs)                             */
+/* ------------------------------------------------------------------------ */
+
+/* LrSchedulerEnum (schedule.rs:365-420): kind and its fields.
+ *   CONSTANT     ConstantLR { value = start }
+ *   STEP         StepLR { start, gamma, step = period }: start * gamma^((sb-1)/step)
+ *   DROP         DropLR { start, gamma, drop = period }
+ *   LINEAR / COSINE / EXPONENTIAL  *DecayLR { initial_lr = start, final_lr = gamma,
+ *                final_superbatch = period }
+ *   ONE_CYCLE    OneCycleLR { initial_lr = start, max_lr, final_lr = gamma,
+ *                warmup_superbatch = period, total_superbatch = total }
+ *                (tatara_lr_schedule_one_cycle builds it as OneCycleLR::new)
+ * warmup_batches > 0 wraps it in WarmupLR (LrSchedulerEnum::with_warmup).
+ * next != NULL: SequenceLR { first = this, second = *next,
+ * first_scheduler_final_superbatch = next_after } (schedule.rs:330-348). */
+#define TATARA_LR_CONSTANT 0
+#define TATARA_LR_STEP 1
+#define TATARA_LR_DROP 2
+#define TATARA_LR_LINEAR 3
+#define TATARA_LR_COSINE 4
+#define TATARA_LR_EXPONENTIAL 5
+#define TATARA_LR_ONE_CYCLE 6
+typedef struct TataraLrSchedule {
+    int32_t kind;
+    float start, gamma, max_lr;
+    uint64_t period, total, warmup_batches;
+    const struct TataraLrSchedule* next;
+    uint64_t next_after;
+} TataraLrSchedule;
+
+/* WdlSchedulerEnum (schedule.rs:539-570): CONSTANT { value = start },
+ * LINEAR { start, end }; warmup_batches > 0 wraps it in WarmupWDL; next !=
+ * NULL: SequenceWDL { first = this, second = *next, midpoint = next_after }. */
+#define TATARA_WDL_CONSTANT 0
+#define TATARA_WDL_LINEAR 1
+typedef struct TataraWdlSchedule {
+    int32_t kind;
+    float start, end;
+    uint64_t warmup_batches;
+    const struct TataraWdlSchedule* next;
+    uint64_t next_after;
+} TataraWdlSchedule;
+
+/* OneCycleLR::new (schedule.rs:233-253). */
+TATARA_API int32_t tatara_lr_schedule_one_cycle(float max_lr, float warmup_pct, float div_factor,
+                                                float final_div_factor, uint64_t total_superbatch,
+                                                TataraLrSchedule* out);
+/* LrScheduler::lr(batch, superbatch) (schedule.rs:26). */
+TATARA_API int32_t tatara_lr_at(const TataraLrSchedule* schedule, uint64_t batch, uint64_t superbatch, float* lr);
+/* LrScheduler::horizon (schedule.rs:32-35): *has_horizon = 0 for none. */
+TATARA_API int32_t tatara_lr_horizon(const TataraLrSchedule* schedule, uint64_t* horizon, int32_t* has_horizon);
+/* WdlScheduler::blend(batch, superbatch, max) (schedule.rs:436); superbatch >= 1. */
+TATARA_API int32_t tatara_wdl_at(const TataraWdlSchedule* schedule, uint64_t batch, uint64_t superbatch,
+                                 uint64_t max, float* wdl);
+
 #define TATARA_ARCH_LAYERSTACK 0
 #define TATARA_ARCH_SIMPLE 1
 
@@ -386,6 +442,53 @@ TATARA_API int32_t tatara_trainer_save_resume(TataraTrainer* trainer, const char
  * Synchronous. */
 TATARA_API int32_t tatara_trainer_load_resume(TataraTrainer* trainer, const char* path, int32_t feature_set,
                                               int32_t bucket_mode, TataraCkptHeader* header);
+
+/* ------------------------------------------------------------------------ */
+/* Superbatch driver (crates/nnue-train/src/trainer.rs:759-1211, run)        */
+/* ------------------------------------------------------------------------ */
+
+/* TrainingConfig (trainer.rs:395-490), the fields the driver uses.  The
+ * PSV records of data_path are read in file order and the file starts over
+ * at its end (PsvEpochReader, dataloader.rs:724-760, one worker); each batch
+ * is decoded on the GPU (tatara_psv_to_batch).  Checkpoints go to
+ * "<output_dir>/<net_id>-<sb>.bin" (quantised, fv_scale when has_fv_scale)
+ * and ".ckpt" (resume, with run_id and the LR horizon) when sb % save_rate
+ * == 0 or sb == end_superbatch; has_keep_raw keeps only the newest
+ * keep_raw_checkpoints ".ckpt" files (0 is ignored with a warning). */
+typedef struct TataraRunConfig {
+    const char* data_path;
+    const char* output_dir;
+    const char* net_id;
+    const char* run_id;
+    uint64_t start_superbatch, end_superbatch, batches_per_superbatch, batch_size, save_rate;
+    int32_t has_fv_scale, fv_scale;
+    int32_t has_keep_raw;
+    uint64_t keep_raw_checkpoints;
+    int32_t feature_set, bucket_mode, num_buckets;
+    const float* progress_weights; /* device, 81*1548 f32, for the progress bucket mode */
+    int32_t print_progress;         /* 1: the reference's per-superbatch line on stdout */
+} TataraRunConfig;
+
+/* One superbatch of a run: the summed (lagged + flushed) loss, positions,
+ * mean loss, lr / wdl at batch 0, wall time, whether checkpoints were written. */
+typedef struct TataraRunSuperbatch {
+    uint64_t superbatch, positions;
+    double loss_sum, mean_loss, seconds;
+    float lr, wdl;
+    int32_t saved;
+} TataraRunSuperbatch;
+
+/* run (trainer.rs:759-1211) over superbatches start..=end: per batch
+ * lr = lr_scheduler.lr(batch_idx, sb), wdl = wdl_scheduler.blend(batch_idx,
+ * sb, end_superbatch), train_step; per superbatch flush_pending_loss, report,
+ * checkpoints.  report (capacity report_cap) receives one record per
+ * superbatch; lr_seen / wdl_seen (capacity seen_cap, may be NULL) every
+ * step's values.  Not covered: control.json polling, experiment.json,
+ * held-out validation, score drop/clamp, shuffle windows, monitors. */
+TATARA_API int32_t tatara_train_run(TataraTrainer* trainer, const TataraRunConfig* config,
+                                    const TataraLrSchedule* lr, const TataraWdlSchedule* wdl,
+                                    const TataraLoss* loss, TataraRunSuperbatch* report, uint64_t report_cap,
+                                    uint64_t* n_report, float* lr_seen, float* wdl_seen, uint64_t seen_cap);
 
 #ifdef __cplusplus
 }

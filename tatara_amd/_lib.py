@@ -98,6 +98,73 @@ class TataraCkptHeader(C.Structure):
     ]
 
 
+class TataraLrSchedule(C.Structure):
+    pass
+
+
+TataraLrSchedule._fields_ = [
+    ("kind", C.c_int32),
+    ("start", C.c_float),
+    ("gamma", C.c_float),
+    ("max_lr", C.c_float),
+    ("period", C.c_uint64),
+    ("total", C.c_uint64),
+    ("warmup_batches", C.c_uint64),
+    ("next", C.POINTER(TataraLrSchedule)),
+    ("next_after", C.c_uint64),
+]
+
+
+class TataraWdlSchedule(C.Structure):
+    pass
+
+
+TataraWdlSchedule._fields_ = [
+    ("kind", C.c_int32),
+    ("start", C.c_float),
+    ("end", C.c_float),
+    ("warmup_batches", C.c_uint64),
+    ("next", C.POINTER(TataraWdlSchedule)),
+    ("next_after", C.c_uint64),
+]
+
+
+class TataraRunConfig(C.Structure):
+    _fields_ = [
+        ("data_path", C.c_char_p),
+        ("output_dir", C.c_char_p),
+        ("net_id", C.c_char_p),
+        ("run_id", C.c_char_p),
+        ("start_superbatch", C.c_uint64),
+        ("end_superbatch", C.c_uint64),
+        ("batches_per_superbatch", C.c_uint64),
+        ("batch_size", C.c_uint64),
+        ("save_rate", C.c_uint64),
+        ("has_fv_scale", C.c_int32),
+        ("fv_scale", C.c_int32),
+        ("has_keep_raw", C.c_int32),
+        ("keep_raw_checkpoints", C.c_uint64),
+        ("feature_set", C.c_int32),
+        ("bucket_mode", C.c_int32),
+        ("num_buckets", C.c_int32),
+        ("progress_weights", C.c_void_p),
+        ("print_progress", C.c_int32),
+    ]
+
+
+class TataraRunSuperbatch(C.Structure):
+    _fields_ = [
+        ("superbatch", C.c_uint64),
+        ("positions", C.c_uint64),
+        ("loss_sum", C.c_double),
+        ("mean_loss", C.c_double),
+        ("seconds", C.c_double),
+        ("lr", C.c_float),
+        ("wdl", C.c_float),
+        ("saved", C.c_int32),
+    ]
+
+
 # name -> (restype, argtypes); every entry point returns an int32 status
 # except the two string getters.
 SIGNATURES = {
@@ -186,6 +253,19 @@ SIGNATURES = {
         [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.POINTER(TataraCkptHeader)],
     ),
     "tatara_trainer_phase_times": (C.c_int32, [C.c_void_p, c_f64p, C.c_int32, c_u64p]),
+    "tatara_lr_schedule_one_cycle": (
+        C.c_int32,
+        [C.c_float, C.c_float, C.c_float, C.c_float, C.c_uint64, C.POINTER(TataraLrSchedule)],
+    ),
+    "tatara_lr_at": (C.c_int32, [C.POINTER(TataraLrSchedule), C.c_uint64, C.c_uint64, c_f32p]),
+    "tatara_lr_horizon": (C.c_int32, [C.POINTER(TataraLrSchedule), c_u64p, c_i32p]),
+    "tatara_wdl_at": (C.c_int32, [C.POINTER(TataraWdlSchedule), C.c_uint64, C.c_uint64, C.c_uint64, c_f32p]),
+    "tatara_train_run": (
+        C.c_int32,
+        [C.c_void_p, C.POINTER(TataraRunConfig), C.POINTER(TataraLrSchedule), C.POINTER(TataraWdlSchedule),
+         C.POINTER(TataraLoss), C.POINTER(TataraRunSuperbatch), C.c_uint64, c_u64p, c_f32p, c_f32p,
+         C.c_uint64],
+    ),
 }
 
 

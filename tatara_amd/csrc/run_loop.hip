@@ -1,0 +1,283 @@
+// Superbatch driver: run (crates/nnue-train/src/trainer.rs:759-1211) over a
+// PSV file with the trainer of this library.
+//
+// Per superbatch sb = start..=end and batch b: lr = LrScheduler::lr(b, sb),
+// wdl = WdlScheduler::blend(b, sb, end), the next batch_size records of the
+// file (read in order; the file starts over at its end, as PsvEpochReader
+// does with one worker, dataloader.rs:724-760), decoded on the GPU, then
+// train_step, whose lagged loss is added to the superbatch's sum; after the
+// last batch flush_pending_loss drains the last step's loss into it.  The
+// reference's per-superbatch line is printed (loss = sum / positions), and
+// checkpoints are written when sb % save_rate == 0 or sb == end: the
+// quantised "<net_id>-<sb>.bin" and the resume "<net_id>-<sb>.ckpt" (run id,
+// LR horizon), then old ".ckpt" files are pruned to keep_raw_checkpoints
+// (prune_old_raw_checkpoints, trainer.rs:1230-1283).  A run with start > 1
+// resumes the schedules at that superbatch and reads the data from the start
+// of the file, as the reference does.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include <dirent.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "../../include/tatara_hip.h"
+#include "common.hpp"
+#include "schedule.hpp"
+
+namespace tatara {
+
+namespace {
+
+constexpr uint64_t kPsvBytes = 40;  // PackedSfenValue record (packed_sfen.rs:255-268)
+
+// format_hms (trainer.rs:1285-1300)
+std::string format_hms(double secs) {
+    if (!(secs >= 0.0) || secs != secs || secs > 1.8e19) return "??";
+    const uint64_t total = (uint64_t)secs;
+    const uint64_t h = total / 3600, m = (total % 3600) / 60, s = total % 60;
+    char buf[64];
+    if (h > 0)
+        snprintf(buf, sizeof buf, "%lluh%02llum%02llus", (unsigned long long)h, (unsigned long long)m,
+                 (unsigned long long)s);
+    else if (m > 0)
+        snprintf(buf, sizeof buf, "%llum%02llus", (unsigned long long)m, (unsigned long long)s);
+    else
+        snprintf(buf, sizeof buf, "%llus", (unsigned long long)s);
+    return buf;
+}
+
+// Rust's `{:.4e}`: four decimals, exponent without sign padding ("8.7500e-4").
+std::string rust_exp4(float v) {
+    char buf[64];
+    snprintf(buf, sizeof buf, "%.4e", (double)v);
+    std::string s = buf;
+    const size_t e = s.find('e');
+    if (e == std::string::npos) return s;
+    std::string mant = s.substr(0, e), ex = s.substr(e + 1);
+    bool neg = false;
+    size_t i = 0;
+    if (i < ex.size() && (ex[i] == '+' || ex[i] == '-')) neg = ex[i++] == '-';
+    while (i + 1 < ex.size() && ex[i] == '0') ++i;
+    return mant + "e" + (neg ? "-" : "") + ex.substr(i);
+}
+
+// Sequential PSV reader that starts over at the end of the file.
+struct EpochReader {
+    FILE* f = nullptr;
+    uint64_t records = 0;
+    ~EpochReader() {
+        if (f) fclose(f);
+    }
+    int32_t open(const char* path) {
+        f = fopen(path, "rb");
+        TATARA_REQUIRE(f, std::string("cannot open data file ") + path);
+        struct stat st;
+        TATARA_REQUIRE(fstat(fileno(f), &st) == 0, "cannot stat the data file");
+        const uint64_t size = (uint64_t)st.st_size;
+        TATARA_REQUIRE(size % kPsvBytes == 0,
+                       "data file size " + std::to_string(size) +
+                           " is not a multiple of the PSV record size (40 bytes)");
+        records = size / kPsvBytes;
+        TATARA_REQUIRE(records > 0, "the data file holds no PSV records");
+        return kOk;
+    }
+    int32_t read(uint8_t* dst, uint64_t n) {
+        uint64_t got = 0;
+        while (got < n) {
+            const size_t r = fread(dst + got * kPsvBytes, kPsvBytes, n - got, f);
+            got += r;
+            if (got < n) {
+                TATARA_REQUIRE(!ferror(f), "read error on the data file");
+                rewind(f);  // next epoch
+            }
+        }
+        return kOk;
+    }
+};
+
+// prune_old_raw_checkpoints (trainer.rs:1230-1283)
+void prune_raw(const std::string& dir, const std::string& net_id, uint64_t keep) {
+    if (keep == 0) {
+        fprintf(stderr, "[train] warning: keep_raw_checkpoints=0 ignored (would delete all raw checkpoints)\n");
+        return;
+    }
+    DIR* d = opendir(dir.c_str());
+    if (!d) {
+        fprintf(stderr, "[train] warning: cannot read %s to prune raw checkpoints\n", dir.c_str());
+        return;
+    }
+    const std::string prefix = net_id + "-", suffix = ".ckpt";
+    std::vector<std::pair<uint64_t, std::string>> found;
+    while (dirent* ent = readdir(d)) {
+        const std::string name = ent->d_name;
+        if (name.size() <= prefix.size() + suffix.size() || name.compare(0, prefix.size(), prefix) != 0 ||
+            name.compare(name.size() - suffix.size(), suffix.size(), suffix) != 0)
+            continue;
+        std::string num = name.substr(prefix.size(), name.size() - prefix.size() - suffix.size());
+        if (!num.empty() && num[0] == '+') num = num.substr(1);  // usize::from_str takes a leading '+'
+        if (num.empty() || num.size() > 19 || num.find_first_not_of("0123456789") != std::string::npos) continue;
+        found.emplace_back(std::stoull(num), dir + "/" + name);
+    }
+    closedir(d);
+    if (found.size() <= keep) return;
+    std::sort(found.begin(), found.end(), [](const auto& x, const auto& y) { return x.first > y.first; });
+    for (size_t i = keep; i < found.size(); ++i) {
+        if (unlink(found[i].second.c_str()) == 0)
+            printf("[train] pruned old raw checkpoint: %s (sb %llu)\n", found[i].second.c_str(),
+                   (unsigned long long)found[i].first);
+        else
+            fprintf(stderr, "[train] warning: failed to prune %s\n", found[i].second.c_str());
+    }
+}
+
+struct DevBatch {
+    int32_t *stm = nullptr, *nstm = nullptr, *nnz = nullptr, *bucket = nullptr;
+    float *score = nullptr, *wdl = nullptr;
+};
+
+struct DevMem {
+    std::vector<void*> ptrs;
+    ~DevMem() {
+        for (void* p : ptrs) (void)hipFree(p);
+    }
+    template <class T>
+    int32_t alloc(T** p, uint64_t n) {
+        TATARA_HIP(hipMalloc((void**)p, (n ? n : 1) * sizeof(T)), "hipMalloc (run)");
+        ptrs.push_back(*p);
+        return kOk;
+    }
+};
+
+int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSchedule& lr,
+            const TataraWdlSchedule& wdl, const TataraLoss* loss, TataraRunSuperbatch* report,
+            uint64_t report_cap, uint64_t* n_report, float* lr_seen, float* wdl_seen, uint64_t seen_cap) {
+    // TrainingConfig::validate (trainer.rs:490-510)
+    TATARA_REQUIRE(c.start_superbatch >= 1, "start_superbatch must be >= 1 (1-indexed)");
+    TATARA_REQUIRE(c.end_superbatch >= c.start_superbatch,
+                   "end_superbatch (" + std::to_string(c.end_superbatch) + ") < start_superbatch (" +
+                       std::to_string(c.start_superbatch) + ")");
+    TATARA_REQUIRE(c.batches_per_superbatch >= 1, "batches_per_superbatch must be >= 1");
+    TATARA_REQUIRE(c.batch_size >= 1 && c.batch_size <= 0x7fffffffull, "batch_size out of range");
+    TATARA_REQUIRE(c.save_rate >= 1, "save_rate must be >= 1");
+    TATARA_REQUIRE(c.data_path && c.output_dir && c.net_id, "data_path, output_dir and net_id are required");
+    if (n_report) *n_report = 0;
+    int32_t st;
+    int32_t max_active = 0;
+    if ((st = tatara_feature_set_info(c.feature_set, nullptr, nullptr, nullptr, &max_active, nullptr))) return st;
+    EpochReader reader;
+    if ((st = reader.open(c.data_path))) return st;
+
+    const uint64_t B = c.batch_size;
+    DevMem mem;
+    uint8_t* psv_dev = nullptr;
+    DevBatch db[2];  // the batch of a step stays valid until the next step returns
+    if ((st = mem.alloc(&psv_dev, B * kPsvBytes))) return st;
+    for (auto& d : db)
+        if ((st = mem.alloc(&d.stm, B * max_active)) || (st = mem.alloc(&d.nstm, B * max_active)) ||
+            (st = mem.alloc(&d.nnz, B)) || (st = mem.alloc(&d.bucket, B)) || (st = mem.alloc(&d.score, B)) ||
+            (st = mem.alloc(&d.wdl, B)))
+            return st;
+    std::vector<uint8_t> psv_host(B * kPsvBytes);
+
+    uint64_t horizon = 0;
+    const bool has_horizon = lr_horizon(lr, horizon);
+    const std::string out_dir = c.output_dir, net_id = c.net_id;
+    const uint64_t positions_per_sb = c.batches_per_superbatch * B;
+    uint64_t step = 0;
+    int cur = 0;
+    for (uint64_t sb = c.start_superbatch;; ++sb) {
+        const auto t0 = std::chrono::steady_clock::now();
+        double sb_loss = 0.0;
+        uint64_t sb_positions = 0;
+        for (uint64_t b = 0; b < c.batches_per_superbatch; ++b, ++step) {
+            const float lr_v = lr_at(lr, b, sb);
+            const float wdl_v = wdl_at(wdl, b, sb, c.end_superbatch);
+            if (lr_seen && step < seen_cap) lr_seen[step] = lr_v;
+            if (wdl_seen && step < seen_cap) wdl_seen[step] = wdl_v;
+            if ((st = reader.read(psv_host.data(), B))) return st;
+            TATARA_HIP(hipMemcpy(psv_dev, psv_host.data(), B * kPsvBytes, hipMemcpyHostToDevice), "PSV upload");
+            const DevBatch& d = db[cur];
+            if ((st = tatara_psv_to_batch(psv_dev, (int32_t)B, c.feature_set, c.bucket_mode, c.num_buckets,
+                                          c.progress_weights, d.stm, d.nstm, d.nnz, d.bucket, d.score, d.wdl)))
+                return st;
+            TataraBatch bt{};
+            bt.n_pos = (int32_t)B;
+            bt.max_active = max_active;
+            bt.stm_indices = d.stm;
+            bt.nstm_indices = d.nstm;
+            bt.nnz = d.nnz;
+            bt.bucket_idx = d.bucket;
+            bt.score = d.score;
+            bt.wdl = d.wdl;
+            bt.on_device = 1;
+            double lagged = 0.0;
+            if ((st = tatara_trainer_train_step(trainer, &bt, lr_v, wdl_v, loss, &lagged))) return st;
+            sb_loss += lagged;
+            sb_positions += B;
+            cur ^= 1;
+        }
+        double flushed = 0.0;
+        if ((st = tatara_trainer_flush_pending_loss(trainer, &flushed))) return st;
+        sb_loss += flushed;
+        const double secs =
+            std::max(1e-9, std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+        const double mean = sb_positions ? sb_loss / (double)sb_positions : NAN;
+        const double pps = (double)sb_positions / secs;
+        const double eta = pps > 0.0 ? (double)(positions_per_sb * (c.end_superbatch - sb)) / pps : NAN;
+        const float lr_now = lr_at(lr, 0, sb), wdl_now = wdl_at(wdl, 0, sb, c.end_superbatch);
+        if (c.print_progress) {
+            printf("[train] superbatch %llu/%llu | loss %.6f | %.0f pos/s | lr %s | wdl %.3f | sb %.1fs | ETA %s\n",
+                   (unsigned long long)sb, (unsigned long long)c.end_superbatch, mean, pps,
+                   rust_exp4(lr_now).c_str(), (double)wdl_now, secs, format_hms(eta).c_str());
+            fflush(stdout);
+        }
+        const bool saved = sb % c.save_rate == 0 || sb == c.end_superbatch;
+        if (saved) {
+            const std::string base = out_dir + "/" + net_id + "-" + std::to_string(sb);
+            if ((st = tatara_trainer_export_quantised(trainer, (base + ".bin").c_str(), c.feature_set,
+                                                      c.has_fv_scale, c.fv_scale)))
+                return st;
+            if (c.print_progress) printf("[train] checkpoint saved: %s.bin\n", base.c_str());
+            if ((st = tatara_trainer_save_resume(trainer, (base + ".ckpt").c_str(), c.feature_set, c.bucket_mode,
+                                                 sb, c.run_id ? c.run_id : "", has_horizon ? horizon : 0)))
+                return st;
+            if (c.print_progress) printf("[train] resume checkpoint saved: %s.ckpt\n", base.c_str());
+            if (c.has_keep_raw) prune_raw(out_dir, net_id, c.keep_raw_checkpoints);
+        }
+        if (report && n_report && *n_report < report_cap) {
+            TataraRunSuperbatch& r = report[(*n_report)++];
+            r.superbatch = sb;
+            r.positions = sb_positions;
+            r.loss_sum = sb_loss;
+            r.mean_loss = mean;
+            r.seconds = secs;
+            r.lr = lr_now;
+            r.wdl = wdl_now;
+            r.saved = saved ? 1 : 0;
+        }
+        if (sb == c.end_superbatch) break;
+    }
+    return kOk;
+}
+
+}  // namespace
+
+}  // namespace tatara
+
+using namespace tatara;
+
+extern "C" int32_t tatara_train_run(TataraTrainer* trainer, const TataraRunConfig* config,
+                                    const TataraLrSchedule* lr, const TataraWdlSchedule* wdl,
+                                    const TataraLoss* loss, TataraRunSuperbatch* report, uint64_t report_cap,
+                                    uint64_t* n_report, float* lr_seen, float* wdl_seen, uint64_t seen_cap) {
+    TATARA_REQUIRE(trainer && config && lr && wdl && loss, "train_run: null argument");
+    return run(trainer, *config, *lr, *wdl, loss, report, report_cap, n_report, lr_seen, wdl_seen, seen_cap);
+}

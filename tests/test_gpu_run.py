@@ -1,0 +1,181 @@
+"""Superbatch driver (tatara_train_run) on the GPU.
+
+Pins: the driver equals a hand-written loop over the same PSV batches
+(GPU decode + train_step with the oracle schedule's lr / wdl, lagged loss
+summed per superbatch and flushed at its end) bit for bit, in weights and
+loss sums; the lr / wdl values it used equal the oracle schedule's; the
+checkpoint cadence, names and resume headers, the start-superbatch offset
+(crates/nnue-train/src/trainer.rs run_with_start_superbatch_offset test:
+start 3, end 5, save_rate 2 saves 4 and 5 only) and the pruning of old
+resume checkpoints follow trainer.rs:759-1283; bad data files and configs
+are rejected before any step.
+"""
+import numpy as np
+import pytest
+
+import oracle.schedule as osch
+from tatara_amd import run as R
+from tatara_amd._lib import TataraError
+from tatara_amd.dataloader import feature_set_info, psv_to_device_batch
+from tatara_amd.psv import synthetic_psv
+from tatara_amd.trainer import (LayerStackConfig, LayerStackTrainer, SimpleConfig, SimpleTrainer, Sigmoid,
+                                Wrm)
+
+pytestmark = pytest.mark.gpu
+
+B = 256
+
+
+def simple_cfg():
+    info = feature_set_info("halfkp")
+    return SimpleConfig(ft_in=info["ft_in"], max_active=info["max_active"], ft_out=32, l1_out=32, l2_out=32,
+                        max_batch=B, optimizer="adamw")
+
+
+def write_psv(tmp_path, n, seed=7):
+    path = tmp_path / "data.psv"
+    recs = synthetic_psv(n, seed)
+    recs.tofile(path)
+    return path, recs
+
+
+def manual(trainer, recs, start, end, bps, lr_o, wdl_o, loss, feature_set="halfkp", bucket_mode="none", nb=1):
+    """The driver's loop written out with the Python API."""
+    n = recs.shape[0]
+    cursor = 0
+    sums = []
+    for sb in range(start, end + 1):
+        s = 0.0
+        for b in range(bps):
+            idx = (cursor + np.arange(B)) % n
+            cursor = (cursor + B) % n
+            db = psv_to_device_batch(recs[idx], feature_set, bucket_mode, nb)
+            lr = float(lr_o.lr(b, sb))
+            wdl = float(wdl_o.blend(b, sb, end))
+            if isinstance(trainer, SimpleTrainer):
+                s += trainer.train_step(db, lr=lr, wdl_lambda=wdl, loss=loss)
+            else:
+                s += trainer.train_step(db, None, lr=lr, wdl_lambda=wdl, loss=loss)
+        s += trainer.flush_pending_loss()
+        sums.append(s)
+    return sums
+
+
+def test_run_equals_manual_loop_and_checkpoints(gpu, tmp_path):
+    path, recs = write_psv(tmp_path, 3 * B + 40)  # the file ends mid-batch: reading starts over
+    cfg = R.TrainingConfig(net_id="net", feature_set="halfkp", output_dir=str(tmp_path / "out"),
+                           start_superbatch=1, end_superbatch=3, batches_per_superbatch=2, batch_size=B,
+                           save_rate=2, fv_scale=16, print_progress=True)
+    lr_p, wdl_p = R.StepLR(1e-3, 0.5, 1), R.LinearWDL(0.0, 1.0)
+    lr_o, wdl_o = osch.StepLR(1e-3, 0.5, 1), osch.LinearWDL(0.0, 1.0)
+    loss = Wrm()
+    with SimpleTrainer(simple_cfg()) as t1, SimpleTrainer(simple_cfg()) as t2:
+        res = R.run(t1, path, lr_p, wdl_p, cfg, loss)
+        sums = manual(t2, recs, 1, 3, 2, lr_o, wdl_o, loss)
+        assert [r["superbatch"] for r in res.superbatches] == [1, 2, 3]
+        assert [r["positions"] for r in res.superbatches] == [2 * B] * 3
+        assert [r["saved"] for r in res.superbatches] == [False, True, True]
+        assert [r["loss_sum"] for r in res.superbatches] == sums
+        for r in res.superbatches:
+            assert r["mean_loss"] == r["loss_sum"] / r["positions"]
+        exp_lr = [np.float32(lr_o.lr(b, sb)) for sb in (1, 2, 3) for b in (0, 1)]
+        exp_wdl = [np.float32(wdl_o.blend(b, sb, 3)) for sb in (1, 2, 3) for b in (0, 1)]
+        assert res.lr_seen.tobytes() == np.array(exp_lr, np.float32).tobytes()
+        assert res.wdl_seen.tobytes() == np.array(exp_wdl, np.float32).tobytes()
+        assert t1.step_count == t2.step_count == 6
+        for g in t1.GROUPS:
+            for k in ("w", "m", "v"):
+                assert np.array_equal(t1.get(g, k), t2.get(g, k)), (g, k)
+        out = tmp_path / "out"
+        names = sorted(p.name for p in out.iterdir())
+        assert names == ["net-2.bin", "net-2.ckpt", "net-3.bin", "net-3.ckpt"]
+        # the last checkpoints hold the final state
+        t2.save_quantised(str(tmp_path / "manual.bin"), "halfkp", 16)
+        assert (out / "net-3.bin").read_bytes() == (tmp_path / "manual.bin").read_bytes()
+    with SimpleTrainer(simple_cfg()) as t3:
+        sb, run_id, horizon = t3.load_resume_checkpoint(str(out / "net-3.ckpt"), "halfkp", None)
+        assert (sb, run_id, horizon) == (3, None, None)
+        assert t3.step_count == 6
+
+
+def test_start_superbatch_offset_saves_only_from_offset(gpu, tmp_path):
+    path, _ = write_psv(tmp_path, 2 * B)
+    cfg = R.TrainingConfig(net_id="offset", feature_set="halfkp", output_dir=str(tmp_path / "out"),
+                           start_superbatch=3, end_superbatch=5, batches_per_superbatch=1, batch_size=B,
+                           save_rate=2, run_id="run-a", fv_scale=16,
+                           print_progress=False)
+    lr = R.CosineDecayLR(2e-3, 1e-5, 5)
+    with SimpleTrainer(simple_cfg()) as t:
+        res = R.run(t, path, lr, R.ConstantWDL(0.25), cfg, Wrm())
+        assert [r["superbatch"] for r in res.superbatches] == [3, 4, 5]
+        assert [r["saved"] for r in res.superbatches] == [False, True, True]
+        o = osch.CosineDecayLR(2e-3, 1e-5, 5)
+        assert res.lr_seen.tolist() == [float(o.lr(0, sb)) for sb in (3, 4, 5)]
+        assert [r["lr"] for r in res.superbatches] == res.lr_seen.tolist()
+        assert set(res.wdl_seen.tolist()) == {0.25}
+        names = sorted(p.name for p in (tmp_path / "out").iterdir())
+        assert names == ["offset-4.bin", "offset-4.ckpt", "offset-5.bin", "offset-5.ckpt"]
+    with SimpleTrainer(simple_cfg()) as t:
+        sb, run_id, horizon = t.load_resume_checkpoint(str(tmp_path / "out" / "offset-4.ckpt"), "halfkp", None)
+        assert (sb, run_id, horizon) == (4, "run-a", 5)
+
+
+def test_keep_raw_checkpoints_prunes_oldest(gpu, tmp_path):
+    path, _ = write_psv(tmp_path, B)
+    out = tmp_path / "out"
+    out.mkdir()
+    (out / "keep-9.ckpt.tmp").write_bytes(b"x")  # not a resume checkpoint name: untouched
+    (out / "other-1.ckpt").write_bytes(b"x")  # another net id: untouched
+    cfg = R.TrainingConfig(net_id="keep", feature_set="halfkp", output_dir=str(out), start_superbatch=1,
+                           end_superbatch=4, batches_per_superbatch=1, batch_size=B, save_rate=1,
+                           keep_raw_checkpoints=2, fv_scale=16, print_progress=False)
+    with SimpleTrainer(simple_cfg()) as t:
+        R.run(t, path, R.ConstantLR(1e-3), R.ConstantWDL(0.0), cfg, Wrm())
+    names = sorted(p.name for p in out.iterdir())
+    assert names == ["keep-1.bin", "keep-2.bin", "keep-3.bin", "keep-3.ckpt", "keep-4.bin", "keep-4.ckpt",
+                     "keep-9.ckpt.tmp", "other-1.ckpt"]
+
+
+def test_layerstack_kingrank9_run_equals_manual_loop(gpu, tmp_path):
+    info = feature_set_info("halfka-hm-merged")
+    lcfg = LayerStackConfig(ft_in=info["ft_in"], max_active=info["max_active"], ft_out=128, l1_out=16,
+                            l2_out=32, num_buckets=9, max_batch=B, optimizer="ranger")
+    path, recs = write_psv(tmp_path, 2 * B, seed=11)
+    cfg = R.TrainingConfig(net_id="ls", feature_set="halfka-hm-merged", output_dir=str(tmp_path / "out"),
+                           start_superbatch=1, end_superbatch=2, batches_per_superbatch=3, batch_size=B,
+                           save_rate=100, bucket_mode="kingrank9", num_buckets=9, print_progress=False)
+    lr_p = R.WarmupLR(R.OneCycleLR(3e-3, 0.5, 25.0, 1e4, 2), 2)
+    lr_o = osch.WarmupLR(osch.OneCycleLR(3e-3, 0.5, 25.0, 1e4, 2), 2)
+    loss = Sigmoid()
+    with LayerStackTrainer(lcfg) as t1, LayerStackTrainer(lcfg) as t2:
+        res = R.run(t1, path, lr_p, R.ConstantWDL(0.3), cfg, loss)
+        sums = manual(t2, recs, 1, 2, 3, lr_o, osch.ConstantWDL(0.3), loss, "halfka-hm-merged", "kingrank9", 9)
+        assert [r["loss_sum"] for r in res.superbatches] == sums
+        for g in t1.GROUPS:
+            assert np.array_equal(t1.get(g), t2.get(g)), g
+        assert sorted(p.name for p in (tmp_path / "out").iterdir()) == ["ls-2.bin", "ls-2.ckpt"]
+    with LayerStackTrainer(lcfg) as t3:
+        sb, _, horizon = t3.load_resume_checkpoint(str(tmp_path / "out" / "ls-2.ckpt"), "halfka-hm-merged",
+                                                   "kingrank9")
+        assert (sb, horizon) == (2, 2)
+
+
+def test_rejects_bad_data_and_config(gpu, tmp_path):
+    bad = tmp_path / "bad.psv"
+    bad.write_bytes(b"\0" * 41)
+    empty = tmp_path / "empty.psv"
+    empty.write_bytes(b"")
+    good, _ = write_psv(tmp_path, B)
+    base = dict(net_id="x", feature_set="halfkp", output_dir=str(tmp_path / "out"), batch_size=B,
+                fv_scale=16, print_progress=False)
+    with SimpleTrainer(simple_cfg()) as t:
+        for path, extra, msg in [(bad, {}, "multiple of the PSV record size"),
+                                 (empty, {}, "no PSV records"),
+                                 (tmp_path / "missing.psv", {}, "cannot open"),
+                                 (good, {"start_superbatch": 0}, "start_superbatch"),
+                                 (good, {"start_superbatch": 3, "end_superbatch": 2}, "end_superbatch"),
+                                 (good, {"save_rate": 0}, "save_rate")]:
+            cfg = R.TrainingConfig(**base, **extra)
+            with pytest.raises(TataraError, match=msg):
+                R.run(t, path, R.ConstantLR(1e-3), R.ConstantWDL(0.0), cfg, Wrm())
+        assert t.step_count == 0
