@@ -4,8 +4,8 @@
 // Per superbatch sb = start..=end and batch b: lr = LrScheduler::lr(b, sb),
 // wdl = WdlScheduler::blend(b, sb, end), the next batch_size records of the
 // file (read in order; the file starts over at its end, as PsvEpochReader
-// does with one worker, dataloader.rs:724-760), decoded on the GPU, then
-// train_step, whose lagged loss is added to the superbatch's sum; after the
+// does with one worker, dataloader.rs:724-760), uploaded and decoded on the
+// trainer's stream while the previous step still runs, then train_step, whose lagged loss is added to the superbatch's sum; after the
 // last batch flush_pending_loss drains the last step's loss into it.  The
 // reference's per-superbatch line is printed (loss = sum / positions), and
 // checkpoints are written when sb % save_rate == 0 or sb == end: the
@@ -30,7 +30,9 @@
 
 #include "../../include/tatara_hip.h"
 #include "common.hpp"
+#include "psv_kernels.hpp"
 #include "schedule.hpp"
+#include "trainer_base.hpp"
 
 namespace tatara {
 
@@ -143,17 +145,50 @@ struct DevBatch {
     float *score = nullptr, *wdl = nullptr;
 };
 
-struct DevMem {
-    std::vector<void*> ptrs;
-    ~DevMem() {
-        for (void* p : ptrs) (void)hipFree(p);
+// The driver's buffers; the trainer's stream is drained before they are freed.
+struct RunMem {
+    hipStream_t stream = nullptr, copy = nullptr;
+    std::vector<void*> dev, host;
+    std::vector<hipEvent_t> events;
+    ~RunMem() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (copy) {
+            (void)hipStreamSynchronize(copy);
+            (void)hipStreamDestroy(copy);
+        }
+        for (void* p : dev) (void)hipFree(p);
+        for (void* p : host) (void)hipHostFree(p);
+        for (hipEvent_t e : events) (void)hipEventDestroy(e);
     }
     template <class T>
     int32_t alloc(T** p, uint64_t n) {
         TATARA_HIP(hipMalloc((void**)p, (n ? n : 1) * sizeof(T)), "hipMalloc (run)");
-        ptrs.push_back(*p);
+        dev.push_back(*p);
         return kOk;
     }
+    int32_t alloc_pinned(uint8_t** p, uint64_t n) {
+        TATARA_HIP(hipHostMalloc((void**)p, n ? n : 1, hipHostMallocDefault), "hipHostMalloc (run)");
+        host.push_back(*p);
+        return kOk;
+    }
+    int32_t event(hipEvent_t* e) {
+        TATARA_HIP(hipEventCreateWithFlags(e, hipEventDisableTiming), "hipEventCreate (run)");
+        events.push_back(*e);
+        return kOk;
+    }
+};
+
+// One in-flight batch: the pinned records, their device copy and the decoded
+// arrays.  `uploaded` (copy stream) completes when the records have reached
+// the device, after which the pinned buffer may be refilled; `decoded` (copy
+// stream) when the arrays are ready for the step; `consumed` (trainer stream)
+// when the step that used them has finished, after which the slot may be
+// refilled.
+struct Slot {
+    uint8_t* psv_host = nullptr;
+    uint8_t* psv_dev = nullptr;
+    hipEvent_t uploaded = nullptr, decoded = nullptr, consumed = nullptr;
+    DevBatch d;
 };
 
 int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSchedule& lr,
@@ -175,17 +210,38 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
     EpochReader reader;
     if ((st = reader.open(c.data_path))) return st;
 
+    FeatureSetShape shape;
+    if ((st = feature_set_shape(c.feature_set, shape))) return st;
     const uint64_t B = c.batch_size;
-    DevMem mem;
-    uint8_t* psv_dev = nullptr;
-    DevBatch db[2];  // the batch of a step stays valid until the next step returns
-    if ((st = mem.alloc(&psv_dev, B * kPsvBytes))) return st;
-    for (auto& d : db)
-        if ((st = mem.alloc(&d.stm, B * max_active)) || (st = mem.alloc(&d.nstm, B * max_active)) ||
-            (st = mem.alloc(&d.nnz, B)) || (st = mem.alloc(&d.bucket, B)) || (st = mem.alloc(&d.score, B)) ||
-            (st = mem.alloc(&d.wdl, B)))
+    RunMem mem;
+    mem.stream = trainer_stream(trainer);
+    TATARA_HIP(hipStreamCreateWithFlags(&mem.copy, hipStreamNonBlocking), "hipStreamCreate (run copy)");
+    // Two slots: the host reads batch k + 1 and a second stream uploads and
+    // decodes it while the trainer's stream runs step k; step k + 1 waits for
+    // that decode on the device, not on the host.
+    Slot slots[2];
+    for (Slot& sl : slots) {
+        DevBatch& d = sl.d;
+        if ((st = mem.alloc_pinned(&sl.psv_host, B * kPsvBytes)) || (st = mem.alloc(&sl.psv_dev, B * kPsvBytes)) ||
+            (st = mem.event(&sl.uploaded)) || (st = mem.event(&sl.decoded)) || (st = mem.event(&sl.consumed)) || (st = mem.alloc(&d.stm, B * max_active)) ||
+            (st = mem.alloc(&d.nstm, B * max_active)) || (st = mem.alloc(&d.nnz, B)) ||
+            (st = mem.alloc(&d.bucket, B)) || (st = mem.alloc(&d.score, B)) || (st = mem.alloc(&d.wdl, B)))
             return st;
-    std::vector<uint8_t> psv_host(B * kPsvBytes);
+        // the events start out complete
+        TATARA_HIP(hipEventRecord(sl.consumed, mem.stream), "run: record the step");
+        TATARA_HIP(hipEventRecord(sl.uploaded, mem.copy), "run: record the upload");
+    }
+    PsvArgs pa{};
+    pa.n = (uint32_t)B;
+    pa.piece_inputs = shape.piece_inputs;
+    pa.max_active = shape.max_active;
+    pa.emit_king = shape.emit_king;
+    pa.fold_enemy = shape.fold_enemy;
+    pa.mirror = shape.mirror;
+    pa.bucket_mode = c.bucket_mode;
+    pa.num_buckets = c.num_buckets;
+    pa.weights = c.progress_weights;
+    pa.progress = nullptr;
 
     uint64_t horizon = 0;
     const bool has_horizon = lr_horizon(lr, horizon);
@@ -202,12 +258,25 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             const float wdl_v = wdl_at(wdl, b, sb, c.end_superbatch);
             if (lr_seen && step < seen_cap) lr_seen[step] = lr_v;
             if (wdl_seen && step < seen_cap) wdl_seen[step] = wdl_v;
-            if ((st = reader.read(psv_host.data(), B))) return st;
-            TATARA_HIP(hipMemcpy(psv_dev, psv_host.data(), B * kPsvBytes, hipMemcpyHostToDevice), "PSV upload");
-            const DevBatch& d = db[cur];
-            if ((st = tatara_psv_to_batch(psv_dev, (int32_t)B, c.feature_set, c.bucket_mode, c.num_buckets,
-                                          c.progress_weights, d.stm, d.nstm, d.nnz, d.bucket, d.score, d.wdl)))
-                return st;
+            Slot& sl = slots[cur];
+            // the upload that last read this pinned buffer has finished
+            TATARA_HIP(hipEventSynchronize(sl.uploaded), "run: wait for the upload");
+            if ((st = reader.read(sl.psv_host, B))) return st;
+            TATARA_HIP(hipStreamWaitEvent(mem.copy, sl.consumed, 0), "run: wait for the slot's last step");
+            TATARA_HIP(hipMemcpyAsync(sl.psv_dev, sl.psv_host, B * kPsvBytes, hipMemcpyHostToDevice, mem.copy),
+                       "PSV upload");
+            TATARA_HIP(hipEventRecord(sl.uploaded, mem.copy), "run: record the upload");
+            const DevBatch& d = sl.d;
+            pa.psv = sl.psv_dev;
+            pa.stm = d.stm;
+            pa.nstm = d.nstm;
+            pa.nnz = d.nnz;
+            pa.bucket = d.bucket;
+            pa.score = d.score;
+            pa.wdl = d.wdl;
+            if ((st = launch_psv_to_batch(pa, mem.copy))) return st;
+            TATARA_HIP(hipEventRecord(sl.decoded, mem.copy), "run: record the decode");
+            TATARA_HIP(hipStreamWaitEvent(mem.stream, sl.decoded, 0), "run: order the step");
             TataraBatch bt{};
             bt.n_pos = (int32_t)B;
             bt.max_active = max_active;
@@ -220,6 +289,7 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             bt.on_device = 1;
             double lagged = 0.0;
             if ((st = tatara_trainer_train_step(trainer, &bt, lr_v, wdl_v, loss, &lagged))) return st;
+            TATARA_HIP(hipEventRecord(sl.consumed, mem.stream), "run: record the step");
             sb_loss += lagged;
             sb_positions += B;
             cur ^= 1;

@@ -653,6 +653,10 @@ struct TataraTrainer {
     std::unique_ptr<TrainerBase> t;
 };
 
+namespace tatara {
+hipStream_t trainer_stream(const TataraTrainer* h) { return h->t->stream; }
+}  // namespace tatara
+
 extern "C" {
 
 int32_t tatara_trainer_create(const TataraTrainerConfig* config, TataraTrainer** out) {

@@ -154,4 +154,8 @@ class TrainerBase {
     int32_t join_side();
 };
 
+// The stream a trainer handle's steps run on (work enqueued there before a
+// step is ordered before it).
+hipStream_t trainer_stream(const TataraTrainer* h);
+
 }  // namespace tatara
