@@ -771,11 +771,35 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     __shared__ Row4 s_rows[2][R][64];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t lane = threadIdx.x % 64;
-    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const uint32_t g = bid % geom.n_groups;
-    const uint32_t t2 = bid / geom.n_groups;
-    const uint32_t K = t2 % s.n_blocks;
-    const uint32_t chunk = t2 / s.n_blocks;
+    // Longest king blocks first, spread over the XCDs.  Workgroups x, x + 8,
+    // x + 16, ... run on XCD x in that order, so (block, chunk) pair p, pairs
+    // ranked by descending block row count, is XCD (p % 8)'s (p / 8)-th pair;
+    // a pair's feature groups sit next to each other (they read the same rows
+    // through that XCD's L2).  The grid holds a multiple of 8 pairs.
+    const uint32_t nb = s.n_blocks;
+    const uint32_t n_chunks = (a.ft_out + kDftChunk - 1) / kDftChunk;
+    const uint32_t xcd = blockIdx.x % kNumXcd, i_xcd = blockIdx.x / kNumXcd;
+    const uint32_t g = i_xcd % geom.n_groups;
+    const uint32_t pair = (i_xcd / geom.n_groups) * kNumXcd + xcd;
+    if (pair >= nb * n_chunks) return;
+    const uint32_t rank = pair / n_chunks, chunk = pair % n_chunks;
+    uint32_t K;
+    {
+        auto block_rows = [&](uint32_t k) -> uint32_t {
+            return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
+                          : 0u;
+        };
+        const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
+        uint32_t r0 = 0, r1 = 0;  // ranks of blocks lane and lane + 64 (ties: lower block first)
+        for (uint32_t m = 0; m < nb; ++m) {
+            const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
+            r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
+            r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
+        }
+        const uint64_t h0 = __ballot(lane < nb && r0 == rank);
+        const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
+        K = __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
+    }
     const uint32_t PI = s.piece_inputs;
     const uint32_t blk_lo = K * PI;
     const uint32_t blk_n = s.cols > blk_lo ? (s.cols - blk_lo < PI ? s.cols - blk_lo : PI) : 0u;
@@ -1225,7 +1249,9 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
                    "block scan: chunk-major dft");
     TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "block scan: shapes");
     const ScanGeom geom = scan_geom(s.piece_inputs);
-    const uint64_t grid = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks * geom.n_groups;
+    TATARA_REQUIRE(s.n_blocks <= 128, "block scan: at most 128 king blocks");
+    const uint64_t pairs = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks;
+    const uint64_t grid = (pairs + kNumXcd - 1) / kNumXcd * kNumXcd * geom.n_groups;
     if (grid > 0) {
         const uint32_t g = (uint32_t)grid, t = kScanWaves * 64;
         if (a.dft16 && a.m16)
