@@ -10,8 +10,9 @@
 // output order is exactly "bin ascending, item index ascending" on every run.
 //
 //   pass 1  per 1024-item tile: histogram -> hist[bin][tile]
-//   pass 2  one workgroup: exclusive scan in (bin, tile) order, bin alignment
-//   pass 3  per tile: wave-match ranks + per-wave prefix -> scatter
+//   pass 2  one workgroup per bin: exclusive scan over its tiles, bin size
+//   pass 3  per tile: aligned bin starts (prefix of rounded-up sizes),
+//           wave-match ranks + per-wave prefix -> scatter
 #include "binsort.hpp"
 
 #include "common.hpp"
@@ -37,55 +38,85 @@ __global__ __launch_bounds__(kTile) void binsort_hist_kernel(const uint8_t* __re
     for (uint32_t i = t; i < n_bins; i += kTile) hist[(uint64_t)i * gridDim.x + blockIdx.x] = h[i];
 }
 
-// hist [n_bins][n_tiles] -> exclusive offsets in place; bin_start[n_bins+1],
-// bin_count[n_bins].  Each bin starts at a multiple of `align`.
-__global__ __launch_bounds__(1024) void binsort_scan_kernel(uint32_t* __restrict__ hist,
-                                                            uint32_t n_tiles, uint32_t n_bins,
-                                                            uint32_t align,
-                                                            uint32_t* __restrict__ bin_start,
-                                                            uint32_t* __restrict__ bin_count) {
-    __shared__ uint32_t tot[kMaxBins];
-    __shared__ uint32_t start[kMaxBins + 1];
-    const uint32_t t = threadIdx.x;
-    // per-bin totals: one thread per bin (n_bins <= 256)
-    if (t < n_bins) {
-        uint32_t s = 0;
-        for (uint32_t k = 0; k < n_tiles; ++k) s += hist[(uint64_t)t * n_tiles + k];
-        tot[t] = s;
+// hist [n_bins][n_tiles] -> each bin's exclusive offsets in place, relative
+// to the bin's start; bin_count[bin] = the bin's size.  One workgroup per bin.
+constexpr int kScanThreads = 256;
+
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d);
+        if (lane >= (uint32_t)d) x += y;
     }
-    __syncthreads();
-    if (t == 0) {
-        uint32_t acc = 0;
-        for (uint32_t b = 0; b < n_bins; ++b) {
-            const uint32_t r = acc % align;
-            if (r) acc += align - r;
-            start[b] = acc;
-            acc += tot[b];
-        }
-        start[n_bins] = acc;
-    }
-    __syncthreads();
-    if (t < n_bins) {
-        uint32_t acc = start[t];
-        for (uint32_t k = 0; k < n_tiles; ++k) {
-            const uint64_t i = (uint64_t)t * n_tiles + k;
-            const uint32_t x = hist[i];
-            hist[i] = acc;
-            acc += x;
-        }
-        bin_count[t] = tot[t];
-    }
-    if (t <= n_bins) bin_start[t] = start[t];
+    return x;
 }
 
+__global__ __launch_bounds__(kScanThreads) void binsort_scan_kernel(uint32_t* __restrict__ hist,
+                                                                    uint32_t n_tiles, uint32_t n_bins,
+                                                                    uint32_t* __restrict__ bin_start,
+                                                                    uint32_t* __restrict__ bin_count) {
+    constexpr int W = kScanThreads / 64;
+    __shared__ uint32_t wsum[W];
+    const uint32_t b = blockIdx.x, t = threadIdx.x, lane = t % 64, wave = t / 64;
+    uint32_t* row = hist + (uint64_t)b * n_tiles;
+    uint32_t carry = 0;
+    for (uint32_t k0 = 0; k0 < n_tiles; k0 += kScanThreads) {
+        const uint32_t k = k0 + t;
+        const uint32_t x = k < n_tiles ? row[k] : 0u;
+        const uint32_t incl = wave_inclusive_sum(x, lane);
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t before = carry, total = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            before += (uint32_t)w < wave ? wsum[w] : 0u;
+            total += wsum[w];
+        }
+        if (k < n_tiles) row[k] = before + incl - x;
+        carry += total;
+        __syncthreads();
+    }
+    if (t == 0) {
+        bin_count[b] = carry;
+        if (n_tiles == 0) {  // no scatter runs: publish the empty bins here
+            bin_start[b] = 0;
+            if (b + 1 == n_bins) bin_start[n_bins] = 0;
+        }
+    }
+}
+
+// Bin starts: start[b] = sum over b' < b of size[b'] rounded up to `align`
+// (every start is a multiple of align, so rounding each running end up is
+// rounding each size up); bin_start[n_bins] = the last bin's end, unrounded.
+// Each scatter workgroup computes them; workgroup 0 publishes them.
 __global__ __launch_bounds__(kTile) void binsort_scatter_kernel(
-    const uint8_t* __restrict__ keys, uint32_t n_items, uint32_t n_bins,
-    const uint32_t* __restrict__ offsets, uint32_t value_mod, int32_t* __restrict__ out,
-    int32_t* __restrict__ out_key) {
+    const uint8_t* __restrict__ keys, uint32_t n_items, uint32_t n_bins, uint32_t align,
+    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ bin_count, uint32_t value_mod,
+    int32_t* __restrict__ out, int32_t* __restrict__ out_key, uint32_t* __restrict__ bin_start) {
     __shared__ uint32_t wcnt[kWaves][kMaxBins];
+    __shared__ uint32_t s_start[kMaxBins];
+    __shared__ uint32_t s_wtot[kMaxBins / 64];
     const uint32_t t = threadIdx.x;
     const uint32_t wave = t / 64, lane = t % 64;
     for (uint32_t i = t; i < kWaves * kMaxBins; i += kTile) (&wcnt[0][0])[i] = 0;
+    uint32_t cnt = 0, rounded = 0, incl = 0;
+    if (t < (uint32_t)kMaxBins) {  // waves 0..3, whole waves
+        cnt = t < n_bins ? bin_count[t] : 0u;
+        rounded = cnt % align ? cnt + (align - cnt % align) : cnt;
+        incl = wave_inclusive_sum(rounded, lane);
+        if (lane == 63) s_wtot[wave] = incl;
+    }
+    __syncthreads();
+    if (t < (uint32_t)kMaxBins) {
+        uint32_t before = 0;
+        for (uint32_t w = 0; w < wave; ++w) before += s_wtot[w];
+        const uint32_t start = before + incl - rounded;
+        s_start[t] = start;
+        if (blockIdx.x == 0 && t < n_bins) {
+            bin_start[t] = start;
+            if (t + 1 == n_bins) bin_start[n_bins] = start + cnt;
+        }
+    }
     __syncthreads();
     const uint64_t item = (uint64_t)blockIdx.x * kTile + t;
     const bool ok = item < n_items;
@@ -105,7 +136,7 @@ __global__ __launch_bounds__(kTile) void binsort_scatter_kernel(
     if (!ok) return;
     uint32_t before = 0;
     for (uint32_t w = 0; w < wave; ++w) before += wcnt[w][key];
-    const uint32_t dst = offsets[(uint64_t)key * gridDim.x + blockIdx.x] + before + rank;
+    const uint32_t dst = s_start[key] + offsets[(uint64_t)key * gridDim.x + blockIdx.x] + before + rank;
     out[dst] = (int32_t)(value_mod ? (uint32_t)(item % value_mod) : (uint32_t)item);
     if (out_key) out_key[dst] = (int32_t)key;
 }
@@ -129,6 +160,7 @@ int32_t launch_fill_i32(int32_t* p, uint64_t n, int32_t v, hipStream_t stream) {
 int32_t launch_binsort(const BinSortArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.n_bins >= 1 && a.n_bins <= (uint32_t)kMaxBins, "binsort: 1 <= n_bins <= 256");
     TATARA_REQUIRE(a.align >= 1, "binsort: align >= 1");
+    TATARA_REQUIRE(a.bin_start && a.bin_count, "binsort: bin_start and bin_count are required");
     if (a.out_fill_len) {
         int32_t st = launch_fill_i32(a.out, a.out_fill_len, -1, stream);
         if (st) return st;
@@ -140,18 +172,19 @@ int32_t launch_binsort(const BinSortArgs& a, hipStream_t stream) {
     const uint32_t tiles = binsort_tiles(a.n_items);
     if (tiles == 0) {
         // still publish empty bin boundaries
-        binsort_scan_kernel<<<1, 1024, 0, stream>>>(a.hist, 0, a.n_bins, a.align, a.bin_start,
-                                                   a.bin_count);
+        binsort_scan_kernel<<<a.n_bins, kScanThreads, 0, stream>>>(a.hist, 0, a.n_bins, a.bin_start,
+                                                                   a.bin_count);
         TATARA_LAUNCHED("binsort_scan");
         return kOk;
     }
     binsort_hist_kernel<<<tiles, kTile, 0, stream>>>(a.keys, a.n_items, a.n_bins, a.hist);
     TATARA_LAUNCHED("binsort_hist");
-    binsort_scan_kernel<<<1, 1024, 0, stream>>>(a.hist, tiles, a.n_bins, a.align, a.bin_start,
-                                               a.bin_count);
+    binsort_scan_kernel<<<a.n_bins, kScanThreads, 0, stream>>>(a.hist, tiles, a.n_bins, a.bin_start,
+                                                               a.bin_count);
     TATARA_LAUNCHED("binsort_scan");
-    binsort_scatter_kernel<<<tiles, kTile, 0, stream>>>(a.keys, a.n_items, a.n_bins, a.hist,
-                                                       a.value_mod, a.out, a.out_key);
+    binsort_scatter_kernel<<<tiles, kTile, 0, stream>>>(a.keys, a.n_items, a.n_bins, a.align, a.hist,
+                                                       a.bin_count, a.value_mod, a.out, a.out_key,
+                                                       a.bin_start);
     TATARA_LAUNCHED("binsort_scatter");
     return kOk;
 }
