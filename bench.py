@@ -429,11 +429,12 @@ def main() -> int:
                                               out_rows=3 if w["arch"] == "layerstack" else 4,
                                               f16=bool(w.get("all_optim")))
     # the f16 forward table is gathered by the eight-column pair kernel; the
-    # trainers run the FT gradient as a block scan for an f32 dft of two
-    # 256-column chunks or more (factorized feature sets), else from
-    # occurrence lists
+    # trainers run the FT gradient as a block scan for an f32 dft (factorized
+    # feature sets; LayerStack from two 256-column chunks, Simple from one),
+    # else from occurrence lists
     fwd_kernel = "ft_forward_pair16_kernel" if w.get("all_optim") else "ft_forward_kernel"
-    grad_kernel = ("ft_grad_scan_kernel" if not w.get("all_optim") and w["ft_out"] >= 512
+    min_scan_cols = 256 if w["arch"] == "simple" else 512
+    grad_kernel = ("ft_grad_scan_kernel" if not w.get("all_optim") and w["ft_out"] >= min_scan_cols
                    else "ft_grad_update_kernel")
     kernels = {
         fwd_kernel: (phase_avg["ft_forward"], fwd_bytes),

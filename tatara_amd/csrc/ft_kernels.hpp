@@ -87,10 +87,10 @@ struct FtBlockScan {
 constexpr uint32_t kDftChunk = 256;
 
 // The trainers' FT backward for factorized feature sets with an f32 dft
-// (with an f16 dft the occurrence lists measure faster) and ft_out of two
-// 256-column chunks or more (with one chunk a batch gives too
-// few workgroups for the scan to pay): block scan (1) or occurrence lists
-// only (0).
+// (with an f16 dft the occurrence lists measure faster): block scan (1) or
+// occurrence lists only (0).  The LayerStack trainer takes the scan from two
+// 256-column chunks up, the Simple trainer from one (measured faster there,
+// mostly because the occurrence sort no longer runs beside the dense layers).
 #ifndef TATARA_FT_SCAN
 #define TATARA_FT_SCAN 1
 #endif

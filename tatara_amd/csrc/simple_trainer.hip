@@ -154,7 +154,7 @@ class SimpleTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
-        use_scan = kUseFtScan && factorized && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
+        use_scan = kUseFtScan && factorized && ft_out >= kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
                          (st = arena.alloc(&scan_multi, 1))))
             return st;

@@ -108,8 +108,9 @@ def test_one_step_matches_oracle(gpu, loss, optimizer):
         assert t.step_count == 1
 
 
-def test_multi_step_ranger_with_lookahead(gpu):
-    sh, cfg = make(optimizer="ranger")
+@pytest.mark.parametrize("ft_out", [128, 256])  # occurrence lists / block scan FT backward
+def test_multi_step_ranger_with_lookahead(gpu, ft_out):
+    sh, cfg = make(optimizer="ranger", ft_out=ft_out)
     b = cfg.max_batch
     st = osi.default_init(sh)
     opt = osi.OptConfig(optimizer="ranger", weight_decay=0.01)
