@@ -360,7 +360,9 @@ TATARA_API int32_t tatara_trainer_get_tensor(TataraTrainer* trainer, const char*
 TATARA_API int32_t tatara_trainer_set_tensor(TataraTrainer* trainer, const char* name, int32_t which,
                                   const float* host, uint64_t n);
 /* Activations of the last step, for parity checks: "ft_stm_out", "ft_nstm_out",
- * "combined", "net_output", "dft_stm", "dft_nstm".  n = elements to copy. */
+ * "combined", "net_output", "dft_stm", "dft_nstm"; LayerStack "l1_total"
+ * ([b][l1], bucket + shared L1 output); Simple "l1_pre", "dl1_pre".
+ * n = elements to copy. */
 TATARA_API int32_t tatara_trainer_get_activation(TataraTrainer* trainer, const char* name, float* host,
                                       uint64_t n);
 /* Phase timing (the NNUE_TRAIN_STEP_PROFILE breakdown, trainer_layerstack.rs:

@@ -30,16 +30,7 @@ constexpr int kWave = 64;
 constexpr int kWavesPerBlock = 4;
 constexpr int kMaxActive = 64;  // one index per lane
 // Floats per lane in the FT gradient gather (a wave covers 64 * this columns).
-#ifndef TATARA_FT_GRAD_LANE_FLOATS
-#define TATARA_FT_GRAD_LANE_FLOATS 4
-#endif
-constexpr int kFtGradLaneFloats = TATARA_FT_GRAD_LANE_FLOATS;
-// Split the FT backward into an stm pass and an nstm pass (needs the
-// gradient buffer for the running sums).
-#ifndef TATARA_FT_GRAD_SPLIT
-#define TATARA_FT_GRAD_SPLIT 0
-#endif
-constexpr bool kFtGradSplit = TATARA_FT_GRAD_SPLIT != 0;
+constexpr int kFtGradLaneFloats = 4;
 
 __device__ __forceinline__ float4 f4add(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
@@ -594,35 +585,25 @@ __device__ __forceinline__ void update_cells(const FtGradArgs& a, uint64_t off, 
 // kDftChunk columns).  HDFT: the dft is f16 and each row sum is multiplied by
 // dft_inv_scale (gather_and_sum_per_feature_*_fp16, native_kernels.cu:
 // 1030-1100).
-// PHASE 0 sums a row's whole list and finishes it.  PHASE 1 sums only the
-// stm part of the list and stores the running sum in grad; PHASE 2 resumes
-// from that sum over the nstm part and finishes the row.  The additions and
-// their order are those of PHASE 0; a split pass gathers from half the dft
-// rows of a king block at a time.
-template <int V, bool HDFT, bool HSTATE, int PHASE>
+template <int V, bool HDFT, bool HSTATE>
 __device__ __forceinline__ void grad_update_task(const FtGradArgs& a, uint64_t task, uint32_t lane) {
     constexpr uint32_t kCols = kWave * V;
     const uint32_t chunk = (uint32_t)(task / a.rows);
     const uint32_t f = (uint32_t)(task - (uint64_t)chunk * a.rows);
     const uint32_t col = chunk * kCols + lane * V;
-    const uint32_t s0 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f + (PHASE == 2 ? 1 : 0)]);
-    const uint32_t s1 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f + (PHASE == 1 ? 1 : 2)]);
+    const uint32_t s0 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f]);
+    const uint32_t s1 = __builtin_amdgcn_readfirstlane(a.occ_off[2 * f + 2]);
     if (col >= a.ft_out) return;
     const uint64_t q = ((uint64_t)(col / kDftChunk) * a.dft_chunk_stride + col % kDftChunk) / V;
     const uint64_t off = ((uint64_t)f * a.ft_out + col) / V;
     vecf<V>* grad = reinterpret_cast<vecf<V>*>(a.grad);
     vecf<V> gr = 0.0f;
-    if constexpr (PHASE == 2) gr = __builtin_nontemporal_load(grad + off);
     if constexpr (HDFT)
         gr = segment_sum_f16<V>(reinterpret_cast<const vech<V>*>(a.dft16), a.dft_row_stride / V, a.occ_vals, s0,
                                 s1, q, gr);
     else
         gr = segment_sum<V>(reinterpret_cast<const vecf<V>*>(a.dft), a.dft_row_stride / V, a.occ_vals, s0, s1, q,
                             gr);
-    if constexpr (PHASE == 1) {
-        __builtin_nontemporal_store(gr, grad + off);  // the running (unscaled) sum
-        return;
-    }
     if constexpr (HDFT) gr *= a.dft_inv_scale;
     if (a.grad) __builtin_nontemporal_store(gr, grad + off);
     if (a.apply_update) update_cells<V, HSTATE>(a, off, gr);
@@ -632,7 +613,7 @@ __device__ __forceinline__ void grad_update_task(const FtGradArgs& a, uint64_t t
 // nothing unless *run_if != 0 and strides its tasks over a bounded grid, so
 // it costs little when skipped (the block scan's fallback); otherwise one
 // task per wave, which keeps the gather loop's code tight.
-template <int V, bool HDFT, bool HSTATE, int PHASE, bool GATED>
+template <int V, bool HDFT, bool HSTATE, bool GATED>
 __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint32_t n_chunks) {
     constexpr uint32_t kCols = kWave * V;
     static_assert(kDftChunk % V == 0 && (kDftChunk % kCols == 0 || kCols % kDftChunk == 0),
@@ -645,10 +626,10 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
         if (__builtin_amdgcn_readfirstlane(*a.run_if) == 0u) return;
         const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock;
         for (uint64_t task = (uint64_t)bid * kWavesPerBlock + wave; task < total; task += stride)
-            grad_update_task<V, HDFT, HSTATE, PHASE>(a, task, lane);
+            grad_update_task<V, HDFT, HSTATE>(a, task, lane);
     } else {
         const uint64_t task = (uint64_t)bid * kWavesPerBlock + wave;
-        if (task < total) grad_update_task<V, HDFT, HSTATE, PHASE>(a, task, lane);
+        if (task < total) grad_update_task<V, HDFT, HSTATE>(a, task, lane);
     }
 }
 
@@ -682,14 +663,8 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
 // the occurrence-list kernel, which runs only in that case.
 // ---------------------------------------------------------------------------
 
-#ifndef TATARA_FT_SCAN_WAVES
-#define TATARA_FT_SCAN_WAVES 8
-#endif
-constexpr int kScanWaves = TATARA_FT_SCAN_WAVES;
-#ifndef TATARA_FT_SCAN_FEAT
-#define TATARA_FT_SCAN_FEAT 16
-#endif
-constexpr int kScanFeat = TATARA_FT_SCAN_FEAT;  // features per wave (low bits of a mask word)
+constexpr int kScanWaves = 8;
+constexpr int kScanFeat = 16;  // features per wave (low bits of a mask word)
 static_assert(kScanFeat <= 32, "a mask word per wave");
 constexpr int kScanStage = 32;  // rows per LDS stage
 
@@ -1195,32 +1170,22 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     const uint32_t c4 = ceil_div(a.ft_out, kWave * 4);
     uint32_t b4 = (uint32_t)(((uint64_t)a.rows * c4 + kWavesPerBlock - 1) / kWavesPerBlock);
     b4 = b4 < cap ? b4 : cap;
-#define TATARA_GRAD_G(PH, G)                                                                         \
-    do {                                                                                             \
-        if (hdft && hstate)                                                                          \
-            ft_grad_update_kernel<4, true, true, PH, G><<<b4, 256, 0, stream>>>(a, c4);              \
-        else if (hdft)                                                                               \
-            ft_grad_update_kernel<4, true, false, PH, G><<<b4, 256, 0, stream>>>(a, c4);             \
-        else if (hstate)                                                                             \
-            ft_grad_update_kernel<V, false, true, PH, G><<<blocks, 256, 0, stream>>>(a, n_chunks);   \
-        else                                                                                         \
-            ft_grad_update_kernel<V, false, false, PH, G><<<blocks, 256, 0, stream>>>(a, n_chunks);  \
-        TATARA_LAUNCHED("ft_grad_update");                                                          \
+#define TATARA_GRAD_G(G)                                                                          \
+    do {                                                                                          \
+        if (hdft && hstate)                                                                       \
+            ft_grad_update_kernel<4, true, true, G><<<b4, 256, 0, stream>>>(a, c4);               \
+        else if (hdft)                                                                            \
+            ft_grad_update_kernel<4, true, false, G><<<b4, 256, 0, stream>>>(a, c4);              \
+        else if (hstate)                                                                          \
+            ft_grad_update_kernel<V, false, true, G><<<blocks, 256, 0, stream>>>(a, n_chunks);    \
+        else                                                                                      \
+            ft_grad_update_kernel<V, false, false, G><<<blocks, 256, 0, stream>>>(a, n_chunks);   \
+        TATARA_LAUNCHED("ft_grad_update");                                                       \
     } while (0)
-#define TATARA_GRAD(PH)              \
-    do {                             \
-        if (a.run_if)                \
-            TATARA_GRAD_G(PH, true);  \
-        else                         \
-            TATARA_GRAD_G(PH, false); \
-    } while (0)
-    if (kFtGradSplit && a.grad) {
-        TATARA_GRAD(1);
-        TATARA_GRAD(2);
-    } else {
-        TATARA_GRAD(0);
-    }
-#undef TATARA_GRAD
+    if (a.run_if)
+        TATARA_GRAD_G(true);
+    else
+        TATARA_GRAD_G(false);
 #undef TATARA_GRAD_G
     return kOk;
 }

@@ -86,15 +86,6 @@ struct FtBlockScan {
 // Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).
 constexpr uint32_t kDftChunk = 256;
 
-// The trainers' FT backward for factorized feature sets with an f32 dft
-// (with an f16 dft the occurrence lists measure faster): block scan (1) or
-// occurrence lists only (0).  The LayerStack trainer takes the scan from two
-// 256-column chunks up, the Simple trainer from one (measured faster there,
-// mostly because the occurrence sort no longer runs beside the dense layers).
-#ifndef TATARA_FT_SCAN
-#define TATARA_FT_SCAN 1
-#endif
-constexpr bool kUseFtScan = TATARA_FT_SCAN != 0;
 
 int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream);
 int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm, const int32_t* nnz,

@@ -5,13 +5,17 @@
 // loss_wrm_cpu (crates/gpu-kernels/src/pointwise/loss_wrm.rs, the plain and the
 // extended form) operation for operation; LossKind is
 // crates/nnue-train/src/trainer.rs:89-221.  The library is built with
-// -ffp-contract=off, and expf / powf are the device library's correctly
-// rounded-to-1ulp routines (the reference CPU path calls glibc's).
+// -ffp-contract=off and every exp is ref_expf (glibc's expf, what the
+// reference's CPU path calls), so for the same net output the sigmoid, the
+// WRM transforms, the error and the plain losses' gradient are the reference
+// CPU values bit for bit; powf (extended WRM only) is the device library's.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+
+#include "ref_expf.hpp"
 
 namespace tatara {
 
@@ -24,12 +28,12 @@ struct LossParams {
     int32_t extended;  // WRM extended form (pow != 2 || asym != 0 || w1 != 0)
 };
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + ref_expf(-x)); }
 
 // Extended-WRM position weight (wrm_weight_sum, native_kernels.cu:520-544).
 __device__ __forceinline__ float wrm_weight_dev(float s, const LossParams& lp) {
-    const float tp = 1.0f / (1.0f + expf(-((s - lp.target_offset) / lp.target_scaling)));
-    const float tn = 1.0f / (1.0f + expf(-((-s - lp.target_offset) / lp.target_scaling)));
+    const float tp = 1.0f / (1.0f + ref_expf(-((s - lp.target_offset) / lp.target_scaling)));
+    const float tn = 1.0f / (1.0f + ref_expf(-((-s - lp.target_offset) / lp.target_scaling)));
     const float t = 0.5f * (1.0f + tp - tn);
     const float wb = (t - 0.5f) * (t - 0.5f) * t * (1.0f - t);
     return 1.0f + (powf(2.0f, lp.w1) - 1.0f) * powf(wb, lp.w2);
@@ -50,13 +54,13 @@ __device__ __forceinline__ double position_loss(float net, float sc, float wd, f
         dy = 2.0f * err * p * (1.0f - p) * lp.scale * per_pos_norm;
         return (double)err * (double)err;
     }
-    const float tp = 1.0f / (1.0f + expf(-((sc - lp.target_offset) / lp.target_scaling)));
-    const float tn = 1.0f / (1.0f + expf(-((-sc - lp.target_offset) / lp.target_scaling)));
+    const float tp = 1.0f / (1.0f + ref_expf(-((sc - lp.target_offset) / lp.target_scaling)));
+    const float tn = 1.0f / (1.0f + ref_expf(-((-sc - lp.target_offset) / lp.target_scaling)));
     const float twrm = 0.5f * (1.0f + tp - tn);
     const float target = lam * wd + (1.0f - lam) * twrm;
     const float sn = net * lp.nnue2score;
-    const float q = 1.0f / (1.0f + expf(-((sn - lp.in_offset) / lp.in_scaling)));
-    const float qm = 1.0f / (1.0f + expf(-((-sn - lp.in_offset) / lp.in_scaling)));
+    const float q = 1.0f / (1.0f + ref_expf(-((sn - lp.in_offset) / lp.in_scaling)));
+    const float qm = 1.0f / (1.0f + ref_expf(-((-sn - lp.in_offset) / lp.in_scaling)));
     const float pred = 0.5f * (1.0f + q - qm);
     const float err = pred - target;
     if (!lp.extended) {

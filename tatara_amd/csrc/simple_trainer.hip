@@ -154,7 +154,7 @@ class SimpleTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
-        use_scan = kUseFtScan && factorized && ft_out >= kDftChunk && ft_scan_mask_words(pi) > 0;
+        use_scan = factorized && ft_out >= kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
                          (st = arena.alloc(&scan_multi, 1))))
             return st;
@@ -452,6 +452,7 @@ class SimpleTrainer final : public TrainerBase {
             return st;
         if ((st = prof_mark(7))) return st;
         last_b = p.b;
+        if ((st = release_batch())) return st;
         return queue_loss(loss_out, slot, lagged);
     }
 
@@ -477,6 +478,7 @@ class SimpleTrainer final : public TrainerBase {
                        "validate net");
         TATARA_HIP(hipStreamSynchronize(stream), "validate");
         last_b = p.b;
+        if ((st = release_batch())) return st;
         if (sse) *sse = v;
         return kOk;
     }

@@ -221,7 +221,7 @@ class LayerStackTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
-        use_scan = kUseFtScan && factorized && !h_out && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
+        use_scan = factorized && !h_out && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
                          (st = arena.alloc(&scan_multi, 1))))
             return st;
@@ -589,6 +589,7 @@ class LayerStackTrainer final : public TrainerBase {
 
         // lagged loss (AsyncLossRing::read_and_queue_next)
         last_b = p.b;
+        if ((st = release_batch())) return st;
         return queue_loss(loss_out, slot, lagged);
     }
 
@@ -613,6 +614,7 @@ class LayerStackTrainer final : public TrainerBase {
             TATARA_HIP(hipMemcpyAsync(net_host, net_out, 4ull * p.b, hipMemcpyDeviceToHost, stream), "validate net");
         TATARA_HIP(hipStreamSynchronize(stream), "validate");
         last_b = p.b;
+        if ((st = release_batch())) return st;
         if (sse) *sse = v;
         return kOk;
     }
@@ -626,6 +628,26 @@ class LayerStackTrainer final : public TrainerBase {
         if (s || ns)
             return copy_chunk_major(h_out ? (const void*)dft16 : (const void*)dft, h_out, last_b, ft_out, ns ? 1 : 0,
                                     host, n);
+        if (!std::strcmp(name, "l1_total")) {
+            // bucket + shared L1 output of each position (original order), the
+            // f32 sum the tail takes (elementwise_add)
+            TATARA_REQUIRE(n <= (uint64_t)last_b * l1, "activation request exceeds the last batch");
+            const uint64_t P = padded_sort_batch(last_b, nb);
+            std::vector<float> ls(P * 2 * l1);
+            std::vector<int32_t> pm(P);
+            TATARA_HIP(hipStreamSynchronize(stream), "get_activation sync");
+            TATARA_HIP(hipMemcpy(ls.data(), l1_sorted, ls.size() * sizeof(float), hipMemcpyDeviceToHost),
+                       "get_activation l1_total");
+            TATARA_HIP(hipMemcpy(pm.data(), perm, P * sizeof(int32_t), hipMemcpyDeviceToHost), "get_activation perm");
+            for (uint64_t r = 0; r < P; ++r) {
+                if (pm[r] < 0) continue;
+                for (uint32_t j = 0; j < l1; ++j) {
+                    const uint64_t i = (uint64_t)pm[r] * l1 + j;
+                    if (i < n) host[i] = ls[r * 2 * l1 + j] + ls[r * 2 * l1 + l1 + j];
+                }
+            }
+            return kOk;
+        }
         if (h_out && (!std::strcmp(name, "ft_stm_out") || !std::strcmp(name, "ft_nstm_out"))) {
             TATARA_REQUIRE(n <= (uint64_t)last_b * ft_out, "activation request exceeds the last batch");
             return copy_f16(!std::strcmp(name, "ft_stm_out") ? ft_stm16 : ft_nstm16, host, n);

@@ -19,6 +19,13 @@ constexpr float kNSmaThreshold = 5.0f;
 
 TrainerBase::~TrainerBase() {
     if (stream) (void)hipStreamSynchronize(stream);
+    if (copy_stream) (void)hipStreamSynchronize(copy_stream);
+    for (int s = 0; s < kRingSlots; ++s) {
+        if (ring_host[s]) (void)hipHostFree(ring_host[s]);
+        if (ring_copied[s]) (void)hipEventDestroy(ring_copied[s]);
+        if (ring_consumed[s]) (void)hipEventDestroy(ring_consumed[s]);
+    }
+    if (copy_stream) (void)hipStreamDestroy(copy_stream);
     for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
     for (auto& e : loss_ev)
         if (e) (void)hipEventDestroy(e);
@@ -44,6 +51,11 @@ int32_t TrainerBase::init_runtime(int device) {
                "hipHostMalloc loss ring");
     TATARA_HIP(hipEventCreateWithFlags(&ev_flag, hipEventDisableTiming), "hipEventCreate");
     TATARA_HIP(hipHostMalloc((void**)&pinned_flag, sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc flag");
+    TATARA_HIP(hipStreamCreateWithFlags(&copy_stream, hipStreamNonBlocking), "hipStreamCreate (copy)");
+    for (int s = 0; s < kRingSlots; ++s) {
+        TATARA_HIP(hipEventCreateWithFlags(&ring_copied[s], hipEventDisableTiming), "hipEventCreate");
+        TATARA_HIP(hipEventCreateWithFlags(&ring_consumed[s], hipEventDisableTiming), "hipEventCreate");
+    }
     return kOk;
 }
 
@@ -59,13 +71,31 @@ int32_t TrainerBase::read_flag(uint32_t& value) {
     return kOk;
 }
 
+namespace {
+
+// Byte offsets of the arrays in an upload-ring slot of capacity B.
+struct SlotLayout {
+    uint64_t stm, nstm, nnz, bucket, score, wdl, bytes;
+    SlotLayout(uint64_t B, uint64_t ma) {
+        stm = 0;
+        nstm = stm + 4 * B * ma;
+        nnz = nstm + 4 * B * ma;
+        bucket = nnz + 4 * B;
+        score = bucket + 4 * B;
+        wdl = score + 4 * B;
+        bytes = wdl + 4 * B;
+    }
+};
+
+}  // namespace
+
 int32_t TrainerBase::alloc_inputs(uint64_t B, uint32_t max_active) {
     in_max_active = max_active;
+    ring_cap = B;
+    const SlotLayout L(B, max_active);
     int32_t st;
-    if ((st = arena.alloc(&in_stm, B * max_active)) || (st = arena.alloc(&in_nstm, B * max_active)) ||
-        (st = arena.alloc(&in_nnz, B)) || (st = arena.alloc(&in_bucket, B)) ||
-        (st = arena.alloc(&in_score, B)) || (st = arena.alloc(&in_wdl, B)))
-        return st;
+    for (int s = 0; s < kRingSlots; ++s)
+        if ((st = arena.alloc(&ring_dev[s], L.bytes))) return st;
     return kOk;
 }
 
@@ -116,6 +146,12 @@ int32_t TrainerBase::stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_
     TATARA_REQUIRE(bt->stm_indices && bt->nstm_indices && bt->nnz && bt->score && bt->wdl,
                    "batch array is null");
     if (need_bucket) TATARA_REQUIRE(bt->bucket_idx, "batch.bucket_idx is null");
+    if (ring_staged >= 0) {
+        // a step that staged a batch ended early (an error): the work it
+        // queued is ordered before everything that follows
+        int32_t st = release_batch();
+        if (st) return st;
+    }
     if (bt->on_device) {
         p.stm = bt->stm_indices;
         p.nstm = bt->nstm_indices;
@@ -125,22 +161,46 @@ int32_t TrainerBase::stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_
         p.wdl = bt->wdl;
         return kOk;
     }
+    // host arrays: copy into a pinned ring slot, upload it on the copy stream
     const uint64_t b = p.b, ma = in_max_active;
-    TATARA_HIP(hipMemcpyAsync(in_stm, bt->stm_indices, 4 * b * ma, hipMemcpyHostToDevice, stream), "H2D stm");
-    TATARA_HIP(hipMemcpyAsync(in_nstm, bt->nstm_indices, 4 * b * ma, hipMemcpyHostToDevice, stream), "H2D nstm");
-    TATARA_HIP(hipMemcpyAsync(in_nnz, bt->nnz, 4 * b, hipMemcpyHostToDevice, stream), "H2D nnz");
-    if (need_bucket)
-        TATARA_HIP(hipMemcpyAsync(in_bucket, bt->bucket_idx, 4 * b, hipMemcpyHostToDevice, stream), "H2D bucket");
-    TATARA_HIP(hipMemcpyAsync(in_score, bt->score, 4 * b, hipMemcpyHostToDevice, stream), "H2D score");
-    TATARA_HIP(hipMemcpyAsync(in_wdl, bt->wdl, 4 * b, hipMemcpyHostToDevice, stream), "H2D wdl");
-    // pageable sources: make sure they were consumed before returning
-    TATARA_HIP(hipStreamSynchronize(stream), "H2D batch");
-    p.stm = in_stm;
-    p.nstm = in_nstm;
-    p.nnz = in_nnz;
-    p.bucket = need_bucket ? in_bucket : nullptr;
-    p.score = in_score;
-    p.wdl = in_wdl;
+    const SlotLayout L(b, ma);  // packed for this batch: one copy moves it
+    const int s = ring_next;
+    if (!ring_host[s])
+        TATARA_HIP(hipHostMalloc((void**)&ring_host[s], SlotLayout(ring_cap, ma).bytes, hipHostMallocDefault),
+                   "hipHostMalloc upload ring");
+    if (ring_busy[s]) {
+        // the slot's previous upload (two steps ago) has left the pinned buffer
+        TATARA_HIP(hipEventSynchronize(ring_copied[s]), "upload ring (pinned slot free)");
+        // and the step that read the device slot has finished with it
+        TATARA_HIP(hipStreamWaitEvent(copy_stream, ring_consumed[s], 0), "upload ring (device slot free)");
+    }
+    uint8_t* h = ring_host[s];
+    std::memcpy(h + L.stm, bt->stm_indices, 4 * b * ma);
+    std::memcpy(h + L.nstm, bt->nstm_indices, 4 * b * ma);
+    std::memcpy(h + L.nnz, bt->nnz, 4 * b);
+    if (need_bucket) std::memcpy(h + L.bucket, bt->bucket_idx, 4 * b);
+    std::memcpy(h + L.score, bt->score, 4 * b);
+    std::memcpy(h + L.wdl, bt->wdl, 4 * b);
+    uint8_t* d = ring_dev[s];
+    TATARA_HIP(hipMemcpyAsync(d, h, L.bytes, hipMemcpyHostToDevice, copy_stream), "H2D batch");
+    TATARA_HIP(hipEventRecord(ring_copied[s], copy_stream), "upload ring record");
+    TATARA_HIP(hipStreamWaitEvent(stream, ring_copied[s], 0), "upload ring wait");
+    ring_busy[s] = true;
+    ring_staged = s;
+    ring_next = (s + 1) % kRingSlots;
+    p.stm = reinterpret_cast<const int32_t*>(d + L.stm);
+    p.nstm = reinterpret_cast<const int32_t*>(d + L.nstm);
+    p.nnz = reinterpret_cast<const int32_t*>(d + L.nnz);
+    p.bucket = need_bucket ? reinterpret_cast<const int32_t*>(d + L.bucket) : nullptr;
+    p.score = reinterpret_cast<const float*>(d + L.score);
+    p.wdl = reinterpret_cast<const float*>(d + L.wdl);
+    return kOk;
+}
+
+int32_t TrainerBase::release_batch() {
+    if (ring_staged < 0) return kOk;
+    TATARA_HIP(hipEventRecord(ring_consumed[ring_staged], stream), "upload ring release");
+    ring_staged = -1;
     return kOk;
 }
 

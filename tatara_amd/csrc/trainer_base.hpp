@@ -106,9 +106,25 @@ class TrainerBase {
     virtual std::vector<const char*> group_names() const = 0;
 
    protected:
-    // device copies of host batches
-    int32_t *in_stm = nullptr, *in_nstm = nullptr, *in_nnz = nullptr, *in_bucket = nullptr;
-    float *in_score = nullptr, *in_wdl = nullptr;
+    // Host batches (on_device = 0) go through a two-slot upload ring
+    // (InputUploadRing, bins/nnue_train/src/trainer_common.rs:1041-1370): the
+    // caller's arrays are copied into a pinned slot before train_step returns,
+    // the slot is uploaded on the copy stream into the matching device slot, and
+    // the step waits for that upload with an event; a slot is refilled only
+    // after the step that used it has finished reading it.  A batch of b
+    // positions is packed the same way in the pinned and the device slot (stm,
+    // nstm [b][ma] i32, nnz, bucket [b] i32, score, wdl [b] f32), so one copy
+    // moves it.
+    static constexpr int kRingSlots = 2;
+    hipStream_t copy_stream = nullptr;
+    uint8_t* ring_dev[kRingSlots] = {nullptr, nullptr};
+    uint8_t* ring_host[kRingSlots] = {nullptr, nullptr};  // pinned, allocated at the first host batch
+    hipEvent_t ring_copied[kRingSlots] = {nullptr, nullptr};   // upload of the slot done (copy stream)
+    hipEvent_t ring_consumed[kRingSlots] = {nullptr, nullptr}; // last step using the slot done (compute stream)
+    bool ring_busy[kRingSlots] = {false, false};
+    int ring_next = 0;
+    int ring_staged = -1;  // slot staged for the current step, released by release_batch
+    uint64_t ring_cap = 0;
     uint32_t in_max_active = 0;
     // lagged loss ring
     double* pinned_loss = nullptr;
@@ -136,6 +152,9 @@ class TrainerBase {
     // need_bucket: bucket_idx is required; multiple: n_pos must be a multiple of it
     int32_t stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_bucket, uint32_t multiple,
                         uint32_t max_b);
+    // Marks the end of the current step's reads of a staged host batch (call
+    // after the step's last kernel is queued).
+    int32_t release_batch();
     OptScalars scalars(int kind, float lr, uint64_t step) const;
     LossParams loss_params(const TataraLoss* l) const;
     int32_t check_loss(const TataraLoss* l) const;

@@ -1,0 +1,391 @@
+"""Trainer parity at the BASELINE.json workload shapes (GPU vs the CPU oracle step).
+
+Every BASELINE config is built at its real shape, fed seeded synthetic PSV
+positions decoded on the GPU (tatara_psv_to_batch), and stepped beside the
+oracle step (oracle/layerstack.py, oracle/simple.py) on the same decoded
+batches, as the reference's native trainer tests do at b = 16,384 for several
+steps (bins/nnue_train/src/tests/native_cuda_tests.rs:801-835, options at
+:590-603):
+
+  c0  Simple HalfKP 256x2-32-32, WRM at 290, AdamW, b = 4096, 8 steps
+  c1  Simple HalfKP 256x2-32-32, AdamW wd 0.01 lr 1e-3, WRM 290, b = 65536
+  c2  LayerStack halfka-hm-merged 768/8/32, kingrank9 (9 buckets), Ranger,
+      b = 16384, 6 steps (the lookahead fires at step 6)
+  c3  LayerStack halfka-hm-merged 1536/16/32, progress8kpabs (8 buckets),
+      Ranger, b = 16384, 3 steps, progress weights N(0, 0.01) read as a
+      variance (std 0.1: every bucket is populated, so every bucket's L1
+      segment runs at full size); and one step at b = 65536 with the weights
+      read as a standard deviation (the bench workload: buckets 3 and 4 only)
+  c4  c3 in the --all-optim mixed-precision modes, b = 16384, 3 steps
+
+Bars:
+  - decoded batches (indices, nnz, buckets, score, wdl): bit-exact with the
+    oracle's decoder;
+  - every step from the trainer's own pre-step state (the oracle step run on
+    the weights, moments and slow weights the GPU step started from):
+      FT raw sums and `combined` bit-exact; net output within 1e-5 relative /
+      1e-6 absolute (north star); post-step weights and slow weights within
+      1e-5 relative / 1e-6 absolute;
+      gradients within 1e-4 relative plus 8 sqrt(b) 2^-24 A, where A is the
+      element's sum of absolute terms (the oracle backward run on |weights|,
+      |dy| and |activations| with the CReLU masks kept): the two sides sum a
+      batch reduction in different orders, and sqrt(b) 2^-24 A is the scale
+      of the rounding difference of a b-term float32 sum, so an element whose
+      terms cancel is held to its condition, not to its (tiny) value;
+      moments within 1e-4 relative plus (1 - beta1) / (1 - beta2) times the
+      gradient bound they inherit;
+      f16 paths (--all-optim, ft_w): the gradient within 1e-3 relative plus
+      2^-11 A (every dft occurrence one f16 step apart, the loose bound), f16
+      moments within one f16 step plus the inherited gradient bound;
+  - the trajectory (the oracle's own state stepped beside the GPU from the
+    same initial weights): step 1's FT raw sums and `combined` bit-exact;
+    every step's raw sums, `combined` and net output, the lagged losses and
+    the final weights and slow weights of every group within 1e-5 relative /
+    1e-6 absolute; the final moments within the reference's own bar for two
+    implementations of this step at b = 16,384 over 3 steps: 2e-6 relative
+    plus 5e-7 (first moment) / 1e-8 (second moment) absolute
+    (native_cuda_tests.rs:22-42).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import features as ofe
+from oracle import ffi
+from oracle import layerstack as ols
+from oracle import simple as osi
+from tatara_amd.dataloader import ProgressWeights, device_batch_to_host, feature_set_info, psv_to_device_batch
+from tatara_amd.psv import synthetic_progress_weights, synthetic_psv
+from tatara_amd.trainer import (GROUPS, SIMPLE_GROUPS, LayerStackConfig, LayerStackTrainer, Sigmoid,
+                                SimpleConfig, SimpleTrainer, Wrm)
+
+pytestmark = pytest.mark.gpu
+
+SUB16 = 2.0 ** -24
+SIGMOID = {"kind": "sigmoid", "scale": 1.0 / 290.0}
+WRM290 = {"kind": "wrm", "nnue2score": 290.0, "in_scaling": 290.0, "in_offset": 0.0, "target_offset": 0.0,
+          "target_scaling": 290.0, "pow_exp": 2.0, "qp_asymmetry": 0.0, "w1": 0.0, "w2": 0.5}
+
+CASES = {
+    "c0_simple_b4096": dict(arch="simple", fs="halfkp", ft_out=256, l1=32, l2=32, nb=1, bucket="none",
+                            opt="adamw", lr=1e-3, b=4096, steps=8),
+    "c1_simple_b65536": dict(arch="simple", fs="halfkp", ft_out=256, l1=32, l2=32, nb=1, bucket="none",
+                             opt="adamw", lr=1e-3, b=65536, steps=1),
+    "c2_ls768_kingrank9": dict(arch="layerstack", fs="halfka-hm-merged", ft_out=768, l1=8, l2=32, nb=9,
+                               bucket="kingrank9", opt="ranger", lr=8.75e-4, b=16384, steps=6),
+    "c3_ls1536_progress_var": dict(arch="layerstack", fs="halfka-hm-merged", ft_out=1536, l1=16, l2=32, nb=8,
+                                   bucket="progress8kpabs", progress_std=0.1, opt="ranger", lr=8.75e-4,
+                                   b=16384, steps=3),
+    "c3_ls1536_b65536": dict(arch="layerstack", fs="halfka-hm-merged", ft_out=1536, l1=16, l2=32, nb=8,
+                             bucket="progress8kpabs", progress_std=0.01, opt="ranger", lr=8.75e-4, b=65536,
+                             steps=1),
+    "c4_ls1536_all_optim": dict(arch="layerstack", fs="halfka-hm-merged", ft_out=1536, l1=16, l2=32, nb=8,
+                                bucket="progress8kpabs", progress_std=0.1, opt="ranger", lr=8.75e-4, b=16384,
+                                steps=3, all_optim=True),
+}
+
+
+def close(got, exp, rtol, atol=0.0, atol_frac=0.0, what="", chunk=1 << 24):
+    """|got - exp| <= atol + atol_frac * max|exp| + rtol * |exp|, elementwise,
+    in float64 over chunks (the FT tables hold 10^8 values)."""
+    got = np.asarray(got).ravel()
+    exp = np.asarray(exp).ravel()
+    assert got.shape == exp.shape, (what, got.shape, exp.shape)
+    scale = float(np.abs(exp).max()) if exp.size else 0.0
+    n_bad, worst = 0, None
+    for s in range(0, exp.size, chunk):
+        g = got[s:s + chunk].astype(np.float64)
+        e = exp[s:s + chunk].astype(np.float64)
+        tol = atol + atol_frac * scale + rtol * np.abs(e)
+        err = np.abs(g - e)
+        bad = ~(err <= tol)  # NaN counts as bad
+        if bad.any():
+            n_bad += int(bad.sum())
+            i = int(np.argmax(np.where(bad, err - tol, -np.inf)))
+            if worst is None or err[i] - tol[i] > worst[3] - worst[4]:
+                worst = (s + i, g[i], e[i], err[i], tol[i])
+    if n_bad:
+        i, g, e, err, tol = worst
+        raise AssertionError(f"{what}: {n_bad} / {exp.size} outside tolerance; worst at {i}: got {g:.9g}, "
+                             f"exp {e:.9g}, err {err:.3e} > tol {tol:.3e}")
+
+
+def decoded_batches(c: dict, seed0: int):
+    """Per step: the GPU-decoded DeviceBatch and the oracle's decode of the same records
+    (checked bit-exact here)."""
+    pw = None
+    if c["bucket"] == "progress8kpabs":
+        pw = ProgressWeights(synthetic_progress_weights(seed=7, std=c["progress_std"]))
+    out = []
+    for k in range(c["steps"]):
+        rec = synthetic_psv(c["b"], seed=seed0 + k)
+        db = psv_to_device_batch(rec, c["fs"], c["bucket"], c["nb"], pw)
+        got = device_batch_to_host(db)
+        mode = {"none": "none", "kingrank9": "kingrank9", "progress8kpabs": "progress"}[c["bucket"]]
+        exp = ofe.psv_to_batch(rec, c["fs"], mode, c["nb"], pw.host if pw is not None else None)
+        for key in ("stm", "nstm", "nnz", "score", "wdl"):
+            assert np.array_equal(got[key].reshape(exp[key].shape), exp[key]), f"step {k + 1}: decoded {key}"
+        if c["arch"] == "layerstack":
+            assert np.array_equal(got["bucket"], exp["bucket"]), f"step {k + 1}: decoded bucket"
+        host = dict(stm=exp["stm"], nstm=exp["nstm"], nnz=exp["nnz"], score=exp["score"], wdl=exp["wdl"],
+                    bucket=exp["bucket"] if c["arch"] == "layerstack" else None)
+        out.append((db, host))
+    return out
+
+
+U32 = 2.0 ** -24
+BETA2 = 0.999
+
+
+def close_tol(got, exp, tol, what):
+    """|got - exp| <= tol elementwise (tol an array or scalar)."""
+    got = np.asarray(got, np.float64).ravel()
+    exp = np.asarray(exp, np.float64).ravel()
+    tol = np.broadcast_to(np.asarray(tol, np.float64).ravel(), exp.shape)
+    err = np.abs(got - exp)
+    bad = ~(err <= tol)
+    if bad.any():
+        i = int(np.argmax(np.where(bad, err - tol, -np.inf)))
+        raise AssertionError(f"{what}: {int(bad.sum())} / {exp.size} outside tolerance; worst at {i}: "
+                             f"got {got[i]:.9g}, exp {exp[i]:.9g}, err {err[i]:.3e} > tol {tol[i]:.3e}")
+
+
+def grad_magnitude(mod, sh, pre, host, a, prec, dy_abs, open_masks=None):
+    """The oracle backward on |weights|, the given per-row |dy| and |activations|,
+    every CReLU mask kept as computed except the entries listed in open_masks
+    (activation name -> boolean array), which pass the gradient: per element the
+    sum of |terms| of its gradient.  The FT bias only enters through masks and
+    keeps its sign."""
+    st_abs = {g: {"w": np.abs(v["w"])} for g, v in pre.items()}
+    st_abs["ft_b"]["w"] = pre["ft_b"]["w"]
+    a_abs = dict(a)
+    a_abs["dy"] = np.ascontiguousarray(dy_abs, np.float32)
+    if "l1_main" in a_abs:
+        a_abs["l1_main"] = np.abs(a["l1_main"])
+    for k, m in (open_masks or {}).items():
+        a_abs[k] = np.where(m.ravel(), np.float32(0.5), a[k]).astype(np.float32)
+    if prec is None:
+        return mod.backward(sh, st_abs, host, a_abs)
+    return mod.backward(sh, st_abs, host, a_abs, prec)
+
+
+def dy_parts(loss, net, host, lam, b):
+    """Per row: dy = factor * err, and one unit in the last place of the larger
+    operand of err = prediction - target, as float64 (the amount by which the two
+    sides' err may differ when the prediction rounds differently)."""
+    net = net.astype(np.float64)
+    score, wdl = host["score"].astype(np.float64), host["wdl"].astype(np.float64)
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))  # noqa: E731
+    if loss["kind"] == "sigmoid":
+        s = loss["scale"]
+        p = sig(net * s)
+        t = lam * wdl + (1 - lam) * sig(score * s)
+        factor = 2.0 * p * (1 - p) * s / b
+    else:
+        to, ts = loss["target_offset"], loss["target_scaling"]
+        t = lam * wdl + (1 - lam) * 0.5 * (1 + sig((score - to) / ts) - sig((-score - to) / ts))
+        sn = net * loss["nnue2score"]
+        q, qm = sig((sn - loss["in_offset"]) / loss["in_scaling"]), sig((-sn - loss["in_offset"]) / loss["in_scaling"])
+        p = 0.5 * (1 + q - qm)
+        factor = (loss["nnue2score"] / loss["in_scaling"]) * (q * (1 - q) + qm * (1 - qm)) / b
+    return factor, 2.0 ** -23 * (np.abs(p) + np.abs(t))
+
+
+def crelu_branch(x):
+    return (x > 0) & (x < 1)
+
+
+def near_kink(x, delta):
+    return (np.abs(x) <= delta) | (np.abs(x - 1.0) <= delta)
+
+
+def kink_entries(arch, sh, pre, host, a, gpu_l1):
+    """CReLU inputs of the tail that may take a different branch on the two sides.
+
+    gpu_l1 is the GPU's L1 output (LayerStack: bucket + shared; Simple: the
+    pre-activation).  Where the next CReLU input is an elementwise function of it
+    the branch is compared exactly; where it is a short dense sum, an entry is
+    open when the CPU value lies within the sum's possible difference of 0 or 1:
+    |W| times the inputs' difference plus the two sides' rounding of the sum
+    (2 n 2^-24 times its sum of |terms|)."""
+    b = host["stm"].shape[0]
+    u = 2.0 ** -24
+    if arch == "layerstack":
+        l1, l1e, l2, l2i, nb = sh.l1, sh.l1e, sh.l2, sh.l2_in, sh.nb
+        g1 = gpu_l1.reshape(b, l1)
+        main = g1[:, :l1e]
+        pre_g = np.concatenate([(main * main * np.float32(127.0 / 128.0)).astype(np.float32), main], axis=1)
+        pre_c = a["l2_pre"].reshape(b, l2i)
+        flip_pre = crelu_branch(pre_g) != crelu_branch(pre_c)
+        in_g, in_c = np.clip(pre_g, 0, 1).astype(np.float64), a["l2_input"].reshape(b, l2i).astype(np.float64)
+        bk = host["bucket"]
+        valid = (bk >= 0) & (bk < nb)
+        gk = np.clip(bk, 0, nb - 1)
+        W = np.abs(pre["l2_w"]["w"].reshape(nb, l2, l2i)[gk].astype(np.float64))
+        B = np.abs(pre["l2_b"]["w"].reshape(nb, l2)[gk].astype(np.float64))
+        delta = np.einsum("boi,bi->bo", W, np.abs(in_g - in_c)) + 2 * l2i * u * (np.einsum("boi,bi->bo", W, np.abs(in_c)) + B)
+        out_open = near_kink(a["l2_out"].reshape(b, l2).astype(np.float64), delta) & valid[:, None]
+        return {"l2_pre": flip_pre, "l2_out": out_open}
+    l1, l2 = sh.l1, sh.l2
+    g1 = gpu_l1.reshape(b, l1)
+    c1 = a["l1_pre"].reshape(b, l1)
+    flip1 = crelu_branch(g1) != crelu_branch(c1)
+    in_g, in_c = np.clip(g1, 0, 1).astype(np.float64), a["l1_act"].reshape(b, l1).astype(np.float64)
+    W = np.abs(pre["l2_w"]["w"].reshape(l1, l2).astype(np.float64))
+    B = np.abs(pre["l2_b"]["w"].astype(np.float64))
+    delta = np.abs(in_g - in_c) @ W + 2 * l1 * u * (np.abs(in_c) @ W + B)
+    return {"l1_pre": flip1, "l2_pre": near_kink(a["l2_pre"].reshape(b, l2).astype(np.float64), delta)}
+
+
+def grad_bounds(arch, mod, sh, pre, host, a, prec, loss, gpu_l1):
+    """(A, A_extra): A the sum of |terms| of every gradient element; A_extra the
+    gradient that may differ outright: every row's dy uncertain by one ulp of its
+    error's larger operand, and the whole contribution of the rows where a CReLU
+    may take the other branch (those masks open)."""
+    b = host["stm"].shape[0]
+    dy = a["dy"].astype(np.float64)
+    A = grad_magnitude(mod, sh, pre, host, a, prec, np.abs(dy))
+    factor, ulp = dy_parts(loss, a["net"], host, 0.0, b)
+    opened = kink_entries(arch, sh, pre, host, a, gpu_l1)
+    rows = np.zeros(b, bool)
+    for m in opened.values():
+        rows |= m.any(axis=1)
+    extra_dy = factor * ulp + np.where(rows, np.abs(dy), 0.0)
+    A_extra = grad_magnitude(mod, sh, pre, host, a, prec, extra_dy, opened)
+    return A, A_extra, int(rows.sum())
+
+
+def occurrences(sh, host):
+    """Slot occurrences of every ft_w row in the batch (virtual rows: summed over
+    their king-bucket rows)."""
+    occ = np.zeros(sh.train_ft_in, np.float64)
+    for key in ("stm", "nstm"):
+        idx = host[key]
+        valid = (np.arange(idx.shape[1])[None, :] < host["nnz"][:, None]) & (idx >= 0) & (idx < sh.ft_in)
+        occ[: sh.ft_in] += np.bincount(idx[valid], minlength=sh.ft_in)
+    if sh.piece_inputs:
+        occ[sh.ft_in:] = occ[: sh.ft_in].reshape(-1, sh.piece_inputs).sum(axis=0)
+    return occ
+
+
+def check_step(t, post, g, A, A_extra, occ, groups, prec, b, beta1, dft_scale, what):
+    """GPU state after one step vs the oracle step from the same pre-step state."""
+    f16_ft = prec is not None and prec.ft_fp16_out
+    f16_state = prec is not None and prec.fp16_opt_state
+    for name in groups:
+        close(t.get(name, "w"), post[name]["w"], 1e-5, atol=1e-6, what=f"{what} {name}.w")
+        close(t.get(name, "slow"), post[name]["slow"], 1e-5, atol=1e-6, what=f"{what} {name}.slow")
+        gx = g[name].astype(np.float64)
+        if name == "ft_w" and f16_ft:
+            cols = gx.size // occ.size
+            tol_g = (1e-3 * np.abs(gx) + 2.0 ** -11 * A[name] + A_extra[name]
+                     + np.repeat(occ, cols) * SUB16 / dft_scale)
+        else:
+            tol_g = 1e-4 * np.abs(gx) + 8.0 * np.sqrt(b) * U32 * A[name] + A_extra[name]
+        close_tol(t.get(name, "grad"), gx, tol_g, f"{what} grad {name}")
+        m, v = post[name]["m"].astype(np.float64), post[name]["v"].astype(np.float64)
+        tol_m = (1.0 - beta1) * tol_g
+        tol_v = (1.0 - BETA2) * (2.0 * np.abs(gx) + tol_g) * tol_g
+        if name == "ft_w" and f16_state:
+            tol_m = tol_m + 2e-3 * np.abs(m) + SUB16 / float(ols.M_SCALE)
+            tol_v = tol_v + 2e-3 * np.abs(v) + SUB16 / float(ols.V_SCALE)
+        else:
+            tol_m = tol_m + 1e-4 * np.abs(m)
+            tol_v = tol_v + 1e-4 * np.abs(v)
+        close_tol(t.get(name, "m"), m, tol_m, f"{what} {name}.m")
+        close_tol(t.get(name, "v"), v, tol_v, f"{what} {name}.v")
+
+
+def check_trajectory(t, st, groups, what):
+    for name in groups:
+        close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"{what} {name}.w")
+        close(t.get(name, "slow"), st[name]["slow"], 1e-5, atol=1e-6, what=f"{what} {name}.slow")
+        close(t.get(name, "m"), st[name]["m"], 2e-6, atol=5e-7, what=f"{what} {name}.m")
+        close(t.get(name, "v"), st[name]["v"], 2e-6, atol=1e-8, what=f"{what} {name}.v")
+
+
+def gpu_state(t, groups, prec):
+    st = {g: {k: t.get(g, k) for k in ("w", "m", "v", "slow")} for g in groups}
+    return ols.to_f16_state(st) if prec is not None and prec.fp16_opt_state else st
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_baseline_config_matches_oracle(gpu, case):
+    c = CASES[case]
+    ffi.set_threads(16)
+    info = feature_set_info(c["fs"])
+    b, ft_out = c["b"], c["ft_out"]
+    batches = decoded_batches(c, seed0=5000 + 100 * list(CASES).index(case))
+    if c["arch"] == "layerstack":
+        sh = ols.LsShape(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"],
+                         ft_out=ft_out, l1=c["l1"], l2=c["l2"], nb=c["nb"])
+        cfg = LayerStackConfig(ft_in=sh.ft_in, max_active=sh.max_active, piece_inputs=sh.piece_inputs,
+                               ft_out=ft_out, l1_out=c["l1"], l2_out=c["l2"], num_buckets=c["nb"], max_batch=b,
+                               optimizer=c["opt"], weight_decay=0.01, keep_grads=True)
+        prec = ols.Precision()
+        if c.get("all_optim"):
+            cfg = cfg.all_optim()
+            prec = ols.Precision.all_optim()
+        trainer, groups, loss, gloss = LayerStackTrainer(cfg), GROUPS, SIGMOID, Sigmoid(1.0 / 290.0)
+        st = ols.default_init(sh)
+        if prec.fp16_opt_state:
+            st = ols.to_f16_state(st)
+        opt = ols.OptConfig(optimizer=c["opt"], weight_decay=0.01)
+        step_fn = lambda t, db: t.train_step(db, None, c["lr"], 0.0, gloss)  # noqa: E731
+        oracle_step = lambda s_, bt, k: ols.train_step(sh, s_, bt, opt, c["lr"], 0.0, loss, k, prec)  # noqa: E731
+        bounds = lambda s_, bt, a_, l1g: grad_bounds("layerstack", ols, sh, s_, bt, a_, prec, loss, l1g)  # noqa: E731
+        l1_name, l1_width = "l1_total", c["l1"]
+        comb_w = ft_out
+    else:
+        sh = osi.SimpleShape(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"],
+                             ft_out=ft_out, l1=c["l1"], l2=c["l2"])
+        cfg = SimpleConfig(ft_in=sh.ft_in, max_active=sh.max_active, piece_inputs=sh.piece_inputs, ft_out=ft_out,
+                           l1_out=c["l1"], l2_out=c["l2"], max_batch=b, optimizer=c["opt"], weight_decay=0.01,
+                           keep_grads=True)
+        prec = None
+        gloss = Wrm(nnue2score=290.0, in_scaling=290.0, in_offset=0.0, target_offset=0.0, target_scaling=290.0)
+        trainer, groups, loss = SimpleTrainer(cfg), SIMPLE_GROUPS, WRM290
+        st = osi.default_init(sh)
+        opt = osi.OptConfig(optimizer=c["opt"], weight_decay=0.01)
+        step_fn = lambda t, db: t.train_step(db, c["lr"], 0.0, gloss)  # noqa: E731
+        oracle_step = lambda s_, bt, k: osi.train_step(sh, s_, bt, opt, c["lr"], 0.0, loss, k)  # noqa: E731
+        bounds = lambda s_, bt, a_, l1g: grad_bounds("simple", osi, sh, s_, bt, a_, None, loss, l1g)  # noqa: E731
+        l1_name, l1_width = "l1_pre", c["l1"]
+        comb_w = 2 * ft_out
+    losses_gpu, losses_ref = [], []
+    with trainer as t:
+        assert np.array_equal(t.get("ft_w"), st["ft_w"]["w"]), "initial ft_w"
+        beta1 = opt.beta1
+        occ = [occurrences(sh, host) for _, host in batches]
+        for k, (db, host) in enumerate(batches, start=1):
+            # the state this step starts from (the forward table derives from w)
+            pre = gpu_state(t, groups, prec) if k > 1 else None
+            pre_w = {g: {"w": (st if pre is None else pre)[g]["w"].copy()} for g in groups}
+            lagged = step_fn(t, db)
+            if k > 1:
+                losses_gpu.append(lagged)
+            acc, a, g_traj = oracle_step(st, host, k)
+            losses_ref.append(acc)
+            bf = b * ft_out
+            got = {"ft_stm": t.activation("ft_stm_out", bf), "ft_nstm": t.activation("ft_nstm_out", bf),
+                   "combined": t.activation("combined", b * comb_w), "net": t.activation("net_output", b)}
+            if pre is None:
+                same, g_same, post = a, g_traj, st
+            else:
+                _, same, g_same = oracle_step(pre, host, k)
+                post = pre
+            for key in ("ft_stm", "ft_nstm", "combined"):
+                assert np.array_equal(got[key], same[key]), f"step {k}: {key} from the pre-step state"
+                close(got[key], a[key], 1e-5, atol=1e-6, what=f"step {k}: {key} (trajectory)")
+            close(got["net"], same["net"], 1e-5, atol=1e-6, what=f"step {k}: net_output from the pre-step state")
+            close(got["net"], a["net"], 1e-5, atol=1e-6, what=f"step {k}: net_output (trajectory)")
+            A, A_extra, n_kink = bounds(pre_w, host, same, t.activation(l1_name, b * l1_width))
+            check_step(t, post, g_same, A, A_extra, occ[k - 1], groups, prec, b, beta1,
+                       ols.DFT_BASE_SCALE * b, f"step {k} from the pre-step state:")
+            del pre, pre_w, same, g_same, post, A, A_extra
+            print(f"{case}: step {k} matches ({n_kink} rows with a CReLU input at a kink)", flush=True)
+        losses_gpu.append(t.flush_pending_loss())
+        close(losses_gpu, losses_ref, 1e-5, what="lagged losses")
+        assert t.step_count == c["steps"]
+        check_trajectory(t, st, groups, f"after {c['steps']} steps (trajectory):")

@@ -192,3 +192,31 @@ def test_full_shape_halfkp_256_learns(gpu):
         assert np.isfinite(net).all()
         assert sse1 < sse0
         assert np.isfinite(t.get("ft_w")).all()
+
+
+def test_host_batches_through_the_upload_ring(gpu):
+    """Host batches through the pinned upload ring equal device batches bit for
+    bit, with the caller's arrays overwritten right after each train_step."""
+    from tatara_amd.trainer import Batch
+    sh, cfg = make(keep=False, b=512)
+    batches = [batch_for(30 + i, n) for i, n in enumerate([512, 200, 512, 37, 512])]
+    states, losses = [], []
+    for mode in ("host", "device"):
+        with SimpleTrainer(cfg) as t:
+            got = []
+            for bt in batches:
+                if mode == "host":
+                    hb = Batch(bt.stm_indices.copy(), bt.nstm_indices.copy(), bt.nnz.copy(), bt.score.copy(),
+                               bt.wdl.copy())
+                    got.append(t.train_step(hb, 1e-3, 0.0, WRM290))
+                    hb.stm_indices[...] = 0
+                    hb.nstm_indices[...] = 0
+                    hb.score[...] = 1e9
+                else:
+                    got.append(t.train_step(DeviceBatch.upload(bt), 1e-3, 0.0, WRM290))
+            got.append(t.flush_pending_loss())
+            losses.append(got)
+            states.append({g: t.get(g) for g in SIMPLE_GROUPS})
+    assert losses[0] == losses[1]
+    for g in SIMPLE_GROUPS:
+        assert np.array_equal(states[0][g], states[1][g]), g

@@ -228,3 +228,36 @@ def test_full_shape_step_properties(gpu):
         assert sse1 < sse0
         w = t.get("ft_w")
         assert np.isfinite(w).all()
+
+
+def test_host_batches_through_the_upload_ring(gpu):
+    """Host batches (on_device = 0) go through the pinned two-slot upload ring
+    on the copy stream: the caller may overwrite its arrays as soon as
+    train_step returns, and the trained state equals a run on device-resident
+    copies of the same batches bit for bit (ragged sizes, consecutive steps
+    reusing each ring slot)."""
+    from tatara_amd.trainer import Batch
+    sh, cfg = make(keep=False, b=512)
+    sizes = [512, 160, 512, 256, 96, 512]
+    batches = [batch_for(20 + i, n, sh.nb) for i, n in enumerate(sizes)]
+    states, losses = [], []
+    for mode in ("host", "device"):
+        with LayerStackTrainer(cfg) as t:
+            got = []
+            for bt, bk in batches:
+                if mode == "host":
+                    hb = Batch(bt.stm_indices.copy(), bt.nstm_indices.copy(), bt.nnz.copy(), bt.score.copy(),
+                               bt.wdl.copy())
+                    hk = bk.copy()
+                    got.append(t.train_step(hb, hk, 1e-3, 0.0, Sigmoid()))
+                    for a in (hb.stm_indices, hb.nstm_indices, hk):
+                        a[...] = 0
+                    hb.score[...] = 1e9
+                else:
+                    got.append(t.train_step(DeviceBatch.upload(bt, bk), None, 1e-3, 0.0, Sigmoid()))
+            got.append(t.flush_pending_loss())
+            losses.append(got)
+            states.append({g: t.get(g) for g in GROUPS})
+    assert losses[0] == losses[1]
+    for g in GROUPS:
+        assert np.array_equal(states[0][g], states[1][g]), g
