@@ -13,11 +13,23 @@ timed region and cycled (inputs resident in HBM, as the metric asks).
 
 Method (after native-bench, bins/nnue_train/src/native_bench.rs:550-575):
 W warm-up steps, synchronize, then exactly K timed steps bracketed by a
-device synchronize on both sides, host wall clock.  A second, profiled pass
-times every phase with HIP events on the trainer's own stream; the dominant
-kernel's average duration gives `roofline.achieved` from its algorithmic
-bytes.  The CPU baseline is the oracle step (restated reference CPU
-kernels, OpenMP) timed on a bounded sample on this host.
+device synchronize on both sides, host wall clock.  The same K steps are then
+timed with host batches (numpy arrays every step, through the trainer's
+pinned upload ring, as native-bench passes a host BatchData per step) and
+reported beside the resident figure.  A profiled pass times every phase with
+HIP events on the trainer's own stream.
+
+Roofline: every kernel of the step has a compulsory-byte count (each input
+read once, each output written once, a gathered table counted once;
+`compulsory_bytes`).  `roofline.achieved` is the dominant FT kernel's
+compulsory bytes over its average launch time; `traffic` is the HBM bytes it
+actually moves (rocprofv3 counters, profiles/hbm_traffic.md); the logical
+rate of SURVEY's per-occurrence formula is kept as `logical_GBps`.  The run
+fails loudly if compulsory bytes / time exceed the HBM peak for the dominant
+kernel or the whole step.  The CPU baseline is the oracle step (restated
+reference CPU kernels, OpenMP) timed on bounded samples on this host: all
+cores, one thread, configs[0]'s CPU-only run, and a GPU cross-check of the
+first step's outputs.
 
 Prints ONE JSON line.
 """
@@ -90,20 +102,18 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_rows, f16=False):
-    """Per-launch algorithmic bytes of the two FT kernels, averaged over the batches.
+def logical_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_rows, f16=False):
+    """Per-launch logical bytes of the two FT kernels (every gathered row counted
+    once per occurrence, as SURVEY's per-position formula counts them), averaged
+    over the batches.  Rows served by L2 / Infinity Cache are counted, so this
+    rate can exceed the HBM peak; it is reported beside the roofline, not as it.
 
-    ft_forward: gathered rows of both perspectives + the per-perspective
-    sums and combined written (out_rows rows of ft_out values per position:
-    3 for LayerStack, whose combined is ft_out wide; 4 for Simple, 2*ft_out)
-    + index rows + nnz.
-    FT gradient + update (ft_grad_scan_kernel or ft_grad_update_kernel, the
-    reference's formula whichever kernel runs): gathered dft rows (one per
-    occurrence) + occurrence list + w, m, v read and written for every real
-    row (+ slow on the lookahead step, 1 in 6) + the row gradient written.
-    f16 (the --all-optim modes): gathered rows, the two raw sums, the dft and
-    the moments are 2 bytes per value; w, slow, combined and the gradient stay 4.
-    """
+    ft_forward: gathered rows of both perspectives + the per-perspective sums
+    and combined written (out_rows rows of ft_out values per position: 3 for
+    LayerStack, 4 for Simple) + index rows + nnz.  FT gradient + update:
+    gathered dft rows (one per occurrence) + occurrence list + w, m, v read and
+    written for every real row (+ slow on lookahead steps) + the gradient
+    written.  f16: gathered rows, raw sums, dft and moments are 2 bytes."""
     nnz_total = np.mean([float(h["nnz"].sum()) for h in host_batches])
     b = host_batches[0]["nnz"].size
     s16 = 2.0 if f16 else 4.0
@@ -116,62 +126,269 @@ def algorithmic_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, o
     return fwd, grad
 
 
+def scan_mask_words(piece_inputs: int) -> int:
+    """Hit-mask words per schedule entry of the block-scan FT backward: feature
+    groups of at most 8 waves x 16 features per king block, one word per wave."""
+    n_groups = -(-piece_inputs // 128)
+    return 8 * n_groups
+
+
+def compulsory_bytes(w: dict, spec: dict, b: int, scan: bool, lookahead_frac: float) -> dict:
+    """Compulsory HBM bytes per launch of every kernel of one step, by phase.
+
+    A kernel's compulsory bytes are what any implementation of it must move:
+    each input it needs read once and each output written once; a gathered
+    table or activation counts once, however many positions gather it (L2 and
+    the Infinity Cache serve the repeats).  Their sum over the step is a lower
+    bound on the step's HBM traffic, so compulsory bytes / time <= 8 TB/s for
+    any kernel and for the whole step.  Small per-workgroup partials (< 1% of
+    the step) are left out, which keeps it a lower bound.
+    """
+    f16 = bool(w.get("all_optim"))
+    ft_in, pi, ma = spec["ft_in"], spec["piece_inputs"], spec["max_active"]
+    fo = w["ft_out"]
+    s_tab = s_o = s_d = s_m = 2 if f16 else 4
+    real, virt = float(ft_in) * fo, float(pi) * fo
+    idx = 2.0 * b * ma * 4 + 4.0 * b              # index rows + nnz
+    sched = 2.0 * b * 4                            # king-block schedule
+    cell = 8.0 + 4.0 * s_m + lookahead_frac * 8.0  # w, m, v read + written (+ slow on lookahead steps)
+    masks = scan_mask_words(pi) * 2.0 * b * 4 if scan else 0.0
+    occ = 0.0 if scan else 2.0 * b * ma * 4 + 8.0 * ft_in  # occurrence values + offsets
+    out = {}
+    if w["arch"] == "layerstack":
+        l1, nb = w["l1"], w["nb"]
+        P = -(-(b + (nb + 1) * 16) // 16) * 16
+        out["prep"] = idx + sched + 4.0 * b + (masks + idx + sched if scan else 2 * occ)
+        out["ft_forward"] = real * s_tab + idx + sched + 4.0 * fo + 2.0 * b * fo * s_o + 4.0 * b * fo
+        out["dense_forward"] = 4.0 * b * fo + 4.0 * (nb * l1 * fo + fo * l1) + 4.0 * P * 3 * l1 + 12.0 * b
+        out["dense_backward"] = 4.0 * b * fo + 2.0 * b * fo * s_o + 4.0 * P * l1 + 2.0 * b * fo * s_d
+        out["ft_grad_update"] = 2.0 * b * fo * s_d + masks + sched + occ + real * (cell + 4.0)
+        out["ft_virtual_fold"] = (8.0 + s_tab) * real + virt * (cell + 4.0)
+        out["dense_opt"] = 4.0 * 4 * (nb * l1 * fo + fo * l1)
+    else:
+        l1 = w["l1"]
+        out["prep"] = idx + sched + (masks + idx + sched if scan else 2 * occ)
+        out["ft_forward"] = real * 4 + idx + sched + 4.0 * fo + 2.0 * b * fo * 4 + 2.0 * b * 2 * fo * 4
+        out["dense_forward"] = 4.0 * b * 2 * fo + 4.0 * 2 * fo * l1 + 4.0 * b * 3 * l1 + 12.0 * b
+        out["dense_backward"] = 4.0 * b * 2 * fo + 2.0 * b * fo * 4 + 4.0 * b * l1 + 2.0 * b * fo * 4
+        out["ft_grad_update"] = 2.0 * b * fo * 4 + masks + sched + occ + real * (cell + 4.0)
+        out["ft_virtual_fold"] = 12.0 * real + virt * (cell + 4.0)
+        out["dense_opt"] = 4.0 * 4 * 2 * fo * l1
+    return out
+
+
 WRM290 = {"kind": "wrm", "nnue2score": 290.0, "in_scaling": 290.0, "in_offset": 0.0,
           "target_offset": 0.0, "target_scaling": 290.0, "pow_exp": 2.0, "qp_asymmetry": 0.0,
           "w1": 0.0, "w2": 0.5}
 SIGMOID = {"kind": "sigmoid", "scale": 1.0 / 290.0}
 
 
-def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int, min_seconds: float = 12.0,
-                 max_steps: int = 40) -> dict:  # noqa: C901
-    """Oracle (CPU restatement) step on this host, bounded sample of the same workload."""
-    from oracle import ffi
+def host_facts() -> dict:
+    """The CPU the baseline ran on: logical CPUs, the ones this process may use,
+    and the model name from /proc/cpuinfo."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count()
+    return {"nproc": os.cpu_count(), "affinity_cores": affinity, "cpu_model": model}
 
-    used = ffi.set_threads(threads)
-    n = 16384 if w["arch"] == "layerstack" else 32768
-    ma = spec["max_active"]
-    bd = dict(stm=hb["stm"].reshape(-1, ma)[:n], nstm=hb["nstm"].reshape(-1, ma)[:n], nnz=hb["nnz"][:n],
-              bucket=hb["bucket"][:n] if w["arch"] == "layerstack" else None, score=hb["score"][:n],
-              wdl=hb["wdl"][:n])
+
+def default_cpu_threads() -> int:
+    """The cores this process may use, capped by OMP_NUM_THREADS when it is set
+    (the GPU box gives one GPU's job a 16-core share whatever nproc shows)."""
+    n = host_facts()["affinity_cores"] or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(env)) if env and env.isdigit() and int(env) > 0 else n
+
+
+def oracle_workload(w: dict, spec: dict):
+    """(shape, fresh state, optimizer config, one-step function) of the oracle for a workload."""
     if w["arch"] == "layerstack":
         from oracle import layerstack as ols
 
         sh = ols.LsShape(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
                          ft_out=w["ft_out"], l1=w["l1"], l2=w["l2"], nb=w["nb"])
         prec = ols.Precision.all_optim() if w.get("all_optim") else ols.Precision()
-        st = ols.default_init(sh)
-        if prec.fp16_opt_state:
-            st = ols.to_f16_state(st)
         opt = ols.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
-        def one(step):
-            ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, step, prec)
+
+        def fresh():
+            st = ols.default_init(sh)
+            return ols.to_f16_state(st) if prec.fp16_opt_state else st
+
+        def one(st, bd, step):
+            return ols.train_step(sh, st, bd, opt, w["lr"], 0.0, SIGMOID, step, prec)
     else:
         from oracle import simple as osi
 
         sh = osi.SimpleShape(ft_in=spec["ft_in"], max_active=spec["max_active"],
                              piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1=w["l1"], l2=w["l2"])
-        st = osi.default_init(sh)
         opt = osi.OptConfig(optimizer=w["optimizer"], weight_decay=0.01)
-        def one(step):
-            osi.train_step(sh, st, bd, opt, w["lr"], 0.0, WRM290, step)
-    # consecutive training steps on the same batch until the sample holds
-    # about min_seconds of CPU work (at least two steps, at most max_steps)
+
+        def fresh():
+            return osi.default_init(sh)
+
+        def one(st, bd, step):
+            return osi.train_step(sh, st, bd, opt, w["lr"], 0.0, WRM290, step)
+    return sh, fresh, one
+
+
+def host_slice(w: dict, spec: dict, hb: dict, n: int) -> dict:
+    ma = spec["max_active"]
+    return dict(stm=np.ascontiguousarray(hb["stm"].reshape(-1, ma)[:n]),
+                nstm=np.ascontiguousarray(hb["nstm"].reshape(-1, ma)[:n]), nnz=hb["nnz"][:n].copy(),
+                bucket=hb["bucket"][:n].copy() if w["arch"] == "layerstack" else None,
+                score=hb["score"][:n].copy(), wdl=hb["wdl"][:n].copy())
+
+
+def timed_steps(one, st, bd, min_seconds: float, max_steps: int, min_steps: int = 1):
+    """Consecutive oracle steps until about min_seconds of work (returns steps, seconds)."""
     steps, t0 = 0, time.perf_counter()
     while True:
         steps += 1
-        one(steps)
+        one(st, bd, steps)
         dt = time.perf_counter() - t0
-        if steps >= max_steps or (steps >= 2 and dt >= min_seconds):
-            break
+        if steps >= max_steps or (steps >= min_steps and dt >= min_seconds):
+            return steps, dt
+
+
+def gpu_check(w: dict, spec: dict, bd: dict, acc: float, a: dict, st1: dict) -> dict:
+    """One GPU step on the CPU sample's batch from the same initial weights, against
+    the oracle's first step: net output, loss, and post-step weights of every group
+    (1e-5 relative / 1e-6 absolute)."""
+    from tatara_amd.trainer import (Batch, LayerStackConfig, LayerStackTrainer, Sigmoid, SimpleConfig,
+                                    SimpleTrainer, Wrm)
+
+    n = bd["nnz"].size
+    batch = Batch(bd["stm"], bd["nstm"], bd["nnz"], bd["score"], bd["wdl"])
+    if w["arch"] == "layerstack":
+        cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
+                               ft_out=w["ft_out"], l1_out=w["l1"], l2_out=w["l2"], num_buckets=w["nb"], max_batch=n,
+                               optimizer=w["optimizer"], weight_decay=0.01)
+        if w.get("all_optim"):
+            cfg = cfg.all_optim()
+        t = LayerStackTrainer(cfg)
+        step = lambda: t.train_step(batch, bd["bucket"], w["lr"], 0.0, Sigmoid(1.0 / 290.0))  # noqa: E731
+    else:
+        cfg = SimpleConfig(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
+                           ft_out=w["ft_out"], l1_out=w["l1"], l2_out=w["l2"], max_batch=n,
+                           optimizer=w["optimizer"], weight_decay=0.01)
+        t = SimpleTrainer(cfg)
+        wrm = Wrm(nnue2score=290.0, in_scaling=290.0, in_offset=0.0, target_offset=0.0, target_scaling=290.0)
+        step = lambda: t.train_step(batch, w["lr"], 0.0, wrm)  # noqa: E731
+
+    def worst(got, exp, rtol=1e-5, atol=1e-6):
+        got, exp = np.asarray(got, np.float64), np.asarray(exp, np.float64)
+        return float(np.max(np.abs(got - exp) / (atol + rtol * np.abs(exp)))) if exp.size else 0.0
+
+    with t:
+        step()
+        loss = t.flush_pending_loss()
+        net = worst(t.activation("net_output", n), a["net"])
+        comb_n = n * w["ft_out"] * (1 if w["arch"] == "layerstack" else 2)
+        comb_exact = bool(np.array_equal(t.activation("combined", comb_n), a["combined"]))
+        weights = {g: float(f"{worst(t.get(g), st1[g]['w']):.3g}") for g in st1}
+    ratios = [net] + list(weights.values())
+    return {"batch": n, "combined_bit_exact": comb_exact, "net_output_worst_ratio": float(f"{net:.3g}"),
+            "loss_rel_diff": float(f"{abs(loss - acc) / max(abs(acc), 1e-30):.3g}"),
+            "post_step_weights_worst_ratio": weights,
+            "within_north_star": comb_exact and max(ratios) <= 1.0,
+            "bar": "|gpu - cpu| / (1e-6 + 1e-5 |cpu|) <= 1 elementwise"}
+
+
+def cpu_baseline(w: dict, spec: dict, hb: dict, threads: int, min_seconds: float = 12.0,
+                 max_steps: int = 40) -> dict:
+    """The oracle step (restated reference CPU kernels, OpenMP) on this host, on
+    bounded samples of the same workload: all cores (the value), one thread,
+    configs[0]'s CPU-only run, and a GPU cross-check of the first step."""
+    from oracle import ffi
+
+    facts = host_facts()
+    n = 16384 if w["arch"] == "layerstack" else 32768
+    bd = host_slice(w, spec, hb, n)
+    sh, fresh, one = oracle_workload(w, spec)
     n_ft = (spec["ft_in"] + spec["piece_inputs"]) * w["ft_out"]
+
+    used = ffi.set_threads(threads)
+    st = fresh()
+    # the first step doubles as the GPU cross-check's reference
+    t0 = time.perf_counter()
+    acc, a, _ = one(st, bd, 1)
+    first = time.perf_counter() - t0
+    st1 = {g: {"w": v["w"].copy()} for g, v in st.items()}
+    try:
+        check = gpu_check(w, spec, bd, acc, a, st1)
+    except Exception as e:  # the baseline must not hide the GPU result
+        check = {"error": repr(e)}
+    del a, st1
+    steps, dt = timed_steps(lambda s_, b_, k: one(s_, b_, k + 1), st, bd, max(min_seconds - first, 0.0),
+                            max_steps - 1)
+    steps, dt = steps + 1, dt + first
+    value = steps * n / dt
+
+    # one thread, a smaller sample of the same workload (two steps: the dense
+    # optimizer pass over every FT parameter is a fixed cost per step)
+    ffi.set_threads(1)
+    n1 = 4096
+    st = fresh()
+    steps1, dt1 = timed_steps(one, st, host_slice(w, spec, hb, n1), 0.0, 2, 2)
+    del st
+
+    # configs[0]: Simple HalfKP 256x2-32-32, WRM 290, AdamW, batch 4096, one
+    # superbatch of 64 steps, CPU only (8 distinct seeded batches cycled)
+    ffi.set_threads(threads)
+    cfg0 = configs0_cpu_run()
     return {
-        "value": round(steps * n / dt, 1),
+        "value": round(value, 1),
         "unit": "pos/s",
         "cores": used,
         "kind": "port",
         "sample": f"{steps} consecutive full oracle steps (fwd+bwd+{w['optimizer']} over all {n_ft / 1e6:.1f}M "
-                  f"FT params) at b={n} of the same workload, {dt:.1f} s",
+                  f"FT params) at b={n} of the same workload on {used} threads, {dt:.1f} s",
+        "host": facts,
+        "single_thread": {"value": round(steps1 * n1 / dt1, 1), "unit": "pos/s", "cores": 1,
+                          "sample": f"{steps1} consecutive full oracle steps at b={n1}, {dt1:.1f} s"},
+        "configs0_cpu_run": cfg0,
+        "gpu_check": check,
     }
+
+
+def configs0_cpu_run(steps: int = 64, b: int = 4096) -> dict:
+    """BASELINE configs[0] on the CPU reference path: Simple HalfKP 256x2-32-32 fp32,
+    crelu, WRM at 290, AdamW (lr 1e-3, wd 0.01), batch 4096, one superbatch of
+    64 steps, on seeded synthetic PSV positions decoded by the oracle."""
+    from oracle import ffi
+    from oracle import features as ofe
+    from tatara_amd.psv import synthetic_psv
+
+    w = WORKLOADS["simple"]
+    info = ofe.feature_set_info("halfkp")
+    spec = dict(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"])
+    _, fresh, one = oracle_workload(w, spec)
+    batches = []
+    for i in range(8):
+        bd = ofe.psv_to_batch(synthetic_psv(b, seed=40000 + i), "halfkp")
+        batches.append(dict(stm=bd["stm"], nstm=bd["nstm"], nnz=bd["nnz"], bucket=None, score=bd["score"],
+                            wdl=bd["wdl"]))
+    st = fresh()
+    t0 = time.perf_counter()
+    loss = 0.0
+    for k in range(steps):
+        loss += one(st, batches[k % 8], k + 1)[0]
+    dt = time.perf_counter() - t0
+    return {"value": round(steps * b / dt, 1), "unit": "pos/s", "threads": ffi.set_threads(0) or None,
+            "steps": steps, "batch": b, "seconds": round(dt, 2),
+            "mean_loss": float(f"{loss / (steps * b):.6g}"),
+            "workload": "configs[0]: Simple HalfKP 256x2-32-32 fp32 crelu, WRM 290, AdamW lr 1e-3 wd 0.01, "
+                        "b=4096, 1 superbatch of 64 steps (8 seeded synthetic PSV batches cycled)"}
 
 
 def quantised_view(t) -> dict:
@@ -318,7 +535,9 @@ def main() -> int:
     ap.add_argument("--n-batches", type=int, default=8)
     ap.add_argument("--profile-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")))
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="oracle threads for the CPU baseline (default: the cores this process may use, "
+                         "capped by OMP_NUM_THREADS)")
     ap.add_argument("--drift", type=int, default=0, metavar="STEPS_PER_SUPERBATCH",
                     help="mixed-precision workloads: train the f32 and the mixed trainer from the same "
                          "initial weights over 8 superbatches of this many steps and report the loss "
@@ -339,7 +558,7 @@ def main() -> int:
     from tatara_amd.dataloader import (ProgressWeights, device_batch_to_host, feature_set_info,
                                        psv_to_device_batch)
     from tatara_amd.psv import synthetic_progress_weights, synthetic_psv
-    from tatara_amd.trainer import (LayerStackConfig, LayerStackTrainer, Sigmoid,
+    from tatara_amd.trainer import (Batch, LayerStackConfig, LayerStackTrainer, Sigmoid,
                                     SimpleConfig, SimpleTrainer, Wrm)
 
     w = WORKLOADS[args.workload]
@@ -407,6 +626,30 @@ def main() -> int:
         pos_s = b * args.steps / elapsed
         log(f"{pos_s:,.0f} pos/s  ({ms_per_step:.3f} ms/step), last loss {last:.4f}")
 
+        # the drop-in path: host batches (on_device = 0) every step, copied into
+        # the trainer's pinned upload ring and uploaded on its copy stream, as
+        # native-bench passes a host BatchData per step
+        host_objs = [(Batch(h["stm"].reshape(b, -1), h["nstm"].reshape(b, -1), h["nnz"], h["score"], h["wdl"]),
+                      h["bucket"]) for h in host_batches]
+        if w["arch"] == "layerstack":
+            hstep = lambda t, hb: t.train_step(hb[0], hb[1], lr, 0.0, loss)  # noqa: E731
+        else:
+            hstep = lambda t, hb: t.train_step(hb[0], lr, 0.0, loss)  # noqa: E731
+        for i in range(args.warmup):
+            hstep(t, host_objs[i % len(host_objs)])
+        t.flush_pending_loss()
+        _lib.check(lib.tatara_synchronize())
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            hstep(t, host_objs[i % len(host_objs)])
+        t.flush_pending_loss()
+        _lib.check(lib.tatara_synchronize())
+        h_elapsed = time.perf_counter() - t0
+        host_pos_s = b * args.steps / h_elapsed
+        h2d = sum(a.nbytes for k, a in host_batches[0].items() if k != "bucket" or w["arch"] == "layerstack")
+        log(f"host batches: {host_pos_s:,.0f} pos/s ({1000.0 * h_elapsed / args.steps:.3f} ms/step, "
+            f"{h2d / 1e6:.1f} MB H2D per step)")
+
         # phase profile (HIP events on the trainer's stream)
         t.set_profiling(True)
         for i in range(args.profile_steps):
@@ -424,25 +667,33 @@ def main() -> int:
     log("phases (ms/step): " + ", ".join(f"{k} {v:.3f}" for k, v in phase_avg.items()))
 
     la = 1.0 / 6.0 if w["optimizer"] == "ranger" else 0.0
-    fwd_bytes, grad_bytes = algorithmic_bytes(host_batches, w["ft_out"], spec["ft_in"], spec["max_active"],
-                                              lookahead_frac=la,
-                                              out_rows=3 if w["arch"] == "layerstack" else 4,
-                                              f16=bool(w.get("all_optim")))
+    f16 = bool(w.get("all_optim"))
+    fwd_logical, grad_logical = logical_bytes(host_batches, w["ft_out"], spec["ft_in"], spec["max_active"],
+                                              lookahead_frac=la, out_rows=3 if w["arch"] == "layerstack" else 4,
+                                              f16=f16)
     # the f16 forward table is gathered by the eight-column pair kernel; the
     # trainers run the FT gradient as a block scan for an f32 dft (factorized
     # feature sets; LayerStack from two 256-column chunks, Simple from one),
     # else from occurrence lists
-    fwd_kernel = "ft_forward_pair16_kernel" if w.get("all_optim") else "ft_forward_kernel"
+    fwd_kernel = "ft_forward_pair16_kernel" if f16 else "ft_forward_kernel"
     min_scan_cols = 256 if w["arch"] == "simple" else 512
-    grad_kernel = ("ft_grad_scan_kernel" if not w.get("all_optim") and w["ft_out"] >= min_scan_cols
-                   else "ft_grad_update_kernel")
+    scan = not f16 and w["ft_out"] >= min_scan_cols
+    grad_kernel = "ft_grad_scan_kernel" if scan else "ft_grad_update_kernel"
+    comp = compulsory_bytes(w, spec, b, scan, la)
+    step_bytes = sum(comp.values())
+    step_frac = step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
+    if step_frac > 1.0:
+        raise SystemExit(f"compulsory bytes per step / ms_per_step = {step_frac:.3f} of the HBM peak: the byte "
+                         f"model or the timing is wrong")
     kernels = {
-        fwd_kernel: (phase_avg["ft_forward"], fwd_bytes),
-        grad_kernel: (phase_avg["ft_grad_update"], grad_bytes),
+        fwd_kernel: (phase_avg["ft_forward"], comp["ft_forward"], fwd_logical),
+        grad_kernel: (phase_avg["ft_grad_update"], comp["ft_grad_update"], grad_logical),
     }
     dom = max(kernels, key=lambda k: kernels[k][0])
-    ms, byts = kernels[dom]
+    ms, byts, logical = kernels[dom]
     achieved = byts / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    if achieved > HBM_PEAK_GBS:
+        raise SystemExit(f"{dom}: compulsory bytes / launch time = {achieved:.0f} GB/s exceeds the HBM peak")
     traffic = hbm_traffic(args.workload, dom)
     roofline = {
         "bound": "hbm",
@@ -453,23 +704,30 @@ def main() -> int:
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
         "avg_launch_ms": round(ms, 4),
-        "algorithmic_bytes_per_launch": int(byts),
-        # the algorithmic (logical) bytes include gathered rows served by L2 /
-        # Infinity Cache; the physical HBM rate is traffic / duration
+        "compulsory_bytes_per_launch": int(byts),
+        # the HBM bytes the kernel actually moves (rocprofv3 counters) and the
+        # logical bytes of the SURVEY formula (every gathered row once per
+        # occurrence, L2 / Infinity Cache hits included)
         "hbm_GBps": round(traffic / (ms * 1e-3) / 1e9, 1) if (traffic and ms > 0) else None,
-        "hbm_frac": round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if (traffic and ms > 0) else None,
+        "traffic_over_compulsory": round(traffic / byts, 3) if traffic else None,
+        "logical_GBps": round(logical / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
         "traffic_source": "profiles/hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
     }
     other = {k: {"avg_launch_ms": round(v[0], 4),
-                 "algorithmic_GBps": round(v[1] / (v[0] * 1e-3) / 1e9, 1) if v[0] > 0 else None,
+                 "compulsory_GB": round(v[1] / 1e9, 4),
+                 "compulsory_frac": round(v[1] / (v[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if v[0] > 0 else None,
+                 "logical_GBps": round(v[2] / (v[0] * 1e-3) / 1e9, 1) if v[0] > 0 else None,
                  "hbm_bytes": hbm_traffic(args.workload, k)}
              for k, v in kernels.items()}
+    phases_out = {k: {"ms": round(v, 4), "compulsory_GB": round(comp[k] / 1e9, 4),
+                      "compulsory_frac": round(comp[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if v > 0 else None}
+                  for k, v in phase_avg.items()}
 
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle step)")
         try:
-            cpu = cpu_baseline(w, spec, host_batches[0], args.cpu_threads)
+            cpu = cpu_baseline(w, spec, host_batches[0], args.cpu_threads or default_cpu_threads())
         except Exception as e:  # the baseline must not hide the GPU result
             cpu = {"value": None, "error": repr(e)}
 
@@ -496,8 +754,17 @@ def main() -> int:
             "step_count_end": step_count,
         },
         "roofline": roofline,
+        "step_hbm": {"compulsory_GB": round(step_bytes / 1e9, 3),
+                     "compulsory_TBps": round(step_bytes / (ms_per_step * 1e-3) / 1e12, 3),
+                     "frac": round(step_frac, 4)},
+        "host_batches": {"value": round(host_pos_s, 1), "unit": "pos/s",
+                         "ms_per_step": round(1000.0 * h_elapsed / args.steps, 4),
+                         "ratio_to_resident": round(host_pos_s / pos_s, 4),
+                         "h2d_MB_per_step": round(h2d / 1e6, 2),
+                         "path": "host arrays every step (on_device = 0): pinned two-slot upload ring, "
+                                 "copy stream, event-gated"},
         "kernels": other,
-        "phases_ms": {k: round(v, 4) for k, v in phase_avg.items()},
+        "phases": phases_out,
         "psv_decode_ms_per_batch": round(decode_ms, 3),
         "cpu_baseline": cpu,
     }
