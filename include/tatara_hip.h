@@ -150,6 +150,18 @@ TATARA_API int32_t tatara_op_expf(const float* x, float* y, uint64_t n);
 TATARA_API int32_t tatara_op_quantise_ft(const float* w, uint64_t rows, uint32_t cols, uint32_t piece_inputs,
                                          double scale, int32_t leb128, uint8_t* out, uint64_t out_capacity,
                                          uint64_t* out_bytes);
+/* tatara_op_quantise_ft without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results, byte for byte; the LEB128 path's per-tile
+ * counts and offsets live in a static device array of 0.8 MB per GPU (held
+ * until the process ends), so rows * cols is limited to 2^28 values (65536
+ * tiles of 4096), larger tables are rejected with TATARA_ERR_INVALID.  Calls
+ * on one GPU share that array: calls that overlap on one GPU race.
+ * Synchronous. */
+TATARA_API int32_t tatara_op_quantise_ft_noalloc(const float* w, uint64_t rows, uint32_t cols,
+                                                 uint32_t piece_inputs, double scale, int32_t leb128, uint8_t* out,
+                                                 uint64_t out_capacity, uint64_t* out_bytes);
 
 /* ------------------------------------------------------------------------ */
 /* Dataloader: PSV records -> batch (Batch::push_decoded + BucketMode)       */

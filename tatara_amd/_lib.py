@@ -206,6 +206,10 @@ SIGNATURES = {
         C.c_int32,
         [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_double, C.c_int32, C.c_void_p, C.c_uint64, c_u64p],
     ),
+    "tatara_op_quantise_ft_noalloc": (
+        C.c_int32,
+        [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_double, C.c_int32, C.c_void_p, C.c_uint64, c_u64p],
+    ),
     "tatara_feature_set_info": (C.c_int32, [C.c_int32, c_i32p, c_i32p, c_i32p, c_i32p, C.POINTER(C.c_uint32)]),
     "tatara_psv_to_batch": (
         C.c_int32,

@@ -70,3 +70,16 @@ def test_radam_host_precompute_matches_oracle():
             assert lib.tatara_radam_step_size_denom(step, beta1, 0.999, 5.0, C.byref(ss), C.byref(dn)) == 0
             ess, edn = ffi.radam_step_size_denom(step, beta1, 0.999, 5.0)
             assert (ss.value, dn.value) == (ess, edn)
+
+
+def test_quantise_noalloc_rejects_tables_beyond_its_scratch():
+    """The allocation-free quantiser refuses more than 2^28 values (65536 tiles of
+    4096) before any device call: the pointers are never touched (CPU only)."""
+    import ctypes as C
+
+    lib = _lib.load()
+    n = C.c_uint64()
+    fake = C.c_void_p(256)
+    st = lib.tatara_op_quantise_ft_noalloc(fake, 1 << 20, 257, 0, 127.0, 1, fake, 1 << 40, C.byref(n))
+    assert st == -3 and b"static scratch" in lib.tatara_last_error()
+    assert n.value == 0
