@@ -483,6 +483,30 @@ typedef struct TataraRunConfig {
     int32_t print_progress;         /* 1: the reference's per-superbatch line on stdout */
 } TataraRunConfig;
 
+/* ControlState (crates/nnue-train/src/trainer.rs:640-656): the run's
+ * effective last superbatch and the stale target last warned about. */
+typedef struct TataraControlState {
+    uint64_t effective_target;
+    uint64_t ignored_stale_target;
+    int32_t has_ignored_stale;
+} TataraControlState;
+
+/* apply_control (trainer.rs:670-731), what tatara_train_run does at the start
+ * of every superbatch: reads control_path ({"target_superbatches": N}; other
+ * fields ignored, null or absent = no request); a missing file is silent, an
+ * unreadable or malformed one is reported on stderr and ignored; N below
+ * start_superbatch is ignored with one warning per value; otherwise the
+ * target is N clamped to [current_superbatch, configured_end] and, when it
+ * differs from state->effective_target, becomes it, is printed and appended
+ * to history_path as {"type":"control","timestamp":"<UTC ISO 8601>",
+ * "target_superbatches":T,"superbatch":S} (a failed append is reported and
+ * ignored).  *applied = 1 and *target = T when a new target was applied.
+ * Host only. */
+TATARA_API int32_t tatara_control_apply(const char* control_path, const char* history_path,
+                                        TataraControlState* state, uint64_t current_superbatch,
+                                        uint64_t start_superbatch, uint64_t configured_end, int32_t* applied,
+                                        uint64_t* target);
+
 /* One superbatch of a run: the summed (lagged + flushed) loss, positions,
  * mean loss, lr / wdl at batch 0, wall time, whether checkpoints were written. */
 typedef struct TataraRunSuperbatch {
@@ -497,8 +521,10 @@ typedef struct TataraRunSuperbatch {
  * sb, end_superbatch), train_step; per superbatch flush_pending_loss, report,
  * checkpoints.  report (capacity report_cap) receives one record per
  * superbatch; lr_seen / wdl_seen (capacity seen_cap, may be NULL) every
- * step's values.  Not covered: control.json polling, experiment.json,
- * held-out validation, score drop/clamp, shuffle windows, monitors. */
+ * step's values.  <output_dir>/control.json is read at the start of every
+ * superbatch (tatara_control_apply) and can end the run early.  Not covered:
+ * experiment.json, held-out validation, score drop/clamp, shuffle windows,
+ * monitors. */
 TATARA_API int32_t tatara_train_run(TataraTrainer* trainer, const TataraRunConfig* config,
                                     const TataraLrSchedule* lr, const TataraWdlSchedule* wdl,
                                     const TataraLoss* loss, TataraRunSuperbatch* report, uint64_t report_cap,

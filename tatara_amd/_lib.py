@@ -152,6 +152,14 @@ class TataraRunConfig(C.Structure):
     ]
 
 
+class TataraControlState(C.Structure):
+    _fields_ = [
+        ("effective_target", C.c_uint64),
+        ("ignored_stale_target", C.c_uint64),
+        ("has_ignored_stale", C.c_int32),
+    ]
+
+
 class TataraRunSuperbatch(C.Structure):
     _fields_ = [
         ("superbatch", C.c_uint64),
@@ -264,6 +272,11 @@ SIGNATURES = {
     "tatara_lr_at": (C.c_int32, [C.POINTER(TataraLrSchedule), C.c_uint64, C.c_uint64, c_f32p]),
     "tatara_lr_horizon": (C.c_int32, [C.POINTER(TataraLrSchedule), c_u64p, c_i32p]),
     "tatara_wdl_at": (C.c_int32, [C.POINTER(TataraWdlSchedule), C.c_uint64, C.c_uint64, C.c_uint64, c_f32p]),
+    "tatara_control_apply": (
+        C.c_int32,
+        [C.c_char_p, C.c_char_p, C.POINTER(TataraControlState), C.c_uint64, C.c_uint64, C.c_uint64, c_i32p,
+         c_u64p],
+    ),
     "tatara_train_run": (
         C.c_int32,
         [C.c_void_p, C.POINTER(TataraRunConfig), C.POINTER(TataraLrSchedule), C.POINTER(TataraWdlSchedule),

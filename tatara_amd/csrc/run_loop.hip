@@ -24,6 +24,11 @@
 #include <string>
 #include <vector>
 
+#include <cctype>
+#include <cerrno>
+#include <cstdlib>
+#include <ctime>
+
 #include <dirent.h>
 #include <sys/stat.h>
 #include <unistd.h>
@@ -140,6 +145,309 @@ void prune_raw(const std::string& dir, const std::string& net_id, uint64_t keep)
     }
 }
 
+// ---------------------------------------------------------------------------
+// control.json (crates/nnue-train/src/trainer.rs:640-744): at the start of
+// every superbatch the driver reads <output_dir>/control.json; a
+// {"target_superbatches": N} there moves the run's effective last superbatch
+// to N clamped to [current superbatch, configured end] (the LR / WDL
+// schedules keep the configured end as their horizon).  Each change is
+// printed and appended to control_history.jsonl.  A missing file is silent;
+// an unreadable or malformed one, and a stale target below the run's start,
+// are reported on stderr and ignored (the stale warning once per value).
+// ---------------------------------------------------------------------------
+
+// Recursive-descent JSON reader (RFC 8259 grammar): validates the text and
+// reports the raw text of the top-level object's "target_superbatches"
+// member, as serde_json deserialises ControlFile { target_superbatches:
+// Option<usize> } (unknown fields ignored, a duplicate field an error).
+struct JsonReader {
+    const char* p;
+    const char* end;
+    std::string err;
+    int depth = 0;
+
+    bool fail(const std::string& m) {
+        if (err.empty()) err = m;
+        return false;
+    }
+    void ws() {
+        while (p < end && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
+    }
+    bool literal(const char* w) {
+        const size_t n = std::strlen(w);
+        if ((size_t)(end - p) < n || std::strncmp(p, w, n) != 0) return fail("expected value");
+        p += n;
+        return true;
+    }
+    bool string(std::string* out) {
+        if (p >= end || *p != '"') return fail("expected string");
+        ++p;
+        while (p < end && *p != '"') {
+            const unsigned char ch = (unsigned char)*p;
+            if (ch < 0x20) return fail("control character in string");
+            if (ch == '\\') {
+                ++p;
+                if (p >= end) return fail("EOF while parsing a string");
+                const char esc = *p;
+                if (esc == 'u') {
+                    for (int i = 1; i <= 4; ++i)
+                        if (p + i >= end || !std::isxdigit((unsigned char)p[i])) return fail("invalid escape");
+                    p += 4;
+                    if (out) out->push_back('?');
+                } else if (std::strchr("\"\\/bfnrt", esc)) {
+                    if (out) out->push_back(esc);
+                } else {
+                    return fail("invalid escape");
+                }
+                ++p;
+                continue;
+            }
+            if (out) out->push_back((char)ch);
+            ++p;
+        }
+        if (p >= end) return fail("EOF while parsing a string");
+        ++p;
+        return true;
+    }
+    bool number() {
+        const char* s0 = p;
+        if (p < end && *p == '-') ++p;
+        if (p >= end || !std::isdigit((unsigned char)*p)) return fail("invalid number");
+        if (*p == '0') {
+            ++p;
+        } else {
+            while (p < end && std::isdigit((unsigned char)*p)) ++p;
+        }
+        if (p < end && *p == '.') {
+            ++p;
+            if (p >= end || !std::isdigit((unsigned char)*p)) return fail("invalid number");
+            while (p < end && std::isdigit((unsigned char)*p)) ++p;
+        }
+        if (p < end && (*p == 'e' || *p == 'E')) {
+            ++p;
+            if (p < end && (*p == '+' || *p == '-')) ++p;
+            if (p >= end || !std::isdigit((unsigned char)*p)) return fail("invalid number");
+            while (p < end && std::isdigit((unsigned char)*p)) ++p;
+        }
+        return p > s0;
+    }
+    bool value(const char** v0 = nullptr, const char** v1 = nullptr) {
+        ws();
+        if (p >= end) return fail("EOF while parsing a value");
+        if (++depth > 128) return fail("recursion limit exceeded");
+        const char* s0 = p;
+        bool ok;
+        switch (*p) {
+            case '{': ok = object(nullptr); break;
+            case '[': ok = array(); break;
+            case '"': ok = string(nullptr); break;
+            case 't': ok = literal("true"); break;
+            case 'f': ok = literal("false"); break;
+            case 'n': ok = literal("null"); break;
+            default: ok = number();
+        }
+        --depth;
+        if (v0) *v0 = s0;
+        if (v1) *v1 = p;
+        return ok;
+    }
+    bool array() {
+        ++p;
+        ws();
+        if (p < end && *p == ']') {
+            ++p;
+            return true;
+        }
+        while (true) {
+            if (!value()) return false;
+            ws();
+            if (p < end && *p == ',') {
+                ++p;
+                continue;
+            }
+            if (p < end && *p == ']') {
+                ++p;
+                return true;
+            }
+            return fail("expected `,` or `]`");
+        }
+    }
+    // target (may be null): receives the raw text of "target_superbatches"
+    bool object(std::string* target, bool* seen = nullptr) {
+        ++p;
+        ws();
+        if (p < end && *p == '}') {
+            ++p;
+            return true;
+        }
+        while (true) {
+            ws();
+            std::string key;
+            if (!string(&key)) return false;
+            ws();
+            if (p >= end || *p != ':') return fail("expected `:`");
+            ++p;
+            const char *v0 = nullptr, *v1 = nullptr;
+            if (!value(&v0, &v1)) return false;
+            if (target && key == "target_superbatches") {
+                if (*seen) return fail("duplicate field `target_superbatches`");
+                *seen = true;
+                target->assign(v0, v1);
+            }
+            ws();
+            if (p < end && *p == ',') {
+                ++p;
+                continue;
+            }
+            if (p < end && *p == '}') {
+                ++p;
+                return true;
+            }
+            return fail("expected `,` or `}`");
+        }
+    }
+};
+
+// Parses control.json text; *has_target = 0 when target_superbatches is
+// absent or null.  Returns false with a message for malformed input or a
+// value that is not a non-negative integer.
+bool parse_control(const std::string& text, bool* has_target, uint64_t* target, std::string* err) {
+    JsonReader r{text.data(), text.data() + text.size(), {}};
+    *has_target = false;
+    r.ws();
+    if (r.p >= r.end) {
+        *err = "EOF while parsing a value";
+        return false;
+    }
+    if (*r.p != '{') {
+        // a valid JSON value of another type is a type error, as serde reports it
+        if (!r.value()) {
+            *err = r.err;
+            return false;
+        }
+        *err = "invalid type, expected struct ControlFile";
+        return false;
+    }
+    std::string raw;
+    bool seen = false;
+    if (!r.object(&raw, &seen)) {
+        *err = r.err;
+        return false;
+    }
+    r.ws();
+    if (r.p != r.end) {
+        *err = "trailing characters";
+        return false;
+    }
+    if (!seen || raw == "null") return true;
+    if (raw.empty() || raw.find_first_not_of("0123456789") != std::string::npos) {
+        *err = "invalid type: " + raw + ", expected usize";
+        return false;
+    }
+    errno = 0;
+    char* endp = nullptr;
+    const unsigned long long v = std::strtoull(raw.c_str(), &endp, 10);
+    if (errno == ERANGE) {
+        *err = "number out of range for usize";
+        return false;
+    }
+    *has_target = true;
+    *target = (uint64_t)v;
+    return true;
+}
+
+// format_utc_iso (crates/nnue-train/src/experiment.rs:564-567)
+std::string utc_iso_now() {
+    const time_t t = time(nullptr);
+    struct tm g;
+    gmtime_r(&t, &g);
+    char buf[32];
+    snprintf(buf, sizeof buf, "%04d-%02d-%02dT%02d:%02d:%02dZ", g.tm_year + 1900, g.tm_mon + 1, g.tm_mday, g.tm_hour,
+             g.tm_min, g.tm_sec);
+    return buf;
+}
+
+// std::io::Error's display of an errno value.
+std::string os_error(int e) { return std::string(std::strerror(e)) + " (os error " + std::to_string(e) + ")"; }
+
+// apply_control (trainer.rs:670-731).  Returns true with *target when a new
+// effective target was applied.
+bool apply_control(const std::string& control_path, const std::string& history_path, TataraControlState& st,
+                   uint64_t current, uint64_t start, uint64_t configured_end, uint64_t* target) {
+    struct stat sst;
+    if (stat(control_path.c_str(), &sst) != 0) {
+        if (errno == ENOENT) return false;
+        fprintf(stderr, "[control] warning: failed to read %s: %s; ignoring\n", control_path.c_str(),
+                os_error(errno).c_str());
+        return false;
+    }
+    std::string text;
+    {
+        if (S_ISDIR(sst.st_mode)) {
+            fprintf(stderr, "[control] warning: failed to read %s: %s; ignoring\n", control_path.c_str(),
+                    os_error(EISDIR).c_str());
+            return false;
+        }
+        FILE* f = fopen(control_path.c_str(), "rb");
+        if (!f) {
+            if (errno == ENOENT) return false;
+            fprintf(stderr, "[control] warning: failed to read %s: %s; ignoring\n", control_path.c_str(),
+                    os_error(errno).c_str());
+            return false;
+        }
+        char buf[4096];
+        size_t n;
+        while ((n = fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, n);
+        const bool bad = ferror(f);
+        fclose(f);
+        if (bad) {
+            fprintf(stderr, "[control] warning: failed to read %s: read error; ignoring\n", control_path.c_str());
+            return false;
+        }
+    }
+    bool has = false;
+    uint64_t requested = 0;
+    std::string err;
+    if (!parse_control(text, &has, &requested, &err)) {
+        fprintf(stderr, "[control] warning: failed to parse %s: %s; ignoring\n", control_path.c_str(), err.c_str());
+        return false;
+    }
+    if (!has) return false;
+    if (requested < start) {
+        // ControlState::should_warn_stale: once per requested value
+        if (!(st.has_ignored_stale && st.ignored_stale_target == requested)) {
+            st.has_ignored_stale = 1;
+            st.ignored_stale_target = requested;
+            fprintf(stderr,
+                    "[control] warning: ignoring stale target_superbatches=%llu from %s below run start_superbatch=%llu\n",
+                    (unsigned long long)requested, control_path.c_str(), (unsigned long long)start);
+        }
+        return false;
+    }
+    st.has_ignored_stale = 0;
+    const uint64_t t = std::min(std::max(requested, current), configured_end);
+    if (t == st.effective_target) return false;
+    st.effective_target = t;
+    printf("[control] applied: target_superbatches=%llu (superbatch=%llu)\n", (unsigned long long)t,
+           (unsigned long long)current);
+    fflush(stdout);
+    const std::string line = std::string("{\"type\":\"control\",\"timestamp\":\"") + utc_iso_now() +
+                             "\",\"target_superbatches\":" + std::to_string(t) +
+                             ",\"superbatch\":" + std::to_string(current) + "}\n";
+    FILE* h = fopen(history_path.c_str(), "ab");
+    bool ok = h != nullptr;
+    const int open_err = errno;
+    if (h) {
+        ok = fwrite(line.data(), 1, line.size(), h) == line.size();
+        ok = (fclose(h) == 0) && ok;
+    }
+    if (!ok)
+        fprintf(stderr, "[control] warning: failed to append %s: %s; training will continue\n", history_path.c_str(),
+                h ? "write error" : os_error(open_err).c_str());
+    *target = t;
+    return true;
+}
+
 struct DevBatch {
     int32_t *stm = nullptr, *nstm = nullptr, *nnz = nullptr, *bucket = nullptr;
     float *score = nullptr, *wdl = nullptr;
@@ -249,7 +557,13 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
     const uint64_t positions_per_sb = c.batches_per_superbatch * B;
     uint64_t step = 0;
     int cur = 0;
+    const std::string control_path = out_dir + "/control.json";
+    const std::string history_path = out_dir + "/control_history.jsonl";
+    TataraControlState control{};
+    control.effective_target = c.end_superbatch;
     for (uint64_t sb = c.start_superbatch;; ++sb) {
+        uint64_t applied = 0;
+        (void)apply_control(control_path, history_path, control, sb, c.start_superbatch, c.end_superbatch, &applied);
         const auto t0 = std::chrono::steady_clock::now();
         double sb_loss = 0.0;
         uint64_t sb_positions = 0;
@@ -301,15 +615,15 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             std::max(1e-9, std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
         const double mean = sb_positions ? sb_loss / (double)sb_positions : NAN;
         const double pps = (double)sb_positions / secs;
-        const double eta = pps > 0.0 ? (double)(positions_per_sb * (c.end_superbatch - sb)) / pps : NAN;
+        const double eta = pps > 0.0 ? (double)(positions_per_sb * (control.effective_target - sb)) / pps : NAN;
         const float lr_now = lr_at(lr, 0, sb), wdl_now = wdl_at(wdl, 0, sb, c.end_superbatch);
         if (c.print_progress) {
             printf("[train] superbatch %llu/%llu | loss %.6f | %.0f pos/s | lr %s | wdl %.3f | sb %.1fs | ETA %s\n",
-                   (unsigned long long)sb, (unsigned long long)c.end_superbatch, mean, pps,
+                   (unsigned long long)sb, (unsigned long long)control.effective_target, mean, pps,
                    rust_exp4(lr_now).c_str(), (double)wdl_now, secs, format_hms(eta).c_str());
             fflush(stdout);
         }
-        const bool saved = sb % c.save_rate == 0 || sb == c.end_superbatch;
+        const bool saved = sb % c.save_rate == 0 || sb == control.effective_target;
         if (saved) {
             const std::string base = out_dir + "/" + net_id + "-" + std::to_string(sb);
             if ((st = tatara_trainer_export_quantised(trainer, (base + ".bin").c_str(), c.feature_set,
@@ -333,7 +647,7 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             r.wdl = wdl_now;
             r.saved = saved ? 1 : 0;
         }
-        if (sb == c.end_superbatch) break;
+        if (sb == control.effective_target) break;
     }
     return kOk;
 }
@@ -343,6 +657,19 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
 }  // namespace tatara
 
 using namespace tatara;
+
+extern "C" int32_t tatara_control_apply(const char* control_path, const char* history_path,
+                                        TataraControlState* state, uint64_t current_superbatch,
+                                        uint64_t start_superbatch, uint64_t configured_end, int32_t* applied,
+                                        uint64_t* target) {
+    TATARA_REQUIRE(control_path && history_path && state && applied && target, "control_apply: null argument");
+    uint64_t t = 0;
+    const bool ok = apply_control(control_path, history_path, *state, current_superbatch, start_superbatch,
+                                  configured_end, &t);
+    *applied = ok ? 1 : 0;
+    *target = ok ? t : 0;
+    return kOk;
+}
 
 extern "C" int32_t tatara_train_run(TataraTrainer* trainer, const TataraRunConfig* config,
                                     const TataraLrSchedule* lr, const TataraWdlSchedule* wdl,

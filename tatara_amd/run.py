@@ -6,7 +6,12 @@ names and fields) and evaluate through the library (`tatara_lr_at`,
 (crates/nnue-train/src/trainer.rs:759-1211): superbatches start..=end of
 batches_per_superbatch PSV batches, lagged-loss accounting with a flush per
 superbatch, quantised and resume checkpoints every save_rate superbatches and
-at the end, pruning of old resume checkpoints.
+at the end, pruning of old resume checkpoints, and <output_dir>/control.json
+read at the start of every superbatch (trainer.rs:640-744): a
+`{"target_superbatches": N}` with start <= N < end_superbatch stops the run
+after superbatch max(N, current), saving there and appending the applied
+target to <output_dir>/control_history.jsonl; the lr / wdl schedules keep the
+configured end as their horizon.
 """
 from __future__ import annotations
 

@@ -99,6 +99,10 @@ int main(void) {
     F(TataraLrSchedule, period); F(TataraLrSchedule, total); F(TataraLrSchedule, warmup_batches);
     F(TataraLrSchedule, next); F(TataraLrSchedule, next_after);
 
+    S(TataraControlState);
+    F(TataraControlState, effective_target); F(TataraControlState, ignored_stale_target);
+    F(TataraControlState, has_ignored_stale);
+
     S(TataraWdlSchedule);
     F(TataraWdlSchedule, kind); F(TataraWdlSchedule, start); F(TataraWdlSchedule, end);
     F(TataraWdlSchedule, warmup_batches); F(TataraWdlSchedule, next); F(TataraWdlSchedule, next_after);

@@ -10,6 +10,8 @@ start 3, end 5, save_rate 2 saves 4 and 5 only) and the pruning of old
 resume checkpoints follow trainer.rs:759-1283; bad data files and configs
 are rejected before any step.
 """
+import json
+
 import numpy as np
 import pytest
 
@@ -179,3 +181,71 @@ def test_rejects_bad_data_and_config(gpu, tmp_path):
             with pytest.raises(TataraError, match=msg):
                 R.run(t, path, R.ConstantLR(1e-3), R.ConstantWDL(0.0), cfg, Wrm())
         assert t.step_count == 0
+
+
+def control_run(tmp_path, name, control, start, end, save_rate, lr, wdl, bps=2):
+    """One run with <output_dir>/control.json holding `control` (None: no file)."""
+    path, _ = write_psv(tmp_path, 2 * B)
+    out = tmp_path / name
+    out.mkdir()
+    if control is not None:
+        (out / "control.json").write_text(control)
+    cfg = R.TrainingConfig(net_id="test", feature_set="halfkp", output_dir=str(out), start_superbatch=start,
+                           end_superbatch=end, batches_per_superbatch=bps, batch_size=B, save_rate=save_rate,
+                           fv_scale=16, print_progress=False)
+    with SimpleTrainer(simple_cfg()) as t:
+        res = R.run(t, path, lr, wdl, cfg, Wrm())
+        steps = t.step_count
+    return res, out, steps
+
+
+def test_control_stops_after_current_superbatch(gpu, tmp_path):
+    # trainer.rs:1805 control_stops_after_current_superbatch_and_records_completion
+    res, out, steps = control_run(tmp_path, "stop", '{"target_superbatches": 1}', 1, 3, 10,
+                                  R.StepLR(1e-3, 0.9, 1), R.ConstantWDL(0.0))
+    assert steps == 2
+    assert [(r["superbatch"], r["saved"]) for r in res.superbatches] == [(1, True)]
+    assert sorted(p.name for p in out.iterdir()) == ["control.json", "control_history.jsonl", "test-1.bin",
+                                                     "test-1.ckpt"]
+    records = [json.loads(s) for s in (out / "control_history.jsonl").read_text().splitlines()]
+    assert len(records) == 1
+    assert (records[0]["type"], records[0]["target_superbatches"], records[0]["superbatch"]) == ("control", 1, 1)
+    assert records[0]["timestamp"].endswith("Z")
+
+
+@pytest.mark.parametrize("target,ran,saved", [(2, [3, 4, 5], "test-5"), (4, [3, 4], "test-4")])
+def test_control_on_a_resumed_run(gpu, tmp_path, target, ran, saved):
+    # trainer.rs:1914 stale_control_before_resume_start_is_ignored,
+    # trainer.rs:1960 valid_control_after_resume_start_stops_at_target
+    res, out, steps = control_run(tmp_path, "resume", json.dumps({"target_superbatches": target}), 3, 5, 10,
+                                  R.StepLR(1e-3, 0.9, 1), R.ConstantWDL(0.0))
+    assert [r["superbatch"] for r in res.superbatches] == ran
+    assert steps == 2 * len(ran)
+    assert sorted(p.name for p in out.iterdir() if p.suffix in (".bin", ".ckpt")) == [saved + ".bin",
+                                                                                     saved + ".ckpt"]
+    hist = out / "control_history.jsonl"
+    assert hist.exists() == (target == 4)
+    if target == 4:
+        assert len(hist.read_text().splitlines()) == 1
+
+
+@pytest.mark.parametrize("control", [None, "{ not json", '{"target_superbatches": 3}',
+                                     '{"target_superbatches": 99}'])
+def test_ignored_control_runs_to_the_configured_end(gpu, tmp_path, control):
+    # trainer.rs:2010 missing_unreadable_and_malformed_control_do_not_stop_training,
+    # trainer.rs:2054 control_target_at_or_above_configured_end_is_noop
+    res, out, steps = control_run(tmp_path, "noop", control, 1, 3, 10, R.ConstantLR(1e-3), R.ConstantWDL(0.0))
+    assert [r["superbatch"] for r in res.superbatches] == [1, 2, 3] and steps == 6
+    assert not (out / "control_history.jsonl").exists()
+
+
+def test_control_keeps_the_schedule_horizon(gpu, tmp_path):
+    # trainer.rs:2134 control_keeps_original_lr_and_wdl_schedule_horizon
+    lr, wdl = R.LinearDecayLR(1e-3, 1e-4, 4), R.LinearWDL(0.1, 0.9)
+    base, _, _ = control_run(tmp_path, "base", None, 1, 4, 10, lr, wdl)
+    ctl, out, steps = control_run(tmp_path, "ctl", '{"target_superbatches": 2, "unknown_field": true}', 1, 4, 10,
+                                  lr, wdl)
+    assert [r["superbatch"] for r in ctl.superbatches] == [1, 2] and steps == 4
+    assert ctl.lr_seen[:4].tobytes() == base.lr_seen[:4].tobytes()
+    assert ctl.wdl_seen[:4].tobytes() == base.wdl_seen[:4].tobytes()
+    assert [r["loss_sum"] for r in ctl.superbatches] == [r["loss_sum"] for r in base.superbatches[:2]]
