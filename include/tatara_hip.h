@@ -116,6 +116,20 @@ TATARA_API int32_t tatara_op_ft_weight_grad_blocked_f16(const uint16_t* dft16, f
                                              const int32_t* nnz, float* grad, uint32_t batch,
                                              uint32_t ft_out, uint32_t cols, uint32_t max_active,
                                              uint32_t piece_inputs, uint32_t* used_block_scan);
+/* The same gradient from an f16 dft on the matrix cores (the mixed-precision
+ * trainer's FT backward, replacing gather_and_sum_per_feature_*_fp16,
+ * native_kernels.cu:1030-1100): per king block, the 0/1 hit matrix of
+ * features x rows times the block's f16 dft rows, as f16 MFMA with f32
+ * sums.  Each cell is the f32 sum of the same values as the sequential sum,
+ * in another order, times dft_inv_scale (equal to within f32 summation
+ * error, not bit for bit).  A batch with a row whose features lie in two
+ * king blocks is computed from occurrence lists (sequential sums) instead;
+ * *used_matrix_cores (optional) reports which path ran.  Synchronises. */
+TATARA_API int32_t tatara_op_ft_weight_grad_mfma_f16(const uint16_t* dft16, float dft_inv_scale,
+                                          const int32_t* stm_idx, const int32_t* nstm_idx,
+                                          const int32_t* nnz, float* grad, uint32_t batch,
+                                          uint32_t ft_out, uint32_t cols, uint32_t max_active,
+                                          uint32_t piece_inputs, uint32_t* used_matrix_cores);
 /* ft_fold_virtual / ft_reduce_virtual_grad, Base mode (native_kernels.cu:204-406). */
 TATARA_API int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,
                                   uint32_t ft_out, uint32_t piece_inputs);

@@ -198,6 +198,10 @@ SIGNATURES = {
         C.c_int32,
         [C.c_void_p, C.c_float] + [C.c_void_p] * 4 + [C.c_uint32] * 5 + [C.c_void_p],
     ),
+    "tatara_op_ft_weight_grad_mfma_f16": (
+        C.c_int32,
+        [C.c_void_p, C.c_float] + [C.c_void_p] * 4 + [C.c_uint32] * 5 + [C.c_void_p],
+    ),
     "tatara_op_ft_fold_virtual": (C.c_int32, [C.c_void_p, C.c_void_p] + [C.c_uint32] * 3),
     "tatara_op_ft_reduce_virtual_grad": (C.c_int32, [C.c_void_p] + [C.c_uint32] * 3),
     "tatara_op_radam_step": (

@@ -490,9 +490,13 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
 // variant reads f16 raw sums and writes the f16 dft, scaled by dft_scale and
 // clamped to +-65504 with a count of every clamp
 // (ft_post_perspective_grad_fused_fp16, native_kernels.cu:2304-2352); the
-// ft_b gradient stays unscaled f32.  One column per lane (86-97 VGPRs, four
-// or five waves per SIMD) measured faster than four columns per lane (193
-// VGPRs) for the f32 dft as well.  The two 16-term input-gradient sums use
+// ft_b gradient stays unscaled f32.  For the f32 dft, two columns per lane
+// with rows loaded four at a time measured 5% faster than one column per
+// lane with all 16 rows loaded ahead (0.555 against 0.586 ms for the whole
+// dense backward at ft_out 1536, b 65536), and faster than four columns per
+// lane (193 VGPRs) or one workgroup per full row; for the f16 dft the
+// one-column form stays faster (0.44 against 0.48 ms per launch).  The two
+// 16-term input-gradient sums use
 // fused multiply-adds (these layers are checked within tolerance, and their
 // reference GPU kernels contract too).
 // ---------------------------------------------------------------------------
@@ -508,14 +512,17 @@ __device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
     return v;
 }
 
-// One lane per combined column c; a wave covers 64 consecutive columns of
-// one perspective's half (ft_out % 128 == 0).  The tile's 16 raw-sum pairs
-// are loaded before any of its rows is computed.  H16: f16 raw sums and dft.
-template <int L1, bool H16>
+// Each lane owns CPL consecutive combined columns c..c+CPL-1 (all on one
+// perspective's half); a 128-lane block covers 128 * CPL columns
+// (ft_out % (128 * CPL) == 0).  The rows of a tile are taken RB at a time:
+// their raw-sum pairs are loaded before any of the RB is computed.
+// H16: f16 raw sums and dft.
+template <int L1, int CPL, int RB, bool H16>
 __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) {
+    static_assert(16 % RB == 0, "RB rows loaded ahead of their compute, a divisor of the tile");
     const uint32_t ft_out = a.ft_out, half = ft_out / 2;
     const uint64_t batch = a.batch;
-    const uint32_t c = blockIdx.x * 128 + threadIdx.x;
+    const uint32_t c = (blockIdx.x * 128 + threadIdx.x) * CPL;
     if (c >= ft_out) return;
     const uint32_t persp = c < half ? 0 : 1;
     const uint32_t p = c - persp * half;
@@ -525,14 +532,21 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
     const uint64_t off_a = (uint64_t)(p / kDftChunk) * cstride + persp * batch * kDftChunk + p % kDftChunk;
     const uint64_t off_b =
         (uint64_t)((p + half) / kDftChunk) * cstride + persp * batch * kDftChunk + (p + half) % kDftChunk;
-    float ws[L1];
+    float ws[CPL][L1];
 #pragma unroll
-    for (int o = 0; o < L1; ++o) ws[o] = a.l1s_w[(uint64_t)c * L1 + o];
-    const float ba = a.ft_b[p], bb = a.ft_b[p + half];
-    float w1[L1];
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int o = 0; o < L1; ++o) ws[j][o] = a.l1s_w[(uint64_t)(c + j) * L1 + o];
+    float ba[CPL], bb[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        ba[j] = a.ft_b[p + j];
+        bb[j] = a.ft_b[p + half + j];
+    }
+    float w1[CPL][L1];
     int32_t cur_bin = -2;
     bool bvalid = false;
-    float acc_a = 0.0f, acc_b = 0.0f;
+    float acc_a[CPL] = {}, acc_b[CPL] = {};
     uint32_t clamps = 0;
     const uint32_t tile0 = blockIdx.y * kPostTiles;
     for (uint32_t tt = 0; tt < kPostTiles; ++tt) {
@@ -544,65 +558,110 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
             cur_bin = bin;
             bvalid = (uint32_t)bin < a.nb;
 #pragma unroll
-            for (int o = 0; o < L1; ++o) w1[o] = bvalid ? a.l1_w[((uint64_t)bin * L1 + o) * ft_out + c] : 0.0f;
-        }
-        int32_t orig[16];
-        float xr[16], yr[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            orig[r] = a.perm[tile * 16 + r];
-            xr[r] = 0.0f;
-            yr[r] = 0.0f;
-            if (orig[r] >= 0) {
-                const uint64_t base = (uint64_t)orig[r] * ft_out + p;
-                if constexpr (H16) {
-                    xr[r] = (float)ft16[base];
-                    yr[r] = (float)ft16[base + half];
+            for (int o = 0; o < L1; ++o) {
+                const uint64_t i = ((uint64_t)bin * L1 + o) * ft_out + c;
+                if constexpr (CPL == 2) {
+                    const float2 w = bvalid ? *reinterpret_cast<const float2*>(a.l1_w + i) : make_float2(0.0f, 0.0f);
+                    w1[0][o] = w.x;
+                    w1[1][o] = w.y;
                 } else {
-                    xr[r] = ft32[base];
-                    yr[r] = ft32[base + half];
+                    w1[0][o] = bvalid ? a.l1_w[i] : 0.0f;
                 }
             }
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if (orig[r] < 0) continue;
-            const float* d = a.dl1_sorted + (tile * 16 + r) * L1;
-            float da = 0.0f;
-            if (bvalid) {
+        for (int r0 = 0; r0 < 16; r0 += RB) {
+            int32_t orig[RB];
+            float xr[RB][CPL], yr[RB][CPL];
 #pragma unroll
-                for (int o = 0; o < L1; ++o) da = __builtin_fmaf(d[o], w1[o], da);
-            }
-            float db = 0.0f;
+            for (int r = 0; r < RB; ++r) {
+                orig[r] = a.perm[tile * 16 + r0 + r];
 #pragma unroll
-            for (int o = 0; o < L1; ++o) db = __builtin_fmaf(d[o], ws[o], db);
-            const float dy = da + db;
-            const float xa = xr[r] + ba, xb = yr[r] + bb;
-            const float ya = crelu01(xa), yb = crelu01(xb);
-            const float ga = (xa > 0.0f && xa < 1.0f) ? dy * yb * a.ft_post_scale : 0.0f;
-            const float gb = (xb > 0.0f && xb < 1.0f) ? dy * ya * a.ft_post_scale : 0.0f;
-            const uint64_t row = (uint64_t)orig[r] * kDftChunk;
-            if constexpr (H16) {
-                const float sc = a.dft_scale;
-                _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
-                d16[off_a + row] = (_Float16)clamp_f16_range(ga * sc, clamps);
-                d16[off_b + row] = (_Float16)clamp_f16_range(gb * sc, clamps);
-            } else {
-                a.dft[off_a + row] = ga;
-                a.dft[off_b + row] = gb;
+                for (int j = 0; j < CPL; ++j) xr[r][j] = yr[r][j] = 0.0f;
+                if (orig[r] >= 0) {
+                    // (written out: a helper taking xr[r] by reference cost
+                    // 7 VGPRs and one wave per SIMD)
+                    const uint64_t base = (uint64_t)orig[r] * ft_out + p;
+                    if constexpr (CPL == 1) {
+                        xr[r][0] = H16 ? (float)ft16[base] : ft32[base];
+                        yr[r][0] = H16 ? (float)ft16[base + half] : ft32[base + half];
+                    } else if constexpr (H16) {
+                        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                        const h2 x = *reinterpret_cast<const h2*>(ft16 + base);
+                        const h2 y = *reinterpret_cast<const h2*>(ft16 + base + half);
+                        xr[r][0] = (float)x.x;
+                        xr[r][1] = (float)x.y;
+                        yr[r][0] = (float)y.x;
+                        yr[r][1] = (float)y.y;
+                    } else {
+                        const float2 x = *reinterpret_cast<const float2*>(ft32 + base);
+                        const float2 y = *reinterpret_cast<const float2*>(ft32 + base + half);
+                        xr[r][0] = x.x;
+                        xr[r][1] = x.y;
+                        yr[r][0] = y.x;
+                        yr[r][1] = y.y;
+                    }
+                }
             }
-            acc_a += ga;
-            acc_b += gb;
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                if (orig[r] < 0) continue;
+                const float* d = a.dl1_sorted + (tile * 16 + r0 + r) * L1;
+                float ga[CPL], gb[CPL];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    float da = 0.0f;
+                    if (bvalid) {
+#pragma unroll
+                        for (int o = 0; o < L1; ++o) da = __builtin_fmaf(d[o], w1[j][o], da);
+                    }
+                    float db = 0.0f;
+#pragma unroll
+                    for (int o = 0; o < L1; ++o) db = __builtin_fmaf(d[o], ws[j][o], db);
+                    const float dy = da + db;
+                    const float xa = xr[r][j] + ba[j], xb = yr[r][j] + bb[j];
+                    const float ya = crelu01(xa), yb = crelu01(xb);
+                    ga[j] = (xa > 0.0f && xa < 1.0f) ? dy * yb * a.ft_post_scale : 0.0f;
+                    gb[j] = (xb > 0.0f && xb < 1.0f) ? dy * ya * a.ft_post_scale : 0.0f;
+                    acc_a[j] += ga[j];
+                    acc_b[j] += gb[j];
+                }
+                const uint64_t row = (uint64_t)orig[r] * kDftChunk;
+                if constexpr (H16) {
+                    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                    const float sc = a.dft_scale;
+                    _Float16* d16 = reinterpret_cast<_Float16*>(a.dft16);
+                    if constexpr (CPL == 2) {
+                        h2 va, vb;
+                        va.x = (_Float16)clamp_f16_range(ga[0] * sc, clamps);
+                        va.y = (_Float16)clamp_f16_range(ga[1] * sc, clamps);
+                        vb.x = (_Float16)clamp_f16_range(gb[0] * sc, clamps);
+                        vb.y = (_Float16)clamp_f16_range(gb[1] * sc, clamps);
+                        *reinterpret_cast<h2*>(d16 + off_a + row) = va;
+                        *reinterpret_cast<h2*>(d16 + off_b + row) = vb;
+                    } else {
+                        d16[off_a + row] = (_Float16)clamp_f16_range(ga[0] * sc, clamps);
+                        d16[off_b + row] = (_Float16)clamp_f16_range(gb[0] * sc, clamps);
+                    }
+                } else if constexpr (CPL == 2) {
+                    *reinterpret_cast<float2*>(a.dft + off_a + row) = make_float2(ga[0], ga[1]);
+                    *reinterpret_cast<float2*>(a.dft + off_b + row) = make_float2(gb[0], gb[1]);
+                } else {
+                    a.dft[off_a + row] = ga[0];
+                    a.dft[off_b + row] = gb[0];
+                }
+            }
         }
     }
     float* pp = a.ftb_partial + ((uint64_t)blockIdx.y * 2 + persp) * ft_out;
-    pp[p] = acc_a;
-    pp[p + half] = acc_b;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        pp[p + j] = acc_a[j];
+        pp[p + half + j] = acc_b[j];
+    }
     if (H16 && clamps) atomicAdd(a.clamp_counter, (unsigned long long)clamps);
 }
 
-// f32 dft: a lane owns one float4 column group (four columns and their four
-// pair partners), so a 128-lane block covers 2 KB of each raw-sum row half.
 // ---------------------------------------------------------------------------
 // Dense gradient finalize + optimizer: one thread per parameter element of
 // the nine non-FT groups (uniform_optim_group_layout order,
@@ -746,20 +805,19 @@ int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
     const uint32_t rows = ls_post_workgroups(a.padded_b);
     if (rows == 0) return kOk;
     TATARA_REQUIRE(a.ft_out % 128 == 0, "ft_out must be a multiple of 128");
-    const dim3 grid(a.ft_out / 128, rows);
-    if (a.l1 == 16) {
-        if (a.dft16)
-            ls_l1_input_post_c_kernel<16, true><<<grid, 128, 0, stream>>>(a);
-        else
-            ls_l1_input_post_c_kernel<16, false><<<grid, 128, 0, stream>>>(a);
-    } else if (a.l1 == 8) {
-        if (a.dft16)
-            ls_l1_input_post_c_kernel<8, true><<<grid, 128, 0, stream>>>(a);
-        else
-            ls_l1_input_post_c_kernel<8, false><<<grid, 128, 0, stream>>>(a);
-    } else {
-        TATARA_REQUIRE(false, "l1 must be 16 or 8");
-    }
+    TATARA_REQUIRE(a.l1 == 16 || a.l1 == 8, "l1 must be 16 or 8");
+    // two columns per lane (f32) where the 256-column blocks tile ft_out
+    const bool two = !a.dft16 && a.ft_out % 256 == 0;
+    const dim3 grid(a.ft_out / (two ? 256 : 128), rows);
+    // f32: two columns per lane, rows four at a time; f16: one column per
+    // lane, all 16 rows of a tile ahead (each measured fastest for its type)
+    auto kernel = a.dft16 ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 16, true>
+                                        : ls_l1_input_post_c_kernel<8, 1, 16, true>)
+                          : two ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 2, 4, false>
+                                              : ls_l1_input_post_c_kernel<8, 2, 4, false>)
+                                : (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 4, false>
+                                              : ls_l1_input_post_c_kernel<8, 1, 4, false>);
+    kernel<<<grid, 128, 0, stream>>>(a);
     TATARA_LAUNCHED("ls_l1_input_post");
     return kOk;
 }

@@ -916,6 +916,260 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
 }
 
 // ---------------------------------------------------------------------------
+// FT backward from an f16 dft on the matrix cores (the mixed-precision
+// trainer).
+//
+// For king block K, a 256-column chunk and a set of features, the gradient
+// rows are G[f][c] = sum over the block's rows e of H[f][e] * D[e][c]: H is
+// the 0/1 hit matrix of the masks above and D the block's f16 dft rows, so
+// the backward is a GEMM whose K dimension is the block's row list, 32 rows
+// per v_mfma_f32_16x16x32_f16.  Products with 0 or 1 are exact and the sums
+// are f32, but in the matrix core's order rather than row by row as
+// gather_and_sum_per_feature_*_fp16 (native_kernels.cu:1030-1100) adds them:
+// a cell equals the sequential sum to within f32 summation error.  Rows past
+// the list are zero and the dft is clamped to +-65504, so every zero of H
+// multiplies a finite value unless a row of the block holds a NaN (which
+// then reaches every feature of its tile, not only the row's own).
+//
+// Workgroups take (block, chunk, feature group) triples in the block scan's
+// order.  Wave w of the four owns 32 features of the group (mask words 2w,
+// 2w+1) and all 256 columns of the chunk: 2 x 16 tiles of 16 x 16, 128 f32
+// accumulators per lane.  The rows go through LDS in stages of 64: wave w
+// loads rows 16w..16w+15 (four columns per lane), transposes them in
+// registers and writes them by
+// column, so the B operand of a lane (8 rows of one column) is one 16-byte
+// read; the stage's mask words sit beside them and the A operand (8 rows of
+// one feature) is built from their bits as f16 1.0 / 0.0.  Stage T+1 is
+// loaded while stage T is multiplied (two LDS buffers, one barrier per
+// stage).  The optimizer update of the workgroup's cells follows.
+// ---------------------------------------------------------------------------
+constexpr int kMfmaWaves = 4;  // 32 features each
+constexpr int kMfmaRows = 64;  // rows per stage: two MFMA steps
+// A stage's rows in LDS: 16-byte slots of (column, row octet), each holding
+// that column's 8 rows.  Columns come in groups of 8 (octet-major, then
+// column); within an octet the 8 columns are rotated by the group index, so
+// the slots a wave writes (lanes 4 columns apart) and the slots it reads (8
+// consecutive columns per 8 lanes) fall in 8 distinct bank groups.
+__device__ __forceinline__ uint32_t stage_slot(uint32_t col, uint32_t oct) {
+    return (col >> 3) * (uint32_t)kMfmaRows + oct * 8 + ((col + (col >> 3)) & 7u);
+}
+constexpr int kMfmaStageHalves = kDftChunk * kMfmaRows;  // 32 KB per buffer
+constexpr int kMfmaUpdRow = 132;                         // floats per update row (128 + padding)
+// the update reuses the stage buffers: 8 waves x 16 rows of kMfmaUpdRow floats
+constexpr int kMfmaLdsHalves = kMfmaWaves * 16 * kMfmaUpdRow * 2 > 2 * kMfmaStageHalves
+                                   ? kMfmaWaves * 16 * kMfmaUpdRow * 2
+                                   : 2 * kMfmaStageHalves;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The king block of rank `rank` when the blocks are ordered by descending
+// row count (ties: lower block first); up to 128 blocks, two per lane.
+__device__ __forceinline__ uint32_t block_of_rank(const FtBlockScan& s, uint32_t rank, uint32_t lane) {
+    const uint32_t nb = s.n_blocks;
+    auto block_rows = [&](uint32_t k) -> uint32_t {
+        return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
+                      : 0u;
+    };
+    const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
+    uint32_t r0 = 0, r1 = 0;
+    for (uint32_t m = 0; m < nb; ++m) {
+        const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
+        r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
+        r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
+    }
+    const uint64_t h0 = __ballot(lane < nb && r0 == rank);
+    const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
+    return __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
+}
+
+// 8 mask words (rows 8o..8o+7 of an MFMA step) -> the A operand of feature
+// bit m: f16 1.0 where the bit is set, 0.0 elsewhere (two halves per dword).
+__device__ __forceinline__ half8 hit_operand(u32x4 w0, u32x4 w1, uint32_t m) {
+    auto pair = [&](uint32_t lo, uint32_t hi) -> uint32_t {
+        return (((lo >> m) & 1u) | (((hi >> m) & 1u) << 16)) * 0x3C00u;
+    };
+    const u32x4 r = {pair(w0.x, w0.y), pair(w0.z, w0.w), pair(w1.x, w1.y), pair(w1.z, w1.w)};
+    return __builtin_bit_cast(half8, r);
+}
+
+template <bool HSTATE>
+__global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArgs a, FtBlockScan s,
+                                                                       ScanGeom geom) {
+    constexpr uint32_t R = kMfmaRows, KS = R / 32, RW = R / kMfmaWaves;  // MFMA steps, rows per wave
+    if (__builtin_amdgcn_readfirstlane(*s.multi)) return;  // the occurrence-list kernel runs instead
+    __shared__ __attribute__((aligned(16))) _Float16 s_lds[kMfmaLdsHalves];  // two stage buffers
+    __shared__ __attribute__((aligned(16))) uint32_t s_m[2][kScanWaves][R];      // [mask word][row]
+    auto s_d = [&](uint32_t buf, uint32_t slot) -> _Float16* { return s_lds + buf * kMfmaStageHalves + slot * 8; };
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t lane = threadIdx.x % 64;
+    // (block, chunk) pairs longest block first, pair p on XCD p % 8, the
+    // groups of a pair next to each other (as the block scan)
+    const uint32_t n_chunks = (a.ft_out + kDftChunk - 1) / kDftChunk;
+    const uint32_t xcd = blockIdx.x % kNumXcd, i_xcd = blockIdx.x / kNumXcd;
+    const uint32_t g = i_xcd % geom.n_groups;
+    const uint32_t pair = (i_xcd / geom.n_groups) * kNumXcd + xcd;
+    if (pair >= s.n_blocks * n_chunks) return;
+    const uint32_t K = block_of_rank(s, pair / n_chunks, lane), chunk = pair % n_chunks;
+    const uint32_t PI = s.piece_inputs;
+    const uint32_t blk_lo = K * PI;
+    const uint32_t blk_n = s.cols > blk_lo ? (s.cols - blk_lo < PI ? s.cols - blk_lo : PI) : 0u;
+    const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
+    const uint32_t b0 = s.sched_start[s.n_blocks + K];
+    const uint32_t n = na + (s.sched_start[s.n_blocks + K + 1] - b0);
+    auto entry = [&](uint32_t j) -> uint32_t {
+        j = j < n ? j : n - 1;
+        return j < na ? a0 + j : b0 + (j - na);
+    };
+    const _Float16* d16 = reinterpret_cast<const _Float16*>(a.dft16) + (uint64_t)chunk * a.dft_chunk_stride;
+    // thread t stages mask word t / 32 of rows t % 32 + 32k
+    const uint32_t mw = threadIdx.x / 32, mr = threadIdx.x % 32;
+    const uint32_t* mplane = s.masks + (uint64_t)(g * kScanWaves + mw) * (2ull * s.batch);
+    const uint32_t n_stages = (n + R - 1) / R;
+
+    // Stage T in registers: wave w's rows RT + RW w + j, the lane's columns
+    // 4 lane .. 4 lane + 3 (rows past the list are zero), and the thread's
+    // mask words.  Stage T+1's rows are loaded while stage T is multiplied;
+    // the positions of a stage's rows are loaded two stages ahead, so the
+    // row loads never wait on them.  (Deeper register pipelines need the
+    // stage loop unrolled, which makes the register allocator copy the
+    // accumulators and halves the occupancy.)
+    struct Stage {
+        uint2 r[RW];
+        uint32_t mw[R / 32];
+    };
+    static_assert(R <= 64, "one row position per lane");
+    auto load_pos = [&](uint32_t T) -> uint32_t { return (uint32_t)s.schedule[entry(T * R + lane % R)]; };
+    auto load_rows = [&](Stage& S, uint32_t pos, uint32_t T) {
+#pragma unroll
+        for (uint32_t j = 0; j < RW; ++j) {
+            const uint32_t jj = T * R + wave * RW + j;
+            const uint32_t e = entry(jj);
+            const uint64_t r = (e >= s.batch ? (uint64_t)s.batch : 0ull) +
+                               (uint32_t)__builtin_amdgcn_readlane(pos, wave * RW + j);
+            S.r[j] = jj < n ? reinterpret_cast<const uint2*>(d16 + r * kDftChunk)[lane] : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < R / 32; ++k) {
+            const uint32_t jm = T * R + mr + 32 * k;
+            S.mw[k] = jm < n ? mplane[entry(jm)] : 0u;
+        }
+    };
+    // registers -> LDS buffer: column 4 lane + c gets this wave's rows
+    auto store_rows = [&](const Stage& S, uint32_t buf) {
+#pragma unroll
+        for (uint32_t o = 0; o < RW / 8; ++o)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                u32x4 v;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t x0 = (c < 2) ? S.r[8 * o + 2 * k].x : S.r[8 * o + 2 * k].y;
+                    const uint32_t x1 = (c < 2) ? S.r[8 * o + 2 * k + 1].x : S.r[8 * o + 2 * k + 1].y;
+                    v[k] = (c % 2 == 0) ? ((x0 & 0xFFFFu) | (x1 << 16)) : ((x0 >> 16) | (x1 & 0xFFFF0000u));
+                }
+                *reinterpret_cast<u32x4*>(s_d(buf, stage_slot(lane * 4 + c, wave * (RW / 8) + o))) = v;
+            }
+#pragma unroll
+        for (uint32_t k = 0; k < R / 32; ++k) s_m[buf][mw][mr + 32 * k] = S.mw[k];
+    };
+
+    const uint32_t m = lane % 16, oct = lane / 16;
+    floatx4 acc[2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    Stage S;
+    uint32_t p1 = 0, p2 = 0;  // positions of stages t+1 and t+2
+    if (n_stages > 0) {
+        load_rows(S, load_pos(0), 0);
+        p1 = load_pos(1);
+        p2 = load_pos(2);
+        store_rows(S, 0);
+    }
+    __syncthreads();
+    for (uint32_t t = 0; t < n_stages; ++t) {
+        const uint32_t buf = t & 1u;
+        const bool more = t + 1 < n_stages;
+        if (more) {
+            load_rows(S, p1, t + 1);
+            p1 = p2;
+            p2 = load_pos(t + 3);
+        }
+#pragma unroll
+        for (uint32_t ks = 0; ks < KS; ++ks) {
+            half8 A[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const u32x4* wp = reinterpret_cast<const u32x4*>(&s_m[buf][wave * 2 + i][32 * ks + oct * 8]);
+                A[i] = hit_operand(wp[0], wp[1], m);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const half8 B = *reinterpret_cast<const half8*>(s_d(buf, stage_slot(j * 16 + m, 4 * ks + oct)));
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B, acc[i][j], 0, 0, 0);
+            }
+        }
+        if (more) store_rows(S, buf ^ 1u);
+        __syncthreads();
+    }
+
+    // Update, 16 features x 128 columns at a time: the wave's tiles go
+    // through its own LDS rows so that each lane then updates four
+    // consecutive columns of a feature row, four rows' state loaded before
+    // any of them is updated.  Lane holds D[4 oct + r][m] of tile (i, j):
+    // feature 32w + 16i + 4 oct + r of the group, column 16j + m.
+    float* s_u = reinterpret_cast<float*>(s_lds) + wave * 16 * kMfmaUpdRow;
+    const uint32_t lo = g * geom.group_size;
+    const uint32_t g_hi = (g + 1) * geom.group_size < blk_n ? (g + 1) * geom.group_size : blk_n;
+    const uint32_t nf = g_hi > lo ? g_hi - lo : 0u;
+    const uint64_t f0 = (uint64_t)blk_lo + lo;
+    const uint32_t fw = 32 * wave;
+    vecf<4>* grad = reinterpret_cast<vecf<4>*>(a.grad);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t col = chunk * kDftChunk + h * 128 + 4 * (lane % 32);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = acc[i][h * 8 + j][r];
+            __syncthreads();
+#pragma unroll
+            for (uint32_t q0 = 0; q0 < 8; q0 += 4) {
+                CellState<4, HSTATE> cs[4];
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t fi = fw + i * 16 + 2 * (q0 + u) + lane / 32;
+                    if (a.apply_update && fi < nf && col < a.ft_out)
+                        cs[u] = load_cells<4, HSTATE>(a, ((f0 + fi) * a.ft_out + col) / 4);
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t row = 2 * (q0 + u) + lane / 32;
+                    const uint32_t fi = fw + i * 16 + row;
+                    if (fi < nf && col < a.ft_out) {
+                        const float4 v = *reinterpret_cast<const float4*>(&s_u[row * kMfmaUpdRow + 4 * (lane % 32)]);
+                        vecf<4> gr = {v.x, v.y, v.z, v.w};
+                        gr *= a.dft_inv_scale;
+                        const uint64_t off = ((f0 + fi) * a.ft_out + col) / 4;
+                        if (a.grad) __builtin_nontemporal_store(gr, grad + off);
+                        if (a.apply_update) apply_cells<4, HSTATE>(a, off, gr, cs[u]);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Backward + optimizer, phase B (factorizer): one wave = (column chunk, piece
 // p).  The virtual row's gradient is the sequential sum of the piece's
 // king-bucket rows p, p + pi, p + 2 pi, ... (ft_reduce_virtual_grad_cpu's
@@ -1228,6 +1482,31 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
         else
             ft_grad_scan_kernel<false, false><<<g, t, 0, stream>>>(a, s, geom);
         TATARA_LAUNCHED("ft_grad_scan");
+    }
+    if (!fallback) return kOk;
+    FtGradArgs gated = a;
+    gated.run_if = s.multi;
+    return launch_ft_grad_update(gated, stream);
+}
+
+int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
+    TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "mfma backward: piece_inputs out of range");
+    TATARA_REQUIRE(a.dft16 && !a.dft, "mfma backward: f16 dft only");
+    TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
+                   "mfma backward: chunk-major dft");
+    TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "mfma backward: shapes");
+    TATARA_REQUIRE(s.n_blocks <= 128, "mfma backward: at most 128 king blocks");
+    const ScanGeom geom = scan_geom(s.piece_inputs);
+    TATARA_REQUIRE(geom.group_size <= 128, "mfma backward: at most 128 features per group");
+    const uint64_t pairs = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks;
+    const uint64_t grid = (pairs + kNumXcd - 1) / kNumXcd * kNumXcd * geom.n_groups;
+    if (grid > 0) {
+        const uint32_t t = kMfmaWaves * 64;
+        if (a.m16)
+            ft_grad_mfma_kernel<true><<<(uint32_t)grid, t, 0, stream>>>(a, s, geom);
+        else
+            ft_grad_mfma_kernel<false><<<(uint32_t)grid, t, 0, stream>>>(a, s, geom);
+        TATARA_LAUNCHED("ft_grad_mfma");
     }
     if (!fallback) return kOk;
     FtGradArgs gated = a;

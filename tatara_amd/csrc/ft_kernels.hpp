@@ -103,6 +103,9 @@ int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream);
 // nothing when *s.multi is set.  With fallback, the occurrence-list kernel
 // (its lists already sorted) is queued behind it and runs only in that case.
 int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback = true);
+// The same gradient and update from an f16 dft as a GEMM of the hit masks
+// and the dft rows on the matrix cores (f32 sums in the matrix core's order).
+int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback = true);
 // comb or comb16 (f16) receives the rewritten forward rows; both may be null.
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
                                hipStream_t stream);

@@ -294,7 +294,8 @@ int32_t tatara_op_ft_weight_grad(const float* dft, const int32_t* stm_idx,
 static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, float inv_scale,
                                       const int32_t* stm_idx, const int32_t* nstm_idx, const int32_t* nnz,
                                       float* grad, uint32_t batch, uint32_t ft_out, uint32_t cols,
-                                      uint32_t max_active, uint32_t piece_inputs, uint32_t* used_block_scan) {
+                                      uint32_t max_active, uint32_t piece_inputs, uint32_t* used_block_scan,
+                                      bool mfma = false) {
     TATARA_REQUIRE(ft_out % 4 == 0, "ft_out must be a multiple of 4");
     TATARA_REQUIRE(max_active <= 64, "max_active must be <= 64");
     TATARA_REQUIRE(ft_scan_mask_words(piece_inputs) > 0, "piece_inputs out of range for the block scan");
@@ -385,7 +386,7 @@ static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, f
     g.ft_out = ft_out;
     g.rows = cols;
     g.apply_update = 0;
-    if ((st = launch_ft_grad_scan(g, sc, 0))) return st;
+    if ((st = mfma ? launch_ft_grad_mfma(g, sc, 0) : launch_ft_grad_scan(g, sc, 0))) return st;
     uint32_t m = 0;
     TATARA_HIP(hipMemcpy(&m, multi.p, 4, hipMemcpyDeviceToHost), "ft_weight_grad_blocked");
     if (used_block_scan) *used_block_scan = m ? 0u : 1u;
@@ -407,6 +408,14 @@ int32_t tatara_op_ft_weight_grad_blocked_f16(const uint16_t* dft16, float dft_in
                                              uint32_t* used_block_scan) {
     return ft_weight_grad_blocked(nullptr, dft16, dft_inv_scale, stm_idx, nstm_idx, nnz, grad, batch, ft_out,
                                   cols, max_active, piece_inputs, used_block_scan);
+}
+
+int32_t tatara_op_ft_weight_grad_mfma_f16(const uint16_t* dft16, float dft_inv_scale, const int32_t* stm_idx,
+                                          const int32_t* nstm_idx, const int32_t* nnz, float* grad, uint32_t batch,
+                                          uint32_t ft_out, uint32_t cols, uint32_t max_active,
+                                          uint32_t piece_inputs, uint32_t* used_matrix_cores) {
+    return ft_weight_grad_blocked(nullptr, dft16, dft_inv_scale, stm_idx, nstm_idx, nnz, grad, batch, ft_out,
+                                  cols, max_active, piece_inputs, used_matrix_cores, true);
 }
 
 int32_t tatara_op_ft_fold_virtual(const float* weight, float* comb, uint32_t ft_in,

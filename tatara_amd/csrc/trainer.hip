@@ -10,12 +10,14 @@
 // of ~100 launches with float atomics):
 //
 //   prep      king-block schedule (stable bin sort), bucket sort (16-aligned),
-//             occurrence sort for the FT backward (radix, stable)
+//             hit masks of the block-scan FT backward (second stream); the
+//             occurrence sort (radix, stable) only where the scan cannot run
 //   forward   FT gather + pairwise CReLU  ->  L1 (MFMA, sorted tiles)
 //             -> tail (L1 glue, L2, L3, loss) per row
 //   backward  tail backward (same kernel)  ->  L1 weight grad (MFMA)
 //             -> L1 input grad + FT-post grad (dft)
-//   optimizer FT gradient (segmented sums) + RAdam/Ranger + fold, fused
+//   optimizer FT gradient (block scan; f16 dft: hit-mask x dft GEMM on the
+//             matrix cores) + RAdam/Ranger + fold, fused
 //             -> dense gradients from partials + RAdam/Ranger
 #include <hip/hip_runtime.h>
 
@@ -221,7 +223,8 @@ class LayerStackTrainer final : public TrainerBase {
             (st = arena.alloc(&occ_off, 2ull * ft_in + 2)) ||
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
-        use_scan = factorized && !h_out && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
+        // the block scan (f32 dft) or its matrix-core form (f16 dft)
+        use_scan = factorized && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
                          (st = arena.alloc(&scan_multi, 1))))
             return st;
@@ -395,8 +398,9 @@ class LayerStackTrainer final : public TrainerBase {
         return launch_occurrence_sort(os, s);
     }
 
-    // FT gradient + update: the block scan, or occurrence lists when the
-    // trainer does not scan or the batch has a row the scan cannot take
+    // FT gradient + update: the block scan (its matrix-core form for an f16
+    // dft), or occurrence lists when the trainer does not scan or the batch
+    // has a row the scan cannot take
     // (the flag posted beside the forward; reading it waits only for the
     // hit-mask pass, which runs early in the step).
     int32_t ft_gradient(const BatchPtrs& p, const FtGradArgs& fb) {
@@ -404,7 +408,9 @@ class LayerStackTrainer final : public TrainerBase {
         if (use_scan) {
             uint32_t multi = 0;
             if ((st = read_flag(multi))) return st;
-            if (!multi) return launch_ft_grad_scan(fb, block_scan(p), stream, false);
+            if (!multi)
+                return h_out ? launch_ft_grad_mfma(fb, block_scan(p), stream, false)
+                             : launch_ft_grad_scan(fb, block_scan(p), stream, false);
             if ((st = sort_occurrences(p, stream))) return st;
         }
         return launch_ft_grad_update(fb, stream);

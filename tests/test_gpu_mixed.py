@@ -64,11 +64,18 @@ def check_moments(t, st, prec, what, floor=1e-5):
                 close(got, exp, 1e-5, atol_frac=1e-5, what=f"{what} {name}.{k}")
 
 
-@pytest.mark.parametrize("mode", list(FLAGS))
-@pytest.mark.parametrize("factorize", [True, False], ids=["factorized", "plain"])
-def test_one_step_matches_oracle(gpu, mode, factorize):
+# ft_out 256: occurrence lists (sequential sums); 512 with a factorizer: the
+# block scan, or with an f16 dft its matrix-core form (f32 sums in the
+# matrix core's order, within the same 1e-3 gradient bar)
+CASES = [(m, f, 256) for m in FLAGS for f in (True, False)] + [("fp16_fwd_out", True, 512),
+                                                               ("all_optim", True, 512)]
+
+
+@pytest.mark.parametrize("mode,factorize,ft_out", CASES,
+                         ids=[f"{m}-{'factorized' if f else 'plain'}-{o}" for m, f, o in CASES])
+def test_one_step_matches_oracle(gpu, mode, factorize, ft_out):
     prec = FLAGS[mode]
-    sh, cfg = mixed(prec, factorize=factorize)
+    sh, cfg = mixed(prec, factorize=factorize, ft_out=ft_out)
     b = cfg.max_batch
     batch, bucket = batch_for(11, b, sh.nb)
     lr, lam, loss = 8.75e-4, 0.25, Sigmoid()
@@ -99,9 +106,10 @@ def test_one_step_matches_oracle(gpu, mode, factorize):
         assert clamps == 0
 
 
-def test_all_optim_seven_steps_with_lookahead(gpu):
+@pytest.mark.parametrize("ft_out", [256, 512])
+def test_all_optim_seven_steps_with_lookahead(gpu, ft_out):
     prec = ols.Precision.all_optim()
-    sh, cfg = mixed(prec)
+    sh, cfg = mixed(prec, ft_out=ft_out)
     b = cfg.max_batch
     st = oracle_state(sh, prec)
     opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)

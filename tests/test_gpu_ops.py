@@ -213,6 +213,95 @@ def test_ft_weight_grad_blocked_f16_bit_exact(gpu, bucketed):
     assert np.array_equal(g.to_host(), exp.astype(np.float32))
 
 
+def _exact_grad(vals, si, ni, nnz, cols):
+    """float64 sums of f16 values, with the sums of their magnitudes and the
+    occurrence counts.  Exact: binary16 values lie in [2^-24, 65504], so a
+    sum of a few thousand of them needs fewer than 53 significand bits."""
+    b, ft_out = vals.shape[1], vals.shape[2]
+    g = np.zeros((cols, ft_out))
+    a = np.zeros((cols, ft_out))
+    h = np.zeros(cols, np.int64)
+    for p, idx in ((0, si), (1, ni)):
+        for r in range(b):
+            f = idx[r, :nnz[r]]
+            f = f[(f >= 0) & (f < cols)]
+            np.add.at(g, f, vals[p, r].astype(np.float64))
+            np.add.at(a, f, np.abs(vals[p, r].astype(np.float64)))
+            np.add.at(h, f, 1)
+    return g, a, h
+
+
+@pytest.mark.parametrize("kb,pi,ma,b,ft_out", [(10, 64, 40, 256, 256), (45, 1629, 40, 1024, 512),
+                                               (81, 1548, 38, 512, 256), (7, 300, 12, 48, 200),
+                                               (3, 40, 8, 16, 64)])
+def test_ft_weight_grad_mfma_f16_within_summation_bound(gpu, kb, pi, ma, b, ft_out):
+    """The matrix-core gradient from an f16 dft: every cell is the f32 sum of
+    the same f16 values as the sequential sum, in the matrix core's order.
+    Bound per cell, against the exact (float64) sum S of its h values with
+    magnitude sum A:  |g - S inv| <= ((h + n_stages) 2^-23 A + 2^-24 |S|) inv,
+    n_stages = ceil(2b / 32) (one rounded f32 add per value and per 32-row
+    MFMA step, then the product with inv).  Values span the f16 range:
+    subnormals, +-65504 and zeros; the cells match the sequential f32 sum
+    within the same bound, and a planted mistake (one occurrence dropped)
+    breaks it."""
+    from tatara_amd.synthetic import small_spec, structured_batch, HALFKA_HM_MERGED, HALFKP
+    spec = {1629: HALFKA_HM_MERGED, 1548: HALFKP}.get(pi) or small_spec(king_buckets=kb, piece_inputs=pi,
+                                                                        max_active=ma)
+    batch, _ = structured_batch(b, spec, num_buckets=1, seed=pi + b + 1, nnz_min=ma // 2)
+    si, ni, nnz = batch.stm_indices, batch.nstm_indices, batch.nnz
+    cols = spec["ft_in"]
+    rng = np.random.default_rng(pi)
+    mag = np.exp2(rng.uniform(-24.0, 15.9, (2, b, ft_out)))
+    vals = (np.sign(rng.standard_normal((2, b, ft_out))) * mag).astype(np.float16)
+    vals[0, 0, :8] = np.float16(65504.0)
+    vals[1, 0, :8] = np.float16(-65504.0)
+    vals[0, 1, 8:16] = np.float16(2.0 ** -24)
+    vals[:, 2, :] = 0
+    inv = np.float32(1.0 / (16384.0 * b))
+    D, S, Nn, N = dev(vals.view(np.uint16)), dev(si), dev(ni), dev(nnz)
+    g = DeviceArray(np.full(cols * ft_out, 7.0, np.float32))
+    used = C.c_uint32(99)
+    check(gpu.tatara_op_ft_weight_grad_mfma_f16(D.ptr, C.c_float(inv), S.ptr, Nn.ptr, N.ptr, g.ptr, b, ft_out,
+                                                cols, ma, spec["piece_inputs"], C.byref(used)))
+    assert used.value == 1
+    got = g.to_host().reshape(cols, ft_out).astype(np.float64)
+    exact, absum, h = _exact_grad(vals, si, ni, nnz, cols)
+    n_stages = -(-2 * b // 32)
+    bound = ((h[:, None] + n_stages) * 2.0 ** -23 * absum + 2.0 ** -24 * np.abs(exact)) * float(inv)
+    err = np.abs(got - exact * float(inv))
+    assert np.all(err <= bound), f"worst {np.max(err / np.maximum(bound, 1e-300)):.3g} of the bound"
+    seq = _oracle_grad(vals.astype(np.float32), si, ni, nnz, b, ft_out, cols, ma).reshape(cols, ft_out)
+    seq = (seq * inv).astype(np.float64)
+    assert np.all(np.abs(got - seq) <= 2 * bound)
+    # a dropped occurrence is far outside the bound
+    f = int(si[3, 0])
+    assert np.any(np.abs(got[f] - (exact[f] - vals[0, 3].astype(np.float64)) * float(inv)) > 2 * bound[f])
+
+
+def test_ft_weight_grad_mfma_f16_falls_back_on_repeated_features(gpu):
+    """A feature twice in one row: the batch goes to the occurrence lists
+    (sequential sums, bit-exact with the oracle)."""
+    from tatara_amd.synthetic import small_spec, structured_batch
+    spec = small_spec(king_buckets=6, piece_inputs=96, max_active=24)
+    b, ma, ft_out = 96, 24, 512
+    batch, _ = structured_batch(b, spec, num_buckets=1, seed=5, nnz_min=4)
+    si, ni, nnz = batch.stm_indices.copy(), batch.nstm_indices.copy(), batch.nnz.copy()
+    nnz[:4] = ma
+    si[0, 5] = si[0, 0]
+    cols = spec["ft_in"]
+    rng = np.random.default_rng(12)
+    vals = (rng.standard_normal((2, b, ft_out)) * 3000.0).astype(np.float16)
+    inv = np.float32(1.0 / (16384.0 * b))
+    D, S, Nn, N = dev(vals.view(np.uint16)), dev(si), dev(ni), dev(nnz)
+    g = DeviceArray(np.full(cols * ft_out, 7.0, np.float32))
+    used = C.c_uint32(99)
+    check(gpu.tatara_op_ft_weight_grad_mfma_f16(D.ptr, C.c_float(inv), S.ptr, Nn.ptr, N.ptr, g.ptr, b, ft_out,
+                                                cols, ma, spec["piece_inputs"], C.byref(used)))
+    assert used.value == 0
+    exp = _oracle_grad(vals.astype(np.float32), si, ni, nnz, b, ft_out, cols, ma) * inv
+    assert np.array_equal(g.to_host(), exp.astype(np.float32))
+
+
 def test_fold_reduce_bit_exact(gpu):
     rng = np.random.default_rng(9)
     ft_in, ft_out, pi = 45 * 12, 256, 12
