@@ -54,7 +54,9 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane
 __global__ __launch_bounds__(kScanThreads) void binsort_scan_kernel(uint32_t* __restrict__ hist,
                                                                     uint32_t n_tiles, uint32_t n_bins,
                                                                     uint32_t* __restrict__ bin_start,
-                                                                    uint32_t* __restrict__ bin_count) {
+                                                                    uint32_t* __restrict__ bin_count,
+                                                                    const uint32_t* __restrict__ run_if) {
+    if (run_if && __builtin_amdgcn_readfirstlane(*run_if) == 0u) return;
     constexpr int W = kScanThreads / 64;
     __shared__ uint32_t wsum[W];
     const uint32_t b = blockIdx.x, t = threadIdx.x, lane = t % 64, wave = t / 64;
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(kScanThreads) void binsort_scan_kernel(uint32_t* __
     }
     if (t == 0) {
         bin_count[b] = carry;
-        if (n_tiles == 0) {  // no scatter runs: publish the empty bins here
+        if (n_tiles == 0 && bin_start) {  // no scatter runs: publish the empty bins here
             bin_start[b] = 0;
             if (b + 1 == n_bins) bin_start[n_bins] = 0;
         }
@@ -141,6 +143,78 @@ __global__ __launch_bounds__(kTile) void binsort_scatter_kernel(
     if (out_key) out_key[dst] = (int32_t)key;
 }
 
+// One LSD radix pass over (key, value) pairs: the stable counting sort of
+// the 8-bit digit (key >> shift) & 255, with the same tiles, scan and
+// ballot ranks as the bin sort above.  The kernels do nothing unless
+// *run_if != 0 (when run_if is set), and stride over the tiles with a
+// bounded grid, so a pass that is skipped costs little.
+__global__ __launch_bounds__(kTile) void radix_hist_kernel(const uint32_t* __restrict__ keys, uint32_t n_items,
+                                                           uint32_t shift, uint32_t n_tiles,
+                                                           uint32_t* __restrict__ hist,
+                                                           const uint32_t* __restrict__ run_if) {
+    if (run_if && __builtin_amdgcn_readfirstlane(*run_if) == 0u) return;
+    __shared__ uint32_t h[kMaxBins];
+    const uint32_t t = threadIdx.x;
+    for (uint32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        if (t < (uint32_t)kMaxBins) h[t] = 0;
+        __syncthreads();
+        const uint64_t item = (uint64_t)tile * kTile + t;
+        if (item < n_items) atomicAdd(&h[(keys[item] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (t < (uint32_t)kMaxBins) hist[(uint64_t)t * n_tiles + tile] = h[t];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(kTile) void radix_scatter_kernel(
+    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals, uint32_t n_items, uint32_t shift,
+    uint32_t n_tiles, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ bin_count,
+    uint32_t* __restrict__ out_keys, uint32_t* __restrict__ out_vals, const uint32_t* __restrict__ run_if) {
+    if (run_if && __builtin_amdgcn_readfirstlane(*run_if) == 0u) return;
+    __shared__ uint32_t wcnt[kWaves][kMaxBins];
+    __shared__ uint32_t s_start[kMaxBins];
+    __shared__ uint32_t s_wtot[kMaxBins / 64];
+    const uint32_t t = threadIdx.x;
+    const uint32_t wave = t / 64, lane = t % 64;
+    uint32_t cnt = 0, incl = 0;
+    if (t < (uint32_t)kMaxBins) {  // digit starts: exclusive prefix of the digit sizes
+        cnt = bin_count[t];
+        incl = wave_inclusive_sum(cnt, lane);
+        if (lane == 63) s_wtot[wave] = incl;
+    }
+    __syncthreads();
+    if (t < (uint32_t)kMaxBins) {
+        uint32_t before = 0;
+        for (uint32_t w = 0; w < wave; ++w) before += s_wtot[w];
+        s_start[t] = before + incl - cnt;
+    }
+    for (uint32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        for (uint32_t i = t; i < kWaves * kMaxBins; i += kTile) (&wcnt[0][0])[i] = 0;
+        __syncthreads();
+        const uint64_t item = (uint64_t)tile * kTile + t;
+        const bool ok = item < n_items;
+        const uint32_t key = ok ? keys[item] : 0u;
+        const uint32_t dig = ok ? (key >> shift) & 255u : 0xFFFFFFFFu;
+        uint64_t match = __ballot(ok);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+            const uint64_t bal = __ballot(ok && ((dig >> bit) & 1u));
+            match &= ((dig >> bit) & 1u) ? bal : ~bal;
+        }
+        const uint32_t rank = __popcll(match & ((1ull << lane) - 1ull));
+        if (ok && (match >> lane) == 1ull) wcnt[wave][dig] = __popcll(match);
+        __syncthreads();
+        if (ok) {
+            uint32_t before = 0;
+            for (uint32_t w = 0; w < wave; ++w) before += wcnt[w][dig];
+            const uint32_t dst = s_start[dig] + offsets[(uint64_t)dig * n_tiles + tile] + before + rank;
+            out_keys[dst] = key;
+            out_vals[dst] = vals[item];
+        }
+        __syncthreads();
+    }
+}
+
 __global__ void fill_i32_kernel(int32_t* __restrict__ p, uint64_t n, int32_t v) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -154,6 +228,23 @@ int32_t launch_fill_i32(int32_t* p, uint64_t n, int32_t v, hipStream_t stream) {
     if (n == 0) return kOk;
     fill_i32_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(p, n, v);
     TATARA_LAUNCHED("fill_i32");
+    return kOk;
+}
+
+int32_t launch_radix_pass(const RadixPassArgs& a, hipStream_t stream) {
+    TATARA_REQUIRE(a.shift < 32, "radix pass: shift < 32");
+    const uint32_t tiles = binsort_tiles(a.n_items);
+    if (tiles == 0) return kOk;
+    // a gated pass strides over a bounded grid
+    const uint32_t grid = a.run_if && tiles > 1024u ? 1024u : tiles;
+    radix_hist_kernel<<<grid, kTile, 0, stream>>>(a.keys, a.n_items, a.shift, tiles, a.hist, a.run_if);
+    TATARA_LAUNCHED("radix_hist");
+    binsort_scan_kernel<<<kMaxBins, kScanThreads, 0, stream>>>(a.hist, tiles, kMaxBins, nullptr, a.digit_count,
+                                                               a.run_if);
+    TATARA_LAUNCHED("radix_scan");
+    radix_scatter_kernel<<<grid, kTile, 0, stream>>>(a.keys, a.vals, a.n_items, a.shift, tiles, a.hist,
+                                                     a.digit_count, a.out_keys, a.out_vals, a.run_if);
+    TATARA_LAUNCHED("radix_scatter");
     return kOk;
 }
 
@@ -173,14 +264,14 @@ int32_t launch_binsort(const BinSortArgs& a, hipStream_t stream) {
     if (tiles == 0) {
         // still publish empty bin boundaries
         binsort_scan_kernel<<<a.n_bins, kScanThreads, 0, stream>>>(a.hist, 0, a.n_bins, a.bin_start,
-                                                                   a.bin_count);
+                                                                   a.bin_count, nullptr);
         TATARA_LAUNCHED("binsort_scan");
         return kOk;
     }
     binsort_hist_kernel<<<tiles, kTile, 0, stream>>>(a.keys, a.n_items, a.n_bins, a.hist);
     TATARA_LAUNCHED("binsort_hist");
     binsort_scan_kernel<<<a.n_bins, kScanThreads, 0, stream>>>(a.hist, tiles, a.n_bins, a.bin_start,
-                                                               a.bin_count);
+                                                               a.bin_count, nullptr);
     TATARA_LAUNCHED("binsort_scan");
     binsort_scatter_kernel<<<tiles, kTile, 0, stream>>>(a.keys, a.n_items, a.n_bins, a.align, a.hist,
                                                        a.bin_count, a.value_mod, a.out, a.out_key,

@@ -21,7 +21,23 @@ struct BinSortArgs {
     uint64_t out_fill_len; // number of out slots pre-filled with -1 (0: none)
 };
 
+// One stable LSD radix pass (8-bit digit (key >> shift) & 255) over
+// (key, value) pairs.  With run_if set, every kernel of the pass does
+// nothing unless *run_if != 0.
+struct RadixPassArgs {
+    const uint32_t* keys;
+    const uint32_t* vals;
+    uint32_t n_items;
+    uint32_t shift;
+    uint32_t* hist;          // scratch [256 * binsort_tiles(n_items)]
+    uint32_t* digit_count;   // scratch [256]
+    uint32_t* out_keys;
+    uint32_t* out_vals;
+    const uint32_t* run_if;  // optional device gate
+};
+
 uint32_t binsort_tiles(uint32_t n_items);
+int32_t launch_radix_pass(const RadixPassArgs& a, hipStream_t stream);
 int32_t launch_binsort(const BinSortArgs& a, hipStream_t stream);
 int32_t launch_fill_i32(int32_t* p, uint64_t n, int32_t v, hipStream_t stream);
 

@@ -17,6 +17,7 @@
 
 #include <hipcub/hipcub.hpp>
 #include <type_traits>
+#include <utility>
 
 #include "binsort.hpp"
 #include "common.hpp"
@@ -374,19 +375,22 @@ __global__ void build_occurrence_keys_kernel(const int32_t* __restrict__ idx_stm
                                              const int32_t* __restrict__ nnz,
                                              uint32_t* __restrict__ keys,
                                              uint32_t* __restrict__ vals, uint32_t batch,
-                                             uint32_t max_active, uint32_t cols) {
+                                             uint32_t max_active, uint32_t cols,
+                                             const uint32_t* __restrict__ run_if) {
+    if (run_if && __builtin_amdgcn_readfirstlane(*run_if) == 0u) return;
     const uint64_t per = (uint64_t)batch * max_active;
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= 2 * per) return;
-    const uint32_t persp = i >= per ? 1u : 0u;
-    const uint64_t j = i - persp * per;
-    const uint32_t b = (uint32_t)(j / max_active);
-    const uint32_t slot = (uint32_t)(j - (uint64_t)b * max_active);
-    const int32_t v = (persp ? idx_nstm : idx_stm)[j];
-    const bool ok = (int)slot < nnz[b] && v >= 0 && (uint32_t)v < cols;
-    const uint32_t key = ok ? 2u * (uint32_t)v + persp : 2u * cols;
-    keys[i] = key;
-    vals[i] = persp * batch + b;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * per;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t persp = i >= per ? 1u : 0u;
+        const uint64_t j = i - persp * per;
+        const uint32_t b = (uint32_t)(j / max_active);
+        const uint32_t slot = (uint32_t)(j - (uint64_t)b * max_active);
+        const int32_t v = (persp ? idx_nstm : idx_stm)[j];
+        const bool ok = (int)slot < nnz[b] && v >= 0 && (uint32_t)v < cols;
+        const uint32_t key = ok ? 2u * (uint32_t)v + persp : 2u * cols;
+        keys[i] = key;
+        vals[i] = persp * batch + b;
+    }
 }
 
 // Segment offsets from the sorted keys: offsets[k] = first sorted position
@@ -395,12 +399,15 @@ __global__ void build_occurrence_keys_kernel(const int32_t* __restrict__ idx_stm
 // no histogram, atomics or scan are needed.
 __global__ void occurrence_offsets_kernel(const uint32_t* __restrict__ sorted_keys,
                                           uint64_t n_items, uint32_t n_keys,
-                                          uint32_t* __restrict__ offsets) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i > n_items) return;
-    const int64_t prev = i == 0 ? -1 : (int64_t)sorted_keys[i - 1];
-    const int64_t cur = i == n_items ? (int64_t)n_keys : (int64_t)sorted_keys[i];
-    for (int64_t k = prev + 1; k <= cur; ++k) offsets[k] = (uint32_t)i;
+                                          uint32_t* __restrict__ offsets,
+                                          const uint32_t* __restrict__ run_if) {
+    if (run_if && __builtin_amdgcn_readfirstlane(*run_if) == 0u) return;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i <= n_items;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const int64_t prev = i == 0 ? -1 : (int64_t)sorted_keys[i - 1];
+        const int64_t cur = i == n_items ? (int64_t)n_keys : (int64_t)sorted_keys[i];
+        for (int64_t k = prev + 1; k <= cur; ++k) offsets[k] = (uint32_t)i;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1388,18 +1395,55 @@ size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols) {
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) {
     const uint64_t n_items = 2ull * a.batch * a.max_active;
     const uint32_t n_keys = 2 * a.cols + 1;  // keys 0..2*cols (2*cols = invalid slot)
-    if (n_items > 0) {
-        build_occurrence_keys_kernel<<<ceil_div(n_items, 256), 256, 0, stream>>>(
-            a.idx_stm, a.idx_nstm, a.nnz, a.keys_in, a.vals_in, a.batch, a.max_active, a.cols);
+    TATARA_REQUIRE(n_items <= 0xFFFFFFFFull, "occurrence sort: at most 2^32 - 1 slots");
+    // a gated sort strides over bounded grids, so skipping it costs little
+    auto grid = [&](uint64_t n) -> uint32_t {
+        const uint64_t g = ceil_div(n, 256);
+        return (uint32_t)(a.run_if && g > 2048 ? 2048 : g);
+    };
+    if (!a.run_if) {
+        if (n_items > 0) {
+            build_occurrence_keys_kernel<<<grid(n_items), 256, 0, stream>>>(
+                a.idx_stm, a.idx_nstm, a.nnz, a.keys_in, a.vals_in, a.batch, a.max_active, a.cols, nullptr);
+            TATARA_LAUNCHED("build_occurrence_keys");
+            size_t bytes = a.temp_bytes;
+            TATARA_HIP(hipcub::DeviceRadixSort::SortPairs(a.temp, bytes, a.keys_in, a.keys_out,
+                                                          a.vals_in, a.vals_out, (int)n_items, 0,
+                                                          (int)occurrence_key_bits(a.cols), stream),
+                       "occurrence radix sort");
+        }
+    } else if (n_items > 0) {
+        // device-gated: stable LSD passes of 8 bits, alternating between the
+        // two buffer pairs and ending in keys_out / vals_out
+        TATARA_REQUIRE(a.radix_hist && a.radix_count, "gated occurrence sort: radix scratch");
+        const uint32_t passes = (occurrence_key_bits(a.cols) + 7) / 8;
+        uint32_t *k0 = a.keys_in, *v0 = a.vals_in, *k1 = a.keys_out, *v1 = a.vals_out;
+        if (passes % 2 == 0) {
+            std::swap(k0, k1);
+            std::swap(v0, v1);
+        }
+        build_occurrence_keys_kernel<<<grid(n_items), 256, 0, stream>>>(a.idx_stm, a.idx_nstm, a.nnz, k0, v0,
+                                                                       a.batch, a.max_active, a.cols, a.run_if);
         TATARA_LAUNCHED("build_occurrence_keys");
-        size_t bytes = a.temp_bytes;
-        TATARA_HIP(hipcub::DeviceRadixSort::SortPairs(a.temp, bytes, a.keys_in, a.keys_out,
-                                                      a.vals_in, a.vals_out, (int)n_items, 0,
-                                                      (int)occurrence_key_bits(a.cols), stream),
-                   "occurrence radix sort");
+        for (uint32_t p = 0; p < passes; ++p) {
+            RadixPassArgs r{};
+            r.keys = k0;
+            r.vals = v0;
+            r.n_items = (uint32_t)n_items;
+            r.shift = 8 * p;
+            r.hist = a.radix_hist;
+            r.digit_count = a.radix_count;
+            r.out_keys = k1;
+            r.out_vals = v1;
+            r.run_if = a.run_if;
+            int32_t st = launch_radix_pass(r, stream);
+            if (st) return st;
+            std::swap(k0, k1);
+            std::swap(v0, v1);
+        }
     }
-    occurrence_offsets_kernel<<<ceil_div(n_items + 1, 256), 256, 0, stream>>>(a.keys_out, n_items,
-                                                                              n_keys, a.offsets);
+    occurrence_offsets_kernel<<<grid(n_items + 1), 256, 0, stream>>>(a.keys_out, n_items, n_keys, a.offsets,
+                                                                     a.run_if);
     TATARA_LAUNCHED("occurrence_offsets");
     return kOk;
 }

@@ -42,8 +42,15 @@ struct OccurrenceSortArgs {
     uint32_t* keys_out;
     uint32_t* vals_out;  // sorted dft row ids
     uint32_t* offsets;   // [2*cols + 2]; key k occupies [offsets[k], offsets[k+1])
-    void* temp;
+    void* temp;          // radix-sort scratch (ungated sort)
     size_t temp_bytes;
+    // Device gate: when set, the sort runs only if *run_if != 0 (stable LSD
+    // passes of the bin-sort kernels, scratch radix_hist [256 *
+    // binsort_tiles(2*batch*max_active)] and radix_count [256]), so a step
+    // can queue it without the host learning whether it is needed.
+    const uint32_t* run_if;
+    uint32_t* radix_hist;
+    uint32_t* radix_count;
 };
 
 struct FtGradArgs {

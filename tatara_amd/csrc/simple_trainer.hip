@@ -56,6 +56,7 @@ class SimpleTrainer final : public TrainerBase {
     uint32_t* occ_off = nullptr;
     void* occ_tmp = nullptr;
     size_t occ_tmp_bytes = 0;
+    uint32_t *radix_hist = nullptr, *radix_count = nullptr;  // the gated occurrence sort's scratch
     // block-scan FT backward (factorized feature sets)
     bool use_scan = false;
     uint32_t *scan_masks = nullptr, *scan_multi = nullptr;
@@ -156,7 +157,9 @@ class SimpleTrainer final : public TrainerBase {
             return st;
         use_scan = factorized && ft_out >= kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
-                         (st = arena.alloc(&scan_multi, 1))))
+                         (st = arena.alloc(&scan_multi, 1)) ||
+                         (st = arena.alloc(&radix_hist, 256ull * binsort_tiles((uint32_t)n_items), false)) ||
+                         (st = arena.alloc(&radix_count, 256))))
             return st;
         if ((st = arena.alloc(&ft_stm, B * ft_out, false)) || (st = arena.alloc(&ft_nstm, B * ft_out, false)) ||
             (st = arena.alloc(&combined, B * K, false)) || (st = arena.alloc(&dft, 2 * B * dft_chunks() * kDftChunk, false)) ||
@@ -282,7 +285,8 @@ class SimpleTrainer final : public TrainerBase {
     }
 
     // Occurrence lists of the batch (key 2*feature + perspective).
-    int32_t sort_occurrences(const BatchPtrs& p, hipStream_t s) {
+    // gated: the sort runs only if the hit-mask pass set scan_multi
+    int32_t sort_occurrences(const BatchPtrs& p, hipStream_t s, bool gated = false) {
         OccurrenceSortArgs os{};
         os.idx_stm = p.stm;
         os.idx_nstm = p.nstm;
@@ -297,19 +301,20 @@ class SimpleTrainer final : public TrainerBase {
         os.offsets = occ_off;
         os.temp = occ_tmp;
         os.temp_bytes = occ_tmp_bytes;
+        if (gated) {
+            os.run_if = scan_multi;
+            os.radix_hist = radix_hist;
+            os.radix_count = radix_count;
+        }
         return launch_occurrence_sort(os, s);
     }
 
-    // FT gradient + update: the block scan, or occurrence lists when the
-    // trainer does not scan or the batch has a row the scan cannot take.
+    // FT gradient + update: the block scan and, gated on the device by the
+    // flag of the hit-mask pass, the occurrence-list kernel for a batch with
+    // a row the scan cannot take; or occurrence lists every step when the
+    // trainer does not scan.
     int32_t ft_gradient(const BatchPtrs& p, const FtGradArgs& fb) {
-        int32_t st;
-        if (use_scan) {
-            uint32_t multi = 0;
-            if ((st = read_flag(multi))) return st;
-            if (!multi) return launch_ft_grad_scan(fb, block_scan(p), stream, false);
-            if ((st = sort_occurrences(p, stream))) return st;
-        }
+        if (use_scan) return launch_ft_grad_scan(fb, block_scan(p), stream, true);
         return launch_ft_grad_update(fb, stream);
     }
 
@@ -359,11 +364,13 @@ class SimpleTrainer final : public TrainerBase {
             if ((st = launch_binsort(bs, stream))) return st;
             sched = schedule;
             if (train && use_scan) {
-                // hit masks of the block-scan backward, beside the forward;
-                // the host learns whether the batch needs occurrence lists
+                // hit masks of the block-scan backward, beside the forward,
+                // then the occurrence sort, which runs only when a row has
+                // features of two king blocks or one feature twice (the
+                // mask pass sets scan_multi); no host wait
                 if ((st = fork_side())) return st;
                 if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
-                if ((st = post_flag(scan_multi, side))) return st;
+                if ((st = sort_occurrences(p, side, true))) return st;
             }
         }
         if (train && (st = prof_mark(1))) return st;

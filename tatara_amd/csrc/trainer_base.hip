@@ -33,8 +33,6 @@ TrainerBase::~TrainerBase() {
     if (ev_fork) (void)hipEventDestroy(ev_fork);
     if (ev_join) (void)hipEventDestroy(ev_join);
     if (pinned_loss) (void)hipHostFree(pinned_loss);
-    if (ev_flag) (void)hipEventDestroy(ev_flag);
-    if (pinned_flag) (void)hipHostFree(pinned_flag);
     if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamDestroy(stream);
 }
@@ -49,25 +47,11 @@ int32_t TrainerBase::init_runtime(int device) {
     TATARA_HIP(hipEventCreateWithFlags(&loss_ev[1], hipEventDisableTiming), "hipEventCreate");
     TATARA_HIP(hipHostMalloc((void**)&pinned_loss, 2 * sizeof(double), hipHostMallocDefault),
                "hipHostMalloc loss ring");
-    TATARA_HIP(hipEventCreateWithFlags(&ev_flag, hipEventDisableTiming), "hipEventCreate");
-    TATARA_HIP(hipHostMalloc((void**)&pinned_flag, sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc flag");
     TATARA_HIP(hipStreamCreateWithFlags(&copy_stream, hipStreamNonBlocking), "hipStreamCreate (copy)");
     for (int s = 0; s < kRingSlots; ++s) {
         TATARA_HIP(hipEventCreateWithFlags(&ring_copied[s], hipEventDisableTiming), "hipEventCreate");
         TATARA_HIP(hipEventCreateWithFlags(&ring_consumed[s], hipEventDisableTiming), "hipEventCreate");
     }
-    return kOk;
-}
-
-int32_t TrainerBase::post_flag(const uint32_t* dev_flag, hipStream_t s) {
-    TATARA_HIP(hipMemcpyAsync(pinned_flag, dev_flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s), "flag copy");
-    TATARA_HIP(hipEventRecord(ev_flag, s), "hipEventRecord (flag)");
-    return kOk;
-}
-
-int32_t TrainerBase::read_flag(uint32_t& value) {
-    TATARA_HIP(hipEventSynchronize(ev_flag), "hipEventSynchronize (flag)");
-    value = *pinned_flag;
     return kOk;
 }
 

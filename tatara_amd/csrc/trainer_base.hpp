@@ -134,15 +134,8 @@ class TrainerBase {
     // phase profiling: kPhases + 1 events per profiled step
     std::vector<hipEvent_t> prof_events;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-    // a device flag copied to pinned host memory (post_flag / read_flag)
-    uint32_t* pinned_flag = nullptr;
-    hipEvent_t ev_flag = nullptr;
 
     int32_t init_runtime(int device);
-    // Queues a copy of *dev_flag to the host on stream s; read_flag waits
-    // for it and returns the value.
-    int32_t post_flag(const uint32_t* dev_flag, hipStream_t s);
-    int32_t read_flag(uint32_t& value);
     int32_t alloc_inputs(uint64_t max_b, uint32_t max_active);
     int32_t alloc_group(ParamGroup& g, const char* name, uint64_t n, float mn, float mx, int kind,
                         bool with_grad, bool f16_moments = false);

@@ -18,11 +18,18 @@ Bars:
     per occurrence in its gradient, which is several percent of a tiny
     moment and accumulates over steps;
   - the dft clamp counter: equal to the oracle's count up to the values that
-    sit within 1e-5 of the clamp threshold.
+    sit within 1e-5 of the clamp threshold;
+  - with an f16 dft the ft_w gradient is also allowed 2^-11 A (A the
+    cell's sum of |dft| over its h occurrences: each value may sit one f16
+    step from the oracle's), and the matrix-core FT backward (king-bucketed
+    rows, ft_out >= 512), which sums each cell in another order than the
+    oracle, another (h + n_stages + 2) 2^-23 A; the f16 moments inherit that
+    gradient bound through (1 - beta1) and (1 - beta2) (2 |g| + bound).
 """
 import numpy as np
 import pytest
 
+from oracle import ffi
 from oracle import layerstack as ols
 from tatara_amd.trainer import GROUPS, LayerStackTrainer, Sigmoid
 
@@ -53,13 +60,47 @@ def oracle_state(sh, prec):
     return ols.to_f16_state(st) if prec.fp16_opt_state else st
 
 
-def check_moments(t, st, prec, what, floor=1e-5):
+def f16_grad_bound(sh, batch, a, b, mfma):
+    """Per-cell bound on the ft_w gradient's difference from the oracle with
+    an f16 dft: 2^-11 A (each of the cell's dft values may sit one f16 step
+    from the oracle's, the dense backward upstream being within 1e-5), plus
+    (h + n_stages + 2) 2^-23 A when the trainer sums on the matrix cores
+    (another order than the oracle's sequential sum); A is the cell's sum of
+    |dft16| / scale over its h occurrences and n_stages the 64-row MFMA
+    stages of a king block (at most ceil(2b / 64)); virtual rows sum their
+    real rows' bounds."""
+    inv = float(1.0 / a["dft_scale"])
+    A = np.zeros(sh.train_ft_in * sh.ft_out, np.float32)
+    h = np.zeros(sh.train_ft_in * sh.ft_out, np.float32)
+    for k, idx in (("dft_stm16", "stm"), ("dft_nstm16", "nstm")):
+        mag = np.abs(a[k].astype(np.float32))
+        ffi.ft_grad_fp16(mag, batch[idx], batch["nnz"], A, b, sh.ft_out, sh.ft_in, sh.max_active, inv,
+                         add=idx == "nstm")
+        ffi.ft_grad_fp16(np.ones_like(mag), batch[idx], batch["nnz"], h, b, sh.ft_out, sh.ft_in, sh.max_active,
+                         1.0, add=idx == "nstm")
+    if sh.piece_inputs:
+        ffi.ft_reduce_virtual_grad(A, sh.ft_in, sh.ft_out, sh.piece_inputs)
+        ffi.ft_reduce_virtual_grad(h, sh.ft_in, sh.ft_out, sh.piece_inputs)
+    n_stages = -(-2 * b // 64)
+    order = (h.astype(np.float64) + n_stages + 2) * 2.0 ** -23 if mfma else 0.0
+    return (2.0 ** -11 + order) * A.astype(np.float64)
+
+
+def check_moments(t, st, prec, what, floor=1e-5, g=None, g_bound=None, opt=None):
+    """f16 ft_w moments within one f16 step; with g_bound (the ft_w gradient's
+    own bound, g the oracle gradient) the moments also inherit it: m through
+    (1 - beta1), v through (1 - beta2) (2 |g| + g_bound)."""
     for name in GROUPS:
         for k in ("m", "v"):
             got, exp = t.get(name, k), st[name][k]
             if name == "ft_w" and prec.fp16_opt_state:
                 scale = ols.M_SCALE if k == "m" else ols.V_SCALE
-                close(got, exp, 2e-3, atol=SUB16 / float(scale), atol_frac=floor, what=f"{what} {name}.{k} (f16)")
+                extra = 0.0
+                if g_bound is not None:
+                    extra = ((1 - opt.beta1) * g_bound if k == "m"
+                             else (1 - ols.BETA2) * (2 * np.abs(g) + g_bound) * g_bound)
+                close(got, exp, 2e-3, atol=SUB16 / float(scale) + extra, atol_frac=floor,
+                      what=f"{what} {name}.{k} (f16)")
             else:
                 close(got, exp, 1e-5, atol_frac=1e-5, what=f"{what} {name}.{k}")
 
@@ -95,11 +136,13 @@ def test_one_step_matches_oracle(gpu, mode, factorize, ft_out):
             else:
                 dmax = max(np.abs(a[k]).max(), 1e-30)
                 close(t.activation(k, bf), a[k], 1e-4, atol=1e-5 * dmax, what=k)
+        bd = as_dict(batch, bucket)
+        gb = f16_grad_bound(sh, bd, a, b, mfma=factorize and ft_out >= 512) if prec.ft_fp16_out else None
         close(t.get("ft_w", "grad"), g["ft_w"], 1e-3 if prec.ft_fp16_out else 1e-4, atol_frac=1e-5,
-              what="grad ft_w")
+              atol=gb if gb is not None else 0.0, what="grad ft_w")
         for name in GROUPS:
             close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"{name}.w")
-        check_moments(t, st, prec, "step 1")
+        check_moments(t, st, prec, "step 1", g=g["ft_w"], g_bound=gb, opt=opt)
         close([t.flush_pending_loss()], [acc], 1e-6, what="loss")
         clamps, elems = t.fp16_clamp_count()
         assert elems == (2 * b * sh.ft_out if prec.ft_fp16_out else 0)
@@ -130,6 +173,36 @@ def test_all_optim_seven_steps_with_lookahead(gpu, ft_out):
             close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"{name}.w after 7 steps")
             close(t.get(name, "slow"), st[name]["slow"], 1e-5, atol=1e-6, what=f"{name}.slow")
         check_moments(t, st, prec, "step 7", floor=1e-4)
+
+
+def test_all_optim_rows_across_king_blocks(gpu):
+    """Mixed precision with ft_out 512 (the matrix-core FT backward): a batch
+    with features of several king blocks in a row and a repeated feature is
+    flagged on the device and takes the gated occurrence sort and the f16
+    occurrence-list kernel; the next batch takes the matrix cores again."""
+    from tatara_amd.trainer import Batch
+    prec = ols.Precision.all_optim()
+    sh, cfg = mixed(prec, ft_out=512)
+    b = cfg.max_batch
+    rng = np.random.default_rng(23)
+    batch, bucket = batch_for(12, b, sh.nb)
+    stm = batch.stm_indices.copy()
+    stm[:, 0] = rng.integers(0, sh.ft_in, b)
+    nstm = batch.nstm_indices.copy()
+    nstm[5, 3] = nstm[5, 2]
+    cross = Batch(stm, nstm, batch.nnz, batch.score, batch.wdl)
+    st = oracle_state(sh, prec)
+    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+    with LayerStackTrainer(cfg) as t:
+        for step, (bt, bk) in enumerate([(cross, bucket), batch_for(13, b, sh.nb)], start=1):
+            t.train_step(bt, bk, 1e-3, 0.0, Sigmoid())
+            bd = as_dict(bt, bk)
+            _, a, g = ols.train_step(sh, st, bd, opt, 1e-3, 0.0, loss_dict(Sigmoid()), step, prec)
+            for name in ("ft_w", "ft_b"):
+                close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"step {step} {name}.w")
+            # step 1: occurrence lists (sequential sums, as the oracle); step 2: matrix cores
+            gb = f16_grad_bound(sh, bd, a, b, mfma=step == 2)
+            check_moments(t, st, prec, f"step {step}", g=g["ft_w"], g_bound=gb, opt=opt)
 
 
 def test_dft_clamp_counter(gpu):

@@ -130,6 +130,33 @@ def test_multi_step_ranger_with_lookahead(gpu, ft_out):
             close(t.get(name, "slow"), st[name]["slow"], 1e-5, atol=1e-6, what=f"{name}.slow")
 
 
+def test_rows_across_king_blocks_and_repeated_features(gpu):
+    """Index rows with features of several king blocks or a repeated feature:
+    the hit-mask pass flags the batch on the device, the gated occurrence
+    sort and occurrence-list kernel run instead of the block scan, and the
+    step still matches the oracle; the next king-bucketed batch takes the
+    block scan again (ft_out 256)."""
+    from tatara_amd.trainer import Batch
+    sh, cfg = make(optimizer="ranger", ft_out=256)
+    b = cfg.max_batch
+    rng = np.random.default_rng(22)
+    batch = batch_for(4, b)
+    stm = batch.stm_indices.copy()
+    stm[:, 0] = rng.integers(0, sh.ft_in, b)  # first slot from any block
+    nstm = batch.nstm_indices.copy()
+    nstm[7, 3] = nstm[7, 2]                   # a repeated feature
+    mixed = Batch(stm, nstm, batch.nnz, batch.score, batch.wdl)
+    st = osi.default_init(sh)
+    opt = osi.OptConfig(optimizer="ranger", weight_decay=0.01)
+    with SimpleTrainer(cfg) as t:
+        for step, bt in enumerate([mixed, batch_for(5, b), mixed], start=1):
+            t.train_step(bt, 1e-3, 0.0, WRM290)
+            osi.train_step(sh, st, as_dict(bt), opt, 1e-3, 0.0, loss_dict(WRM290), step)
+            for k in ("w", "m", "v"):
+                close(t.get("ft_w", k), st["ft_w"][k], 1e-5, atol=1e-6 if k == "w" else 0.0,
+                      atol_frac=1e-5 if k != "w" else 0.0, what=f"step {step} ft_w.{k}")
+
+
 def test_unfactorized_l1_16_ragged_batch(gpu):
     """No factorizer, l1 = 16, RAdam, and a batch that is not a multiple of 16."""
     sh, cfg = make(factorize=False, l1=16, optimizer="radam", ft_out=64, b=256)
