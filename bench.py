@@ -677,8 +677,10 @@ def main() -> int:
     # else from occurrence lists
     fwd_kernel = "ft_forward_pair16_kernel" if f16 else "ft_forward_kernel"
     min_scan_cols = 256 if w["arch"] == "simple" else 512
-    scan = not f16 and w["ft_out"] >= min_scan_cols
-    grad_kernel = "ft_grad_scan_kernel" if scan else "ft_grad_update_kernel"
+    # the block scan (f32 dft) or its matrix-core form (f16 dft) takes every
+    # king-bucketed batch from min_scan_cols columns up
+    scan = w["ft_out"] >= min_scan_cols
+    grad_kernel = ("ft_grad_mfma_kernel" if f16 else "ft_grad_scan_kernel") if scan else "ft_grad_update_kernel"
     comp = compulsory_bytes(w, spec, b, scan, la)
     step_bytes = sum(comp.values())
     step_frac = step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS

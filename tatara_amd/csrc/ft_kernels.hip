@@ -938,11 +938,13 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
 // multiplies a finite value unless a row of the block holds a NaN (which
 // then reaches every feature of its tile, not only the row's own).
 //
-// Workgroups take (block, chunk, feature group) triples in the block scan's
-// order.  Wave w of the four owns 32 features of the group (mask words 2w,
-// 2w+1) and all 256 columns of the chunk: 2 x 16 tiles of 16 x 16, 128 f32
-// accumulators per lane.  The rows go through LDS in stages of 64: wave w
-// loads rows 16w..16w+15 (four columns per lane), transposes them in
+// Workgroups take (block, chunk, feature group, column half) in the block
+// scan's order (the two halves of a chunk next to each other).  Wave w of
+// the four owns 32 features of the group (mask words 2w, 2w+1) and the 128
+// columns of the half: 2 x 8 tiles of 16 x 16, 64 f32 accumulators per lane
+// (three waves per SIMD; 128 accumulators and 256 columns allow two, and
+// measured 3% slower).  The rows go through LDS in stages of 64: wave w
+// loads rows 16w..16w+15 (two columns per lane), transposes them in
 // registers and writes them by
 // column, so the B operand of a lane (8 rows of one column) is one 16-byte
 // read; the stage's mask words sit beside them and the A operand (8 rows of
@@ -955,12 +957,13 @@ constexpr int kMfmaRows = 64;  // rows per stage: two MFMA steps
 // A stage's rows in LDS: 16-byte slots of (column, row octet), each holding
 // that column's 8 rows.  Columns come in groups of 8 (octet-major, then
 // column); within an octet the 8 columns are rotated by the group index, so
-// the slots a wave writes (lanes 4 columns apart) and the slots it reads (8
+// the slots a wave writes (lanes 2 columns apart) and the slots it reads (8
 // consecutive columns per 8 lanes) fall in 8 distinct bank groups.
+constexpr int kMfmaCols = 128;  // columns per workgroup (half a dft chunk)
 __device__ __forceinline__ uint32_t stage_slot(uint32_t col, uint32_t oct) {
     return (col >> 3) * (uint32_t)kMfmaRows + oct * 8 + ((col + (col >> 3)) & 7u);
 }
-constexpr int kMfmaStageHalves = kDftChunk * kMfmaRows;  // 32 KB per buffer
+constexpr int kMfmaStageHalves = kMfmaCols * kMfmaRows;  // 16 KB per buffer
 constexpr int kMfmaUpdRow = 132;                         // floats per update row (128 + padding)
 // the update reuses the stage buffers: 8 waves x 16 rows of kMfmaUpdRow floats
 constexpr int kMfmaLdsHalves = kMfmaWaves * 16 * kMfmaUpdRow * 2 > 2 * kMfmaStageHalves
@@ -1015,8 +1018,9 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     // groups of a pair next to each other (as the block scan)
     const uint32_t n_chunks = (a.ft_out + kDftChunk - 1) / kDftChunk;
     const uint32_t xcd = blockIdx.x % kNumXcd, i_xcd = blockIdx.x / kNumXcd;
-    const uint32_t g = i_xcd % geom.n_groups;
-    const uint32_t pair = (i_xcd / geom.n_groups) * kNumXcd + xcd;
+    const uint32_t sub = i_xcd % (2 * geom.n_groups);
+    const uint32_t g = sub >> 1, half = sub & 1u;
+    const uint32_t pair = (i_xcd / (2 * geom.n_groups)) * kNumXcd + xcd;
     if (pair >= s.n_blocks * n_chunks) return;
     const uint32_t K = block_of_rank(s, pair / n_chunks, lane), chunk = pair % n_chunks;
     const uint32_t PI = s.piece_inputs;
@@ -1029,7 +1033,8 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
         j = j < n ? j : n - 1;
         return j < na ? a0 + j : b0 + (j - na);
     };
-    const _Float16* d16 = reinterpret_cast<const _Float16*>(a.dft16) + (uint64_t)chunk * a.dft_chunk_stride;
+    const _Float16* d16 =
+        reinterpret_cast<const _Float16*>(a.dft16) + (uint64_t)chunk * a.dft_chunk_stride + half * kMfmaCols;
     // thread t stages mask word t / 32 of rows t % 32 + 32k
     const uint32_t mw = threadIdx.x / 32, mr = threadIdx.x % 32;
     const uint32_t* mplane = s.masks + (uint64_t)(g * kScanWaves + mw) * (2ull * s.batch);
@@ -1043,7 +1048,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     // stage loop unrolled, which makes the register allocator copy the
     // accumulators and halves the occupancy.)
     struct Stage {
-        uint2 r[RW];
+        uint32_t r[RW];
         uint32_t mw[R / 32];
     };
     static_assert(R <= 64, "one row position per lane");
@@ -1055,7 +1060,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
             const uint32_t e = entry(jj);
             const uint64_t r = (e >= s.batch ? (uint64_t)s.batch : 0ull) +
                                (uint32_t)__builtin_amdgcn_readlane(pos, wave * RW + j);
-            S.r[j] = jj < n ? reinterpret_cast<const uint2*>(d16 + r * kDftChunk)[lane] : make_uint2(0u, 0u);
+            S.r[j] = jj < n ? reinterpret_cast<const uint32_t*>(d16 + r * kDftChunk)[lane] : 0u;
         }
 #pragma unroll
         for (uint32_t k = 0; k < R / 32; ++k) {
@@ -1063,31 +1068,30 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
             S.mw[k] = jm < n ? mplane[entry(jm)] : 0u;
         }
     };
-    // registers -> LDS buffer: column 4 lane + c gets this wave's rows
+    // registers -> LDS buffer: column 2 lane + c gets this wave's rows
     auto store_rows = [&](const Stage& S, uint32_t buf) {
 #pragma unroll
         for (uint32_t o = 0; o < RW / 8; ++o)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < 2; ++c) {
                 u32x4 v;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const uint32_t x0 = (c < 2) ? S.r[8 * o + 2 * k].x : S.r[8 * o + 2 * k].y;
-                    const uint32_t x1 = (c < 2) ? S.r[8 * o + 2 * k + 1].x : S.r[8 * o + 2 * k + 1].y;
-                    v[k] = (c % 2 == 0) ? ((x0 & 0xFFFFu) | (x1 << 16)) : ((x0 >> 16) | (x1 & 0xFFFF0000u));
+                    const uint32_t x0 = S.r[8 * o + 2 * k], x1 = S.r[8 * o + 2 * k + 1];
+                    v[k] = c == 0 ? ((x0 & 0xFFFFu) | (x1 << 16)) : ((x0 >> 16) | (x1 & 0xFFFF0000u));
                 }
-                *reinterpret_cast<u32x4*>(s_d(buf, stage_slot(lane * 4 + c, wave * (RW / 8) + o))) = v;
+                *reinterpret_cast<u32x4*>(s_d(buf, stage_slot(lane * 2 + c, wave * (RW / 8) + o))) = v;
             }
 #pragma unroll
         for (uint32_t k = 0; k < R / 32; ++k) s_m[buf][mw][mr + 32 * k] = S.mw[k];
     };
 
     const uint32_t m = lane % 16, oct = lane / 16;
-    floatx4 acc[2][16];
+    floatx4 acc[2][8];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     Stage S;
     uint32_t p1 = 0, p2 = 0;  // positions of stages t+1 and t+2
@@ -1115,7 +1119,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
                 A[i] = hit_operand(wp[0], wp[1], m);
             }
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
+            for (int j = 0; j < 8; ++j) {
                 const half8 B = *reinterpret_cast<const half8*>(s_d(buf, stage_slot(j * 16 + m, 4 * ks + oct)));
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
@@ -1140,13 +1144,12 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     vecf<4>* grad = reinterpret_cast<vecf<4>*>(a.grad);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t col = chunk * kDftChunk + h * 128 + 4 * (lane % 32);
+        {
+            const uint32_t col = chunk * kDftChunk + half * kMfmaCols + 4 * (lane % 32);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = acc[i][h * 8 + j][r];
+                for (int r = 0; r < 4; ++r) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = acc[i][j][r];
             __syncthreads();
 #pragma unroll
             for (uint32_t q0 = 0; q0 < 8; q0 += 4) {
@@ -1543,7 +1546,7 @@ int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream
     const ScanGeom geom = scan_geom(s.piece_inputs);
     TATARA_REQUIRE(geom.group_size <= 128, "mfma backward: at most 128 features per group");
     const uint64_t pairs = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks;
-    const uint64_t grid = (pairs + kNumXcd - 1) / kNumXcd * kNumXcd * geom.n_groups;
+    const uint64_t grid = (pairs + kNumXcd - 1) / kNumXcd * kNumXcd * geom.n_groups * 2;
     if (grid > 0) {
         const uint32_t t = kMfmaWaves * 64;
         if (a.m16)
