@@ -113,12 +113,13 @@ def logical_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_r
     LayerStack, 4 for Simple) + index rows + nnz.  FT gradient + update:
     gathered dft rows (one per occurrence) + occurrence list + w, m, v read and
     written for every real row (+ slow on lookahead steps) + the gradient
-    written.  f16: gathered rows, raw sums, dft and moments are 2 bytes."""
+    written.  f16 (--all-optim): gathered rows, raw sums, dft, moments and
+    `combined` are 2 bytes."""
     nnz_total = np.mean([float(h["nnz"].sum()) for h in host_batches])
     b = host_batches[0]["nnz"].size
     s16 = 2.0 if f16 else 4.0
     gather = 2.0 * nnz_total * ft_out * s16
-    outs = (2 * s16 + 4.0 * (out_rows - 2)) * b * ft_out
+    outs = (2 * s16 + (s16 if f16 else 4.0) * (out_rows - 2)) * b * ft_out
     fwd = gather + outs + 2.0 * b * max_active * 4 + 4.0 * b
     cells = float(ft_in) * ft_out
     grad = (gather + 2.0 * nnz_total * 4 + cells * (2 * 4.0 + 4 * s16) + lookahead_frac * 2.0 * 4.0 * cells
@@ -148,6 +149,7 @@ def compulsory_bytes(w: dict, spec: dict, b: int, scan: bool, lookahead_frac: fl
     ft_in, pi, ma = spec["ft_in"], spec["piece_inputs"], spec["max_active"]
     fo = w["ft_out"]
     s_tab = s_o = s_d = s_m = 2 if f16 else 4
+    s_c = 2 if f16 else 4  # `combined` (held as f16 with --all-optim's tf32)
     real, virt = float(ft_in) * fo, float(pi) * fo
     idx = 2.0 * b * ma * 4 + 4.0 * b              # index rows + nnz
     sched = 2.0 * b * 4                            # king-block schedule
@@ -159,9 +161,9 @@ def compulsory_bytes(w: dict, spec: dict, b: int, scan: bool, lookahead_frac: fl
         l1, nb = w["l1"], w["nb"]
         P = -(-(b + (nb + 1) * 16) // 16) * 16
         out["prep"] = idx + sched + 4.0 * b + (masks + idx + sched if scan else 2 * occ)
-        out["ft_forward"] = real * s_tab + idx + sched + 4.0 * fo + 2.0 * b * fo * s_o + 4.0 * b * fo
-        out["dense_forward"] = 4.0 * b * fo + 4.0 * (nb * l1 * fo + fo * l1) + 4.0 * P * 3 * l1 + 12.0 * b
-        out["dense_backward"] = 4.0 * b * fo + 2.0 * b * fo * s_o + 4.0 * P * l1 + 2.0 * b * fo * s_d
+        out["ft_forward"] = real * s_tab + idx + sched + 4.0 * fo + 2.0 * b * fo * s_o + s_c * b * fo
+        out["dense_forward"] = s_c * b * fo + 4.0 * (nb * l1 * fo + fo * l1) + 4.0 * P * 3 * l1 + 12.0 * b
+        out["dense_backward"] = s_c * b * fo + 2.0 * b * fo * s_o + 4.0 * P * l1 + 2.0 * b * fo * s_d
         out["ft_grad_update"] = 2.0 * b * fo * s_d + masks + sched + occ + real * (cell + 4.0)
         out["ft_virtual_fold"] = (8.0 + s_tab) * real + virt * (cell + 4.0)
         out["dense_opt"] = 4.0 * 4 * (nb * l1 * fo + fo * l1)

@@ -312,6 +312,15 @@ typedef struct TataraTrainerConfig {
      * fp16_opt_state: the ft_w moments stored f16, scaled by 2^28 (m) and
      * 2^40 (v).  Master weights stay f32. */
     int32_t ft_fp16, ft_fp16_out, fp16_opt_state;
+    /* PrecisionFlags.tf32 (--tf32, the fourth --all-optim flag): the L1
+     * products (bucket and shared forward, weight and input gradients;
+     * trainer_layerstack.rs:2388-2510, 3335-3540) with TF32-class operands.
+     * gfx950 has no TF32 matrix instructions: `combined` is held as f16 and
+     * the forward multiplies it by f16-rounded weights (10 fraction bits, as
+     * TF32) on the f16 matrix cores; the weight gradients take that f16
+     * `combined` with f32 dl1, and the input gradient stays f32; every sum
+     * is f32.  LayerStack only. */
+    int32_t tf32;
 } TataraTrainerConfig;
 
 /* LossKind (crates/nnue-train/src/trainer.rs:89-135). */

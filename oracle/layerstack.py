@@ -77,10 +77,18 @@ class Precision:
     ft_fp16: bool = False
     ft_fp16_out: bool = False
     fp16_opt_state: bool = False
+    # TF32-class L1 products (the reference's --tf32, cuBLAS TF32 GEMMs,
+    # trainer_layerstack.rs:2388-2510, 3335-3540), as the HIP trainer forms
+    # them on gfx950 (no TF32 matrix instructions): `combined` rounded to f16
+    # once and held so; forward products of it with f16-rounded weights, the
+    # bucket bias added after the bucket sum; the weight gradients take that
+    # f16 `combined` with f32 dl1, the input gradient f32 dl1 and f32
+    # weights; f32 sums throughout.
+    tf32: bool = False
 
     @classmethod
     def all_optim(cls):
-        return cls(True, True, True)
+        return cls(True, True, True, True)
 
 
 FP32 = Precision()
@@ -203,10 +211,21 @@ def forward(sh: LsShape, st: dict, batch: dict, wdl_lambda: float, loss: dict, p
     a["combined"] = ffi.ft_post_perspective_fwd(a["ft_stm"], a["ft_nstm"], st["ft_b"]["w"], b,
                                                 sh.ft_out, FT_POST_SCALE)
     bk = batch["bucket"]
-    a["l1_bucket"] = ffi.dense_mm_fwd_bucket(a["combined"], st["l1_w"]["w"], st["l1_b"]["w"], bk, b,
-                                             sh.ft_out, sh.l1, sh.nb)
-    a["l1_shared"] = ffi.dense_mm_fwd(a["combined"], st["l1_shared_weight"]["w"],
-                                      st["l1_shared_bias"]["w"], b, sh.ft_out, sh.l1)
+    if prec.tf32:
+        a["combined"] = f16(a["combined"])
+        zero_b = np.zeros_like(st["l1_b"]["w"])
+        l1b = ffi.dense_mm_fwd_bucket(a["combined"], f16(st["l1_w"]["w"]), zero_b, bk, b, sh.ft_out, sh.l1,
+                                      sh.nb).reshape(b, sh.l1)
+        valid = (bk >= 0) & (bk < sh.nb)
+        l1b[valid] += st["l1_b"]["w"].reshape(sh.nb, sh.l1)[bk[valid]]
+        a["l1_bucket"] = l1b.reshape(-1)
+        a["l1_shared"] = ffi.dense_mm_fwd(a["combined"], f16(st["l1_shared_weight"]["w"]),
+                                          st["l1_shared_bias"]["w"], b, sh.ft_out, sh.l1)
+    else:
+        a["l1_bucket"] = ffi.dense_mm_fwd_bucket(a["combined"], st["l1_w"]["w"], st["l1_b"]["w"], bk, b,
+                                                 sh.ft_out, sh.l1, sh.nb)
+        a["l1_shared"] = ffi.dense_mm_fwd(a["combined"], st["l1_shared_weight"]["w"],
+                                          st["l1_shared_bias"]["w"], b, sh.ft_out, sh.l1)
     a["l1_total"] = ffi.elementwise_add(a["l1_bucket"], a["l1_shared"])
     a["l1_main"] = ffi.slice_extract_2d(a["l1_total"], b, sh.l1, 0, sh.l1e)
     a["l1_skip"] = ffi.slice_extract_2d(a["l1_total"], b, sh.l1, sh.l1e, 1)
@@ -254,6 +273,7 @@ def backward(sh: LsShape, st: dict, batch: dict, a: dict, prec: Precision = FP32
     ffi.slice_scatter_2d(dl1_main, dl1_total, b, sh.l1e, sh.l1, 0)
     ffi.slice_scatter_2d(dy, dl1_total, b, 1, sh.l1, sh.l1e)
     a["dl1_total"] = dl1_total
+    # (under tf32 `combined` is the f16 value the forward held)
     dcomb_shared = ffi.dense_mm_bwd_input(dl1_total, st["l1_shared_weight"]["w"], b, sh.ft_out, sh.l1)
     g["l1_shared_weight"] = ffi.dense_mm_bwd_weight(a["combined"], dl1_total, b, sh.ft_out, sh.l1)
     g["l1_shared_bias"] = ffi.bias_grad(dl1_total, np.zeros(sh.l1, np.float32), b, sh.l1)

@@ -40,6 +40,7 @@ class TataraTrainerConfig(C.Structure):
         ("ft_fp16", C.c_int32),
         ("ft_fp16_out", C.c_int32),
         ("fp16_opt_state", C.c_int32),
+        ("tf32", C.c_int32),
     ]
 
 

@@ -235,8 +235,9 @@ int32_t launch_radix_pass(const RadixPassArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.shift < 32, "radix pass: shift < 32");
     const uint32_t tiles = binsort_tiles(a.n_items);
     if (tiles == 0) return kOk;
-    // a gated pass strides over a bounded grid
-    const uint32_t grid = a.run_if && tiles > 1024u ? 1024u : tiles;
+    // a gated pass strides over a small grid (64 workgroups of 1024 lanes):
+    // its no-op workgroups cost the kernels it overlaps little
+    const uint32_t grid = a.run_if && tiles > 64u ? 64u : tiles;
     radix_hist_kernel<<<grid, kTile, 0, stream>>>(a.keys, a.n_items, a.shift, tiles, a.hist, a.run_if);
     TATARA_LAUNCHED("radix_hist");
     binsort_scan_kernel<<<kMaxBins, kScanThreads, 0, stream>>>(a.hist, tiles, kMaxBins, nullptr, a.digit_count,

@@ -31,6 +31,8 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
 
 // ---------------------------------------------------------------------------
 // L1 forward.  One wave per 16-row sorted tile.
@@ -107,6 +109,82 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
         const uint64_t row = (uint64_t)tile * 16 + 4 * q + r;
         float* o = a.l1_sorted + row * 2 * l1;
         o[j] = bvalid ? accb[r] : 0.0f;
+        o[l1 + j] = accs[r] + bs;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// L1 forward with TF32-class products: f16 operands on the matrix cores
+// (v_mfma_f32_16x16x32_f16, f32 sums).  Lane l supplies A[l%16][8(l/16)+e]
+// (row l%16 of the tile, 8 consecutive K from the f16 `combined`, one
+// 16-byte load) and B[8(l/16)+e][l%16] (output l%16: 8 consecutive K of its
+// bucket weight row, rounded to f16, and 8 strided shared weights).  As the
+// reference's tf32 path (per-bucket sgemm, then the bias,
+// trainer_layerstack.rs:2388-2480) the bucket bias is added after the sum.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ls_l1_fwd_tf32_kernel(LsDenseArgs a) {
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t tile = blockIdx.x * 4 + wave;
+    if ((uint64_t)tile * 16 >= a.padded_b) return;
+    const int32_t bin = a.sorted_bin[tile * 16];
+    if (bin < 0) return;  // trailing all-padding tile
+    const uint32_t i = lane % 16, q = lane / 16;
+    const uint32_t ft_out = a.ft_out, l1 = a.l1;
+    const int32_t orig = a.perm[tile * 16 + i];
+    const bool bvalid = (uint32_t)bin < a.nb;
+    const bool jvalid = i < l1;
+    // unconditional loads from always-valid addresses, masked afterwards
+    const bool xvalid = orig >= 0, wbvalid = bvalid && jvalid;
+    const uint32_t ic = jvalid ? i : l1 - 1;
+    const half8* X = reinterpret_cast<const half8*>(
+        reinterpret_cast<const _Float16*>(a.combined16) + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
+    const float4* W1 = reinterpret_cast<const float4*>(a.l1_w + ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
+    const float* Ws = a.l1s_w + ic;
+    floatx4 accb = {0.f, 0.f, 0.f, 0.f}, accs = accb;
+    const half8 zero8 = {};
+    // ft_out % 64 == 0: K blocks of 32, two loaded before their MFMAs
+    const uint32_t nk = ft_out / 32;
+    constexpr uint32_t kU = 2;
+    for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
+        half8 x[kU];
+        float4 w0[kU], w1[kU];
+        float ws[kU][8];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) {
+            const uint32_t k = (kb0 + u) * 32 + 8 * q;
+            x[u] = X[k / 8];
+            w0[u] = W1[k / 4];
+            w1[u] = W1[k / 4 + 1];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ws[u][e] = Ws[(uint64_t)(k + e) * l1];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) {
+            const half8 xv = xvalid ? x[u] : zero8;
+            half8 wb, wsh;
+            wb[0] = (_Float16)w0[u].x;
+            wb[1] = (_Float16)w0[u].y;
+            wb[2] = (_Float16)w0[u].z;
+            wb[3] = (_Float16)w0[u].w;
+            wb[4] = (_Float16)w1[u].x;
+            wb[5] = (_Float16)w1[u].y;
+            wb[6] = (_Float16)w1[u].z;
+            wb[7] = (_Float16)w1[u].w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wsh[e] = (_Float16)ws[u][e];
+            accb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wbvalid ? wb : zero8, accb, 0, 0, 0);
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, jvalid ? wsh : zero8, accs, 0, 0, 0);
+        }
+    }
+    const uint32_t j = lane % 16;
+    if (j >= l1) return;
+    const float bb = bvalid ? a.l1_b[bin * l1 + j] : 0.0f;
+    const float bs = a.l1s_b[j];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint64_t row = (uint64_t)tile * 16 + 4 * q + r;
+        float* o = a.l1_sorted + row * 2 * l1;
+        o[j] = bvalid ? accb[r] + bb : 0.0f;
         o[l1 + j] = accs[r] + bs;
     }
 }
@@ -423,7 +501,10 @@ void reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols, const uint32_
 // L1 weight gradient partials: P[chunk][o][k] = sum over the chunk's rows of
 // dl1[row][o] * combined[row][k].  One wave owns 64 columns; lane (k, q) loads
 // a float4 of combined so block c of its four MFMAs holds columns k0+4k+c.
+// TF32: `combined` read as f16 (as the forward stored it); dl1 and the
+// products stay f32.
 // ---------------------------------------------------------------------------
+template <bool TF32>
 __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t n_chunks = a.chunk_info[3 * a.max_chunks];
@@ -451,7 +532,14 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
             const uint64_t row = (uint64_t)(t0 + tt) * 16 + 4 * s + q;
             const int32_t orig = a.perm[row];
             rvs[s] = orig >= 0;
-            xs[s] = *reinterpret_cast<const float4*>(a.combined + (uint64_t)(orig >= 0 ? orig : 0) * ft_out + kc);
+            const uint64_t xo = (uint64_t)(orig >= 0 ? orig : 0) * ft_out + kc;
+            if constexpr (TF32) {
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 h = *reinterpret_cast<const h4*>(reinterpret_cast<const _Float16*>(a.combined16) + xo);
+                xs[s] = make_float4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
+            } else {
+                xs[s] = *reinterpret_cast<const float4*>(a.combined + xo);
+            }
             ds[s] = a.dl1_sorted[row * l1 + oc];
         }
 #pragma unroll
@@ -756,7 +844,12 @@ int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.ft_out % 64 == 0, "ft_out must be a multiple of 64");
     const uint32_t tiles = a.padded_b / 16;
     if (tiles == 0) return kOk;
-    ls_l1_fwd_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    if (a.combined16) {
+        TATARA_REQUIRE(a.l1 <= 16, "l1 must be <= 16");
+        ls_l1_fwd_tf32_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    } else {
+        ls_l1_fwd_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    }
     TATARA_LAUNCHED("ls_l1_forward");
     return kOk;
 }
@@ -794,7 +887,10 @@ int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream) {
                                                a.chunk_info);
     TATARA_LAUNCHED("ls_chunk_table");
     dim3 grid(a.max_chunks, ceil_div(a.ft_out, 256));
-    ls_l1_wgrad_kernel<<<grid, 256, 0, stream>>>(a);
+    if (a.combined16)
+        ls_l1_wgrad_kernel<true><<<grid, 256, 0, stream>>>(a);
+    else
+        ls_l1_wgrad_kernel<false><<<grid, 256, 0, stream>>>(a);
     TATARA_LAUNCHED("ls_l1_weight_grad");
     return kOk;
 }

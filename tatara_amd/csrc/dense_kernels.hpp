@@ -40,6 +40,13 @@ struct LsDenseArgs {
     uint32_t max_chunks;
     // activations
     const float* combined;      // [batch][ft_out]
+    // TF32-class L1 products (the reference's --tf32; gfx950 has no TF32
+    // matrix instructions): when non-null, `combined` is held as f16 here
+    // (read instead of `combined`) and the L1 forward multiplies f16
+    // operands (combined, f16-rounded weights) on the matrix cores with f32
+    // sums; the L1 weight gradient takes the f16 `combined` with f32 dl1,
+    // and the input gradient stays f32.
+    const uint16_t* combined16;
     const float* ft_stm;        // [batch][ft_out] raw FT sums
     const float* ft_nstm;
     float* l1_sorted;           // [padded_b][2*l1]  bucket part | shared part (biases added)

@@ -162,8 +162,8 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
     const int32_t* __restrict__ schedule,  // [n_persp][batch] position order, or null
     const float* __restrict__ bias, float* __restrict__ out_stm, float* __restrict__ out_nstm,
     _Float16* __restrict__ out16_stm, _Float16* __restrict__ out16_nstm,
-    float* __restrict__ combined, uint32_t batch, uint32_t ft_out, uint32_t cols,
-    uint32_t max_active, uint32_t n_chunks, uint32_t n_persp, float scale) {
+    float* __restrict__ combined, _Float16* __restrict__ combined16, uint32_t batch, uint32_t ft_out,
+    uint32_t cols, uint32_t max_active, uint32_t n_chunks, uint32_t n_persp, float scale) {
     __shared__ int s_idx_all[kWavesPerBlock][kMaxActive];
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
@@ -219,7 +219,11 @@ __global__ __launch_bounds__(256) void ft_forward_kernel(
         c.y = crelu01(a0.y + b0.y) * crelu01(p.y + b1.y) * scale;
         c.z = crelu01(a0.z + b0.z) * crelu01(p.z + b1.z) * scale;
         c.w = crelu01(a0.w + b0.w) * crelu01(p.w + b1.w) * scale;
-        st_nt(reinterpret_cast<float4*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2)) + qp, c);
+        const uint64_t co = (uint64_t)pos * ft_out + persp * (ft_out / 2);
+        if (combined16)
+            __builtin_nontemporal_store(f4_to_h4(c), reinterpret_cast<h4*>(combined16 + co) + qp);
+        else
+            st_nt(reinterpret_cast<float4*>(combined + co) + qp, c);
     } else {
         const uint32_t q = chunk * kWave + lane;
         const bool active = q < row4;
@@ -260,8 +264,9 @@ __global__ __launch_bounds__(256) void ft_forward_pair16_kernel(
     const _Float16* __restrict__ W, const int32_t* __restrict__ idx_stm, const int32_t* __restrict__ idx_nstm,
     const int32_t* __restrict__ nnz, const int32_t* __restrict__ schedule, const float* __restrict__ bias,
     float* __restrict__ out_stm, float* __restrict__ out_nstm, _Float16* __restrict__ out16_stm,
-    _Float16* __restrict__ out16_nstm, float* __restrict__ combined, uint32_t batch, uint32_t ft_out,
-    uint32_t cols, uint32_t max_active, uint32_t n_chunks, uint32_t n_persp, float scale) {
+    _Float16* __restrict__ out16_nstm, float* __restrict__ combined, _Float16* __restrict__ combined16,
+    uint32_t batch, uint32_t ft_out, uint32_t cols, uint32_t max_active, uint32_t n_chunks, uint32_t n_persp,
+    float scale) {
     __shared__ int s_idx_all[kWavesPerBlock][kMaxActive];
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
@@ -328,8 +333,11 @@ __global__ __launch_bounds__(256) void ft_forward_pair16_kernel(
     f8v c;
 #pragma unroll
     for (int e = 0; e < 8; ++e) c[e] = crelu01(acc[e] + b0[e]) * crelu01(p[e] + b1[e]) * scale;
-    __builtin_nontemporal_store(
-        c, reinterpret_cast<f8v*>(combined + (uint64_t)pos * ft_out + persp * (ft_out / 2)) + qp);
+    const uint64_t co = (uint64_t)pos * ft_out + persp * (ft_out / 2);
+    if (combined16)
+        __builtin_nontemporal_store(__builtin_convertvector(c, h8), reinterpret_cast<h8*>(combined16 + co) + qp);
+    else
+        __builtin_nontemporal_store(c, reinterpret_cast<f8v*>(combined + co) + qp);
 }
 
 // ---------------------------------------------------------------------------
@@ -1330,10 +1338,12 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
     _Float16* o16s = reinterpret_cast<_Float16*>(a.out_stm16);
     _Float16* o16n = reinterpret_cast<_Float16*>(a.out_nstm16);
     const _Float16* W16 = reinterpret_cast<const _Float16*>(a.W16);
+    _Float16* c16p = reinterpret_cast<_Float16*>(a.combined16);
+    TATARA_REQUIRE(!c16p || a.mode == kPair, "an f16 combined is written by the pairwise mode only");
 #define TATARA_FWD(MODE, T, HOUT, WPTR)                                                                      \
     ft_forward_kernel<MODE, T, HOUT><<<blocks, 256, 0, stream>>>(                                          \
         WPTR, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm, o16s, o16n, a.combined, \
-        a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale)
+        c16p, a.batch, a.ft_out, a.cols, a.max_active, n_chunks, a.n_persp, a.scale)
     switch (a.mode) {
         case kRaw:
             TATARA_FWD(kRaw, float, false, a.W);
@@ -1348,11 +1358,11 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
                 if (h_out)
                     ft_forward_pair16_kernel<true><<<b16, 256, 0, stream>>>(
                         W16, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm, o16s, o16n,
-                        a.combined, a.batch, a.ft_out, a.cols, a.max_active, c16, a.n_persp, a.scale);
+                        a.combined, c16p, a.batch, a.ft_out, a.cols, a.max_active, c16, a.n_persp, a.scale);
                 else
                     ft_forward_pair16_kernel<false><<<b16, 256, 0, stream>>>(
                         W16, a.idx_stm, a.idx_nstm, a.nnz, a.schedule, a.bias, a.out_stm, a.out_nstm, o16s, o16n,
-                        a.combined, a.batch, a.ft_out, a.cols, a.max_active, c16, a.n_persp, a.scale);
+                        a.combined, c16p, a.batch, a.ft_out, a.cols, a.max_active, c16, a.n_persp, a.scale);
             } else {
                 TATARA_FWD(kPair, float, false, a.W);
             }
@@ -1399,10 +1409,12 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) 
     const uint64_t n_items = 2ull * a.batch * a.max_active;
     const uint32_t n_keys = 2 * a.cols + 1;  // keys 0..2*cols (2*cols = invalid slot)
     TATARA_REQUIRE(n_items <= 0xFFFFFFFFull, "occurrence sort: at most 2^32 - 1 slots");
-    // a gated sort strides over bounded grids, so skipping it costs little
+    // a gated sort strides over small grids, so that skipping it costs
+    // little beside the kernels it overlaps (its no-op workgroups still pass
+    // through the dispatcher); the rare sort that runs is slower for it
     auto grid = [&](uint64_t n) -> uint32_t {
         const uint64_t g = ceil_div(n, 256);
-        return (uint32_t)(a.run_if && g > 2048 ? 2048 : g);
+        return (uint32_t)(a.run_if && g > 256 ? 256 : g);
     };
     if (!a.run_if) {
         if (n_items > 0) {
@@ -1462,7 +1474,7 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
     // a gated launch (the block scan's fallback) strides over a bounded grid
-    const uint32_t cap = a.run_if ? 8192u : 0xFFFFFFFFu;
+    const uint32_t cap = a.run_if ? 1024u : 0xFFFFFFFFu;
     uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
     blocks = blocks < cap ? blocks : cap;
     // four f16 values per lane: a wave's rows are 512 bytes, so a king

@@ -28,6 +28,7 @@ struct FtForwardArgs {
     uint16_t* out_stm16;  // pairwise mode: f16 raw sums, written instead of out_* when non-null
     uint16_t* out_nstm16;
     float* combined;
+    uint16_t* combined16;  // pairwise mode: `combined` rounded to f16, written instead when non-null
     uint32_t batch, ft_out, cols, max_active, n_persp;
     float scale;
 };

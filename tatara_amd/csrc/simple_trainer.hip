@@ -77,7 +77,7 @@ class SimpleTrainer final : public TrainerBase {
                        "Simple (l1, l2) must be (32, 32) or (16, 32)");
         TATARA_REQUIRE(c.optimizer >= 0 && c.optimizer <= 2, "unknown optimizer");
         TATARA_REQUIRE(c.piece_inputs >= 0, "piece_inputs >= 0");
-        TATARA_REQUIRE(!c.ft_fp16 && !c.ft_fp16_out && !c.fp16_opt_state,
+        TATARA_REQUIRE(!c.ft_fp16 && !c.ft_fp16_out && !c.fp16_opt_state && !c.tf32,
                        "the f16 modes are built for the LayerStack architecture only");
         if (c.piece_inputs > 0)
             TATARA_REQUIRE(c.ft_in % c.piece_inputs == 0, "ft_in must be a multiple of piece_inputs");

@@ -81,8 +81,10 @@ class LayerStackTrainer final : public TrainerBase {
     // mixed precision (PrecisionFlags): f16 forward table, f16 FT activations
     // and dft, f16 ft_w moments
     bool h_fwd = false, h_out = false, h_state = false;
+    bool l1_lowp = false;  // tf32: TF32-class L1 products (f16 / bf16 operands, f32 sums)
     uint16_t* fwd16 = nullptr;  // [ft_in][ft_out] f16 comb (factorizer) or mirror of the real rows
     uint16_t *ft_stm16 = nullptr, *ft_nstm16 = nullptr, *dft16 = nullptr;
+    uint16_t* combined16 = nullptr;  // `combined` held as f16 (tf32)
     unsigned long long* clamp_ctr = nullptr;  // cumulative dft clamps
     uint64_t clamp_elems = 0;                 // cumulative dft values written
 
@@ -138,6 +140,7 @@ class LayerStackTrainer final : public TrainerBase {
         h_fwd = c.ft_fp16 != 0;
         h_out = c.ft_fp16_out != 0;
         h_state = c.fp16_opt_state != 0;
+        l1_lowp = c.tf32 != 0;
         ft_in = c.ft_in;
         pi = c.piece_inputs;
         factorized = pi > 0;
@@ -240,7 +243,9 @@ class LayerStackTrainer final : public TrainerBase {
                    (st = arena.alloc(&ft_nstm, B * ft_out, false)) || (st = arena.alloc(&dft, dft_n, false))) {
             return st;
         }
-        if ((st = arena.alloc(&combined, B * ft_out, false)) || (st = arena.alloc(&l1_sorted, P * 2 * l1)) ||
+        if ((l1_lowp ? (st = arena.alloc(&combined16, B * ft_out, false))
+                     : (st = arena.alloc(&combined, B * ft_out, false))) ||
+            (st = arena.alloc(&l1_sorted, P * 2 * l1)) ||
             (st = arena.alloc(&dl1_sorted, P * l1)) || (st = arena.alloc(&net_out, B)))
             return st;
         const TailDims td{l1, l2, nb};
@@ -340,6 +345,7 @@ class LayerStackTrainer final : public TrainerBase {
         a.chunk_info = chunk_info;
         a.max_chunks = max_chunks;
         a.combined = combined;
+        a.combined16 = combined16;
         a.ft_stm = ft_stm;
         a.ft_nstm = ft_nstm;
         a.l1_sorted = l1_sorted;
@@ -511,6 +517,7 @@ class LayerStackTrainer final : public TrainerBase {
         fa.out_stm = ft_stm;
         fa.out_nstm = ft_nstm;
         fa.combined = combined;
+        fa.combined16 = combined16;
         fa.batch = b;
         fa.ft_out = ft_out;
         fa.cols = ft_in;
@@ -661,6 +668,10 @@ class LayerStackTrainer final : public TrainerBase {
         if (h_out && (!std::strcmp(name, "ft_stm_out") || !std::strcmp(name, "ft_nstm_out"))) {
             TATARA_REQUIRE(n <= (uint64_t)last_b * ft_out, "activation request exceeds the last batch");
             return copy_f16(!std::strcmp(name, "ft_stm_out") ? ft_stm16 : ft_nstm16, host, n);
+        }
+        if (l1_lowp && !std::strcmp(name, "combined")) {
+            TATARA_REQUIRE(n <= (uint64_t)last_b * ft_out, "activation request exceeds the last batch");
+            return copy_f16(combined16, host, n);
         }
         return TrainerBase::copy_activation(name, host, n);
     }

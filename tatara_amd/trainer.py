@@ -229,16 +229,17 @@ class LayerStackConfig:
     bias_lr_mult: float = 1.0
     device: int = 0
     keep_grads: bool = False
-    # PrecisionFlags (trainer_common.rs:49-61); all_optim() sets the three
+    # PrecisionFlags (trainer_common.rs:49-61); all_optim() sets the four
     ft_fp16: bool = False
     ft_fp16_out: bool = False
     fp16_opt_state: bool = False
+    tf32: bool = False
 
     def all_optim(self) -> "LayerStackConfig":
         """The --all-optim precision flags (cli.rs:627-638) on a copy of this config."""
         import dataclasses
 
-        return dataclasses.replace(self, ft_fp16=True, ft_fp16_out=True, fp16_opt_state=True)
+        return dataclasses.replace(self, ft_fp16=True, ft_fp16_out=True, fp16_opt_state=True, tf32=True)
 
     def to_c(self) -> TataraTrainerConfig:
         wd = self.weight_decay
@@ -264,6 +265,7 @@ class LayerStackConfig:
             ft_fp16=int(self.ft_fp16),
             ft_fp16_out=int(self.ft_fp16_out),
             fp16_opt_state=int(self.fp16_opt_state),
+            tf32=int(self.tf32),
         )
 
     @property

@@ -13,7 +13,7 @@
 
 #define CHECK(T, f, off) static_assert(offsetof(T, f) == (off), #T "." #f " moved")
 
-static_assert(sizeof(TataraTrainerConfig) == 84, "TataraTrainerConfig size");
+static_assert(sizeof(TataraTrainerConfig) == 88, "TataraTrainerConfig size");
 CHECK(TataraTrainerConfig, arch, 0);
 CHECK(TataraTrainerConfig, optimizer, 40);
 CHECK(TataraTrainerConfig, ft_weight_decay, 44);
@@ -22,6 +22,7 @@ CHECK(TataraTrainerConfig, keep_grads, 68);
 CHECK(TataraTrainerConfig, ft_fp16, 72);
 CHECK(TataraTrainerConfig, ft_fp16_out, 76);
 CHECK(TataraTrainerConfig, fp16_opt_state, 80);
+CHECK(TataraTrainerConfig, tf32, 84);
 
 static_assert(sizeof(TataraLoss) == 44, "TataraLoss size");
 CHECK(TataraLoss, scale, 4);
@@ -58,7 +59,7 @@ int main(void) {
     F(TataraTrainerConfig, bias_weight_decay); F(TataraTrainerConfig, ft_lr_mult);
     F(TataraTrainerConfig, dense_lr_mult); F(TataraTrainerConfig, bias_lr_mult);
     F(TataraTrainerConfig, keep_grads); F(TataraTrainerConfig, ft_fp16); F(TataraTrainerConfig, ft_fp16_out);
-    F(TataraTrainerConfig, fp16_opt_state);
+    F(TataraTrainerConfig, fp16_opt_state); F(TataraTrainerConfig, tf32);
 
     S(TataraLoss);
     F(TataraLoss, kind); F(TataraLoss, scale); F(TataraLoss, nnue2score); F(TataraLoss, in_scaling);

@@ -4,7 +4,8 @@ modes) on the GPU vs the oracle step with the same f16 rounding points
 
 Bars:
   - FT raw sums and `combined`: bit-exact (the same f32 slot-order sums of the
-    same f16 rows, rounded once to f16);
+    same f16 rows, rounded once to f16; with tf32 `combined` is held as f16,
+    rounded once from the same f32 value);
   - the f16 dft (scaled by 2^14 b): within 2e-3 relative, the bar of the
     reference's own fp16 kernel tests (gpu_cpu_equivalence_tests.rs:2791),
     plus one f16 subnormal step: the dense backward upstream is within 1e-5,
@@ -41,6 +42,7 @@ FLAGS = {
     "fp16_fwd": ols.Precision(True, False, False),
     "fp16_fwd_out": ols.Precision(True, True, False),
     "fp16_state": ols.Precision(False, False, True),
+    "tf32": ols.Precision(tf32=True),
     "all_optim": ols.Precision.all_optim(),
 }
 SUB16 = 2.0 ** -24  # smallest f16 subnormal
@@ -51,7 +53,7 @@ def mixed(prec: ols.Precision, **kw):
     import dataclasses
 
     cfg = dataclasses.replace(cfg, ft_fp16=prec.ft_fp16, ft_fp16_out=prec.ft_fp16_out,
-                              fp16_opt_state=prec.fp16_opt_state)
+                              fp16_opt_state=prec.fp16_opt_state, tf32=prec.tf32)
     return sh, cfg
 
 

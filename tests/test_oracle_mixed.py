@@ -12,7 +12,14 @@ pinned independently of its own formulas.
     equal the fp32 path's exactly and the stored moments are f16(m 2^28),
     f16(v 2^40) of the fp32 moments; later steps stay within f16 precision;
   - all flags off is the fp32 step, bit for bit; each f16 mode moves the
-    step's outputs by no more than f16 precision allows.
+    step's outputs by no more than f16 precision allows;
+  - the TF32-class L1 products (tf32): the L1 outputs, the L1 weight
+    gradients and the L1 input gradient equal float64 products of the
+    stated operands (forward: f16 combined and f16 weights, the bucket bias
+    added after the bucket sum; weight gradients: f16 combined and f32 dl1;
+    input gradient: f32 dl1 and f32 weights) within f32 summation error,
+    and planted mistakes (an operand rounded where it is not, or left
+    unrounded where it is) fall outside that.
 """
 import numpy as np
 import pytest
@@ -118,3 +125,71 @@ def test_each_mode_within_f16_precision_of_fp32(prec):
     assert abs(acc_m - acc_r) <= 1e-3 * abs(acc_r)
     gm, gr = g_m["ft_w"], g_r["ft_w"]
     assert np.abs(gm - gr).max() <= 1e-2 * np.abs(gr).max()
+
+
+def test_tf32_l1_products():
+    """The oracle's tf32 step against float64 products of the stated operands."""
+    sh, bd = _setup(5)
+    opt = ols.OptConfig()
+    st = ols.default_init(sh)
+    prec = ols.Precision(tf32=True)
+    a, acc = ols.forward(sh, st, bd, 0.0, LOSS, prec)
+    g = ols.backward(sh, st, bd, a, prec)
+    b, fo, l1, nb = bd["stm"].shape[0], sh.ft_out, sh.l1, sh.nb
+    comb32, _ = ols.forward(sh, ols.default_init(sh), bd, 0.0, LOSS)
+    c = ols.f16(comb32["combined"]).reshape(b, fo).astype(np.float64)
+    assert np.array_equal(a["combined"], ols.f16(comb32["combined"]))
+    w1 = ols.f16(st["l1_w"]["w"]).reshape(nb, l1, fo).astype(np.float64)
+    ws = ols.f16(st["l1_shared_weight"]["w"]).reshape(fo, l1).astype(np.float64)
+    bk = bd["bucket"]
+    valid = (bk >= 0) & (bk < nb)
+    exp_b = np.zeros((b, l1))
+    exp_b[valid] = np.einsum("rk,rok->ro", c[valid], w1[bk[valid]]) + st["l1_b"]["w"].reshape(nb, l1)[bk[valid]]
+    exp_s = c @ ws + st["l1_shared_bias"]["w"]
+    mag_b = np.zeros((b, l1))
+    mag_b[valid] = np.einsum("rk,rok->ro", np.abs(c[valid]), np.abs(w1[bk[valid]]))
+    tol = fo * 2.0 ** -24 * (mag_b + np.abs(c) @ np.abs(ws)) + 1e-12
+    assert np.all(np.abs(a["l1_bucket"].reshape(b, l1) - exp_b) <= tol)
+    assert np.all(np.abs(a["l1_shared"].reshape(b, l1) - exp_s) <= tol)
+    # a planted mistake: the forward with unrounded weights is far outside the bound
+    plant = np.einsum("rk,rok->ro", c[valid], st["l1_w"]["w"].reshape(nb, l1, fo)[bk[valid]].astype(np.float64))
+    assert np.max(np.abs(plant + st["l1_b"]["w"].reshape(nb, l1)[bk[valid]] - exp_b[valid]) - tol[valid]) > 0
+    # weight gradients: f32 dl1 times the f16 combined
+    d = a["dl1_total"].reshape(b, l1).astype(np.float64)
+    exp_ws = c.T @ d
+    tol_ws = b * 2.0 ** -24 * (np.abs(c).T @ np.abs(d)) + 1e-30
+    assert np.all(np.abs(g["l1_shared_weight"].reshape(fo, l1) - exp_ws) <= tol_ws)
+    # a planted mistake: the f32 combined in the weight gradient
+    c32 = comb32["combined"].reshape(b, fo).astype(np.float64)
+    assert np.max(np.abs(c32.T @ d - exp_ws) - tol_ws) > 0
+    exp_w1 = np.zeros((nb, l1, fo))
+    for k in range(nb):
+        rows = bk == k
+        exp_w1[k] = d[rows].T @ c[rows]
+    mag_w1 = np.zeros((nb, l1, fo))
+    for k in range(nb):
+        rows = bk == k
+        mag_w1[k] = np.abs(d[rows]).T @ np.abs(c[rows])
+    assert np.all(np.abs(g["l1_w"].reshape(nb, l1, fo) - exp_w1) <= b * 2.0 ** -24 * mag_w1 + 1e-30)
+    # the L1 input gradient: f32 dl1 times the f32 weights, bucket + shared
+    w1_32 = st["l1_w"]["w"].reshape(nb, l1, fo).astype(np.float64)
+    ws_32 = st["l1_shared_weight"]["w"].reshape(fo, l1).astype(np.float64)
+    exp_dc = np.zeros((b, fo))
+    mag_dc = np.zeros((b, fo))
+    exp_dc[valid] = np.einsum("ro,rok->rk", d[valid], w1_32[bk[valid]])
+    mag_dc[valid] = np.einsum("ro,rok->rk", np.abs(d[valid]), np.abs(w1_32[bk[valid]]))
+    exp_dc += d @ ws_32.T
+    mag_dc += np.abs(d) @ np.abs(ws_32).T
+    tol_dc = 2 * l1 * 2.0 ** -24 * mag_dc + 1e-30
+    assert np.all(np.abs(a["dcombined"].reshape(b, fo) - exp_dc) <= tol_dc)
+    # a planted mistake: the f16-rounded weights in the input gradient
+    plant_dc = np.zeros((b, fo))
+    plant_dc[valid] = np.einsum("ro,rok->rk", d[valid], w1[bk[valid]])
+    plant_dc += d @ ws.T
+    assert np.max(np.abs(plant_dc - exp_dc) - tol_dc) > 0
+    # and the step recomputed with f32 operands agrees only within the
+    # f16 rounding
+    a32, _ = ols.forward(sh, ols.default_init(sh), bd, 0.0, LOSS, ols.Precision())
+    g32 = ols.backward(sh, ols.default_init(sh), bd, a32, ols.Precision())
+    assert np.abs(g["ft_b"] - g32["ft_b"]).max() <= 2e-2 * np.abs(g32["ft_b"]).max()
+    assert abs(acc - ols.forward(sh, ols.default_init(sh), bd, 0.0, LOSS)[1]) <= 1e-3 * abs(acc)
