@@ -481,6 +481,64 @@ TATARA_API int32_t tatara_trainer_load_resume(TataraTrainer* trainer, const char
                                               int32_t bucket_mode, TataraCkptHeader* header);
 
 /* ------------------------------------------------------------------------ */
+/* Structured run log (crates/nnue-train/src/experiment.rs): one             */
+/* experiment.json per run.  Host only.                                      */
+/* ------------------------------------------------------------------------ */
+
+/* ExperimentLogger (experiment.rs:356-540) with its document. */
+typedef struct TataraExperiment TataraExperiment;
+
+/* ExperimentDoc::new (experiment.rs:293-340): the document at the start of a
+ * run (status "running", empty history, zeroed results; date and
+ * last_updated_at from start_epoch_secs).  params_json is the "params" object
+ * (experiment.rs:80-232), serialised by the caller that holds the run's
+ * options; it is written as given.  NULL commit / lineage_parent_id omit
+ * those fields; has_lineage = 0 omits "lineage"; has_fv_scale = 0 writes
+ * "fv_scale": null. */
+typedef struct TataraExperimentInit {
+    const char* path;
+    const char* id;
+    const char* name;
+    uint64_t start_epoch_secs;
+    const char* commit;
+    const char* command;
+    const char* generator_version;
+    int32_t has_lineage;
+    const char* lineage_parent_id;
+    const char* lineage_checkpoint;
+    uint64_t lineage_superbatch;
+    const char* params_json;
+    const char* data_name;
+    uint64_t data_positions;
+    int32_t has_fv_scale, fv_scale;
+} TataraExperimentInit;
+
+TATARA_API int32_t tatara_experiment_create(const TataraExperimentInit* init, TataraExperiment** out);
+TATARA_API int32_t tatara_experiment_destroy(TataraExperiment* e);
+/* set_target_superbatches (experiment.rs:392-396) */
+TATARA_API int32_t tatara_experiment_set_target_superbatches(TataraExperiment* e, uint64_t target);
+/* record_superbatch (experiment.rs:398-487): one history entry; best loss and
+ * best held-out loss (finite values only; a non-finite loss is recorded as
+ * 0.0 with a warning on stderr, a non-finite held-out metric is omitted);
+ * training_time_seconds = round(elapsed), mean_pos_per_sec =
+ * round(positions so far / elapsed), total_positions and dataset_passes.
+ * test_loss / test_accuracy may be NULL (no held-out validation). */
+TATARA_API int32_t tatara_experiment_record_superbatch(TataraExperiment* e, uint64_t superbatch, double mean_loss,
+                                                       uint64_t sb_positions, double elapsed_seconds,
+                                                       const double* test_loss, const double* test_accuracy);
+/* note_checkpoint, mark_finished, mark_interrupted (experiment.rs:489-507) */
+TATARA_API int32_t tatara_experiment_note_checkpoint(TataraExperiment* e, const char* file_name);
+TATARA_API int32_t tatara_experiment_mark_finished(TataraExperiment* e, double elapsed_seconds);
+TATARA_API int32_t tatara_experiment_mark_interrupted(TataraExperiment* e);
+/* write (experiment.rs:509-540): the pretty-printed document to <path>.tmp
+ * (parent directories created), then renamed over <path>. */
+TATARA_API int32_t tatara_experiment_write(TataraExperiment* e);
+/* format_utc_iso / format_utc_compact (experiment.rs:562-576):
+ * "YYYY-MM-DDTHH:MM:SSZ" (out: 21 bytes) and "YYYYMMDDtHHMMSSz" (17 bytes). */
+TATARA_API int32_t tatara_format_utc_iso(uint64_t epoch_secs, char* out);
+TATARA_API int32_t tatara_format_utc_compact(uint64_t epoch_secs, char* out);
+
+/* ------------------------------------------------------------------------ */
 /* Superbatch driver (crates/nnue-train/src/trainer.rs:759-1211, run)        */
 /* ------------------------------------------------------------------------ */
 
@@ -504,6 +562,14 @@ typedef struct TataraRunConfig {
     int32_t feature_set, bucket_mode, num_buckets;
     const float* progress_weights; /* device, 81*1548 f32, for the progress bucket mode */
     int32_t print_progress;         /* 1: the reference's per-superbatch line on stdout */
+    /* The run's experiment.json, or NULL (run's `experiment`, trainer.rs:747-766):
+     * written at the start, when control.json sets a new target, after every
+     * superbatch (with the checkpoint names it saved) and, marked completed,
+     * at the end; a failed write is reported on stderr and the run goes on.
+     * Its id is the run id written into resume checkpoints (run_id is then
+     * not used).  An error return leaves marking it interrupted to the
+     * caller, as the reference's CLI does. */
+    TataraExperiment* experiment;
 } TataraRunConfig;
 
 /* ControlState (crates/nnue-train/src/trainer.rs:640-656): the run's
@@ -546,8 +612,7 @@ typedef struct TataraRunSuperbatch {
  * superbatch; lr_seen / wdl_seen (capacity seen_cap, may be NULL) every
  * step's values.  <output_dir>/control.json is read at the start of every
  * superbatch (tatara_control_apply) and can end the run early.  Not covered:
- * experiment.json, held-out validation, score drop/clamp, shuffle windows,
- * monitors. */
+ * held-out validation, score drop/clamp, shuffle windows, monitors. */
 TATARA_API int32_t tatara_train_run(TataraTrainer* trainer, const TataraRunConfig* config,
                                     const TataraLrSchedule* lr, const TataraWdlSchedule* wdl,
                                     const TataraLoss* loss, TataraRunSuperbatch* report, uint64_t report_cap,

@@ -150,6 +150,28 @@ class TataraRunConfig(C.Structure):
         ("num_buckets", C.c_int32),
         ("progress_weights", C.c_void_p),
         ("print_progress", C.c_int32),
+        ("experiment", C.c_void_p),
+    ]
+
+
+class TataraExperimentInit(C.Structure):
+    _fields_ = [
+        ("path", C.c_char_p),
+        ("id", C.c_char_p),
+        ("name", C.c_char_p),
+        ("start_epoch_secs", C.c_uint64),
+        ("commit", C.c_char_p),
+        ("command", C.c_char_p),
+        ("generator_version", C.c_char_p),
+        ("has_lineage", C.c_int32),
+        ("lineage_parent_id", C.c_char_p),
+        ("lineage_checkpoint", C.c_char_p),
+        ("lineage_superbatch", C.c_uint64),
+        ("params_json", C.c_char_p),
+        ("data_name", C.c_char_p),
+        ("data_positions", C.c_uint64),
+        ("has_fv_scale", C.c_int32),
+        ("fv_scale", C.c_int32),
     ]
 
 
@@ -282,6 +304,19 @@ SIGNATURES = {
         [C.c_char_p, C.c_char_p, C.POINTER(TataraControlState), C.c_uint64, C.c_uint64, C.c_uint64, c_i32p,
          c_u64p],
     ),
+    "tatara_experiment_create": (C.c_int32, [C.POINTER(TataraExperimentInit), C.POINTER(C.c_void_p)]),
+    "tatara_experiment_destroy": (C.c_int32, [C.c_void_p]),
+    "tatara_experiment_set_target_superbatches": (C.c_int32, [C.c_void_p, C.c_uint64]),
+    "tatara_experiment_record_superbatch": (
+        C.c_int32,
+        [C.c_void_p, C.c_uint64, C.c_double, C.c_uint64, C.c_double, c_f64p, c_f64p],
+    ),
+    "tatara_experiment_note_checkpoint": (C.c_int32, [C.c_void_p, C.c_char_p]),
+    "tatara_experiment_mark_finished": (C.c_int32, [C.c_void_p, C.c_double]),
+    "tatara_experiment_mark_interrupted": (C.c_int32, [C.c_void_p]),
+    "tatara_experiment_write": (C.c_int32, [C.c_void_p]),
+    "tatara_format_utc_iso": (C.c_int32, [C.c_uint64, C.c_char_p]),
+    "tatara_format_utc_compact": (C.c_int32, [C.c_uint64, C.c_char_p]),
     "tatara_train_run": (
         C.c_int32,
         [C.c_void_p, C.POINTER(TataraRunConfig), C.POINTER(TataraLrSchedule), C.POINTER(TataraWdlSchedule),

@@ -35,6 +35,7 @@
 
 #include "../../include/tatara_hip.h"
 #include "common.hpp"
+#include "experiment.hpp"
 #include "psv_kernels.hpp"
 #include "schedule.hpp"
 #include "trainer_base.hpp"
@@ -561,9 +562,30 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
     const std::string history_path = out_dir + "/control_history.jsonl";
     TataraControlState control{};
     control.effective_target = c.end_superbatch;
-    for (uint64_t sb = c.start_superbatch;; ++sb) {
+    TataraExperiment* exp = c.experiment;
+    // the run id resume checkpoints carry: the experiment's when there is one
+    const std::string run_id = exp ? exp->id : (c.run_id ? c.run_id : "");
+    // a failed experiment.json write is reported and the run goes on
+    auto write_experiment = [&]() {
+        if (!exp) return;
+        const std::string err = exp->write();
+        if (!err.empty())
+            fprintf(stderr, "[train] warning: failed to write experiment log %s: %s\n", exp->path.c_str(),
+                    err.c_str());
+    };
+    write_experiment();  // status "running", before the first superbatch
+    const auto run_start = std::chrono::steady_clock::now();
+    auto run_seconds = [&]() {
+        return std::chrono::duration<double>(std::chrono::steady_clock::now() - run_start).count();
+    };
+    uint64_t sb = c.start_superbatch;
+    for (;; ++sb) {
         uint64_t applied = 0;
-        (void)apply_control(control_path, history_path, control, sb, c.start_superbatch, c.end_superbatch, &applied);
+        if (apply_control(control_path, history_path, control, sb, c.start_superbatch, c.end_superbatch, &applied) &&
+            exp) {
+            tatara_experiment_set_target_superbatches(exp, applied);
+            write_experiment();
+        }
         const auto t0 = std::chrono::steady_clock::now();
         double sb_loss = 0.0;
         uint64_t sb_positions = 0;
@@ -631,7 +653,7 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
                 return st;
             if (c.print_progress) printf("[train] checkpoint saved: %s.bin\n", base.c_str());
             if ((st = tatara_trainer_save_resume(trainer, (base + ".ckpt").c_str(), c.feature_set, c.bucket_mode,
-                                                 sb, c.run_id ? c.run_id : "", has_horizon ? horizon : 0)))
+                                                 sb, run_id.c_str(), has_horizon ? horizon : 0)))
                 return st;
             if (c.print_progress) printf("[train] resume checkpoint saved: %s.ckpt\n", base.c_str());
             if (c.has_keep_raw) prune_raw(out_dir, net_id, c.keep_raw_checkpoints);
@@ -647,7 +669,26 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             r.wdl = wdl_now;
             r.saved = saved ? 1 : 0;
         }
+        // after the superbatch's checkpoints exist (trainer.rs:1157-1173)
+        if (exp) {
+            tatara_experiment_record_superbatch(exp, sb, mean, sb_positions, run_seconds(), nullptr, nullptr);
+            if (saved) {
+                const std::string base = net_id + "-" + std::to_string(sb);
+                exp->checkpoints.push_back(base + ".bin");
+                exp->checkpoints.push_back(base + ".ckpt");
+            }
+            write_experiment();
+        }
         if (sb == control.effective_target) break;
+    }
+    if (c.print_progress) {
+        printf("[train] done in %s (%llu superbatches)\n", format_hms(run_seconds()).c_str(),
+               (unsigned long long)(sb + 1 - c.start_superbatch));
+        fflush(stdout);
+    }
+    if (exp) {
+        tatara_experiment_mark_finished(exp, run_seconds());
+        write_experiment();
     }
     return kOk;
 }

@@ -16,6 +16,7 @@ configured end as their horizon.
 from __future__ import annotations
 
 import ctypes as C
+import sys
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Optional
@@ -28,6 +29,13 @@ from .dataloader import BUCKET_MODES, FEATURE_SETS
 
 LR_CONSTANT, LR_STEP, LR_DROP, LR_LINEAR, LR_COSINE, LR_EXPONENTIAL, LR_ONE_CYCLE = range(7)
 WDL_CONSTANT, WDL_LINEAR = range(2)
+
+
+def _f(x: float) -> str:
+    """An f32 field as the schedules' Display impls print it."""
+    from .experiment import rust_display
+
+    return rust_display(x)
 
 
 class _LrBase:
@@ -63,6 +71,9 @@ class ConstantLR(_LrBase):
     def _c(self):
         return TataraLrSchedule(kind=LR_CONSTANT, start=self.value)
 
+    def __str__(self):  # schedule.rs:50-54
+        return f"constant {_f(self.value)}"
+
 
 @dataclass
 class StepLR(_LrBase):
@@ -73,6 +84,9 @@ class StepLR(_LrBase):
     def _c(self):
         return TataraLrSchedule(kind=LR_STEP, start=self.start, gamma=self.gamma, period=self.step)
 
+    def __str__(self):  # schedule.rs:100-108
+        return f"start {_f(self.start)} gamma {_f(self.gamma)} drop every {self.step} superbatches"
+
 
 @dataclass
 class DropLR(_LrBase):
@@ -82,6 +96,9 @@ class DropLR(_LrBase):
 
     def _c(self):
         return TataraLrSchedule(kind=LR_DROP, start=self.start, gamma=self.gamma, period=self.drop)
+
+    def __str__(self):  # schedule.rs:74-82
+        return f"start {_f(self.start)} gamma {_f(self.gamma)} drop at {self.drop} superbatches"
 
 
 @dataclass
@@ -94,6 +111,10 @@ class LinearDecayLR(_LrBase):
         return TataraLrSchedule(kind=LR_LINEAR, start=self.initial_lr, gamma=self.final_lr,
                                 period=self.final_superbatch)
 
+    def __str__(self):  # schedule.rs:132-140
+        return (f"start at {_f(self.initial_lr)} and linearly decay to {_f(self.final_lr)} at superbatch "
+                f"{self.final_superbatch}")
+
 
 @dataclass
 class CosineDecayLR(_LrBase):
@@ -105,6 +126,10 @@ class CosineDecayLR(_LrBase):
         return TataraLrSchedule(kind=LR_COSINE, start=self.initial_lr, gamma=self.final_lr,
                                 period=self.final_superbatch)
 
+    def __str__(self):  # schedule.rs:165-173
+        return (f"start at {_f(self.initial_lr)} and cosine decay to {_f(self.final_lr)} at superbatch "
+                f"{self.final_superbatch}")
+
 
 @dataclass
 class ExponentialDecayLR(_LrBase):
@@ -115,6 +140,10 @@ class ExponentialDecayLR(_LrBase):
     def _c(self):
         return TataraLrSchedule(kind=LR_EXPONENTIAL, start=self.initial_lr, gamma=self.final_lr,
                                 period=self.final_superbatch)
+
+    def __str__(self):  # schedule.rs:197-205
+        return (f"start at {_f(self.initial_lr)} and exponentially decay to {_f(self.final_lr)} at superbatch "
+                f"{self.final_superbatch}")
 
 
 class OneCycleLR(_LrBase):
@@ -132,6 +161,11 @@ class OneCycleLR(_LrBase):
         return TataraLrSchedule(kind=LR_ONE_CYCLE, start=self.initial_lr, gamma=self.final_lr, max_lr=self.max_lr,
                                 period=self.warmup_superbatch, total=self.total_superbatch)
 
+    def __str__(self):  # schedule.rs:282-294
+        return (f"one-cycle {_f(self.initial_lr)} \u2192 max {_f(self.max_lr)} (warmup to superbatch "
+                f"{self.warmup_superbatch}) \u2192 cosine anneal to {_f(self.final_lr)} at superbatch "
+                f"{self.total_superbatch}")
+
 
 @dataclass
 class WarmupLR(_LrBase):
@@ -144,6 +178,9 @@ class WarmupLR(_LrBase):
         s.warmup_batches = self.warmup_batches
         self._inner_keep = self.inner
         return s
+
+    def __str__(self):  # schedule.rs:321-329
+        return f"{self.inner}, warmup over {self.warmup_batches} batches"
 
 
 @dataclass
@@ -158,6 +195,9 @@ class SequenceLR(_LrBase):
         s.next = C.pointer(self._second)
         s.next_after = self.first_scheduler_final_superbatch
         return s
+
+    def __str__(self):  # schedule.rs:350-358
+        return f"{self.first}, then after {self.first_scheduler_final_superbatch} superbatches, {self.second}"
 
 
 class _WdlBase:
@@ -184,6 +224,9 @@ class ConstantWDL(_WdlBase):
     def _c(self):
         return TataraWdlSchedule(kind=WDL_CONSTANT, start=self.value)
 
+    def __str__(self):  # schedule.rs:451-455
+        return f"constant {_f(self.value)}"
+
 
 @dataclass
 class LinearWDL(_WdlBase):
@@ -192,6 +235,9 @@ class LinearWDL(_WdlBase):
 
     def _c(self):
         return TataraWdlSchedule(kind=WDL_LINEAR, start=self.start, end=self.end)
+
+    def __str__(self):  # schedule.rs:472-476
+        return f"linear taper start {_f(self.start)} end {_f(self.end)}"
 
 
 @dataclass
@@ -203,6 +249,9 @@ class WarmupWDL(_WdlBase):
         s = TataraWdlSchedule.from_buffer_copy(self.inner.to_c())
         s.warmup_batches = self.warmup_batches
         return s
+
+    def __str__(self):  # schedule.rs:496-504
+        return f"{self.inner}, warmup over {self.warmup_batches} batches"
 
 
 @dataclass
@@ -217,6 +266,9 @@ class SequenceWDL(_WdlBase):
         s.next = C.pointer(self._second)
         s.next_after = self.first_scheduler_final_superbatch
         return s
+
+    def __str__(self):  # schedule.rs:526-534
+        return f"{self.first}, then after {self.first_scheduler_final_superbatch} superbatches, {self.second}"
 
 
 @dataclass
@@ -238,6 +290,8 @@ class TrainingConfig:
     progress_weights: Optional[object] = None  # DeviceArray of f32, for progress8kpabs
     run_id: str = ""
     print_progress: bool = True
+    # the run's experiment.json (tatara_amd.experiment.ExperimentLogger), or None
+    experiment: Optional[object] = None
 
 
 @dataclass
@@ -272,11 +326,24 @@ def run(trainer, data_path, lr_scheduler, wdl_scheduler, cfg: TrainingConfig, lo
     c.num_buckets = cfg.num_buckets
     c.progress_weights = cfg.progress_weights.ptr if cfg.progress_weights is not None else None
     c.print_progress = int(cfg.print_progress)
+    c.experiment = cfg.experiment.handle if cfg.experiment is not None else None
     lr_c, wdl_c, loss_c = lr_scheduler.to_c(), wdl_scheduler.to_c(), loss.to_c()
-    check(trainer._lib.tatara_train_run(
-        trainer._h, C.byref(c), C.byref(lr_c), C.byref(wdl_c), C.byref(loss_c), rep, len(rep), C.byref(n_rep),
-        lr_seen.ctypes.data_as(C.POINTER(C.c_float)), wdl_seen.ctypes.data_as(C.POINTER(C.c_float)),
-        steps))
+    try:
+        check(trainer._lib.tatara_train_run(
+            trainer._h, C.byref(c), C.byref(lr_c), C.byref(wdl_c), C.byref(loss_c), rep, len(rep), C.byref(n_rep),
+            lr_seen.ctypes.data_as(C.POINTER(C.c_float)), wdl_seen.ctypes.data_as(C.POINTER(C.c_float)),
+            steps))
+    except Exception:
+        # an interrupted run keeps status "running" with results.interrupted
+        # set (training.rs:912-923)
+        if cfg.experiment is not None:
+            cfg.experiment.mark_interrupted()
+            try:
+                cfg.experiment.write()
+            except Exception as e:  # reported, as a failed write is
+                print(f"[train] warning: failed to write experiment log {cfg.experiment.path}: {e}",
+                      file=sys.stderr)
+        raise
     out = RunResult(lr_seen=lr_seen[:steps], wdl_seen=wdl_seen[:steps])
     for r in rep[:n_rep.value]:
         out.superbatches.append(dict(superbatch=r.superbatch, positions=r.positions, loss_sum=r.loss_sum,

@@ -39,12 +39,21 @@ CHECK(TataraCkptHeader, superbatch, 8);
 CHECK(TataraCkptHeader, header_bytes, 40);
 CHECK(TataraCkptHeader, run_id, 48);
 
-static_assert(sizeof(TataraRunConfig) == 128, "TataraRunConfig size");
+static_assert(sizeof(TataraRunConfig) == 136, "TataraRunConfig size");
 CHECK(TataraRunConfig, start_superbatch, 32);
 CHECK(TataraRunConfig, has_fv_scale, 72);
 CHECK(TataraRunConfig, keep_raw_checkpoints, 88);
 CHECK(TataraRunConfig, progress_weights, 112);
 CHECK(TataraRunConfig, print_progress, 120);
+CHECK(TataraRunConfig, experiment, 128);
+
+static_assert(sizeof(TataraExperimentInit) == 120, "TataraExperimentInit size");
+CHECK(TataraExperimentInit, start_epoch_secs, 24);
+CHECK(TataraExperimentInit, has_lineage, 56);
+CHECK(TataraExperimentInit, lineage_parent_id, 64);
+CHECK(TataraExperimentInit, params_json, 88);
+CHECK(TataraExperimentInit, has_fv_scale, 112);
+CHECK(TataraExperimentInit, fv_scale, 116);
 
 #define F(T, f) printf("%s %s %zu %zu\n", #T, #f, offsetof(T, f), sizeof(((T*)0)->f))
 #define S(T) printf("%s sizeof %zu %zu\n", #T, (size_t)0, sizeof(T))
@@ -89,6 +98,16 @@ int main(void) {
     F(TataraRunConfig, has_fv_scale); F(TataraRunConfig, fv_scale); F(TataraRunConfig, has_keep_raw);
     F(TataraRunConfig, keep_raw_checkpoints); F(TataraRunConfig, feature_set); F(TataraRunConfig, bucket_mode);
     F(TataraRunConfig, num_buckets); F(TataraRunConfig, progress_weights); F(TataraRunConfig, print_progress);
+    F(TataraRunConfig, experiment);
+
+    S(TataraExperimentInit);
+    F(TataraExperimentInit, path); F(TataraExperimentInit, id); F(TataraExperimentInit, name);
+    F(TataraExperimentInit, start_epoch_secs); F(TataraExperimentInit, commit); F(TataraExperimentInit, command);
+    F(TataraExperimentInit, generator_version); F(TataraExperimentInit, has_lineage);
+    F(TataraExperimentInit, lineage_parent_id); F(TataraExperimentInit, lineage_checkpoint);
+    F(TataraExperimentInit, lineage_superbatch); F(TataraExperimentInit, params_json);
+    F(TataraExperimentInit, data_name); F(TataraExperimentInit, data_positions);
+    F(TataraExperimentInit, has_fv_scale); F(TataraExperimentInit, fv_scale);
 
     S(TataraRunSuperbatch);
     F(TataraRunSuperbatch, superbatch); F(TataraRunSuperbatch, positions); F(TataraRunSuperbatch, loss_sum);

@@ -249,3 +249,94 @@ def test_control_keeps_the_schedule_horizon(gpu, tmp_path):
     assert ctl.lr_seen[:4].tobytes() == base.lr_seen[:4].tobytes()
     assert ctl.wdl_seen[:4].tobytes() == base.wdl_seen[:4].tobytes()
     assert [r["loss_sum"] for r in ctl.superbatches] == [r["loss_sum"] for r in base.superbatches[:2]]
+
+
+def _logger(out, run_id, data_path, cfg, lr, wdl, loss):
+    from tatara_amd import experiment as X
+
+    info = feature_set_info("halfkp")
+    params = X.simple_params(simple_cfg(), cfg, loss, lr, wdl, ft_in=info["ft_in"])
+    return X.ExperimentLogger.for_data(out / "experiments" / f"{run_id}.json", run_id, cfg.net_id, params,
+                                       data_path, command="pytest", start_epoch_secs=1_700_000_000,
+                                       fv_scale=cfg.fv_scale)
+
+
+def test_run_writes_experiment_json(gpu, tmp_path):
+    # trainer.rs:1746 run_writes_experiment_json: start 1, end 3, save_rate 2
+    import oracle.experiment as oex
+
+    path, recs = write_psv(tmp_path, 3 * B + 40)
+    out = tmp_path / "out"
+    lr, wdl, loss = R.StepLR(1e-3, 0.9, 1), R.ConstantWDL(0.0), Wrm()
+    cfg = R.TrainingConfig(net_id="net", feature_set="halfkp", output_dir=str(out), start_superbatch=1,
+                           end_superbatch=3, batches_per_superbatch=2, batch_size=B, save_rate=2, fv_scale=16,
+                           print_progress=False, run_id="ignored-when-logged")
+    log = _logger(out, "exp-test", path, cfg, lr, wdl, loss)
+    cfg.experiment = log
+    with SimpleTrainer(simple_cfg()) as t:
+        res = R.run(t, path, lr, wdl, cfg, loss)
+    doc = json.loads((out / "experiments" / "exp-test.json").read_text())
+    assert doc["status"] == "completed" and doc["results"]["interrupted"] is False
+    assert len(doc["history"]) == 3
+    assert doc["checkpoints"] == ["net-2.bin", "net-2.ckpt", "net-3.bin", "net-3.ckpt"]
+    # the oracle document after the same calls, the wall-clock fields apart
+    ora = oex.Experiment("exp-test", "net", 1_700_000_000, "pytest", doc["params"], "data.psv", 3 * B + 40,
+                         fv_scale=16, generator_version=doc["generator"]["version"])
+    for r in res.superbatches:
+        ora.record_superbatch(r["superbatch"], r["mean_loss"], r["positions"], 1.0)
+        if r["saved"]:
+            for ext in ("bin", "ckpt"):
+                ora.note_checkpoint(f"net-{r['superbatch']}.{ext}")
+    ora.mark_finished(1.0)
+    want = ora.document()
+    for d in (doc, want):
+        d["last_updated_at"] = None
+        d["results"]["training_time_seconds"] = d["results"]["mean_pos_per_sec"] = None
+    assert doc == want
+    assert doc["params"]["lr_schedule"] == "start 0.001 gamma 0.9 drop every 1 superbatches"
+    # resume checkpoints carry the experiment's id as the producer run id
+    with SimpleTrainer(simple_cfg()) as t3:
+        for sb in (2, 3):
+            got_sb, run_id, _ = t3.load_resume_checkpoint(str(out / f"net-{sb}.ckpt"), "halfkp", None)
+            assert (got_sb, run_id) == (sb, "exp-test")
+    log.close()
+
+
+def test_control_stop_records_target_in_experiment_json(gpu, tmp_path):
+    # trainer.rs:1805 control_stops_after_current_superbatch_and_records_completion
+    path, _ = write_psv(tmp_path, 2 * B)
+    out = tmp_path / "stop"
+    out.mkdir()
+    (out / "control.json").write_text('{"target_superbatches": 1}')
+    lr, wdl, loss = R.StepLR(1e-3, 0.9, 1), R.ConstantWDL(0.0), Wrm()
+    cfg = R.TrainingConfig(net_id="test", feature_set="halfkp", output_dir=str(out), start_superbatch=1,
+                           end_superbatch=3, batches_per_superbatch=2, batch_size=B, save_rate=10, fv_scale=16,
+                           print_progress=False)
+    log = _logger(out, "control-stop", path, cfg, lr, wdl, loss)
+    cfg.experiment = log
+    with SimpleTrainer(simple_cfg()) as t:
+        R.run(t, path, lr, wdl, cfg, loss)
+    doc = json.loads((out / "experiments" / "control-stop.json").read_text())
+    assert doc["status"] == "completed"
+    assert doc["results"]["target_superbatches"] == 1
+    assert len(doc["history"]) == 1
+    assert doc["checkpoints"] == ["test-1.bin", "test-1.ckpt"]
+    log.close()
+
+
+def test_failed_run_marks_experiment_interrupted(gpu, tmp_path):
+    # training.rs:912-923: an error leaves status "running" with interrupted set
+    bad = tmp_path / "bad.psv"
+    bad.write_bytes(b"\x00" * 39)  # not a whole record
+    out = tmp_path / "out"
+    lr, wdl, loss = R.ConstantLR(1e-3), R.ConstantWDL(0.0), Wrm()
+    cfg = R.TrainingConfig(net_id="net", feature_set="halfkp", output_dir=str(out), start_superbatch=1,
+                           end_superbatch=2, batches_per_superbatch=1, batch_size=B, print_progress=False)
+    log = _logger(out, "failed", bad, cfg, lr, wdl, loss)
+    cfg.experiment = log
+    with SimpleTrainer(simple_cfg()) as t, pytest.raises(TataraError):
+        R.run(t, bad, lr, wdl, cfg, loss)
+    doc = json.loads((out / "experiments" / "failed.json").read_text())
+    assert doc["status"] == "running" and doc["results"]["interrupted"] is True
+    assert doc["history"] == []
+    log.close()
