@@ -60,6 +60,15 @@ __device__ __forceinline__ uint32_t xcd_swizzle(uint32_t bid, uint32_t nblocks) 
     return (bid % kNumXcd) * per + bid / kNumXcd;
 }
 
+// A wave-uniform load of data the kernel only reads, through the scalar
+// cache (s_load, given a uniform address).  Its wait (lgkmcnt) leaves the
+// wave's vector loads in flight, where a vector load of the same address
+// would be waited for (vmcnt) behind all of them.
+template <typename T>
+__device__ __forceinline__ T scalar_load(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
+
 __device__ __forceinline__ float crelu01(float x) {
     return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x);
 }

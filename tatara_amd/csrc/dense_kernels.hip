@@ -602,16 +602,25 @@ __device__ __forceinline__ float clamp_f16_range(float v, uint32_t& clamps) {
 
 // Each lane owns CPL consecutive combined columns c..c+CPL-1 (all on one
 // perspective's half); a 128-lane block covers 128 * CPL columns
-// (ft_out % (128 * CPL) == 0).  The rows of a tile are taken RB at a time:
-// their raw-sum pairs are loaded before any of the RB is computed.
-// H16: f16 raw sums and dft.
+// (ft_out % (128 * CPL) == 0).  A tile's rows are taken in groups of RB, an
+// even number of groups per tile.  A tile's row ids, dl1 rows and bin are
+// loaded one tile ahead (lane r holds row r's id, lane i float4 i of the
+// dl1 rows; readlane hands each lane a row's values, which are the same for
+// every lane), and each group's raw-sum pairs are loaded while the group
+// before it is computed (two register sets; the loads are unconditional,
+// from row 0 where a row is padding, so the wait before a group counts only
+// the loads issued after it).  H16: f16 raw sums and dft.
 template <int L1, int CPL, int RB, bool H16>
 __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) {
-    static_assert(16 % RB == 0, "RB rows loaded ahead of their compute, a divisor of the tile");
+    static_assert(16 % RB == 0 && (16 / RB) % 2 == 0, "an even number of RB-row groups per tile");
+    constexpr int G = 16 / RB;
+    constexpr int DL = 16 * L1 / 4;  // float4 of a tile's dl1 rows
+    static_assert(DL <= 64, "a tile's dl1 rows in one float4 per lane");
     const uint32_t ft_out = a.ft_out, half = ft_out / 2;
     const uint64_t batch = a.batch;
     const uint32_t c = (blockIdx.x * 128 + threadIdx.x) * CPL;
     if (c >= ft_out) return;
+    const uint32_t lane = threadIdx.x % 64;
     const uint32_t persp = c < half ? 0 : 1;
     const uint32_t p = c - persp * half;
     const _Float16* ft16 = reinterpret_cast<const _Float16*>(persp ? a.ft_nstm16 : a.ft_stm16);
@@ -637,12 +646,59 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
     float acc_a[CPL] = {}, acc_b[CPL] = {};
     uint32_t clamps = 0;
     const uint32_t tile0 = blockIdx.y * kPostTiles;
-    for (uint32_t tt = 0; tt < kPostTiles; ++tt) {
-        const uint64_t tile = tile0 + tt;
-        if (tile * 16 >= a.padded_b) break;
-        const int32_t bin = a.sorted_bin[tile * 16];
-        if (bin < 0) continue;
-        if (bin != cur_bin) {
+    const uint32_t tiles_total = (uint32_t)(a.padded_b / 16);
+    const uint32_t n_tiles = tile0 < tiles_total ? min((uint32_t)kPostTiles, tiles_total - tile0) : 0u;
+    auto tile_perm = [&](uint32_t tile) -> int32_t { return a.perm[(uint64_t)tile * 16 + (lane & 15u)]; };
+    auto tile_dl1 = [&](uint32_t tile) -> float4 {
+        return reinterpret_cast<const float4*>(a.dl1_sorted + (uint64_t)tile * 16 * L1)[lane % DL];
+    };
+    auto bcast_i = [](int32_t v, int l) -> int32_t { return __builtin_amdgcn_readlane(v, l); };
+    auto bcast_f = [](float v, int l) -> float {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+    };
+    float xr[2][RB][CPL], yr[2][RB][CPL];
+    // group G0's raw-sum pairs (row ids from PERMV) into register set BUF
+#define TATARA_POST_LOAD(BUF, PERMV, G0)                                                      \
+    _Pragma("unroll") for (int r = 0; r < RB; ++r) {                                         \
+        const int32_t o_ = bcast_i((PERMV), (G0) * RB + r);                                  \
+        const uint64_t base = (uint64_t)(o_ >= 0 ? o_ : 0) * ft_out + p;                      \
+        if constexpr (CPL == 1) {                                                             \
+            xr[BUF][r][0] = H16 ? (float)ft16[base] : ft32[base];                             \
+            yr[BUF][r][0] = H16 ? (float)ft16[base + half] : ft32[base + half];               \
+        } else if constexpr (H16) {                                                           \
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));                          \
+            const h2 x_ = *reinterpret_cast<const h2*>(ft16 + base);                          \
+            const h2 y_ = *reinterpret_cast<const h2*>(ft16 + base + half);                   \
+            xr[BUF][r][0] = (float)x_.x;                                                      \
+            xr[BUF][r][1] = (float)x_.y;                                                      \
+            yr[BUF][r][0] = (float)y_.x;                                                      \
+            yr[BUF][r][1] = (float)y_.y;                                                      \
+        } else {                                                                              \
+            const float2 x_ = *reinterpret_cast<const float2*>(ft32 + base);                  \
+            const float2 y_ = *reinterpret_cast<const float2*>(ft32 + base + half);           \
+            xr[BUF][r][0] = x_.x;                                                             \
+            xr[BUF][r][1] = x_.y;                                                             \
+            yr[BUF][r][0] = y_.x;                                                             \
+            yr[BUF][r][1] = y_.y;                                                             \
+        }                                                                                     \
+    }
+    int32_t perm_c = 0, bin_c = -1;
+    float4 dl1_c = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n_tiles) {
+        perm_c = tile_perm(tile0);
+        dl1_c = tile_dl1(tile0);
+        bin_c = scalar_load(a.sorted_bin + (uint64_t)tile0 * 16);
+        TATARA_POST_LOAD(0, perm_c, 0)
+    }
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const uint32_t tile = tile0 + t;
+        const bool has_next = t + 1 < n_tiles;
+        const uint32_t tn = has_next ? tile + 1 : tile;  // the last tile re-reads itself, unused
+        const int32_t perm_n = tile_perm(tn);
+        const float4 dl1_n = tile_dl1(tn);
+        const int32_t bin_n = has_next ? scalar_load(a.sorted_bin + (uint64_t)tn * 16) : -1;
+        const int32_t bin = bin_c;  // < 0: a trailing all-padding tile
+        if (bin >= 0 && bin != cur_bin) {
             cur_bin = bin;
             bvalid = (uint32_t)bin < a.nb;
 #pragma unroll
@@ -658,43 +714,26 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
             }
         }
 #pragma unroll
-        for (int r0 = 0; r0 < 16; r0 += RB) {
-            int32_t orig[RB];
-            float xr[RB][CPL], yr[RB][CPL];
-#pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                orig[r] = a.perm[tile * 16 + r0 + r];
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) xr[r][j] = yr[r][j] = 0.0f;
-                if (orig[r] >= 0) {
-                    // (written out: a helper taking xr[r] by reference cost
-                    // 7 VGPRs and one wave per SIMD)
-                    const uint64_t base = (uint64_t)orig[r] * ft_out + p;
-                    if constexpr (CPL == 1) {
-                        xr[r][0] = H16 ? (float)ft16[base] : ft32[base];
-                        yr[r][0] = H16 ? (float)ft16[base + half] : ft32[base + half];
-                    } else if constexpr (H16) {
-                        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                        const h2 x = *reinterpret_cast<const h2*>(ft16 + base);
-                        const h2 y = *reinterpret_cast<const h2*>(ft16 + base + half);
-                        xr[r][0] = (float)x.x;
-                        xr[r][1] = (float)x.y;
-                        yr[r][0] = (float)y.x;
-                        yr[r][1] = (float)y.y;
-                    } else {
-                        const float2 x = *reinterpret_cast<const float2*>(ft32 + base);
-                        const float2 y = *reinterpret_cast<const float2*>(ft32 + base + half);
-                        xr[r][0] = x.x;
-                        xr[r][1] = x.y;
-                        yr[r][0] = y.x;
-                        yr[r][1] = y.y;
-                    }
-                }
+        for (int g = 0; g < G; ++g) {
+            // the next group's loads first: of this tile, or the next tile's first
+            if (g + 1 < G) {
+                TATARA_POST_LOAD((g + 1) & 1, perm_c, g + 1)
+            } else {
+                TATARA_POST_LOAD(0, perm_n, 0)
             }
+            if (bin < 0) continue;
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
-                if (orig[r] < 0) continue;
-                const float* d = a.dl1_sorted + (tile * 16 + r0 + r) * L1;
+                const int row_in_tile = g * RB + r;
+                const int32_t orig = bcast_i(perm_c, row_in_tile);
+                if (orig < 0) continue;
+                float d[L1];
+#pragma unroll
+                for (int o = 0; o < L1; ++o) {
+                    const int e = row_in_tile * L1 + o;
+                    const float comp = (e & 3) == 0 ? dl1_c.x : (e & 3) == 1 ? dl1_c.y : (e & 3) == 2 ? dl1_c.z : dl1_c.w;
+                    d[o] = bcast_f(comp, e >> 2);
+                }
                 float ga[CPL], gb[CPL];
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
@@ -707,14 +746,14 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
 #pragma unroll
                     for (int o = 0; o < L1; ++o) db = __builtin_fmaf(d[o], ws[j][o], db);
                     const float dy = da + db;
-                    const float xa = xr[r][j] + ba[j], xb = yr[r][j] + bb[j];
+                    const float xa = xr[g & 1][r][j] + ba[j], xb = yr[g & 1][r][j] + bb[j];
                     const float ya = crelu01(xa), yb = crelu01(xb);
                     ga[j] = (xa > 0.0f && xa < 1.0f) ? dy * yb * a.ft_post_scale : 0.0f;
                     gb[j] = (xb > 0.0f && xb < 1.0f) ? dy * ya * a.ft_post_scale : 0.0f;
                     acc_a[j] += ga[j];
                     acc_b[j] += gb[j];
                 }
-                const uint64_t row = (uint64_t)orig[r] * kDftChunk;
+                const uint64_t row = (uint64_t)orig * kDftChunk;
                 if constexpr (H16) {
                     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
                     const float sc = a.dft_scale;
@@ -740,7 +779,11 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
                 }
             }
         }
+        perm_c = perm_n;
+        dl1_c = dl1_n;
+        bin_c = bin_n;
     }
+#undef TATARA_POST_LOAD
     float* pp = a.ftb_partial + ((uint64_t)blockIdx.y * 2 + persp) * ft_out;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -907,8 +950,8 @@ int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
     const dim3 grid(a.ft_out / (two ? 256 : 128), rows);
     // f32: two columns per lane, rows four at a time; f16: one column per
     // lane, all 16 rows of a tile ahead (each measured fastest for its type)
-    auto kernel = a.dft16 ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 16, true>
-                                        : ls_l1_input_post_c_kernel<8, 1, 16, true>)
+    auto kernel = a.dft16 ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 8, true>
+                                        : ls_l1_input_post_c_kernel<8, 1, 8, true>)
                           : two ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 2, 4, false>
                                               : ls_l1_input_post_c_kernel<8, 2, 4, false>)
                                 : (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 4, false>

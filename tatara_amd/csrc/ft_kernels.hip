@@ -1050,10 +1050,13 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
 
     // Stage T in registers: wave w's rows RT + RW w + j, the lane's columns
     // 4 lane .. 4 lane + 3 (rows past the list are zero), and the thread's
-    // mask words.  Stage T+1's rows are loaded while stage T is multiplied;
-    // the positions of a stage's rows are loaded two stages ahead, so the
-    // row loads never wait on them.  (Deeper register pipelines need the
-    // stage loop unrolled, which makes the register allocator copy the
+    // mask words.  Stage T+1's rows are loaded while stage T is multiplied.
+    // The positions of a stage's rows are loaded one stage ahead, into the
+    // register the row addresses have just been read from: a ring of two
+    // position registers needs a copy of a load in flight, and waiting for
+    // that load (loads complete in order) waited for the stage's row loads
+    // too, before any multiply.  (Deeper register pipelines need the stage
+    // loop unrolled, which makes the register allocator copy the
     // accumulators and halves the occupancy.)
     struct Stage {
         uint32_t r[RW];
@@ -1102,11 +1105,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
         for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     Stage S;
-    uint32_t p1 = 0, p2 = 0;  // positions of stages t+1 and t+2
+    uint32_t P = 0;  // positions of the next stage to load
     if (n_stages > 0) {
         load_rows(S, load_pos(0), 0);
-        p1 = load_pos(1);
-        p2 = load_pos(2);
+        P = load_pos(1);
         store_rows(S, 0);
     }
     __syncthreads();
@@ -1114,9 +1116,8 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
         const uint32_t buf = t & 1u;
         const bool more = t + 1 < n_stages;
         if (more) {
-            load_rows(S, p1, t + 1);
-            p1 = p2;
-            p2 = load_pos(t + 3);
+            load_rows(S, P, t + 1);
+            P = load_pos(t + 2);
         }
 #pragma unroll
         for (uint32_t ks = 0; ks < KS; ++ks) {
