@@ -529,15 +529,13 @@ __device__ __forceinline__ CellState<V, HSTATE> load_cells(const FtGradArgs& a, 
     return c;
 }
 
-// RAdam (+ Ranger lerp every lookahead step) of the loaded cells with
-// gradient g, and the stores: weights, moments (f16 moments as
-// radam_step_f16state, native_kernels.cu:1118-1170: read back as f16 / scale,
-// stored as f16(m * m_scale) clamped to +-65504 and f16(v * v_scale) clamped
-// above at 65504, a NaN staying NaN), and the f16 mirror of the new weights
-// when the forward reads one.
+// RAdam of the loaded cells with gradient g: the new weights, and the new
+// moments in c (f16 moments as radam_step_f16state,
+// native_kernels.cu:1118-1170: read back as f16 / scale, stored as
+// f16(m * m_scale) clamped to +-65504 and f16(v * v_scale) clamped above at
+// 65504, a NaN staying NaN).
 template <int V, bool HSTATE>
-__device__ __forceinline__ void apply_cells(const FtGradArgs& a, uint64_t off, vecf<V> g,
-                                            CellState<V, HSTATE> c) {
+__device__ __forceinline__ vecf<V> radam_cells(const FtGradArgs& a, vecf<V> g, CellState<V, HSTATE>& c) {
     const OptScalars& s = a.opt;
     vecf<V> W = c.w;
 #pragma unroll
@@ -564,18 +562,26 @@ __device__ __forceinline__ void apply_cells(const FtGradArgs& a, uint64_t off, v
             c.v[k] = v;
         }
     }
-    if (s.lookahead) {
-        vecf<V>* s_ = reinterpret_cast<vecf<V>*>(a.slow) + off;
-        vecf<V> S = __builtin_nontemporal_load(s_);
+    return W;
+}
+
+// The Ranger lerp of the new weights W and the slow weights S.
+template <int V>
+__device__ __forceinline__ void lerp_cells(const FtGradArgs& a, vecf<V>& W, vecf<V>& S) {
 #pragma unroll
-        for (int k = 0; k < V; ++k) {
-            float x = W[k], y = S[k];
-            lerp_elem(x, y, s.alpha);
-            W[k] = x;
-            S[k] = y;
-        }
-        __builtin_nontemporal_store(S, s_);
+    for (int k = 0; k < V; ++k) {
+        float x = W[k], y = S[k];
+        lerp_elem(x, y, a.opt.alpha);
+        W[k] = x;
+        S[k] = y;
     }
+}
+
+// The stores of updated cells: weights, moments, and the f16 mirror of the
+// new weights when the forward reads one.
+template <int V, bool HSTATE>
+__device__ __forceinline__ void store_cells(const FtGradArgs& a, uint64_t off, vecf<V> W,
+                                            const CellState<V, HSTATE>& c) {
     using Mom = typename CellState<V, HSTATE>::Mom;
     __builtin_nontemporal_store(W, reinterpret_cast<vecf<V>*>(a.w) + off);
     if constexpr (HSTATE) {
@@ -588,6 +594,82 @@ __device__ __forceinline__ void apply_cells(const FtGradArgs& a, uint64_t off, v
     if (a.mirror16)
         __builtin_nontemporal_store(__builtin_convertvector(W, vech<V>),
                                     reinterpret_cast<vech<V>*>(a.mirror16) + off);
+}
+
+// RAdam (+ Ranger lerp every lookahead step) of the loaded cells with
+// gradient g, and the stores.
+template <int V, bool HSTATE>
+__device__ __forceinline__ void apply_cells(const FtGradArgs& a, uint64_t off, vecf<V> g,
+                                            CellState<V, HSTATE> c) {
+    vecf<V> W = radam_cells<V, HSTATE>(a, g, c);
+    if (a.opt.lookahead) {
+        vecf<V>* s_ = reinterpret_cast<vecf<V>*>(a.slow) + off;
+        vecf<V> S = __builtin_nontemporal_load(s_);
+        lerp_cells<V>(a, W, S);
+        __builtin_nontemporal_store(S, s_);
+    }
+    store_cells<V, HSTATE>(a, off, W, c);
+}
+
+// The fused update of F feature rows f0 + k (k < nf, nf >= 1) at the lane's
+// columns col .. col + 3, with gradients g[k], each row's state loaded D rows
+// ahead of its update.  The loads are unconditional (rows past nf re-load
+// row nf - 1 and are not stored) and come before the earlier rows' stores in
+// program order, so the wave keeps loads in flight and the wait before a
+// row's update counts only the loads issued after its own.  A row's address
+// is a wave-uniform base plus the lane's 32-bit column offset.  LA: this
+// step's Ranger lerp, the slow weights loaded with the rest of the state.
+template <int F, int D, bool HSTATE, bool LA>
+__device__ __forceinline__ void update_rows_pipelined(const FtGradArgs& a, uint64_t f0, uint32_t col, uint32_t nf,
+                                                      const vecf<4>* g) {
+    using Mom = typename CellState<4, HSTATE>::Mom;
+    const uint64_t ft_out = a.ft_out;
+    // the lane's byte offsets within a row: f32 values and f16 moments
+    const uint32_t b32 = col * 4u, b16 = col * 2u;
+    auto at = [](auto* base, uint64_t row_elem, uint32_t lane_bytes) {
+        using T = typename std::remove_pointer<decltype(base)>::type;
+        return reinterpret_cast<T*>(reinterpret_cast<char*>(base + row_elem) + lane_bytes);
+    };
+    auto row_of = [&](int j) -> uint64_t { return (f0 + ((uint32_t)j < nf ? (uint32_t)j : nf - 1)) * ft_out; };
+    CellState<4, HSTATE> cs[F];
+    vecf<4> sl[F];
+    auto load = [&](int j) {
+        const uint64_t r = row_of(j);
+        cs[j].w = __builtin_nontemporal_load(reinterpret_cast<const vecf<4>*>(at(a.w, r, b32)));
+        if constexpr (HSTATE) {
+            cs[j].m = __builtin_nontemporal_load(reinterpret_cast<const Mom*>(at(a.m16, r, b16)));
+            cs[j].v = __builtin_nontemporal_load(reinterpret_cast<const Mom*>(at(a.v16, r, b16)));
+        } else {
+            cs[j].m = __builtin_nontemporal_load(reinterpret_cast<const Mom*>(at(a.m, r, b32)));
+            cs[j].v = __builtin_nontemporal_load(reinterpret_cast<const Mom*>(at(a.v, r, b32)));
+        }
+        if constexpr (LA) sl[j] = __builtin_nontemporal_load(reinterpret_cast<const vecf<4>*>(at(a.slow, r, b32)));
+    };
+#pragma unroll
+    for (int j = 0; j < D && j < F; ++j) load(j);
+#pragma unroll
+    for (int k = 0; k < F; ++k) {
+        if (k + D < F) load(k + D);
+        if ((uint32_t)k < nf) {
+            const uint64_t r = (f0 + (uint32_t)k) * ft_out;
+            vecf<4> W = radam_cells<4, HSTATE>(a, g[k], cs[k]);
+            if constexpr (LA) {
+                lerp_cells<4>(a, W, sl[k]);
+                __builtin_nontemporal_store(sl[k], reinterpret_cast<vecf<4>*>(at(a.slow, r, b32)));
+            }
+            __builtin_nontemporal_store(W, reinterpret_cast<vecf<4>*>(at(a.w, r, b32)));
+            if constexpr (HSTATE) {
+                __builtin_nontemporal_store(cs[k].m, reinterpret_cast<Mom*>(at(a.m16, r, b16)));
+                __builtin_nontemporal_store(cs[k].v, reinterpret_cast<Mom*>(at(a.v16, r, b16)));
+            } else {
+                __builtin_nontemporal_store(cs[k].m, reinterpret_cast<Mom*>(at(a.m, r, b32)));
+                __builtin_nontemporal_store(cs[k].v, reinterpret_cast<Mom*>(at(a.v, r, b32)));
+            }
+            if (a.mirror16)
+                __builtin_nontemporal_store(__builtin_convertvector(W, vech<4>),
+                                            reinterpret_cast<vech<4>*>(at(a.mirror16, r, b16)));
+        }
+    }
 }
 
 // One cell group's update in the moment format the trainer uses.
@@ -752,7 +834,8 @@ __global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanG
 // and the sum is multiplied by dft_inv_scale at the end, as the
 // occurrence-list kernel does.
 template <bool HDFT, bool HSTATE>
-__global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArgs a, FtBlockScan s,
+__global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void ft_grad_scan_kernel(
+    FtGradArgs a, FtBlockScan s,
                                                                        ScanGeom geom) {
     constexpr int R = kScanStage, RPW = kScanStage / kScanWaves;
     static_assert(R == 32 && (RPW == 2 || RPW == 4), "32 rows per stage, two or four per wave");
@@ -905,28 +988,40 @@ __global__ __launch_bounds__(kScanWaves * 64) void ft_grad_scan_kernel(FtGradArg
     if (col >= a.ft_out) return;
     vecf<4>* grad = reinterpret_cast<vecf<4>*>(a.grad);
     const uint64_t off0 = ((uint64_t)f0 * a.ft_out + col) / 4, row4 = a.ft_out / 4;
-    // the state of two features is loaded before either is updated
-    constexpr int kB = 2;
-    static_assert(kScanFeat % kB == 0, "feature batches");
+    if (nf == 0) return;
+    vecf<4> gv[kScanFeat];
 #pragma unroll
-    for (int kb = 0; kb < kScanFeat; kb += kB) {
-        CellState<4, HSTATE> cs[kB];
-        if (a.apply_update) {
+    for (int k = 0; k < kScanFeat; ++k) {
+        gv[k] = vecf<4>{acc[k].x, acc[k].y, acc[k].z, acc[k].w};
+        if constexpr (HDFT) gv[k] *= a.dft_inv_scale;
+        if (a.grad && (uint32_t)k < nf) __builtin_nontemporal_store(gv[k], grad + off0 + k * row4);
+    }
+    if (!a.apply_update) return;
+    // The update loads each row's state two rows ahead of it (one on a
+    // lookahead step, which also loads the slow weights).  To make room for
+    // that, the gradients of the wave's first kParked rows wait in the stage
+    // buffers (free after the last barrier; each wave its own part) while
+    // the other rows are updated from registers.
+    constexpr int kParked = (int)(sizeof(s_rows) / (kScanWaves * 64 * sizeof(vecf<4>))) < kScanFeat / 2
+                                ? (int)(sizeof(s_rows) / (kScanWaves * 64 * sizeof(vecf<4>)))
+                                : kScanFeat / 2;
+    vecf<4>* parked = reinterpret_cast<vecf<4>*>(&s_rows[0][0][0]) + (uint32_t)wave * kParked * 64 + lane;
 #pragma unroll
-            for (int u = 0; u < kB; ++u)
-                if ((uint32_t)(kb + u) < nf) cs[u] = load_cells<4, HSTATE>(a, off0 + (kb + u) * row4);
-        }
+    for (int k = 0; k < kParked; ++k) parked[k * 64] = gv[k];
+    const uint32_t nf_hi = nf > (uint32_t)kParked ? nf - kParked : 0u;
+    vecf<4> g_lo[kParked];
+    if (a.opt.lookahead) {
+        if (nf_hi)
+            update_rows_pipelined<kScanFeat - kParked, 1, HSTATE, true>(a, f0 + kParked, col, nf_hi, gv + kParked);
 #pragma unroll
-        for (int u = 0; u < kB; ++u) {
-            const int k = kb + u;
-            if ((uint32_t)k < nf) {
-                const uint64_t off = off0 + k * row4;
-                vecf<4> gr = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
-            if constexpr (HDFT) gr *= a.dft_inv_scale;
-                if (a.grad) __builtin_nontemporal_store(gr, grad + off);
-                if (a.apply_update) apply_cells<4, HSTATE>(a, off, gr, cs[u]);
-            }
-        }
+        for (int k = 0; k < kParked; ++k) g_lo[k] = parked[k * 64];
+        update_rows_pipelined<kParked, 1, HSTATE, true>(a, f0, col, nf < (uint32_t)kParked ? nf : kParked, g_lo);
+    } else {
+        if (nf_hi)
+            update_rows_pipelined<kScanFeat - kParked, 2, HSTATE, false>(a, f0 + kParked, col, nf_hi, gv + kParked);
+#pragma unroll
+        for (int k = 0; k < kParked; ++k) g_lo[k] = parked[k * 64];
+        update_rows_pipelined<kParked, 2, HSTATE, false>(a, f0, col, nf < (uint32_t)kParked ? nf : kParked, g_lo);
     }
 }
 
