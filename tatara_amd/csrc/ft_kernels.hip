@@ -611,17 +611,18 @@ __device__ __forceinline__ void apply_cells(const FtGradArgs& a, uint64_t off, v
     store_cells<V, HSTATE>(a, off, W, c);
 }
 
-// The fused update of F feature rows f0 + k (k < nf, nf >= 1) at the lane's
-// columns col .. col + 3, with gradients g[k], each row's state loaded D rows
-// ahead of its update.  The loads are unconditional (rows past nf re-load
-// row nf - 1 and are not stored) and come before the earlier rows' stores in
-// program order, so the wave keeps loads in flight and the wait before a
-// row's update counts only the loads issued after its own.  A row's address
-// is a wave-uniform base plus the lane's 32-bit column offset.  LA: this
-// step's Ranger lerp, the slow weights loaded with the rest of the state.
-template <int F, int D, bool HSTATE, bool LA>
-__device__ __forceinline__ void update_rows_pipelined(const FtGradArgs& a, uint64_t f0, uint32_t col, uint32_t nf,
-                                                      const vecf<4>* g) {
+// The fused update of F feature rows f0 + k * step (k < nf) at the lane's
+// columns col .. col + 3, with gradients gfn(k), each row's state loaded D
+// rows ahead of its update.  The loads are unconditional (rows past nload >=
+// max(nf, 1) re-load row nload - 1, and rows past nf are not stored) and
+// come before the earlier rows' stores in program order, so the wave keeps loads in flight and the
+// wait before a row's update counts only the loads issued after its own.  A
+// row's address is a row base plus the lane's 32-bit column offset (a
+// wave-uniform base when f0 is).  LA: this step's Ranger lerp, the slow
+// weights loaded with the rest of the state.
+template <int F, int D, bool HSTATE, bool LA, typename G>
+__device__ __forceinline__ void update_rows_pipelined(const FtGradArgs& a, uint64_t f0, uint32_t step, uint32_t col,
+                                                      uint32_t nf, uint32_t nload, G gfn) {
     using Mom = typename CellState<4, HSTATE>::Mom;
     const uint64_t ft_out = a.ft_out;
     // the lane's byte offsets within a row: f32 values and f16 moments
@@ -630,7 +631,9 @@ __device__ __forceinline__ void update_rows_pipelined(const FtGradArgs& a, uint6
         using T = typename std::remove_pointer<decltype(base)>::type;
         return reinterpret_cast<T*>(reinterpret_cast<char*>(base + row_elem) + lane_bytes);
     };
-    auto row_of = [&](int j) -> uint64_t { return (f0 + ((uint32_t)j < nf ? (uint32_t)j : nf - 1)) * ft_out; };
+    auto row_of = [&](int j) -> uint64_t {
+        return (f0 + (uint64_t)((uint32_t)j < nload ? (uint32_t)j : nload - 1) * step) * ft_out;
+    };
     CellState<4, HSTATE> cs[F];
     vecf<4> sl[F];
     auto load = [&](int j) {
@@ -651,8 +654,8 @@ __device__ __forceinline__ void update_rows_pipelined(const FtGradArgs& a, uint6
     for (int k = 0; k < F; ++k) {
         if (k + D < F) load(k + D);
         if ((uint32_t)k < nf) {
-            const uint64_t r = (f0 + (uint32_t)k) * ft_out;
-            vecf<4> W = radam_cells<4, HSTATE>(a, g[k], cs[k]);
+            const uint64_t r = (f0 + (uint64_t)k * step) * ft_out;
+            vecf<4> W = radam_cells<4, HSTATE>(a, gfn(k), cs[k]);
             if constexpr (LA) {
                 lerp_cells<4>(a, W, sl[k]);
                 __builtin_nontemporal_store(sl[k], reinterpret_cast<vecf<4>*>(at(a.slow, r, b32)));
@@ -1009,19 +1012,15 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
     for (int k = 0; k < kParked; ++k) parked[k * 64] = gv[k];
     const uint32_t nf_hi = nf > (uint32_t)kParked ? nf - kParked : 0u;
-    vecf<4> g_lo[kParked];
+    auto grad_hi = [&](int k) { return gv[kParked + k]; };
+    auto grad_lo = [&](int k) { return parked[k * 64]; };
+    const uint32_t nf_lo = nf < (uint32_t)kParked ? nf : kParked;
     if (a.opt.lookahead) {
-        if (nf_hi)
-            update_rows_pipelined<kScanFeat - kParked, 1, HSTATE, true>(a, f0 + kParked, col, nf_hi, gv + kParked);
-#pragma unroll
-        for (int k = 0; k < kParked; ++k) g_lo[k] = parked[k * 64];
-        update_rows_pipelined<kParked, 1, HSTATE, true>(a, f0, col, nf < (uint32_t)kParked ? nf : kParked, g_lo);
+        if (nf_hi) update_rows_pipelined<kScanFeat - kParked, 1, HSTATE, true>(a, f0 + kParked, 1, col, nf_hi, nf_hi, grad_hi);
+        update_rows_pipelined<kParked, 1, HSTATE, true>(a, f0, 1, col, nf_lo, nf_lo, grad_lo);
     } else {
-        if (nf_hi)
-            update_rows_pipelined<kScanFeat - kParked, 2, HSTATE, false>(a, f0 + kParked, col, nf_hi, gv + kParked);
-#pragma unroll
-        for (int k = 0; k < kParked; ++k) g_lo[k] = parked[k * 64];
-        update_rows_pipelined<kParked, 2, HSTATE, false>(a, f0, col, nf < (uint32_t)kParked ? nf : kParked, g_lo);
+        if (nf_hi) update_rows_pipelined<kScanFeat - kParked, 2, HSTATE, false>(a, f0 + kParked, 1, col, nf_hi, nf_hi, grad_hi);
+        update_rows_pipelined<kParked, 2, HSTATE, false>(a, f0, 1, col, nf_lo, nf_lo, grad_lo);
     }
 }
 
@@ -1255,27 +1254,31 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = acc[i][j][r];
             __syncthreads();
+            // the lane's rows 2 j + lane / 32 of the tile (j < 8): features
+            // first + 2 j of the group, nfl of them real (none past the
+            // group's end; a lane without any loads the tile's first row)
+            const uint32_t tile_lo = fw + i * 16, rsel = lane / 32, first = tile_lo + rsel;
+            const uint32_t nfl = first < nf ? min(8u, (nf - first + 1) / 2) : 0u;
+            auto gfn = [&](int j) {
+                const float4 v =
+                    *reinterpret_cast<const float4*>(&s_u[(2 * j + rsel) * kMfmaUpdRow + 4 * (lane % 32)]);
+                vecf<4> gr = {v.x, v.y, v.z, v.w};
+                return gr * a.dft_inv_scale;
+            };
+            if (tile_lo < nf && col < a.ft_out) {
+                if (a.grad) {
 #pragma unroll
-            for (uint32_t q0 = 0; q0 < 8; q0 += 4) {
-                CellState<4, HSTATE> cs[4];
-#pragma unroll
-                for (uint32_t u = 0; u < 4; ++u) {
-                    const uint32_t fi = fw + i * 16 + 2 * (q0 + u) + lane / 32;
-                    if (a.apply_update && fi < nf && col < a.ft_out)
-                        cs[u] = load_cells<4, HSTATE>(a, ((f0 + fi) * a.ft_out + col) / 4);
+                    for (int j = 0; j < 8; ++j)
+                        if ((uint32_t)j < nfl)
+                            __builtin_nontemporal_store(gfn(j), grad + ((f0 + first + 2 * j) * a.ft_out + col) / 4);
                 }
-#pragma unroll
-                for (uint32_t u = 0; u < 4; ++u) {
-                    const uint32_t row = 2 * (q0 + u) + lane / 32;
-                    const uint32_t fi = fw + i * 16 + row;
-                    if (fi < nf && col < a.ft_out) {
-                        const float4 v = *reinterpret_cast<const float4*>(&s_u[row * kMfmaUpdRow + 4 * (lane % 32)]);
-                        vecf<4> gr = {v.x, v.y, v.z, v.w};
-                        gr *= a.dft_inv_scale;
-                        const uint64_t off = ((f0 + fi) * a.ft_out + col) / 4;
-                        if (a.grad) __builtin_nontemporal_store(gr, grad + off);
-                        if (a.apply_update) apply_cells<4, HSTATE>(a, off, gr, cs[u]);
-                    }
+                if (a.apply_update) {
+                    const uint64_t fl = f0 + (nfl ? first : tile_lo);
+                    // state loaded two rows ahead (one with the slow weights)
+                    if (a.opt.lookahead)
+                        update_rows_pipelined<8, 1, HSTATE, true>(a, fl, 2, col, nfl, nfl ? nfl : 1u, gfn);
+                    else
+                        update_rows_pipelined<8, 2, HSTATE, false>(a, fl, 2, col, nfl, nfl ? nfl : 1u, gfn);
                 }
             }
             __syncthreads();
