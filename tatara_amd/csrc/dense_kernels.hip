@@ -35,7 +35,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 
 // ---------------------------------------------------------------------------
-// L1 forward.  One wave per 16-row sorted tile.
+// L1 forward.  One wave per 16-row sorted tile (two with one bucket, the
+// f32 form).
 //   bucket part: l1_b[g] + combined . l1_w[g]^T   (accumulator starts at the bias,
 //                as dense_mm_fwd_bucket_tiled_l1_sorted does); 0 for an invalid bucket
 //   shared part: combined . l1s_w + l1s_b         (bias after the sum, as the
@@ -45,41 +46,50 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 // loads float4 column runs and feeds their components to four successive
 // MFMAs, which permutes the K order consistently for A and B.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
-    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const uint32_t tile = blockIdx.x * 4 + wave;
-    if ((uint64_t)tile * 16 >= a.padded_b) return;
-    const int32_t bin = a.sorted_bin[tile * 16];
-    if (bin < 0) return;  // trailing all-padding tile
+// T (1 or 2) consecutive tiles of bucket `bin`: the weights of each K-block
+// are loaded once for all T tiles.
+template <int T>
+__device__ __forceinline__ void ls_l1_fwd_tiles(const LsDenseArgs& a, uint32_t tile0, int32_t bin, uint32_t lane) {
     const uint32_t i = lane % 16, q = lane / 16;
     const uint32_t ft_out = a.ft_out, l1 = a.l1;
-    const int32_t orig = a.perm[tile * 16 + i];
     const bool bvalid = (uint32_t)bin < a.nb;
     const bool jvalid = i < l1;
     // Operands are loaded unconditionally from always-valid addresses (row 0,
     // bucket 0, column l1-1) and masked afterwards: a guarded load would be
     // split into predicated dword loads and lose the 16-byte accesses.
-    const bool xvalid = orig >= 0, wbvalid = bvalid && jvalid;
+    const bool wbvalid = bvalid && jvalid;
     const uint32_t ic = jvalid ? i : l1 - 1;
-    const float4* X = reinterpret_cast<const float4*>(a.combined + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
+    const float4* X[T];
+    bool xvalid[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int32_t orig = a.perm[(tile0 + t) * 16 + i];
+        xvalid[t] = orig >= 0;
+        X[t] = reinterpret_cast<const float4*>(a.combined + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
+    }
     const float4* W1 = reinterpret_cast<const float4*>(
         a.l1_w + ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
     const float* Ws = a.l1s_w + ic;
     const float binit = (bvalid && jvalid) ? a.l1_b[bin * l1 + i] : 0.0f;
-    floatx4 accb = {binit, binit, binit, binit};
-    floatx4 accs = {0.f, 0.f, 0.f, 0.f};
+    floatx4 accb[T], accs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        accb[t] = floatx4{binit, binit, binit, binit};
+        accs[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
     // ft_out % 64 == 0: whole groups of kU K-blocks; a group's operands are
     // loaded before its MFMAs so each wave keeps several loads in flight
     const uint32_t nk = ft_out / 16;
-    constexpr uint32_t kU = 4;
+    constexpr uint32_t kU = T == 1 ? 4 : 2;
     for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
-        float4 x[kU], wb[kU];
+        float4 x[kU][T], wb[kU];
         float ws[kU][4];
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
             const uint32_t kb = kb0 + u;
-            x[u] = X[kb * 4 + q];
+#pragma unroll
+            for (int t = 0; t < T; ++t) x[u][t] = X[t][kb * 4 + q];
             wb[u] = W1[kb * 4 + q];
             const uint32_t k = kb * 16 + 4 * q;
 #pragma unroll
@@ -87,29 +97,68 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
         }
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
-            const float4 xv = xvalid ? x[u] : zero4;
             const float4 wv = wbvalid ? wb[u] : zero4;
             const float w0 = jvalid ? ws[u][0] : 0.f, w1 = jvalid ? ws[u][1] : 0.f;
             const float w2 = jvalid ? ws[u][2] : 0.f, w3 = jvalid ? ws[u][3] : 0.f;
-            accb = mfma4(xv.x, wv.x, accb);
-            accs = mfma4(xv.x, w0, accs);
-            accb = mfma4(xv.y, wv.y, accb);
-            accs = mfma4(xv.y, w1, accs);
-            accb = mfma4(xv.z, wv.z, accb);
-            accs = mfma4(xv.z, w2, accs);
-            accb = mfma4(xv.w, wv.w, accb);
-            accs = mfma4(xv.w, w3, accs);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float4 xv = xvalid[t] ? x[u][t] : zero4;
+                accb[t] = mfma4(xv.x, wv.x, accb[t]);
+                accs[t] = mfma4(xv.x, w0, accs[t]);
+                accb[t] = mfma4(xv.y, wv.y, accb[t]);
+                accs[t] = mfma4(xv.y, w1, accs[t]);
+                accb[t] = mfma4(xv.z, wv.z, accb[t]);
+                accs[t] = mfma4(xv.z, w2, accs[t]);
+                accb[t] = mfma4(xv.w, wv.w, accb[t]);
+                accs[t] = mfma4(xv.w, w3, accs[t]);
+            }
         }
     }
     const uint32_t j = lane % 16;
     if (j >= l1) return;
     const float bs = a.l1s_b[j];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint64_t row = (uint64_t)tile * 16 + 4 * q + r;
-        float* o = a.l1_sorted + row * 2 * l1;
-        o[j] = bvalid ? accb[r] : 0.0f;
-        o[l1 + j] = accs[r] + bs;
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint64_t row = (uint64_t)(tile0 + t) * 16 + 4 * q + r;
+            float* o = a.l1_sorted + row * 2 * l1;
+            o[j] = bvalid ? accb[t][r] : 0.0f;
+            o[l1 + j] = accs[t][r] + bs;
+        }
+}
+
+// The TF32 L1 forward's weight operands, once per forward: f16 copies of
+// l1_w and of l1s_w transposed ([l1][ft_out], a lane's K values
+// consecutive).  Thread i: bucket weight i, and shared weight i when
+// i < l1 * ft_out (nb >= 1).  (The f32 forward reads the weights as they
+// are: the transposed copy cost more than the strided loads it saved.)
+__global__ __launch_bounds__(256) void ls_l1_weights_f16_kernel(LsDenseArgs a) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t n_w = (uint64_t)a.nb * a.l1 * a.ft_out, n_s = (uint64_t)a.l1 * a.ft_out;
+    if (i >= n_w) return;
+    reinterpret_cast<_Float16*>(a.l1_w16)[i] = (_Float16)a.l1_w[i];
+    if (i < n_s) {
+        const uint64_t j = i / a.ft_out, k = i % a.ft_out;  // transposed [j][k] <- [k][j]
+        reinterpret_cast<_Float16*>(a.l1s_wt16)[i] = (_Float16)a.l1s_w[k * a.l1 + j];
+    }
+}
+
+// One wave per pair of 16-row sorted tiles: both in one pass when they
+// belong to one bucket, else (at a bucket boundary) one pass each; a tile
+// of bin -1 (all padding) is skipped.
+__global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t tile0 = (blockIdx.x * 4 + wave) * 2;
+    const uint32_t n_tiles = (uint32_t)(a.padded_b / 16);
+    if (tile0 >= n_tiles) return;
+    const int32_t bin0 = scalar_load(a.sorted_bin + (uint64_t)tile0 * 16);
+    const int32_t bin1 = tile0 + 1 < n_tiles ? scalar_load(a.sorted_bin + (uint64_t)(tile0 + 1) * 16) : -1;
+    if (bin0 >= 0 && bin0 == bin1) {
+        ls_l1_fwd_tiles<2>(a, tile0, bin0, lane);
+    } else {
+        if (bin0 >= 0) ls_l1_fwd_tiles<1>(a, tile0, bin0, lane);
+        if (bin1 >= 0) ls_l1_fwd_tiles<1>(a, tile0 + 1, bin1, lane);
     }
 }
 
@@ -138,42 +187,29 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_tf32_kernel(LsDenseArgs a) {
     const uint32_t ic = jvalid ? i : l1 - 1;
     const half8* X = reinterpret_cast<const half8*>(
         reinterpret_cast<const _Float16*>(a.combined16) + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
-    const float4* W1 = reinterpret_cast<const float4*>(a.l1_w + ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
-    const float* Ws = a.l1s_w + ic;
+    const half8* W1 = reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(a.l1_w16) +
+                                                     ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
+    const half8* Ws = reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(a.l1s_wt16) +
+                                                     (uint64_t)ic * ft_out);
     floatx4 accb = {0.f, 0.f, 0.f, 0.f}, accs = accb;
     const half8 zero8 = {};
-    // ft_out % 64 == 0: K blocks of 32, two loaded before their MFMAs
+    // ft_out % 64 == 0: K blocks of 32, four loaded before their MFMAs
     const uint32_t nk = ft_out / 32;
-    constexpr uint32_t kU = 2;
+    constexpr uint32_t kU = 4;
     for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
-        half8 x[kU];
-        float4 w0[kU], w1[kU];
-        float ws[kU][8];
+        half8 x[kU], wb[kU], wsh[kU];
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
-            const uint32_t k = (kb0 + u) * 32 + 8 * q;
-            x[u] = X[k / 8];
-            w0[u] = W1[k / 4];
-            w1[u] = W1[k / 4 + 1];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ws[u][e] = Ws[(uint64_t)(k + e) * l1];
+            const uint32_t k8 = (kb0 + u) * 4 + q;
+            x[u] = X[k8];
+            wb[u] = W1[k8];
+            wsh[u] = Ws[k8];
         }
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
             const half8 xv = xvalid ? x[u] : zero8;
-            half8 wb, wsh;
-            wb[0] = (_Float16)w0[u].x;
-            wb[1] = (_Float16)w0[u].y;
-            wb[2] = (_Float16)w0[u].z;
-            wb[3] = (_Float16)w0[u].w;
-            wb[4] = (_Float16)w1[u].x;
-            wb[5] = (_Float16)w1[u].y;
-            wb[6] = (_Float16)w1[u].z;
-            wb[7] = (_Float16)w1[u].w;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) wsh[e] = (_Float16)ws[u][e];
-            accb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wbvalid ? wb : zero8, accb, 0, 0, 0);
-            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, jvalid ? wsh : zero8, accs, 0, 0, 0);
+            accb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wbvalid ? wb[u] : zero8, accb, 0, 0, 0);
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, jvalid ? wsh[u] : zero8, accs, 0, 0, 0);
         }
     }
     const uint32_t j = lane % 16;
@@ -430,25 +466,40 @@ __global__ __launch_bounds__(64) void ls_tail_kernel(LsDenseArgs a, int32_t trai
 // bin nb, whose rows still feed the shared weight) is split into chunks of at
 // most kChunkTiles 16-row tiles.
 // ---------------------------------------------------------------------------
-__global__ void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
-                                      const uint32_t* __restrict__ bin_count, uint32_t nb,
-                                      uint32_t max_chunks, uint32_t* __restrict__ info) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    uint32_t c = 0;
-    uint32_t* seg = info + 3 * max_chunks + 1;  // seg[g] = first chunk of bin g, seg[nb+1] = end
-    for (uint32_t g = 0; g <= nb; ++g) {
-        seg[g] = c;
-        const uint32_t t0 = bin_start[g] / 16;
-        const uint32_t t1 = (bin_start[g] + bin_count[g] + 15) / 16;
-        for (uint32_t t = t0; t < t1 && c < max_chunks; t += kChunkTiles) {
-            info[3 * c + 0] = g;
-            info[3 * c + 1] = t;
-            info[3 * c + 2] = min(kChunkTiles, t1 - t);
-            ++c;
-        }
+__global__ __launch_bounds__(256) void ls_chunk_table_kernel(const uint32_t* __restrict__ bin_start,
+                                                             const uint32_t* __restrict__ bin_count, uint32_t nb,
+                                                             uint32_t max_chunks, uint32_t* __restrict__ info) {
+    // the bins' tile ranges and first chunks (at most 17 bins: nb <= 16 plus
+    // the invalid bin), then one thread per chunk entry
+    __shared__ uint32_t s_t0[17], s_t1[17], s_first[18];
+    const uint32_t t = threadIdx.x;
+    if (t <= nb) {
+        s_t0[t] = bin_start[t] / 16;
+        s_t1[t] = (bin_start[t] + bin_count[t] + 15) / 16;
     }
-    info[3 * max_chunks] = c;
-    seg[nb + 1] = c;
+    __syncthreads();
+    if (t == 0) {
+        uint32_t c = 0;
+        for (uint32_t g = 0; g <= nb; ++g) {
+            s_first[g] = c;
+            const uint32_t n = s_t1[g] > s_t0[g] ? (s_t1[g] - s_t0[g] + kChunkTiles - 1) / kChunkTiles : 0u;
+            c = c + n < max_chunks ? c + n : max_chunks;
+        }
+        s_first[nb + 1] = c;
+    }
+    __syncthreads();
+    const uint32_t total = s_first[nb + 1];
+    for (uint32_t ci = t; ci < total; ci += blockDim.x) {
+        uint32_t g = 0;
+        while (g < nb && s_first[g + 1] <= ci) ++g;  // the bin whose chunks hold ci
+        const uint32_t tile = s_t0[g] + (ci - s_first[g]) * kChunkTiles;
+        info[3 * ci + 0] = g;
+        info[3 * ci + 1] = tile;
+        info[3 * ci + 2] = min(kChunkTiles, s_t1[g] - tile);
+    }
+    uint32_t* seg = info + 3 * max_chunks + 1;  // seg[g] = first chunk of bin g, seg[nb+1] = end
+    if (t <= nb + 1) seg[t] = s_first[t];
+    if (t == 0) info[3 * max_chunks] = total;
 }
 
 // ---------------------------------------------------------------------------
@@ -885,13 +936,17 @@ uint32_t ls_max_chunks(uint32_t padded_b, uint32_t nb) {
 int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.l1 >= 2 && a.l1 <= 16, "l1 must be in [2, 16]");
     TATARA_REQUIRE(a.ft_out % 64 == 0, "ft_out must be a multiple of 64");
+    TATARA_REQUIRE(!a.combined16 || (a.l1_w16 && a.l1s_wt16), "the TF32 L1 forward needs its f16 weights");
     const uint32_t tiles = a.padded_b / 16;
     if (tiles == 0) return kOk;
     if (a.combined16) {
+        const uint64_t n_w = (uint64_t)a.nb * a.l1 * a.ft_out;
+        ls_l1_weights_f16_kernel<<<ceil_div(n_w, 256), 256, 0, stream>>>(a);
+        TATARA_LAUNCHED("ls_l1_weights_f16");
         TATARA_REQUIRE(a.l1 <= 16, "l1 must be <= 16");
         ls_l1_fwd_tf32_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
     } else {
-        ls_l1_fwd_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+        ls_l1_fwd_kernel<<<ceil_div(tiles, 8), 256, 0, stream>>>(a);
     }
     TATARA_LAUNCHED("ls_l1_forward");
     return kOk;
@@ -926,7 +981,7 @@ int32_t launch_ls_tail(const LsDenseArgs& a, int32_t train, hipStream_t stream) 
 }
 
 int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream) {
-    ls_chunk_table_kernel<<<1, 64, 0, stream>>>(a.bin_start, a.bin_count, a.nb, a.max_chunks,
+    ls_chunk_table_kernel<<<1, 256, 0, stream>>>(a.bin_start, a.bin_count, a.nb, a.max_chunks,
                                                a.chunk_info);
     TATARA_LAUNCHED("ls_chunk_table");
     dim3 grid(a.max_chunks, ceil_div(a.ft_out, 256));

@@ -73,6 +73,11 @@ struct LsDenseArgs {
     const float* l1_b;          // [nb][l1]
     const float* l1s_w;         // [ft_out][l1]
     const float* l1s_b;         // [l1]
+    // the TF32 forward's weight operands (combined16 set), written from l1_w
+    // and l1s_w at the start of each forward: f16 copies, l1s_w transposed
+    // so that a lane's K values are consecutive
+    uint16_t* l1_w16;           // [nb][l1][ft_out] f16
+    uint16_t* l1s_wt16;         // [l1][ft_out] f16
     const float* l2_w;          // [nb][l2][l2_in]
     const float* l2_b;          // [nb][l2]
     const float* l3_w;          // [nb][l2]

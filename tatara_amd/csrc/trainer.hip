@@ -85,6 +85,8 @@ class LayerStackTrainer final : public TrainerBase {
     uint16_t* fwd16 = nullptr;  // [ft_in][ft_out] f16 comb (factorizer) or mirror of the real rows
     uint16_t *ft_stm16 = nullptr, *ft_nstm16 = nullptr, *dft16 = nullptr;
     uint16_t* combined16 = nullptr;  // `combined` held as f16 (tf32)
+    // the tf32 L1 forward's f16 weight copies (shared weights transposed)
+    uint16_t *l1_w16 = nullptr, *l1s_wt16 = nullptr;
     unsigned long long* clamp_ctr = nullptr;  // cumulative dft clamps
     uint64_t clamp_elems = 0;                 // cumulative dft values written
 
@@ -243,7 +245,9 @@ class LayerStackTrainer final : public TrainerBase {
                    (st = arena.alloc(&ft_nstm, B * ft_out, false)) || (st = arena.alloc(&dft, dft_n, false))) {
             return st;
         }
-        if ((l1_lowp ? (st = arena.alloc(&combined16, B * ft_out, false))
+        if ((l1_lowp ? ((st = arena.alloc(&combined16, B * ft_out, false)) ||
+                        (st = arena.alloc(&l1_w16, (uint64_t)nb * l1 * ft_out, false)) ||
+                        (st = arena.alloc(&l1s_wt16, (uint64_t)l1 * ft_out, false)))
                      : (st = arena.alloc(&combined, B * ft_out, false))) ||
             (st = arena.alloc(&l1_sorted, P * 2 * l1)) ||
             (st = arena.alloc(&dl1_sorted, P * l1)) || (st = arena.alloc(&net_out, B)))
@@ -367,6 +371,8 @@ class LayerStackTrainer final : public TrainerBase {
         a.l1_w = small[1].w;
         a.l1_b = small[2].w;
         a.l1s_w = small[3].w;
+        a.l1_w16 = l1_w16;
+        a.l1s_wt16 = l1s_wt16;
         a.l1s_b = small[4].w;
         a.l2_w = small[5].w;
         a.l2_b = small[6].w;
