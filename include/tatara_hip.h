@@ -67,6 +67,70 @@ TATARA_API int32_t tatara_memset(void* dst, int32_t byte, uint64_t bytes);
 /* Waits for all work on the device (CudaStream::synchronize). */
 TATARA_API int32_t tatara_synchronize(void);
 
+/* Streams, events, asynchronous copies, pinned host memory and code-object
+ * modules: the rest of the runtime surface (native_backend.rs:33-300,
+ * lib.rs:186-390).  Handles are opaque.  Every stream is created at the
+ * default priority and does not synchronise with the null stream; a NULL
+ * stream argument is the device's null stream.  The calls that take a device
+ * make it current on the calling thread (CudaContext::bind_to_thread). */
+typedef struct TataraStream TataraStream;
+typedef struct TataraEvent TataraEvent;
+typedef struct TataraModule TataraModule;
+
+/* (multiprocessor count, max threads per multiprocessor) as
+ * device_occupancy_attributes (lib.rs:364-390, native_backend.rs:81-88);
+ * here compute units and their thread capacity. */
+TATARA_API int32_t tatara_device_occupancy_attributes(int32_t device, int32_t* cu_count,
+                                                      int32_t* max_threads_per_cu);
+/* CudaContext::compute_capability (native_backend.rs:72-79): the HIP
+ * (major, minor) of the device, 9.5 for gfx950. */
+TATARA_API int32_t tatara_device_compute_capability(int32_t device, int32_t* major, int32_t* minor);
+/* CudaContext::new_stream / CudaStream::synchronize / CudaStream::wait
+ * (native_backend.rs:54-60, :105-112). */
+TATARA_API int32_t tatara_stream_create(int32_t device, TataraStream** out);
+TATARA_API int32_t tatara_stream_destroy(TataraStream* stream);
+TATARA_API int32_t tatara_stream_synchronize(TataraStream* stream);
+TATARA_API int32_t tatara_stream_wait_event(TataraStream* stream, TataraEvent* event);
+/* CudaContext::new_event / CudaEvent::record / CudaEvent::synchronize
+ * (native_backend.rs:61-67, :129-136).  flags: a combination of the two
+ * below (0: timing enabled, spin wait). */
+#define TATARA_EVENT_BLOCKING_SYNC 1
+#define TATARA_EVENT_DISABLE_TIMING 2
+TATARA_API int32_t tatara_event_create(int32_t device, uint32_t flags, TataraEvent** out);
+TATARA_API int32_t tatara_event_destroy(TataraEvent* event);
+TATARA_API int32_t tatara_event_record(TataraEvent* event, TataraStream* stream);
+TATARA_API int32_t tatara_event_synchronize(TataraEvent* event);
+/* 1 when the event's recorded work has finished, 0 while it is pending. */
+TATARA_API int32_t tatara_event_query(TataraEvent* event, int32_t* done);
+/* Milliseconds between two completed events (both created with timing). */
+TATARA_API int32_t tatara_event_elapsed_ms(TataraEvent* start, TataraEvent* end, float* ms);
+/* memset_d8_async / memcpy_htod_async / memcpy_dtoh_async (lib.rs:232-310):
+ * ordered on `stream`; the host buffer must stay alive (and, for dtoh,
+ * untouched) until the stream has passed the copy, and overlaps other work
+ * only when it is pinned (tatara_host_alloc_pinned). */
+TATARA_API int32_t tatara_memset_d8_async(void* dst, uint8_t value, uint64_t bytes, TataraStream* stream);
+TATARA_API int32_t tatara_memcpy_htod_async(void* dst, const void* src, uint64_t bytes, TataraStream* stream);
+TATARA_API int32_t tatara_memcpy_dtoh_async(void* dst, const void* src, uint64_t bytes, TataraStream* stream);
+/* alloc_pinned_host / free_pinned_host (lib.rs:318-360): page-locked host
+ * memory, freed only after every copy that uses it has completed. */
+TATARA_API int32_t tatara_host_alloc_pinned(uint64_t bytes, void** out);
+TATARA_API int32_t tatara_host_free_pinned(void* ptr);
+/* CudaContext::load_module_from_image (native_backend.rs:90-97): loads a
+ * gfx950 code object (hipcc --genco) from memory; the image may be freed
+ * after the call. */
+TATARA_API int32_t tatara_module_load_image(int32_t device, const void* image, uint64_t bytes,
+                                            TataraModule** out);
+TATARA_API int32_t tatara_module_destroy(TataraModule* module);
+/* CudaModule::launch (native_backend.rs:149-184): looks the kernel up by name
+ * (cached per module) and launches it on `stream`.  args[i] points at the
+ * i-th kernel argument's value, as KernelArgs holds them (push_slice is two
+ * arguments: the device pointer and a u64 length); the caller guarantees
+ * they match the kernel's parameters.  An unknown name fails with
+ * TATARA_ERR_HIP before anything is launched. */
+TATARA_API int32_t tatara_module_launch(TataraModule* module, const char* kernel, TataraStream* stream,
+                                        const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
+                                        void** args);
+
 /* ------------------------------------------------------------------------ */
 /* Kernel-level ops (device pointers, default stream, synchronous errors)   */
 /* ------------------------------------------------------------------------ */

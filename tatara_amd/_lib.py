@@ -210,6 +210,30 @@ SIGNATURES = {
     "tatara_memcpy_dtoh": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "tatara_memset": (C.c_int32, [C.c_void_p, C.c_int32, C.c_uint64]),
     "tatara_synchronize": (C.c_int32, []),
+    "tatara_device_occupancy_attributes": (C.c_int32, [C.c_int32, c_i32p, c_i32p]),
+    "tatara_device_compute_capability": (C.c_int32, [C.c_int32, c_i32p, c_i32p]),
+    "tatara_stream_create": (C.c_int32, [C.c_int32, C.POINTER(C.c_void_p)]),
+    "tatara_stream_destroy": (C.c_int32, [C.c_void_p]),
+    "tatara_stream_synchronize": (C.c_int32, [C.c_void_p]),
+    "tatara_stream_wait_event": (C.c_int32, [C.c_void_p, C.c_void_p]),
+    "tatara_event_create": (C.c_int32, [C.c_int32, C.c_uint32, C.POINTER(C.c_void_p)]),
+    "tatara_event_destroy": (C.c_int32, [C.c_void_p]),
+    "tatara_event_record": (C.c_int32, [C.c_void_p, C.c_void_p]),
+    "tatara_event_synchronize": (C.c_int32, [C.c_void_p]),
+    "tatara_event_query": (C.c_int32, [C.c_void_p, c_i32p]),
+    "tatara_event_elapsed_ms": (C.c_int32, [C.c_void_p, C.c_void_p, C.POINTER(C.c_float)]),
+    "tatara_memset_d8_async": (C.c_int32, [C.c_void_p, C.c_uint8, C.c_uint64, C.c_void_p]),
+    "tatara_memcpy_htod_async": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "tatara_memcpy_dtoh_async": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "tatara_host_alloc_pinned": (C.c_int32, [C.c_uint64, C.POINTER(C.c_void_p)]),
+    "tatara_host_free_pinned": (C.c_int32, [C.c_void_p]),
+    "tatara_module_load_image": (C.c_int32, [C.c_int32, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]),
+    "tatara_module_destroy": (C.c_int32, [C.c_void_p]),
+    "tatara_module_launch": (
+        C.c_int32,
+        [C.c_void_p, C.c_char_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_uint32,
+         C.POINTER(C.c_void_p)],
+    ),
     "tatara_op_sparse_ft_forward": (C.c_int32, [C.c_void_p] * 4 + [C.c_uint32] * 4),
     "tatara_op_ft_forward_pairwise": (
         C.c_int32,

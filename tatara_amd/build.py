@@ -57,6 +57,20 @@ def build(jobs: int | None = None) -> Path:
     return LIB
 
 
+def build_code_object(src: Path, out: Path | None = None) -> Path:
+    """Compiles one HIP source into a gfx950 code object (hipcc --genco) for
+    tatara_module_load_image; returns its path (default: src with .hsaco)."""
+    src = Path(src)
+    out = Path(out) if out else src.with_suffix(".hsaco")
+    tmp = out.with_suffix(out.suffix + ".tmp")
+    cmd = [HIPCC, "--genco", *FLAGS, str(src), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc --genco failed for {src.name}:\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build())
     sys.exit(0)

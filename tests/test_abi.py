@@ -83,3 +83,41 @@ def test_quantise_noalloc_rejects_tables_beyond_its_scratch():
     st = lib.tatara_op_quantise_ft_noalloc(fake, 1 << 20, 257, 0, 127.0, 1, fake, 1 << 40, C.byref(n))
     assert st == -3 and b"static scratch" in lib.tatara_last_error()
     assert n.value == 0
+
+
+def test_runtime_surface_rejects_bad_arguments_without_gpu_work():
+    """Null outputs, unknown event flags, and an image that is not a code
+    object are refused before any device call (CPU only)."""
+    import ctypes as C
+
+    lib = _lib.load()
+    assert lib.tatara_stream_create(0, None) == -3
+    assert lib.tatara_event_create(0, 0, None) == -3
+    h = C.c_void_p()
+    assert lib.tatara_event_create(0, 4, C.byref(h)) == -3 and h.value is None
+    assert b"event flags" in lib.tatara_last_error()
+    junk = b"not a code object at all"
+    assert lib.tatara_module_load_image(0, junk, len(junk), C.byref(h)) == -3
+    assert b"code object" in lib.tatara_last_error()
+    assert lib.tatara_module_load_image(0, None, 0, C.byref(h)) == -3
+    grid = (C.c_uint32 * 3)(1, 1, 1)
+    assert lib.tatara_module_launch(None, b"k", None, grid, grid, 0, None) == -3
+    assert lib.tatara_host_alloc_pinned(16, None) == -3
+    # destroying a null handle is a no-op
+    assert lib.tatara_stream_destroy(None) == 0 and lib.tatara_event_destroy(None) == 0
+    assert lib.tatara_module_destroy(None) == 0
+
+
+def test_launch_geometry_helpers():
+    from tatara_amd import runtime as rt
+
+    assert rt.grid_dim_1d(0) == (1, 1, 1) and rt.grid_dim_1d(256) == (1, 1, 1)
+    assert rt.grid_dim_1d(257) == (2, 1, 1) and rt.grid_dim_1d(1000, 128) == (8, 1, 1)
+    cfg = rt.LaunchConfig.for_num_elems(1000)
+    assert cfg.grid_dim == (4, 1, 1) and cfg.block_dim == (256, 1, 1) and cfg.shared_mem_bytes == 0
+
+
+def test_selftest_code_object_is_built_for_gfx950():
+    img = (ROOT / "tests" / "kernels" / "runtime_selftest.hsaco").read_bytes()
+    assert img.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or img.startswith(b"\x7fELF")
+    assert b"gfx950" in img and b"selftest_axpy" in img

@@ -6,7 +6,9 @@ field's offset and size.  Those are compared with
   - the fields the header declares (so the program misses none),
   - the ctypes structs of tatara_amd/_lib.py (the Python host mirror),
   - the Rust #[repr(C)] structs INTEGRATION.md gives a maintainer: field
-    names, order and the layout repr(C) gives them on x86-64 Linux.
+    names, order and the layout repr(C) gives them on x86-64 Linux;
+and every Rust `extern "C"` function INTEGRATION.md binds is checked against
+the header's parameter list, type by type.
 CPU only.
 """
 from __future__ import annotations
@@ -112,7 +114,7 @@ def test_integration_doc_rust_structs_match_the_header(c_layout):
     rust = rust_structs()
     assert {"TataraTrainerConfig", "TataraLoss", "TataraBatch", "TataraCkptHeader"} <= set(rust), set(rust)
     for name, fields in rust.items():
-        if name == "TataraTrainer":  # opaque handle
+        if [f for f, _ in fields] == ["_p"]:  # opaque handle
             continue
         lay = c_layout[name]
         assert [f for f, _ in fields] == [f for f, _, _ in lay["fields"]], \
@@ -122,3 +124,51 @@ def test_integration_doc_rust_structs_match_the_header(c_layout):
             d = getattr(cls, field)
             assert (d.offset, d.size) == (off, size), f"INTEGRATION.md {name}.{field}"
         assert C.sizeof(cls) == lay["size"], f"INTEGRATION.md {name}: {C.sizeof(cls)} bytes vs {lay['size']}"
+
+
+_RUST_SCALARS = {"i32": "int32_t", "u32": "uint32_t", "u64": "uint64_t", "u8": "uint8_t", "f32": "float",
+                 "f64": "double", "c_void": "void", "c_char": "char"}
+
+
+def _rust_param(t: str) -> str:
+    """A Rust FFI parameter type as the C type it binds (const-ness kept on the pointee)."""
+    t = t.strip()
+    if t.startswith("*const "):
+        inner = _rust_param(t[len("*const "):])
+        return ("const " + inner if "*" not in inner else inner) + "*"
+    if t.startswith("*mut "):
+        return _rust_param(t[len("*mut "):]) + "*"
+    return _RUST_SCALARS.get(t, t)
+
+
+def _c_param(decl: str) -> str:
+    """A C parameter declaration without its name; an array parameter is a pointer."""
+    decl = " ".join(decl.split())
+    m = re.fullmatch(r"(.*?)(\w+)\s*\[\s*\d*\s*\]", decl)
+    if m:
+        return _c_param(m.group(1) + "* " + m.group(2))
+    return re.sub(r"\b\w+$", "", decl)  # without the parameter name
+
+
+def _header_functions() -> dict[str, list[str]]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"TATARA_API\s+[\w\s\*]+?\b(tatara_\w+)\s*\(([^)]*)\)\s*;", text):
+        ps = [p for p in params.split(",") if p.strip() and p.strip() != "void"]
+        out[name] = [_c_param(p) for p in ps]
+    return out
+
+
+def test_integration_doc_rust_functions_match_the_header():
+    """Every `pub fn tatara_*` INTEGRATION.md gives a maintainer has the
+    header's parameter list: count, and each type as repr(C) binds it."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    header = _header_functions()
+    fns = re.findall(r"pub fn (tatara_\w+)\s*\((.*?)\)\s*(?:->\s*([\w\s\*]+?))?\s*;", text, re.S)
+    assert len(fns) >= 30, len(fns)
+    for name, params, _ in fns:
+        assert name in header, f"INTEGRATION.md binds {name}, which the header does not declare"
+        rust = [_rust_param(p.split(":", 1)[1]) for p in params.split(",") if p.strip()]
+        want = [p.replace(" ", "") for p in header[name]]
+        got = [p.replace(" ", "") for p in rust]
+        assert got == want, f"{name}: INTEGRATION.md {got} vs header {want}"
