@@ -31,6 +31,10 @@ int32_t hip_status(hipError_t e, const char* what) {
     std::string msg = "HIP error " + std::to_string((int)e) + ": " + hipGetErrorName(e) + ": " +
                       hipGetErrorString(e) + " [" + what + "]";
     set_error(msg);
+    // The runtime keeps a failed call's error as the thread's last error
+    // until it is read; the error is reported here, so it is cleared, and a
+    // later launch check (hipGetLastError) sees only its own launch.
+    (void)hipGetLastError();
     if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return kErrOutOfMemory;
     return kErrHip;
 }

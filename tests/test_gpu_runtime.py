@@ -163,6 +163,17 @@ def test_cross_stream_order_through_an_event(module):
 def test_unknown_kernel_name_fails_before_launch(module):
     with pytest.raises(TataraError, match="no_such_kernel"):
         module.launch("no_such_kernel", None, rt.LaunchConfig((1, 1, 1), (64, 1, 1)), rt.KernelArgs())
+    # the reported error does not linger: the library's next launch check
+    # (here tatara_op_copy's) sees only its own launch
+    src, dst = Dev(1024, np.float32), Dev(1024, np.float32)
+    vals = np.arange(1024, dtype=np.float32)
+    check(load().tatara_memcpy_htod(src.ptr, vals.ctypes.data, src.nbytes))
+    check(load().tatara_op_copy(dst.ptr, src.ptr, src.nbytes))
+    got = np.zeros(1024, np.float32)
+    check(load().tatara_memcpy_dtoh(got.ctypes.data, dst.ptr, dst.nbytes))
+    assert np.array_equal(got, vals)
+    src.free()
+    dst.free()
     # the module still launches its own kernels afterwards
     d = Dev(64, np.uint32)
     args = (rt.KernelArgs().push_slice(d.ptr, 64).push_scalar(64, C.c_uint32).push_scalar(1, C.c_uint32)
