@@ -747,20 +747,27 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
 // bit.
 //
 // A workgroup owns one 256-column chunk and a group of GS features of one
-// block (wave w: features g*GS + 32w .. +31 of the block, accumulated in
+// block (wave w: features g*GS + 16w .. +15 of the block, accumulated in
 // registers, four columns per lane).  It stages each row's chunk in LDS once
 // (a dft row is read once per group instead of once per occurrence) and
 // every wave adds it to those of its features whose bit is set in the row's
-// hit mask.  Per stage of 32 rows a wave turns its 32 row masks into 32
-// feature masks (one ballot each), so feature k's accumulator is a fixed
+// hit mask.  Per stage of 32 rows a wave reads 16 feature masks (bit r: the
+// stage's row r holds the feature), so feature k's accumulator is a fixed
 // register and its rows are added in list order.  The optimizer update of
 // the group's cells follows the scan in the same workgroup.
 //
 // Hit masks (ft_scan_masks_kernel): for schedule entry e (a row) and word
-// q = g*W + w, bit k of masks[q][e] is set when block feature g*GS + 32w + k
+// q = g*W + w, bit k of masks[q][e] is set when block feature g*GS + 16w + k
 // occurs in the row.  A row with a feature outside its own block, or with
 // one feature in two slots, sets *multi; the scan then leaves the step to
 // the occurrence-list kernel, which runs only in that case.
+//
+// Stage tables (ft_scan_stage_table_kernel, once per step for all column
+// chunks): the blocks' stages numbered consecutively, block K's first at
+// sum over k < K of ceil(rows_k / 32); for each stage the dft row of each
+// of its 32 slots (perspective * batch + position; slots past the block's
+// list repeat its last row) and, per mask word q, the 16 feature masks of
+// the stage (the hit masks transposed).
 // ---------------------------------------------------------------------------
 
 constexpr int kScanWaves = 8;
@@ -832,6 +839,62 @@ __global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanG
     }
 }
 
+// One wave per stage.  Thread 0 of each workgroup numbers the blocks'
+// stages (at most 128 blocks); a wave finds its block by binary search.
+__global__ __launch_bounds__(256) void ft_scan_stage_table_kernel(FtBlockScan s, ScanGeom geom) {
+    static_assert(kScanFeat == 16 && kScanStage == 32, "two mask words of 16 features per ballot");
+    __shared__ uint32_t s_base[129];
+    const uint32_t nb = s.n_blocks;
+    if (threadIdx.x == 0) {
+        uint32_t acc = 0;
+        for (uint32_t k = 0; k < nb; ++k) {
+            s_base[k] = acc;
+            const uint32_t rows = (s.sched_start[k + 1] - s.sched_start[k]) +
+                                  (s.sched_start[nb + k + 1] - s.sched_start[nb + k]);
+            acc += (rows + 31u) / 32u;
+        }
+        s_base[nb] = acc;
+    }
+    __syncthreads();
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t gs = blockIdx.x * 4 + wave;
+    if (gs >= s_base[nb]) return;
+    // the block: the last K with s_base[K] <= gs (an empty block shares its
+    // base with the next one, so the last is the one the stage belongs to)
+    uint32_t lo = 0, hi = nb - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) / 2;
+        if (s_base[mid] <= gs) lo = mid;
+        else hi = mid - 1;
+    }
+    const uint32_t K = lo, T = gs - s_base[K];
+    const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
+    const uint32_t b0 = s.sched_start[nb + K];
+    const uint32_t n = na + (s.sched_start[nb + K + 1] - b0);  // >= 1: the block has this stage
+    const uint32_t r = lane & 31u, j = T * 32u + r;
+    const bool valid = j < n;
+    const uint32_t jc = valid ? j : n - 1;
+    const uint32_t e = jc < na ? a0 + jc : b0 + (jc - na);
+    if (lane < 32) s.stage_rows[(uint64_t)gs * 32 + r] = (e >= s.batch ? s.batch : 0u) + (uint32_t)s.schedule[e];
+    const uint64_t two_b = 2ull * s.batch;
+    const uint32_t W = geom.words;
+    uint32_t* out = s.stage_masks + (uint64_t)gs * W * kScanFeat;
+    for (uint32_t q = 0; q < W; q += 2) {
+        // lanes 0..31: word q of slots 0..31, lanes 32..63: word q + 1
+        const uint32_t qq = q + (lane >> 5);
+        const uint32_t m = (valid && qq < W) ? s.masks[(uint64_t)qq * two_b + e] : 0u;
+        uint32_t v = 0;
+#pragma unroll
+        for (int k = 0; k < kScanFeat; ++k) {
+            const uint64_t b = __ballot((m >> k) & 1u);
+            // lane k keeps word q's mask of feature k, lane 16 + k word q + 1's
+            v = lane == (uint32_t)k ? (uint32_t)b : v;
+            v = lane == (uint32_t)(16 + k) ? (uint32_t)(b >> 32) : v;
+        }
+        if (lane < 32 && q + (lane >> 4) < W) out[(uint64_t)q * kScanFeat + lane] = v;
+    }
+}
+
 // HDFT: the dft is f16 (the --ft-fp16-out mode): rows are staged as f16
 // (512 bytes per 256-column chunk), each added value is converted to f32,
 // and the sum is multiplied by dft_inv_scale at the end, as the
@@ -859,7 +922,7 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t pair = (i_xcd / geom.n_groups) * kNumXcd + xcd;
     if (pair >= nb * n_chunks) return;
     const uint32_t rank = pair / n_chunks, chunk = pair % n_chunks;
-    uint32_t K;
+    uint32_t K, sb = 0;  // the block, and its first stage in the stage tables
     {
         auto block_rows = [&](uint32_t k) -> uint32_t {
             return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
@@ -875,6 +938,10 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
         const uint64_t h0 = __ballot(lane < nb && r0 == rank);
         const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
         K = __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
+        for (uint32_t m = 0; m < K; ++m) {
+            const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
+            sb += (zm + 31u) / 32u;
+        }
     }
     const uint32_t PI = s.piece_inputs;
     const uint32_t blk_lo = K * PI;
@@ -887,32 +954,29 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
     const uint32_t b0 = s.sched_start[s.n_blocks + K];
     const uint32_t n = na + (s.sched_start[s.n_blocks + K + 1] - b0);
-    const uint32_t* mrow = s.masks + (uint64_t)(g * kScanWaves + wave) * (2ull * s.batch);
     const Row4* dft4 =
         HDFT ? reinterpret_cast<const Row4*>(reinterpret_cast<const _Float16*>(a.dft16) + (uint64_t)chunk * a.dft_chunk_stride) +
                    lane
              : reinterpret_cast<const Row4*>(a.dft + (uint64_t)chunk * a.dft_chunk_stride) + lane;
-    auto entry = [&](uint32_t j) -> uint32_t {
-        j = j < n ? j : n - 1;  // stage slots past the list repeat its last row (never used)
-        return j < na ? a0 + j : b0 + (j - na);
+    const uint32_t n_stages = (n + R - 1) / R;
+    const uint32_t last = n_stages ? n_stages - 1 : 0u;  // stages past the list repeat the last (never summed)
+    // Lane l < 32 loads the dft row of slot l and lane k < 16 the wave's
+    // mask of feature k (the other lanes repeat them), a stage or two before
+    // the stage needs them, so no load is waited for early.
+    const uint32_t* srow = s.stage_rows + (uint64_t)sb * R + (lane & 31u);
+    const uint32_t* smask =
+        s.stage_masks + ((uint64_t)sb * geom.words + g * kScanWaves + wave) * kScanFeat + (lane % kScanFeat);
+    auto positions = [&](uint32_t T) -> uint32_t { return srow[(uint64_t)(T < last ? T : last) * R]; };
+    auto masks = [&](uint32_t T) -> uint32_t {
+        return smask[(uint64_t)(T < last ? T : last) * geom.words * kScanFeat];
     };
-    // Lane l < 32 loads the position of row 32T + l (its dft row adds the
-    // perspective offset where it is used) and its mask word (lanes 32..63
-    // and rows past the list count as 0 where it is used), so no load is
-    // waited for before its stage needs it.
-    auto positions = [&](uint32_t T) -> uint32_t { return (uint32_t)s.schedule[entry(T * R + (lane & 31u))]; };
-    auto masks = [&](uint32_t T) -> uint32_t { return mrow[entry(T * R + (lane & 31u))]; };
-    auto dft_row = [&](uint32_t pos_lanes, uint32_t j) -> const Row4* {
-        const uint32_t e = entry(j);
-        const uint64_t r = (e >= s.batch ? (uint64_t)s.batch : 0ull) +
-                           (uint32_t)__builtin_amdgcn_readlane(pos_lanes, j % R);
-        return dft4 + r * (kDftChunk / 4);
+    auto dft_row = [&](uint32_t row_lanes, uint32_t j) -> const Row4* {
+        return dft4 + (uint64_t)(uint32_t)__builtin_amdgcn_readlane(row_lanes, j % R) * (kDftChunk / 4);
     };
 
     float4 acc[kScanFeat];
 #pragma unroll
     for (int k = 0; k < kScanFeat; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const uint32_t n_stages = (n + R - 1) / R;
     // Stage T = rows 32T .. 32T+31 of the list; wave w stages rows 32T + 4w
     // .. +3 in LDS buffer T % 2.  Register sets A / B belong to even / odd
     // stages.  While stage T is summed, the rows of stage T+2 are in flight
@@ -942,11 +1006,10 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     } while (0)
 #define TATARA_SUM_STAGE(BUF, M, T)                                       \
     do {                                                                  \
-        const uint32_t mm = (lane < (uint32_t)R && (T) * R + lane < n) ? (M) : 0u; \
         if (nf) {                                                         \
             _Pragma("unroll") for (int k = 0; k < kScanFeat; ++k) {       \
                 /* the stage's rows that hold feature k, ascending */     \
-                uint32_t rows = (uint32_t)__ballot((mm >> k) & 1u);       \
+                uint32_t rows = __builtin_amdgcn_readlane((M), k);        \
                 while (rows) {                                            \
                     const uint32_t jj = __builtin_ctz(rows);              \
                     rows &= rows - 1u;                                    \
@@ -1619,8 +1682,23 @@ int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream) {
     return kOk;
 }
 
+uint64_t ft_scan_max_stages(uint32_t batch, uint32_t n_blocks) {
+    return (2ull * batch + kScanStage - 1) / kScanStage + n_blocks;
+}
+
+int32_t launch_ft_scan_stage_table(const FtBlockScan& s, hipStream_t stream) {
+    TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
+    TATARA_REQUIRE(s.n_blocks >= 1 && s.n_blocks <= 128, "block scan: 1 to 128 king blocks");
+    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables");
+    const uint64_t stages = ft_scan_max_stages(s.batch, s.n_blocks);
+    ft_scan_stage_table_kernel<<<(uint32_t)((stages + 3) / 4), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
+    TATARA_LAUNCHED("ft_scan_stage_table");
+    return kOk;
+}
+
 int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
+    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables (launch_ft_scan_stage_table)");
     TATARA_REQUIRE((a.dft != nullptr) != (a.dft16 != nullptr), "block scan: one dft (f32 or f16)");
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
                    "block scan: chunk-major dft");

@@ -108,6 +108,7 @@ class LayerStackTrainer final : public TrainerBase {
     // block-scan FT backward (f32 dft, factorized feature sets)
     bool use_scan = false;
     uint32_t *scan_masks = nullptr, *scan_multi = nullptr;
+    uint32_t *scan_stage_rows = nullptr, *scan_stage_masks = nullptr;  // the f32 block scan's stage tables
     // activations
     float *ft_stm = nullptr, *ft_nstm = nullptr, *combined = nullptr, *dft = nullptr;
     float *l1_sorted = nullptr, *dl1_sorted = nullptr, *net_out = nullptr;
@@ -233,6 +234,10 @@ class LayerStackTrainer final : public TrainerBase {
         use_scan = factorized && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
                          (st = arena.alloc(&scan_multi, 1)) ||
+                         (!h_out && ((st = arena.alloc(&scan_stage_rows, ft_scan_max_stages(B, n_king_bins) * 32, false)) ||
+                                     (st = arena.alloc(&scan_stage_masks,
+                                                       ft_scan_max_stages(B, n_king_bins) * ft_scan_mask_words(pi) * 16,
+                                                       false)))) ||
                          (st = arena.alloc(&radix_hist, 256ull * binsort_tiles((uint32_t)n_items), false)) ||
                          (st = arena.alloc(&radix_count, 256))))
             return st;
@@ -439,6 +444,8 @@ class LayerStackTrainer final : public TrainerBase {
         sc.sched_start = sched_start;
         sc.masks = scan_masks;
         sc.multi = scan_multi;
+        sc.stage_rows = scan_stage_rows;
+        sc.stage_masks = scan_stage_masks;
         sc.batch = p.b;
         sc.max_active = max_active;
         sc.cols = ft_in;
@@ -486,6 +493,7 @@ class LayerStackTrainer final : public TrainerBase {
                 // mask pass sets scan_multi); no host wait
                 if ((st = fork_side())) return st;
                 if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
+                if (!h_out && (st = launch_ft_scan_stage_table(block_scan(p), side))) return st;
                 if ((st = sort_occurrences(p, side, true))) return st;
             }
         }
