@@ -537,10 +537,14 @@ __global__ __launch_bounds__(1024) void reduce_rows_kernel(const float* __restri
     if (phase == 0 && c < n_cols) out[(uint64_t)seg * n_cols + c] = part[0][lane];
 }
 
-// The reduce_rows_kernel shape for a matrix n_cols wide.
+// The reduce_rows_kernel shape for a matrix n_cols wide: 16-column
+// workgroups for narrow matrices, and for tall ones whose 64-column
+// workgroups would not fill the chip (fewer rows per thread).
 void reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols, const uint32_t* seg_rows, uint32_t n_seg,
                  float* out, hipStream_t stream) {
-    if (n_cols <= 16)
+    // (n_rows: all segments' rows; 0 when unknown on the host)
+    const bool tall = n_rows >= 256ull * n_seg && (uint64_t)ceil_div(n_cols, 64) * n_seg < 256;
+    if (n_cols <= 16 || tall)
         reduce_rows_kernel<16><<<dim3(ceil_div(n_cols, 16), n_seg), 1024, 0, stream>>>(P, n_rows, n_cols, seg_rows,
                                                                                       out);
     else
