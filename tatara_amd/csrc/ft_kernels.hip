@@ -839,6 +839,41 @@ __global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanG
     }
 }
 
+// The king block of rank `rank` when the blocks are ordered by descending
+// row count (ties: lower block first); up to 128 blocks, two per lane.
+__device__ __forceinline__ uint32_t block_of_rank(const FtBlockScan& s, uint32_t rank, uint32_t lane) {
+    const uint32_t nb = s.n_blocks;
+    auto block_rows = [&](uint32_t k) -> uint32_t {
+        return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
+                      : 0u;
+    };
+    const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
+    uint32_t r0 = 0, r1 = 0;
+    for (uint32_t m = 0; m < nb; ++m) {
+        const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
+        r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
+        r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
+    }
+    const uint64_t h0 = __ballot(lane < nb && r0 == rank);
+    const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
+    return __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
+}
+
+// The first stage of block K in the stage tables: the blocks before it
+// hold ceil(rows / 32) stages each (at most 128 blocks, two per lane).
+__device__ __forceinline__ uint32_t block_stage_base(const FtBlockScan& s, uint32_t K, uint32_t lane) {
+    const uint32_t nb = s.n_blocks;
+    auto stages = [&](uint32_t k) -> uint32_t {
+        return k < K ? ((s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k]) +
+                        31u) / 32u
+                     : 0u;
+    };
+    uint32_t v = stages(lane) + stages(lane + 64);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
 // One wave per stage.  Thread 0 of each workgroup numbers the blocks'
 // stages (at most 128 blocks); a wave finds its block by binary search.
 __global__ __launch_bounds__(256) void ft_scan_stage_table_kernel(FtBlockScan s, ScanGeom geom) {
@@ -922,27 +957,8 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t pair = (i_xcd / geom.n_groups) * kNumXcd + xcd;
     if (pair >= nb * n_chunks) return;
     const uint32_t rank = pair / n_chunks, chunk = pair % n_chunks;
-    uint32_t K, sb = 0;  // the block, and its first stage in the stage tables
-    {
-        auto block_rows = [&](uint32_t k) -> uint32_t {
-            return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
-                          : 0u;
-        };
-        const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
-        uint32_t r0 = 0, r1 = 0;  // ranks of blocks lane and lane + 64 (ties: lower block first)
-        for (uint32_t m = 0; m < nb; ++m) {
-            const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
-            r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
-            r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
-        }
-        const uint64_t h0 = __ballot(lane < nb && r0 == rank);
-        const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
-        K = __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
-        for (uint32_t m = 0; m < K; ++m) {
-            const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
-            sb += (zm + 31u) / 32u;
-        }
-    }
+    const uint32_t K = block_of_rank(s, rank, lane);
+    const uint32_t sb = block_stage_base(s, K, lane);  // its first stage in the stage tables
     const uint32_t PI = s.piece_inputs;
     const uint32_t blk_lo = K * PI;
     const uint32_t blk_n = s.cols > blk_lo ? (s.cols - blk_lo < PI ? s.cols - blk_lo : PI) : 0u;
@@ -1139,33 +1155,12 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// The king block of rank `rank` when the blocks are ordered by descending
-// row count (ties: lower block first); up to 128 blocks, two per lane.
-__device__ __forceinline__ uint32_t block_of_rank(const FtBlockScan& s, uint32_t rank, uint32_t lane) {
-    const uint32_t nb = s.n_blocks;
-    auto block_rows = [&](uint32_t k) -> uint32_t {
-        return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
-                      : 0u;
-    };
-    const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
-    uint32_t r0 = 0, r1 = 0;
-    for (uint32_t m = 0; m < nb; ++m) {
-        const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
-        r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
-        r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
-    }
-    const uint64_t h0 = __ballot(lane < nb && r0 == rank);
-    const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
-    return __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
-}
 
-// 8 mask words (rows 8o..8o+7 of an MFMA step) -> the A operand of feature
-// bit m: f16 1.0 where the bit is set, 0.0 elsewhere (two halves per dword).
-__device__ __forceinline__ half8 hit_operand(u32x4 w0, u32x4 w1, uint32_t m) {
-    auto pair = [&](uint32_t lo, uint32_t hi) -> uint32_t {
-        return (((lo >> m) & 1u) | (((hi >> m) & 1u) << 16)) * 0x3C00u;
-    };
-    const u32x4 r = {pair(w0.x, w0.y), pair(w0.z, w0.w), pair(w1.x, w1.y), pair(w1.z, w1.w)};
+// A feature's slot bits of 8 rows (bit e: row e) -> its A operand: f16 1.0
+// where the bit is set, 0.0 elsewhere (two halves per dword).
+__device__ __forceinline__ half8 hit_operand(uint32_t b) {
+    auto pair = [&](uint32_t e) -> uint32_t { return (((b >> e) & 1u) | (((b >> (e + 1)) & 1u) << 16)) * 0x3C00u; };
+    const u32x4 r = {pair(0), pair(2), pair(4), pair(6)};
     return __builtin_bit_cast(half8, r);
 }
 
@@ -1175,7 +1170,8 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     constexpr uint32_t R = kMfmaRows, KS = R / 32, RW = R / kMfmaWaves;  // MFMA steps, rows per wave
     if (__builtin_amdgcn_readfirstlane(*s.multi)) return;  // the occurrence-list kernel runs instead
     __shared__ __attribute__((aligned(16))) _Float16 s_lds[kMfmaLdsHalves];  // two stage buffers
-    __shared__ __attribute__((aligned(16))) uint32_t s_m[2][kScanWaves][R];      // [mask word][row]
+    // [K-step][mask word][feature]: the stage's slot masks (bit r: row r of the K-step)
+    __shared__ uint32_t s_mt[2][KS * kScanWaves * kScanFeat];
     auto s_d = [&](uint32_t buf, uint32_t slot) -> _Float16* { return s_lds + buf * kMfmaStageHalves + slot * 8; };
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t lane = threadIdx.x % 64;
@@ -1188,21 +1184,23 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     const uint32_t pair = (i_xcd / (2 * geom.n_groups)) * kNumXcd + xcd;
     if (pair >= s.n_blocks * n_chunks) return;
     const uint32_t K = block_of_rank(s, pair / n_chunks, lane), chunk = pair % n_chunks;
+    const uint32_t sb = block_stage_base(s, K, lane);
     const uint32_t PI = s.piece_inputs;
     const uint32_t blk_lo = K * PI;
     const uint32_t blk_n = s.cols > blk_lo ? (s.cols - blk_lo < PI ? s.cols - blk_lo : PI) : 0u;
     const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
     const uint32_t b0 = s.sched_start[s.n_blocks + K];
     const uint32_t n = na + (s.sched_start[s.n_blocks + K + 1] - b0);
-    auto entry = [&](uint32_t j) -> uint32_t {
-        j = j < n ? j : n - 1;
-        return j < na ? a0 + j : b0 + (j - na);
-    };
     const _Float16* d16 =
         reinterpret_cast<const _Float16*>(a.dft16) + (uint64_t)chunk * a.dft_chunk_stride + half * kMfmaCols;
-    // thread t stages mask word t / 32 of rows t % 32 + 32k
-    const uint32_t mw = threadIdx.x / 32, mr = threadIdx.x % 32;
-    const uint32_t* mplane = s.masks + (uint64_t)(g * kScanWaves + mw) * (2ull * s.batch);
+    // Thread t loads slot mask t of a stage: K-step t / 128, mask word
+    // (t / 16) % 8 of the group, feature t % 16, from the stage tables (the
+    // block's 32-row stages; a K-step past them has no hits).
+    static_assert(KS * kScanWaves * kScanFeat == kMfmaWaves * 64, "one slot mask per thread");
+    const uint32_t mks = threadIdx.x / (kScanWaves * kScanFeat);
+    const uint32_t* tmask = s.stage_masks + (uint64_t)(g * kScanWaves) * kScanFeat + threadIdx.x % (kScanWaves * kScanFeat);
+    const uint32_t n32 = (n + 31) / 32;
+    const uint32_t* trow = s.stage_rows + (uint64_t)sb * 32;
     const uint32_t n_stages = (n + R - 1) / R;
 
     // Stage T in registers: wave w's rows RT + RW w + j, the lane's columns
@@ -1217,24 +1215,24 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     // accumulators and halves the occupancy.)
     struct Stage {
         uint32_t r[RW];
-        uint32_t mw[R / 32];
+        uint32_t mt;
     };
-    static_assert(R <= 64, "one row position per lane");
-    auto load_pos = [&](uint32_t T) -> uint32_t { return (uint32_t)s.schedule[entry(T * R + lane % R)]; };
+    static_assert(R <= 64, "one row id per lane");
+    // the dft rows of stage T's slots (slots past the block's stages repeat
+    // its last table slot; their rows are zeroed below)
+    auto load_pos = [&](uint32_t T) -> uint32_t {
+        const uint32_t j = T * R + lane % R;
+        return trow[j < 32 * n32 ? j : 32 * n32 - 1];
+    };
     auto load_rows = [&](Stage& S, uint32_t pos, uint32_t T) {
 #pragma unroll
         for (uint32_t j = 0; j < RW; ++j) {
             const uint32_t jj = T * R + wave * RW + j;
-            const uint32_t e = entry(jj);
-            const uint64_t r = (e >= s.batch ? (uint64_t)s.batch : 0ull) +
-                               (uint32_t)__builtin_amdgcn_readlane(pos, wave * RW + j);
+            const uint64_t r = (uint32_t)__builtin_amdgcn_readlane(pos, wave * RW + j);
             S.r[j] = jj < n ? reinterpret_cast<const uint32_t*>(d16 + r * kDftChunk)[lane] : 0u;
         }
-#pragma unroll
-        for (uint32_t k = 0; k < R / 32; ++k) {
-            const uint32_t jm = T * R + mr + 32 * k;
-            S.mw[k] = jm < n ? mplane[entry(jm)] : 0u;
-        }
+        const uint32_t ts = T * KS + mks;
+        S.mt = ts < n32 ? tmask[(uint64_t)(sb + ts) * geom.words * kScanFeat] : 0u;
     };
     // registers -> LDS buffer: column 2 lane + c gets this wave's rows
     auto store_rows = [&](const Stage& S, uint32_t buf) {
@@ -1250,8 +1248,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
                 }
                 *reinterpret_cast<u32x4*>(s_d(buf, stage_slot(lane * 2 + c, wave * (RW / 8) + o))) = v;
             }
-#pragma unroll
-        for (uint32_t k = 0; k < R / 32; ++k) s_m[buf][mw][mr + 32 * k] = S.mw[k];
+        s_mt[buf][threadIdx.x] = S.mt;
     };
 
     const uint32_t m = lane % 16, oct = lane / 16;
@@ -1280,10 +1277,8 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
         for (uint32_t ks = 0; ks < KS; ++ks) {
             half8 A[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const u32x4* wp = reinterpret_cast<const u32x4*>(&s_m[buf][wave * 2 + i][32 * ks + oct * 8]);
-                A[i] = hit_operand(wp[0], wp[1], m);
-            }
+            for (int i = 0; i < 2; ++i)
+                A[i] = hit_operand(s_mt[buf][(ks * kScanWaves + wave * 2 + i) * kScanFeat + m] >> (8 * oct));
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const half8 B = *reinterpret_cast<const half8*>(s_d(buf, stage_slot(j * 16 + m, 4 * ks + oct)));
@@ -1726,6 +1721,7 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
 }
 
 int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
+    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables (launch_ft_scan_stage_table)");
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "mfma backward: piece_inputs out of range");
     TATARA_REQUIRE(a.dft16 && !a.dft, "mfma backward: f16 dft only");
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,

@@ -356,7 +356,7 @@ static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, f
     sc.piece_inputs = piece_inputs;
     sc.n_blocks = n_blocks;
     if ((st = launch_ft_scan_masks(sc, 0))) return st;
-    if (!mfma && (st = launch_ft_scan_stage_table(sc, 0))) return st;
+    if ((st = launch_ft_scan_stage_table(sc, 0))) return st;
     // occurrence lists for the fallback (a row with features of two blocks)
     const uint64_t n_items = two_b * max_active;
     const uint32_t n_keys = 2 * cols + 1;

@@ -234,10 +234,9 @@ class LayerStackTrainer final : public TrainerBase {
         use_scan = factorized && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
         if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
                          (st = arena.alloc(&scan_multi, 1)) ||
-                         (!h_out && ((st = arena.alloc(&scan_stage_rows, ft_scan_max_stages(B, n_king_bins) * 32, false)) ||
-                                     (st = arena.alloc(&scan_stage_masks,
-                                                       ft_scan_max_stages(B, n_king_bins) * ft_scan_mask_words(pi) * 16,
-                                                       false)))) ||
+                         (st = arena.alloc(&scan_stage_rows, ft_scan_max_stages(B, n_king_bins) * 32, false)) ||
+                         (st = arena.alloc(&scan_stage_masks,
+                                           ft_scan_max_stages(B, n_king_bins) * ft_scan_mask_words(pi) * 16, false)) ||
                          (st = arena.alloc(&radix_hist, 256ull * binsort_tiles((uint32_t)n_items), false)) ||
                          (st = arena.alloc(&radix_count, 256))))
             return st;
@@ -493,7 +492,7 @@ class LayerStackTrainer final : public TrainerBase {
                 // mask pass sets scan_multi); no host wait
                 if ((st = fork_side())) return st;
                 if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
-                if (!h_out && (st = launch_ft_scan_stage_table(block_scan(p), side))) return st;
+                if ((st = launch_ft_scan_stage_table(block_scan(p), side))) return st;
                 if ((st = sort_occurrences(p, side, true))) return st;
             }
         }
