@@ -756,18 +756,15 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
 // register and its rows are added in list order.  The optimizer update of
 // the group's cells follows the scan in the same workgroup.
 //
-// Hit masks (ft_scan_masks_kernel): for schedule entry e (a row) and word
-// q = g*W + w, bit k of masks[q][e] is set when block feature g*GS + 16w + k
-// occurs in the row.  A row with a feature outside its own block, or with
-// one feature in two slots, sets *multi; the scan then leaves the step to
-// the occurrence-list kernel, which runs only in that case.
-//
-// Stage tables (ft_scan_stage_table_kernel, once per step for all column
+// Stage tables (ft_scan_tables_kernel, once per step for all column
 // chunks): the blocks' stages numbered consecutively, block K's first at
 // sum over k < K of ceil(rows_k / 32); for each stage the dft row of each
 // of its 32 slots (perspective * batch + position; slots past the block's
-// list repeat its last row) and, per mask word q, the 16 feature masks of
-// the stage (the hit masks transposed).
+// list repeat its last row) and, for mask word q = g*W + w and feature k,
+// a slot mask whose bit r is set when slot r's row holds block feature
+// g*GS + 16w + k.  A row with a feature outside its own block, or with one
+// feature in two slots, sets *multi; the scan then leaves the step to the
+// occurrence-list kernel, which runs only in that case.
 // ---------------------------------------------------------------------------
 
 constexpr int kScanWaves = 8;
@@ -788,55 +785,6 @@ __host__ __device__ inline ScanGeom scan_geom(uint32_t piece_inputs) {
     g.group_size = g.n_groups ? (piece_inputs + g.n_groups - 1) / g.n_groups : 0;
     g.words = g.n_groups * kScanWaves;
     return g;
-}
-
-// 64 schedule entries per workgroup: a wave builds the masks of one entry at
-// a time (lane = slot) in LDS, then every mask plane's 64 words are written
-// as one coalesced segment.
-__global__ __launch_bounds__(256) void ft_scan_masks_kernel(FtBlockScan s, ScanGeom geom) {
-    __shared__ uint32_t s_m[kScanMaxWords][65];  // [word][entry], padded against bank conflicts
-    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const uint64_t e0 = (uint64_t)blockIdx.x * 64;
-    const uint64_t two_b = 2ull * s.batch;
-    for (uint32_t i = threadIdx.x; i < geom.words * 64; i += 256) s_m[i / 64][i % 64] = 0u;
-    __syncthreads();
-    bool multi = false;
-    for (uint32_t r = wave; r < 64 && e0 + r < two_b; r += 4) {
-        const uint64_t e = e0 + r;
-        const uint32_t persp = e >= s.batch ? 1u : 0u;
-        const uint32_t pos = (uint32_t)s.schedule[e];
-        const int32_t* row = (persp ? s.idx_nstm : s.idx_stm) + (uint64_t)pos * s.max_active;
-        const int nn = s.nnz[pos] < (int)s.max_active ? s.nnz[pos] : (int)s.max_active;
-        int v = -1;
-        if (lane < (uint32_t)nn) v = row[lane];
-        const bool ok = lane < (uint32_t)nn && v >= 0 && (uint32_t)v < s.cols;
-        // the row's block: that of its first valid feature, as king_block_keys
-        const uint64_t okm = __ballot(ok);
-        uint32_t blk = 0;
-        if (okm) {
-            blk = (uint32_t)__shfl(v, (int)__builtin_ctzll(okm)) / s.piece_inputs;
-            if (blk >= s.n_blocks) blk = s.n_blocks - 1;
-        }
-        if (ok) {
-            const int64_t local = (int64_t)v - (int64_t)blk * s.piece_inputs;
-            if (local < 0 || local >= (int64_t)s.piece_inputs) {
-                multi = true;  // a feature outside the row's block
-            } else {
-                const uint32_t g = (uint32_t)local / geom.group_size;
-                const uint32_t rr = (uint32_t)local - g * geom.group_size;
-                const uint32_t q = g * kScanWaves + rr / kScanFeat;
-                const uint32_t bit = 1u << (rr % kScanFeat);
-                const uint32_t old = atomicOr(&s_m[q][r], bit);
-                if (old & bit) multi = true;  // the feature is in the row twice
-            }
-        }
-    }
-    if (multi) atomicOr(s.multi, 1u);
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < geom.words * 64; i += 256) {
-        const uint32_t q = i / 64, r = i % 64;
-        if (e0 + r < two_b) s.masks[(uint64_t)q * two_b + e0 + r] = s_m[q][r];
-    }
 }
 
 // The king block of rank `rank` when the blocks are ordered by descending
@@ -875,10 +823,14 @@ __device__ __forceinline__ uint32_t block_stage_base(const FtBlockScan& s, uint3
 }
 
 // One wave per stage.  Thread 0 of each workgroup numbers the blocks'
-// stages (at most 128 blocks); a wave finds its block by binary search.
-__global__ __launch_bounds__(256) void ft_scan_stage_table_kernel(FtBlockScan s, ScanGeom geom) {
-    static_assert(kScanFeat == 16 && kScanStage == 32, "two mask words of 16 features per ballot");
+// stages (at most 128 blocks); a wave finds its block by binary search,
+// loads its 32 slots' schedule entries and feature counts at once (lane =
+// slot), then the slots' feature indices four rows at a time (lane =
+// feature slot), and sets the slot bits of its feature masks in LDS.
+__global__ __launch_bounds__(256) void ft_scan_tables_kernel(FtBlockScan s, ScanGeom geom) {
+    static_assert(kScanFeat == 16 && kScanStage == 32, "32 slots per stage, 16 features per mask word");
     __shared__ uint32_t s_base[129];
+    __shared__ uint32_t s_t[4][kScanMaxWords * kScanFeat];  // per wave: [mask word][feature]
     const uint32_t nb = s.n_blocks;
     if (threadIdx.x == 0) {
         uint32_t acc = 0;
@@ -906,28 +858,50 @@ __global__ __launch_bounds__(256) void ft_scan_stage_table_kernel(FtBlockScan s,
     const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
     const uint32_t b0 = s.sched_start[nb + K];
     const uint32_t n = na + (s.sched_start[nb + K + 1] - b0);  // >= 1: the block has this stage
-    const uint32_t r = lane & 31u, j = T * 32u + r;
-    const bool valid = j < n;
-    const uint32_t jc = valid ? j : n - 1;
+    const uint32_t W = geom.words, WK = W * kScanFeat;
+    uint32_t* st = s_t[wave];
+    for (uint32_t i = lane; i < WK; i += 64) st[i] = 0u;
+    // slot lane % 32: its row (slots past the block's list repeat its last row)
+    const uint32_t slots = n - T * 32u < 32u ? n - T * 32u : 32u;
+    const uint32_t jc = T * 32u + ((lane & 31u) < slots ? (lane & 31u) : slots - 1);
     const uint32_t e = jc < na ? a0 + jc : b0 + (jc - na);
-    if (lane < 32) s.stage_rows[(uint64_t)gs * 32 + r] = (e >= s.batch ? s.batch : 0u) + (uint32_t)s.schedule[e];
-    const uint64_t two_b = 2ull * s.batch;
-    const uint32_t W = geom.words;
-    uint32_t* out = s.stage_masks + (uint64_t)gs * W * kScanFeat;
-    for (uint32_t q = 0; q < W; q += 2) {
-        // lanes 0..31: word q of slots 0..31, lanes 32..63: word q + 1
-        const uint32_t qq = q + (lane >> 5);
-        const uint32_t m = (valid && qq < W) ? s.masks[(uint64_t)qq * two_b + e] : 0u;
-        uint32_t v = 0;
+    const uint32_t persp = e >= s.batch ? 1u : 0u;
+    const uint32_t pos = (uint32_t)s.schedule[e];
+    if (lane < 32) s.stage_rows[(uint64_t)gs * 32 + lane] = persp * s.batch + pos;
+    const int32_t nz = s.nnz[pos];
+    const uint32_t nn = nz <= 0 ? 0u : ((uint32_t)nz < s.max_active ? (uint32_t)nz : s.max_active);
+    const int64_t blk_lo = (int64_t)K * s.piece_inputs;
+    bool multi = false;
+    for (uint32_t r0 = 0; r0 < slots; r0 += 4) {
+        int32_t v[4];
 #pragma unroll
-        for (int k = 0; k < kScanFeat; ++k) {
-            const uint64_t b = __ballot((m >> k) & 1u);
-            // lane k keeps word q's mask of feature k, lane 16 + k word q + 1's
-            v = lane == (uint32_t)k ? (uint32_t)b : v;
-            v = lane == (uint32_t)(16 + k) ? (uint32_t)(b >> 32) : v;
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t r = (r0 + u) & 31u;
+            const uint32_t pr = __builtin_amdgcn_readlane(pos, r), pp = __builtin_amdgcn_readlane(persp, r);
+            const uint32_t nr = __builtin_amdgcn_readlane(nn, r);
+            v[u] = (r0 + u < slots && lane < nr) ? (pp ? s.idx_nstm : s.idx_stm)[(uint64_t)pr * s.max_active + lane]
+                                                 : -1;
         }
-        if (lane < 32 && q + (lane >> 4) < W) out[(uint64_t)q * kScanFeat + lane] = v;
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const int32_t x = v[u];
+            if (x < 0 || (uint32_t)x >= s.cols) continue;  // an empty or invalid slot
+            const int64_t local = (int64_t)x - blk_lo;
+            if (local < 0 || local >= (int64_t)s.piece_inputs) {
+                multi = true;  // a feature outside the row's block
+                continue;
+            }
+            const uint32_t g = (uint32_t)local / geom.group_size;
+            const uint32_t rr = (uint32_t)local - g * geom.group_size;
+            const uint32_t q = g * kScanWaves + rr / kScanFeat;
+            const uint32_t bit = 1u << (r0 + u);
+            const uint32_t old = atomicOr(&st[q * kScanFeat + rr % kScanFeat], bit);
+            if (old & bit) multi = true;  // the feature is in the row twice
+        }
     }
+    if (multi) atomicOr(s.multi, 1u);
+    uint32_t* out = s.stage_masks + (uint64_t)gs * WK;
+    for (uint32_t i = lane; i < WK; i += 64) out[i] = st[i];
 }
 
 // HDFT: the dft is f16 (the --ft-fp16-out mode): rows are staged as f16
@@ -1665,35 +1639,27 @@ uint32_t ft_scan_mask_words(uint32_t piece_inputs) {
     return piece_inputs > 0 && g.words <= (uint32_t)kScanMaxWords ? g.words : 0u;
 }
 
-int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream) {
-    TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
-    TATARA_REQUIRE(s.max_active <= (uint32_t)kMaxActive, "max_active must be <= 64");
-    TATARA_REQUIRE(s.n_blocks >= 1, "block scan: n_blocks >= 1");
-    int32_t st = launch_fill_i32(reinterpret_cast<int32_t*>(s.multi), 1, 0, stream);
-    if (st) return st;
-    if (s.batch == 0) return kOk;
-    ft_scan_masks_kernel<<<ceil_div(2ull * s.batch, 64), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
-    TATARA_LAUNCHED("ft_scan_masks");
-    return kOk;
-}
-
 uint64_t ft_scan_max_stages(uint32_t batch, uint32_t n_blocks) {
     return (2ull * batch + kScanStage - 1) / kScanStage + n_blocks;
 }
 
-int32_t launch_ft_scan_stage_table(const FtBlockScan& s, hipStream_t stream) {
+int32_t launch_ft_scan_tables(const FtBlockScan& s, hipStream_t stream) {
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
+    TATARA_REQUIRE(s.max_active <= (uint32_t)kMaxActive, "max_active must be <= 64");
     TATARA_REQUIRE(s.n_blocks >= 1 && s.n_blocks <= 128, "block scan: 1 to 128 king blocks");
-    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables");
+    TATARA_REQUIRE(s.stage_rows && s.stage_masks && s.multi, "block scan: stage tables and flag");
+    int32_t st = launch_fill_i32(reinterpret_cast<int32_t*>(s.multi), 1, 0, stream);
+    if (st) return st;
+    if (s.batch == 0) return kOk;
     const uint64_t stages = ft_scan_max_stages(s.batch, s.n_blocks);
-    ft_scan_stage_table_kernel<<<(uint32_t)((stages + 3) / 4), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
-    TATARA_LAUNCHED("ft_scan_stage_table");
+    ft_scan_tables_kernel<<<(uint32_t)((stages + 3) / 4), 256, 0, stream>>>(s, scan_geom(s.piece_inputs));
+    TATARA_LAUNCHED("ft_scan_tables");
     return kOk;
 }
 
 int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "block scan: piece_inputs out of range");
-    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables (launch_ft_scan_stage_table)");
+    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables (launch_ft_scan_tables)");
     TATARA_REQUIRE((a.dft != nullptr) != (a.dft16 != nullptr), "block scan: one dft (f32 or f16)");
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
                    "block scan: chunk-major dft");
@@ -1721,7 +1687,7 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
 }
 
 int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback) {
-    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables (launch_ft_scan_stage_table)");
+    TATARA_REQUIRE(s.stage_rows && s.stage_masks, "block scan: stage tables (launch_ft_scan_tables)");
     TATARA_REQUIRE(ft_scan_mask_words(s.piece_inputs) > 0, "mfma backward: piece_inputs out of range");
     TATARA_REQUIRE(a.dft16 && !a.dft, "mfma backward: f16 dft only");
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,

@@ -86,9 +86,8 @@ struct FtBlockScan {
     const int32_t* nnz;
     const int32_t* schedule;      // [2*batch] positions grouped by (perspective, block), ascending
     const uint32_t* sched_start;  // [2*n_blocks + 1] first entry of each (perspective, block) bin
-    uint32_t* masks;              // [ft_scan_mask_words(piece_inputs)][2*batch]
     uint32_t* multi;              // [1] set when a row has features of two blocks, or one twice
-    // per-stage tables of the f32 block scan (ft_scan_max_stages stages)
+    // per-stage tables of the block scan (ft_scan_max_stages stages)
     uint32_t* stage_rows;         // [stages][32] dft row of each stage slot
     uint32_t* stage_masks;        // [stages][mask words][16] per-feature slot masks
     uint32_t batch, max_active, cols, piece_inputs, n_blocks;
@@ -108,12 +107,11 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream);
 int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream);
 // Mask words per schedule entry (0 when the block scan cannot serve piece_inputs).
 uint32_t ft_scan_mask_words(uint32_t piece_inputs);
-// Hit masks and the multi flag of a batch (after its schedule).
-int32_t launch_ft_scan_masks(const FtBlockScan& s, hipStream_t stream);
 // Stages of 32 rows the block scan's tables hold at most for a batch.
 uint64_t ft_scan_max_stages(uint32_t batch, uint32_t n_blocks);
-// The f32 block scan's stage tables (after the hit masks).
-int32_t launch_ft_scan_stage_table(const FtBlockScan& s, hipStream_t stream);
+// The block scan's stage tables and the multi flag of a batch (after its
+// schedule).
+int32_t launch_ft_scan_tables(const FtBlockScan& s, hipStream_t stream);
 // FT gradient + update by block scan (chunk-major dft, f32 or f16); the kernel does
 // nothing when *s.multi is set.  With fallback, the occurrence-list kernel
 // (its lists already sorted) is queued behind it and runs only in that case.

@@ -309,13 +309,12 @@ static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, f
     const uint64_t two_b = 2ull * batch;
     const uint32_t chunks = ceil_div(ft_out, kDftChunk);
     // king-block schedule, as the trainer builds it for the forward
-    DevScratch keys, sched, hist, start, count, cm, masks, multi, srows, smasks;
+    DevScratch keys, sched, hist, start, count, cm, multi, srows, smasks;
     const uint64_t stages = ft_scan_max_stages(batch, n_blocks);
     if ((st = keys.alloc(two_b)) || (st = sched.alloc(4 * two_b)) ||
         (st = hist.alloc(4ull * 2 * n_blocks * binsort_tiles((uint32_t)two_b))) ||
         (st = start.alloc(4ull * (2 * n_blocks + 1))) || (st = count.alloc(4ull * 2 * n_blocks)) ||
         (st = cm.alloc(4ull * chunks * two_b * kDftChunk)) ||
-        (st = masks.alloc(4ull * ft_scan_mask_words(piece_inputs) * two_b)) ||
         (st = multi.alloc(4)) || (st = srows.alloc(4ull * stages * 32)) ||
         (st = smasks.alloc(4ull * stages * ft_scan_mask_words(piece_inputs) * 16)))
         return st;
@@ -346,7 +345,6 @@ static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, f
     sc.nnz = nnz;
     sc.schedule = sched.as<int32_t>();
     sc.sched_start = start.as<uint32_t>();
-    sc.masks = masks.as<uint32_t>();
     sc.multi = multi.as<uint32_t>();
     sc.stage_rows = srows.as<uint32_t>();
     sc.stage_masks = smasks.as<uint32_t>();
@@ -355,8 +353,7 @@ static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, f
     sc.cols = cols;
     sc.piece_inputs = piece_inputs;
     sc.n_blocks = n_blocks;
-    if ((st = launch_ft_scan_masks(sc, 0))) return st;
-    if ((st = launch_ft_scan_stage_table(sc, 0))) return st;
+    if ((st = launch_ft_scan_tables(sc, 0))) return st;
     // occurrence lists for the fallback (a row with features of two blocks)
     const uint64_t n_items = two_b * max_active;
     const uint32_t n_keys = 2 * cols + 1;

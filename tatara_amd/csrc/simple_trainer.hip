@@ -59,8 +59,8 @@ class SimpleTrainer final : public TrainerBase {
     uint32_t *radix_hist = nullptr, *radix_count = nullptr;  // the gated occurrence sort's scratch
     // block-scan FT backward (factorized feature sets)
     bool use_scan = false;
-    uint32_t *scan_masks = nullptr, *scan_multi = nullptr;
-    uint32_t *scan_stage_rows = nullptr, *scan_stage_masks = nullptr;  // the f32 block scan's stage tables
+    uint32_t* scan_multi = nullptr;
+    uint32_t *scan_stage_rows = nullptr, *scan_stage_masks = nullptr;  // the block scan's stage tables
     // activations
     float *ft_stm = nullptr, *ft_nstm = nullptr, *combined = nullptr, *dft = nullptr;
     float *l1_pre = nullptr, *dl1 = nullptr, *net_out = nullptr;
@@ -157,8 +157,7 @@ class SimpleTrainer final : public TrainerBase {
             (st = arena.alloc((uint8_t**)&occ_tmp, occ_tmp_bytes, false)))
             return st;
         use_scan = factorized && ft_out >= kDftChunk && ft_scan_mask_words(pi) > 0;
-        if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
-                         (st = arena.alloc(&scan_multi, 1)) ||
+        if (use_scan && ((st = arena.alloc(&scan_multi, 1)) ||
                          (st = arena.alloc(&scan_stage_rows, ft_scan_max_stages(B, n_king_bins) * 32, false)) ||
                          (st = arena.alloc(&scan_stage_masks,
                                            ft_scan_max_stages(B, n_king_bins) * ft_scan_mask_words(pi) * 16, false)) ||
@@ -329,7 +328,6 @@ class SimpleTrainer final : public TrainerBase {
         sc.nnz = p.nnz;
         sc.schedule = schedule;
         sc.sched_start = sched_start;
-        sc.masks = scan_masks;
         sc.multi = scan_multi;
         sc.stage_rows = scan_stage_rows;
         sc.stage_masks = scan_stage_masks;
@@ -375,8 +373,7 @@ class SimpleTrainer final : public TrainerBase {
                 // features of two king blocks or one feature twice (the
                 // mask pass sets scan_multi); no host wait
                 if ((st = fork_side())) return st;
-                if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
-                if ((st = launch_ft_scan_stage_table(block_scan(p), side))) return st;
+                if ((st = launch_ft_scan_tables(block_scan(p), side))) return st;
                 if ((st = sort_occurrences(p, side, true))) return st;
             }
         }

@@ -107,8 +107,8 @@ class LayerStackTrainer final : public TrainerBase {
     uint32_t *radix_hist = nullptr, *radix_count = nullptr;  // the gated occurrence sort's scratch
     // block-scan FT backward (f32 dft, factorized feature sets)
     bool use_scan = false;
-    uint32_t *scan_masks = nullptr, *scan_multi = nullptr;
-    uint32_t *scan_stage_rows = nullptr, *scan_stage_masks = nullptr;  // the f32 block scan's stage tables
+    uint32_t* scan_multi = nullptr;
+    uint32_t *scan_stage_rows = nullptr, *scan_stage_masks = nullptr;  // the block scan's stage tables
     // activations
     float *ft_stm = nullptr, *ft_nstm = nullptr, *combined = nullptr, *dft = nullptr;
     float *l1_sorted = nullptr, *dl1_sorted = nullptr, *net_out = nullptr;
@@ -232,8 +232,7 @@ class LayerStackTrainer final : public TrainerBase {
             return st;
         // the block scan (f32 dft) or its matrix-core form (f16 dft)
         use_scan = factorized && ft_out >= 2 * kDftChunk && ft_scan_mask_words(pi) > 0;
-        if (use_scan && ((st = arena.alloc(&scan_masks, (uint64_t)ft_scan_mask_words(pi) * 2 * B, false)) ||
-                         (st = arena.alloc(&scan_multi, 1)) ||
+        if (use_scan && ((st = arena.alloc(&scan_multi, 1)) ||
                          (st = arena.alloc(&scan_stage_rows, ft_scan_max_stages(B, n_king_bins) * 32, false)) ||
                          (st = arena.alloc(&scan_stage_masks,
                                            ft_scan_max_stages(B, n_king_bins) * ft_scan_mask_words(pi) * 16, false)) ||
@@ -441,7 +440,6 @@ class LayerStackTrainer final : public TrainerBase {
         sc.nnz = p.nnz;
         sc.schedule = schedule;
         sc.sched_start = sched_start;
-        sc.masks = scan_masks;
         sc.multi = scan_multi;
         sc.stage_rows = scan_stage_rows;
         sc.stage_masks = scan_stage_masks;
@@ -491,8 +489,7 @@ class LayerStackTrainer final : public TrainerBase {
                 // features of two king blocks or one feature twice (the
                 // mask pass sets scan_multi); no host wait
                 if ((st = fork_side())) return st;
-                if ((st = launch_ft_scan_masks(block_scan(p), side))) return st;
-                if ((st = launch_ft_scan_stage_table(block_scan(p), side))) return st;
+                if ((st = launch_ft_scan_tables(block_scan(p), side))) return st;
                 if ((st = sort_occurrences(p, side, true))) return st;
             }
         }
