@@ -1110,13 +1110,14 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
 constexpr int kMfmaWaves = 4;  // 32 features each
 constexpr int kMfmaRows = 64;  // rows per stage: two MFMA steps
 // A stage's rows in LDS: 16-byte slots of (column, row octet), each holding
-// that column's 8 rows.  Columns come in groups of 8 (octet-major, then
-// column); within an octet the 8 columns are rotated by the group index, so
-// the slots a wave writes (lanes 2 columns apart) and the slots it reads (8
-// consecutive columns per 8 lanes) fall in 8 distinct bank groups.
+// that column's 8 rows.  Columns come in groups of 16 (octet-major, then
+// column); within an octet the 16 columns are rotated by the group index, so
+// the 16 slots that 16 lanes write (2 columns apart) or read (16
+// consecutive columns) at once fall in 16 distinct groups of the 64 LDS
+// banks.
 constexpr int kMfmaCols = 128;  // columns per workgroup (half a dft chunk)
 __device__ __forceinline__ uint32_t stage_slot(uint32_t col, uint32_t oct) {
-    return (col >> 3) * (uint32_t)kMfmaRows + oct * 8 + ((col + (col >> 3)) & 7u);
+    return (col >> 4) * (uint32_t)(kMfmaRows * 2) + oct * 16 + ((col + (col >> 4)) & 15u);
 }
 constexpr int kMfmaStageHalves = kMfmaCols * kMfmaRows;  // 16 KB per buffer
 constexpr int kMfmaUpdRow = 132;                         // floats per update row (128 + padding)
