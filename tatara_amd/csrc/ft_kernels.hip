@@ -1218,8 +1218,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
                 u32x4 v;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
+                    // column c of rows 2k and 2k + 1: low halves (c = 0) or high halves (c = 1)
+                    // of the two row words, as one byte permute
                     const uint32_t x0 = S.r[8 * o + 2 * k], x1 = S.r[8 * o + 2 * k + 1];
-                    v[k] = c == 0 ? ((x0 & 0xFFFFu) | (x1 << 16)) : ((x0 >> 16) | (x1 & 0xFFFF0000u));
+                    v[k] = __builtin_amdgcn_perm(x1, x0, c == 0 ? 0x05040100u : 0x07060302u);
                 }
                 *reinterpret_cast<u32x4*>(s_d(buf, stage_slot(lane * 2 + c, wave * (RW / 8) + o))) = v;
             }
