@@ -1147,6 +1147,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     __shared__ __attribute__((aligned(16))) _Float16 s_lds[kMfmaLdsHalves];  // two stage buffers
     // [K-step][mask word][feature]: the stage's slot masks (bit r: row r of the K-step)
     __shared__ uint32_t s_mt[2][KS * kScanWaves * kScanFeat];
+    // the A operand of each slot byte (bit e: row e -> f16 1.0 / 0.0)
+    __shared__ __attribute__((aligned(16))) half8 s_hit[256];
+    static_assert(kMfmaWaves * 64 == 256, "one operand table entry per thread");
+    s_hit[threadIdx.x] = hit_operand(threadIdx.x);
     auto s_d = [&](uint32_t buf, uint32_t slot) -> _Float16* { return s_lds + buf * kMfmaStageHalves + slot * 8; };
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t lane = threadIdx.x % 64;
@@ -1255,7 +1259,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
             half8 A[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                A[i] = hit_operand(s_mt[buf][(ks * kScanWaves + wave * 2 + i) * kScanFeat + m] >> (8 * oct));
+                A[i] = s_hit[(s_mt[buf][(ks * kScanWaves + wave * 2 + i) * kScanFeat + m] >> (8 * oct)) & 0xFFu];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const half8 B = *reinterpret_cast<const half8*>(s_d(buf, stage_slot(j * 16 + m, 4 * ks + oct)));
