@@ -5,9 +5,9 @@ compiler: its static assertions pin sizes and offsets, and it prints every
 field's offset and size.  Those are compared with
   - the fields the header declares (so the program misses none),
   - the ctypes structs of tatara_amd/_lib.py (the Python host mirror),
-  - the Rust #[repr(C)] structs INTEGRATION.md gives a maintainer: field
+  - the Rust #[repr(C)] structs the integration guide gives a maintainer: field
     names, order and the layout repr(C) gives them on x86-64 Linux;
-and every Rust `extern "C"` function INTEGRATION.md binds is checked against
+and every Rust `extern "C"` function the integration guide binds is checked against
 the header's parameter list, type by type.
 CPU only.
 """
@@ -70,7 +70,7 @@ RUST_TYPES = {"i32": C.c_int32, "u32": C.c_uint32, "i64": C.c_int64, "u64": C.c_
 
 
 def rust_structs() -> dict[str, list[tuple[str, str]]]:
-    """(field, type) lists of the #[repr(C)] structs in INTEGRATION.md's Rust blocks."""
+    """(field, type) lists of the #[repr(C)] structs in the integration guide's Rust blocks."""
     text = (ROOT / "INTEGRATION.md").read_text()
     out = {}
     for name, body in re.findall(r"#\[repr\(C\)\]\s*pub struct (\w+)\s*\{([^{}]*)\}", text):
@@ -160,7 +160,7 @@ def _header_functions() -> dict[str, list[str]]:
 
 
 def test_integration_doc_rust_functions_match_the_header():
-    """Every `pub fn tatara_*` INTEGRATION.md gives a maintainer has the
+    """Every `pub fn tatara_*` the integration guide gives a maintainer has the
     header's parameter list: count, and each type as repr(C) binds it."""
     text = (ROOT / "INTEGRATION.md").read_text()
     header = _header_functions()
