@@ -399,7 +399,17 @@ typedef struct TataraLoss {
  * [n_pos][max_active], -1 padding; valid slots are [0, nnz[b]).  With
  * on_device = 0 the arrays are host memory and are copied before the call
  * returns; with on_device = 1 they are device pointers (tatara_malloc) that
- * must stay valid until the next train_step/validate_step/flush returns. */
+ * must stay valid until the next train_step/validate_step/flush returns.
+ * on_device = TATARA_BATCH_KING_BLOCKED (2) is on_device = 1 plus the
+ * caller's statement that every row's active features lie in the king block
+ * of its perspective and none repeats (true for tatara_psv_to_batch output of
+ * a king-bucketed feature set from records whose two king squares differ):
+ * the step then queues no occurrence-list fallback for its FT backward.  A
+ * batch for which the statement is false trains without its FT weight
+ * gradient, and the next tatara_trainer_flush_pending_loss returns
+ * TATARA_ERR_STATE (no counterpart in the reference, whose host batches
+ * carry no such statement). */
+#define TATARA_BATCH_KING_BLOCKED 2
 typedef struct TataraBatch {
     int32_t n_pos;
     int32_t max_active;

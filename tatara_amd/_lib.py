@@ -356,6 +356,7 @@ class TataraError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"status {status}: {message}")
         self.status = status
+        self.message = message
 
 
 class OutOfMemory(TataraError):

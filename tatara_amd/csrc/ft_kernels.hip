@@ -15,7 +15,6 @@
 //   optimizer crates/gpu-kernels/src/pointwise/radam_step.rs:116-149
 #include "ft_kernels.hpp"
 
-#include <hipcub/hipcub.hpp>
 #include <type_traits>
 #include <utility>
 
@@ -899,7 +898,10 @@ __global__ __launch_bounds__(256) void ft_scan_tables_kernel(FtBlockScan s, Scan
             if (old & bit) multi = true;  // the feature is in the row twice
         }
     }
-    if (multi) atomicOr(s.multi, 1u);
+    if (multi) {
+        atomicOr(s.multi, 1u);
+        if (s.multi_sticky) atomicOr(s.multi_sticky, 1u);
+    }
     uint32_t* out = s.stage_masks + (uint64_t)gs * WK;
     for (uint32_t i = lane; i < WK; i += 64) out[i] = st[i];
 }
@@ -1535,12 +1537,10 @@ uint32_t occurrence_key_bits(uint32_t cols) {
 }
 
 size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols) {
-    size_t bytes = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr,
-                                             (uint32_t*)nullptr, (const uint32_t*)nullptr,
-                                             (uint32_t*)nullptr, (int)n_items, 0,
-                                             (int)occurrence_key_bits(cols));
-    return bytes;
+    (void)cols;
+    // the LSD passes' digit histograms and digit counts
+    const uint64_t n = n_items < 0xFFFFFFFFull ? n_items : 0xFFFFFFFFull;
+    return 4ull * (256ull * binsort_tiles((uint32_t)n) + 256ull);
 }
 
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) {
@@ -1554,21 +1554,18 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) 
         const uint64_t g = ceil_div(n, 256);
         return (uint32_t)(a.run_if && g > 256 ? 256 : g);
     };
-    if (!a.run_if) {
-        if (n_items > 0) {
-            build_occurrence_keys_kernel<<<grid(n_items), 256, 0, stream>>>(
-                a.idx_stm, a.idx_nstm, a.nnz, a.keys_in, a.vals_in, a.batch, a.max_active, a.cols, nullptr);
-            TATARA_LAUNCHED("build_occurrence_keys");
-            size_t bytes = a.temp_bytes;
-            TATARA_HIP(hipcub::DeviceRadixSort::SortPairs(a.temp, bytes, a.keys_in, a.keys_out,
-                                                          a.vals_in, a.vals_out, (int)n_items, 0,
-                                                          (int)occurrence_key_bits(a.cols), stream),
-                       "occurrence radix sort");
+    if (n_items > 0) {
+        // stable LSD passes of 8 bits (the bin-sort kernels), alternating
+        // between the two buffer pairs and ending in keys_out / vals_out;
+        // their scratch is radix_hist / radix_count, or carved from temp
+        uint32_t* hist = a.radix_hist;
+        uint32_t* count = a.radix_count;
+        if (!hist || !count) {
+            TATARA_REQUIRE(a.temp && a.temp_bytes >= occurrence_sort_temp_bytes(n_items, a.cols),
+                           "occurrence sort: scratch (occurrence_sort_temp_bytes)");
+            hist = static_cast<uint32_t*>(a.temp);
+            count = hist + 256ull * binsort_tiles((uint32_t)n_items);
         }
-    } else if (n_items > 0) {
-        // device-gated: stable LSD passes of 8 bits, alternating between the
-        // two buffer pairs and ending in keys_out / vals_out
-        TATARA_REQUIRE(a.radix_hist && a.radix_count, "gated occurrence sort: radix scratch");
         const uint32_t passes = (occurrence_key_bits(a.cols) + 7) / 8;
         uint32_t *k0 = a.keys_in, *v0 = a.vals_in, *k1 = a.keys_out, *v1 = a.vals_out;
         if (passes % 2 == 0) {
@@ -1584,8 +1581,8 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) 
             r.vals = v0;
             r.n_items = (uint32_t)n_items;
             r.shift = 8 * p;
-            r.hist = a.radix_hist;
-            r.digit_count = a.radix_count;
+            r.hist = hist;
+            r.digit_count = count;
             r.out_keys = k1;
             r.out_vals = v1;
             r.run_if = a.run_if;

@@ -43,11 +43,13 @@ struct OccurrenceSortArgs {
     uint32_t* keys_out;
     uint32_t* vals_out;  // sorted dft row ids
     uint32_t* offsets;   // [2*cols + 2]; key k occupies [offsets[k], offsets[k+1])
-    void* temp;          // radix-sort scratch (ungated sort)
+    // The sort is stable LSD passes of 8 bits (the bin-sort kernels) with
+    // scratch radix_hist [256 * binsort_tiles(2*batch*max_active)] and
+    // radix_count [256], or, when those are null, temp
+    // (occurrence_sort_temp_bytes).
+    void* temp;
     size_t temp_bytes;
-    // Device gate: when set, the sort runs only if *run_if != 0 (stable LSD
-    // passes of the bin-sort kernels, scratch radix_hist [256 *
-    // binsort_tiles(2*batch*max_active)] and radix_count [256]), so a step
+    // Device gate: when set, the sort runs only if *run_if != 0, so a step
     // can queue it without the host learning whether it is needed.
     const uint32_t* run_if;
     uint32_t* radix_hist;
@@ -91,6 +93,9 @@ struct FtBlockScan {
     uint32_t* stage_rows;         // [stages][32] dft row of each stage slot
     uint32_t* stage_masks;        // [stages][mask words][16] per-feature slot masks
     uint32_t batch, max_active, cols, piece_inputs, n_blocks;
+    // optional: also set (and never cleared by the kernels) with *multi, for
+    // a batch whose caller said its rows are king-blocked
+    uint32_t* multi_sticky;
 };
 
 // Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).

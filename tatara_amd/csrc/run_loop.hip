@@ -97,16 +97,36 @@ struct EpochReader {
         TATARA_REQUIRE(records > 0, "the data file holds no PSV records");
         return kOk;
     }
-    int32_t read(uint8_t* dst, uint64_t n) {
+    // n records into dst (pinned memory) through a cached staging buffer,
+    // where the host checks them: *king_blocked is false when, in a feature
+    // set with merged king planes, a record has both kings on one square (its
+    // rows would repeat the king feature); board, hand and king features
+    // occupy disjoint ranges of a king block otherwise, so every decoded row
+    // is king-blocked.  (CPU reads of the pinned buffer itself are uncached.)
+    std::vector<uint8_t> stage;
+    int32_t read(uint8_t* dst, uint64_t n, bool merged_kings, bool* king_blocked) {
+        stage.resize(n * kPsvBytes);
         uint64_t got = 0;
         while (got < n) {
-            const size_t r = fread(dst + got * kPsvBytes, kPsvBytes, n - got, f);
+            const size_t r = fread(stage.data() + got * kPsvBytes, kPsvBytes, n - got, f);
             got += r;
             if (got < n) {
                 TATARA_REQUIRE(!ferror(f), "read error on the data file");
                 rewind(f);  // next epoch
             }
         }
+        bool ok = true;
+        if (merged_kings) {
+            // bit 0: side to move; bits 1..7, 8..14: the king squares (LSB first)
+            for (uint64_t i = 0; i < n && ok; ++i) {
+                const uint8_t* r = stage.data() + i * kPsvBytes;
+                const uint32_t w = (uint32_t)r[0] | ((uint32_t)r[1] << 8);
+                const uint32_t k0 = (w >> 1) & 127u, k1 = (w >> 8) & 127u;
+                ok = !(k0 == k1 && k0 < 81);
+            }
+        }
+        *king_blocked = ok;
+        std::memcpy(dst, stage.data(), n * kPsvBytes);
         return kOk;
     }
 };
@@ -597,7 +617,8 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             Slot& sl = slots[cur];
             // the upload that last read this pinned buffer has finished
             TATARA_HIP(hipEventSynchronize(sl.uploaded), "run: wait for the upload");
-            if ((st = reader.read(sl.psv_host, B))) return st;
+            bool king_blocked = false;
+            if ((st = reader.read(sl.psv_host, B, shape.emit_king && shape.fold_enemy, &king_blocked))) return st;
             TATARA_HIP(hipStreamWaitEvent(mem.copy, sl.consumed, 0), "run: wait for the slot's last step");
             TATARA_HIP(hipMemcpyAsync(sl.psv_dev, sl.psv_host, B * kPsvBytes, hipMemcpyHostToDevice, mem.copy),
                        "PSV upload");
@@ -622,7 +643,7 @@ int32_t run(TataraTrainer* trainer, const TataraRunConfig& c, const TataraLrSche
             bt.bucket_idx = d.bucket;
             bt.score = d.score;
             bt.wdl = d.wdl;
-            bt.on_device = 1;
+            bt.on_device = king_blocked ? TATARA_BATCH_KING_BLOCKED : 1;
             double lagged = 0.0;
             if ((st = tatara_trainer_train_step(trainer, &bt, lr_v, wdl_v, loss, &lagged))) return st;
             TATARA_HIP(hipEventRecord(sl.consumed, mem.stream), "run: record the step");

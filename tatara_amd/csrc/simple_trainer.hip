@@ -317,7 +317,7 @@ class SimpleTrainer final : public TrainerBase {
     // a row the scan cannot take; or occurrence lists every step when the
     // trainer does not scan.
     int32_t ft_gradient(const BatchPtrs& p, const FtGradArgs& fb) {
-        if (use_scan) return launch_ft_grad_scan(fb, block_scan(p), stream, true);
+        if (use_scan) return launch_ft_grad_scan(fb, block_scan(p), stream, !batch_king_blocked);
         return launch_ft_grad_update(fb, stream);
     }
 
@@ -336,6 +336,7 @@ class SimpleTrainer final : public TrainerBase {
         sc.cols = ft_in;
         sc.piece_inputs = pi;
         sc.n_blocks = n_king_bins;
+        sc.multi_sticky = batch_king_blocked ? kb_broken_dev : nullptr;
         return sc;
     }
 
@@ -371,10 +372,12 @@ class SimpleTrainer final : public TrainerBase {
                 // hit masks of the block-scan backward, beside the forward,
                 // then the occurrence sort, which runs only when a row has
                 // features of two king blocks or one feature twice (the
-                // mask pass sets scan_multi); no host wait
+                // mask pass sets scan_multi); no host wait.  A batch passed
+                // as king-blocked (on_device = 2) queues no sort.
                 if ((st = fork_side())) return st;
                 if ((st = launch_ft_scan_tables(block_scan(p), side))) return st;
-                if ((st = sort_occurrences(p, side, true))) return st;
+                if ((st = batch_king_blocked ? note_king_blocked_tables() : sort_occurrences(p, side, true)))
+                    return st;
             }
         }
         if (train && (st = prof_mark(1))) return st;

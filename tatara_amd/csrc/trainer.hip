@@ -428,8 +428,8 @@ class LayerStackTrainer final : public TrainerBase {
     // occurrence lists every step when the trainer does not scan.
     int32_t ft_gradient(const BatchPtrs& p, const FtGradArgs& fb) {
         if (use_scan)
-            return h_out ? launch_ft_grad_mfma(fb, block_scan(p), stream, true)
-                         : launch_ft_grad_scan(fb, block_scan(p), stream, true);
+            return h_out ? launch_ft_grad_mfma(fb, block_scan(p), stream, !batch_king_blocked)
+                         : launch_ft_grad_scan(fb, block_scan(p), stream, !batch_king_blocked);
         return launch_ft_grad_update(fb, stream);
     }
 
@@ -448,6 +448,7 @@ class LayerStackTrainer final : public TrainerBase {
         sc.cols = ft_in;
         sc.piece_inputs = pi;
         sc.n_blocks = n_king_bins;
+        sc.multi_sticky = batch_king_blocked ? kb_broken_dev : nullptr;
         return sc;
     }
 
@@ -487,10 +488,12 @@ class LayerStackTrainer final : public TrainerBase {
                 // hit masks of the block-scan backward, beside the forward,
                 // then the occurrence sort, which runs only when a row has
                 // features of two king blocks or one feature twice (the
-                // mask pass sets scan_multi); no host wait
+                // mask pass sets scan_multi); no host wait.  A batch passed
+                // as king-blocked (on_device = 2) queues no sort.
                 if ((st = fork_side())) return st;
                 if ((st = launch_ft_scan_tables(block_scan(p), side))) return st;
-                if ((st = sort_occurrences(p, side, true))) return st;
+                if ((st = batch_king_blocked ? note_king_blocked_tables() : sort_occurrences(p, side, true)))
+                    return st;
             }
         }
         // bucket sort (16-aligned, invalid buckets in bin nb)

@@ -1,6 +1,8 @@
 // Shared trainer services (see trainer_base.hpp).
 #include "trainer_base.hpp"
 
+#include "binsort.hpp"
+
 #include <cstring>
 
 #include <cmath>
@@ -33,6 +35,8 @@ TrainerBase::~TrainerBase() {
     if (ev_fork) (void)hipEventDestroy(ev_fork);
     if (ev_join) (void)hipEventDestroy(ev_join);
     if (pinned_loss) (void)hipHostFree(pinned_loss);
+    if (kb_ev) (void)hipEventDestroy(kb_ev);
+    if (kb_broken_host) (void)hipHostFree(kb_broken_host);
     if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamDestroy(stream);
 }
@@ -48,6 +52,12 @@ int32_t TrainerBase::init_runtime(int device) {
     TATARA_HIP(hipHostMalloc((void**)&pinned_loss, 2 * sizeof(double), hipHostMallocDefault),
                "hipHostMalloc loss ring");
     TATARA_HIP(hipStreamCreateWithFlags(&copy_stream, hipStreamNonBlocking), "hipStreamCreate (copy)");
+    TATARA_HIP(hipEventCreateWithFlags(&kb_ev, hipEventDisableTiming), "hipEventCreate");
+    TATARA_HIP(hipHostMalloc((void**)&kb_broken_host, sizeof(uint32_t), hipHostMallocDefault),
+               "hipHostMalloc king-block check");
+    *kb_broken_host = 0;
+    int32_t st = arena.alloc(&kb_broken_dev, 1);
+    if (st) return st;
     for (int s = 0; s < kRingSlots; ++s) {
         TATARA_HIP(hipEventCreateWithFlags(&ring_copied[s], hipEventDisableTiming), "hipEventCreate");
         TATARA_HIP(hipEventCreateWithFlags(&ring_consumed[s], hipEventDisableTiming), "hipEventCreate");
@@ -136,6 +146,8 @@ int32_t TrainerBase::stage_batch(const TataraBatch* bt, BatchPtrs& p, bool need_
         int32_t st = release_batch();
         if (st) return st;
     }
+    TATARA_REQUIRE(bt->on_device >= 0 && bt->on_device <= 2, "batch.on_device must be 0, 1 or 2");
+    batch_king_blocked = bt->on_device == 2;
     if (bt->on_device) {
         p.stm = bt->stm_indices;
         p.nstm = bt->nstm_indices;
@@ -285,6 +297,27 @@ int32_t TrainerBase::flush(double* out) {
         pending = -1;
     }
     if (out) *out = v;
+    if (kb_pending) {
+        TATARA_HIP(hipEventSynchronize(kb_ev), "king-block check");
+        kb_pending = false;
+        if (*kb_broken_host) {
+            *kb_broken_host = 0;
+            const int32_t st = launch_fill_i32(reinterpret_cast<int32_t*>(kb_broken_dev), 1, 0, side);
+            if (st) return st;
+            set_error("a batch passed with on_device = 2 had a row with features of two king blocks or one "
+                      "feature twice, so its FT weight gradient was left out; pass such batches with "
+                      "on_device = 1");
+            return kErrState;
+        }
+    }
+    return kOk;
+}
+
+int32_t TrainerBase::note_king_blocked_tables() {
+    TATARA_HIP(hipMemcpyAsync(kb_broken_host, kb_broken_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, side),
+               "king-block check copy");
+    TATARA_HIP(hipEventRecord(kb_ev, side), "king-block check record");
+    kb_pending = true;
     return kOk;
 }
 

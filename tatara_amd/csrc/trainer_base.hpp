@@ -91,6 +91,9 @@ class TrainerBase {
         return kOk;
     }
 
+    // Returns the pending loss; also reports (kErrState) a step whose batch
+    // was passed as king-blocked (on_device = 2) but had a row the block
+    // scan cannot take.
     int32_t flush(double* out);
     int32_t prof_collect();
 
@@ -131,6 +134,17 @@ class TrainerBase {
     hipEvent_t loss_ev[2] = {nullptr, nullptr};
     int pending = -1;  // slot holding the last queued loss
     int next_slot = 0;
+    // A batch passed with on_device = 2: its rows are king-blocked, so the
+    // step queues no occurrence-list fallback.  The stage-table pass latches
+    // a violation into kb_broken_dev; a copy of it into kb_broken_host on the
+    // side stream (event kb_ev) is read by the next flush.
+    bool batch_king_blocked = false;
+    uint32_t* kb_broken_dev = nullptr;
+    uint32_t* kb_broken_host = nullptr;
+    hipEvent_t kb_ev = nullptr;
+    bool kb_pending = false;
+    // after the stage tables of a king-blocked batch (queued on side)
+    int32_t note_king_blocked_tables();
     // phase profiling: kPhases + 1 events per profiled step
     std::vector<hipEvent_t> prof_events;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;

@@ -51,6 +51,31 @@ class ProgressWeights:
         return cls(raw)
 
 
+# feature sets whose friend- and enemy-king planes are one (halfka-*-merged):
+# a record with both kings on one square gives that feature twice
+MERGED_KING_PLANES = ("halfka-merged", "halfka-hm-merged")
+
+
+def king_squares(records) -> tuple[np.ndarray, np.ndarray]:
+    """The two 7-bit king squares of each record: bits 1..7 and 8..14 of its
+    LSB-first bit stream (after the side-to-move bit, packed_sfen.rs:387-430)."""
+    rec = np.ascontiguousarray(records, dtype=np.uint8).reshape(-1, 40)
+    w = rec[:, 0].astype(np.uint32) | (rec[:, 1].astype(np.uint32) << 8)
+    return (w >> 1) & 127, (w >> 8) & 127
+
+
+def records_king_blocked(records, feature_set: str) -> bool:
+    """Whether the decoded rows of these records are king-blocked (every
+    feature in its perspective's king block, none twice).  Board, hand and
+    king features occupy disjoint ranges of a block and one square holds one
+    piece, so only the merged king plane can repeat a feature: when both kings
+    are on one square."""
+    if feature_set not in MERGED_KING_PLANES:
+        return True
+    a, b = king_squares(records)
+    return not bool(np.any((a == b) & (a < 81)))
+
+
 def psv_to_device_batch(records, feature_set: str, bucket_mode: str = "none", num_buckets: int = 1,
                         progress: ProgressWeights | None = None) -> DeviceBatch:
     """Decodes [n, 40] uint8 records on the GPU into a DeviceBatch (+ bucket)."""
@@ -77,6 +102,7 @@ def psv_to_device_batch(records, feature_set: str, bucket_mode: str = "none", nu
                                   a["stm"].ptr, a["nstm"].ptr, a["nnz"].ptr, a["bucket"].ptr,
                                   a["score"].ptr, a["wdl"].ptr))
     src.free()
+    db.king_blocked = records_king_blocked(rec, feature_set)
     return db
 
 

@@ -20,7 +20,7 @@ from typing import Optional
 import numpy as np
 
 from . import _lib
-from ._lib import TataraBatch, TataraLoss, TataraTrainerConfig, check
+from ._lib import OutOfMemory, TataraBatch, TataraLoss, TataraTrainerConfig, check
 
 OPTIMIZERS = {"ranger": 0, "radam": 1, "adamw": 2}
 GROUPS = (
@@ -148,11 +148,17 @@ class DeviceArray:
 
 @dataclass
 class DeviceBatch:
-    """A batch resident in device memory (inputs already in HBM)."""
+    """A batch resident in device memory (inputs already in HBM).
+
+    king_blocked: every row's features lie in its perspective's king block
+    and none repeats (set by psv_to_device_batch when the records guarantee
+    it); the trainer then queues no occurrence-list fallback for the step
+    (on_device = TATARA_BATCH_KING_BLOCKED)."""
 
     n_pos: int
     max_active: int
     arrays: dict = field(default_factory=dict)
+    king_blocked: bool = False
 
     @classmethod
     def upload(cls, batch: Batch, bucket_idx: Optional[np.ndarray] = None) -> "DeviceBatch":
@@ -180,7 +186,7 @@ class DeviceBatch:
             bucket_idx=a["bucket"].ptr if "bucket" in a else None,
             score=a["score"].ptr,
             wdl=a["wdl"].ptr,
-            on_device=1,
+            on_device=2 if self.king_blocked else 1,
         )
 
 
@@ -321,6 +327,27 @@ class SimpleConfig:
         return self.ft_in + self.piece_inputs
 
 
+def oom_remedy(config) -> str:
+    """The actionable message of a trainer whose buffers did not fit in GPU
+    memory (gpu_oom_error, bins/nnue_train/src/training.rs:100-146): the
+    configuration that sizes the buffers, then the ways to shrink them.  The
+    f16 forward modes are reported but not recommended (they trade accuracy);
+    f16 optimizer moments are, as they only save memory."""
+    layerstack = isinstance(config, LayerStackConfig)
+    flag, dim = ("--ft-out", config.ft_out) if layerstack else ("--l1", config.ft_out)
+    fp16 = getattr(config, "ft_fp16", False), getattr(config, "ft_fp16_out", False)
+    opt16 = getattr(config, "fp16_opt_state", False)
+    lines = [f"GPU out of memory while allocating training buffers (batch-size={config.max_batch}, "
+             f"{flag}={dim}, ft-fp16={str(fp16[0]).lower()}, ft-fp16-out={str(fp16[1]).lower()}, "
+             f"fp16-opt-state={str(opt16).lower()}).",
+             "Reduce GPU memory by one or more of:"]
+    if not opt16:
+        lines.append("  - add `--fp16-opt-state` (f16 optimizer moments, about half their memory)")
+    lines.append(f"  - lower `{flag}` (the FT output width; the buffers grow about linearly with it)")
+    lines.append("  - smaller `--batch-size`")
+    return "\n".join(lines)
+
+
 class _Trainer:
     """Shared TrainerBackend surface over an opaque C trainer handle."""
 
@@ -331,7 +358,11 @@ class _Trainer:
         self._lib = _lib.load()
         h = C.c_void_p()
         cfg = config.to_c()
-        check(self._lib.tatara_trainer_create(C.byref(cfg), C.byref(h)))
+        try:
+            check(self._lib.tatara_trainer_create(C.byref(cfg), C.byref(h)))
+        except OutOfMemory as e:
+            # the library freed whatever the failed create had allocated
+            raise OutOfMemory(e.status, f"{e.message}\n{oom_remedy(config)}") from None
         self._h = h.value
         self._keep = None  # host arrays referenced by the in-flight step
 

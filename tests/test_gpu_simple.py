@@ -247,3 +247,37 @@ def test_host_batches_through_the_upload_ring(gpu):
     assert losses[0] == losses[1]
     for g in SIMPLE_GROUPS:
         assert np.array_equal(states[0][g], states[1][g]), g
+
+
+def test_king_blocked_batches(gpu):
+    """Simple: device batches passed as king-blocked (on_device = 2, no
+    occurrence-list fallback queued) train bit-identically to on_device = 1
+    (block scan at 256 columns); a batch that repeats a feature is reported
+    by the next flush."""
+    from tatara_amd import _lib
+    from tatara_amd.trainer import Batch
+    sh, cfg = make(keep=False, ft_out=256)
+    b = cfg.max_batch
+    batches = [batch_for(s, b) for s in (51, 52, 53, 54, 55, 56, 57)]
+    states = []
+    for king_blocked in (False, True):
+        with SimpleTrainer(cfg) as t:
+            for bt in batches:
+                db = DeviceBatch.upload(bt)
+                db.king_blocked = king_blocked
+                t.train_step(db, 1e-3, 0.0, WRM290)
+            t.flush_pending_loss()
+            states.append({g: (t.get(g), t.get(g, "m"), t.get(g, "v")) for g in SIMPLE_GROUPS})
+    for g in SIMPLE_GROUPS:
+        for a0, a1 in zip(states[0][g], states[1][g]):
+            assert np.array_equal(a0, a1), g
+    bt = batches[0]
+    stm = bt.stm_indices.copy()
+    stm[7, 1] = stm[7, 0]
+    bad = DeviceBatch.upload(Batch(stm, bt.nstm_indices, bt.nnz, bt.score, bt.wdl))
+    bad.king_blocked = True
+    with SimpleTrainer(cfg) as t:
+        t.train_step(bad, 1e-3, 0.0, WRM290)
+        with pytest.raises(_lib.TataraError) as ei:
+            t.flush_pending_loss()
+        assert ei.value.status == -4

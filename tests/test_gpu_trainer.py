@@ -261,3 +261,56 @@ def test_host_batches_through_the_upload_ring(gpu):
     assert losses[0] == losses[1]
     for g in GROUPS:
         assert np.array_equal(states[0][g], states[1][g]), g
+
+
+@pytest.mark.parametrize("ft_out", [512, 256], ids=["block_scan", "occurrence_lists"])
+def test_king_blocked_batches(gpu, ft_out):
+    """Device batches passed as king-blocked (on_device = 2: no occurrence-list
+    fallback queued) train bit-identically to the same batches passed with
+    on_device = 1, with the block scan and with the occurrence lists."""
+    sh, cfg = make(keep=False, ft_out=ft_out)
+    b = cfg.max_batch
+    batches = [batch_for(s, b, sh.nb) for s in (31, 32, 33, 34, 35, 36, 37)]
+    states, losses = [], []
+    for king_blocked in (False, True):
+        with LayerStackTrainer(cfg) as t:
+            got = []
+            for bt, bk in batches:
+                db = DeviceBatch.upload(bt, bk)
+                db.king_blocked = king_blocked
+                assert db.to_c().on_device == (2 if king_blocked else 1)
+                got.append(t.train_step(db, None, 1e-3, 0.0, Sigmoid()))
+            got.append(t.flush_pending_loss())
+            losses.append(got)
+            states.append({g: (t.get(g), t.get(g, "m"), t.get(g, "v")) for g in GROUPS})
+    assert losses[0] == losses[1]
+    for g in GROUPS:
+        for a0, a1 in zip(states[0][g], states[1][g]):
+            assert np.array_equal(a0, a1), g
+
+
+def test_king_blocked_batch_that_is_not_is_reported(gpu):
+    """A batch passed as king-blocked whose rows span king blocks or repeat a
+    feature (the caller's statement is false): the step trains without the FT
+    weight gradient, the next flush reports TATARA_ERR_STATE, and the trainer
+    goes on: later king-blocked batches train as before and flush cleanly."""
+    from tatara_amd import _lib
+    from tatara_amd.trainer import Batch
+    sh, cfg = make(keep=False, ft_out=512)
+    b = cfg.max_batch
+    batch, bucket = batch_for(41, b, sh.nb)
+    nstm = batch.nstm_indices.copy()
+    nstm[5, 3] = nstm[5, 2]  # a repeated feature
+    bad = DeviceBatch.upload(Batch(batch.stm_indices, nstm, batch.nnz, batch.score, batch.wdl), bucket)
+    bad.king_blocked = True
+    good = DeviceBatch.upload(*batch_for(42, b, sh.nb))
+    good.king_blocked = True
+    with LayerStackTrainer(cfg) as t:
+        w0 = t.get("ft_w")
+        t.train_step(bad, None, 1e-3, 0.0, Sigmoid())
+        with pytest.raises(_lib.TataraError) as ei:
+            t.flush_pending_loss()
+        assert ei.value.status == -4 and "on_device = 1" in str(ei.value)
+        t.train_step(good, None, 1e-3, 0.0, Sigmoid())
+        assert np.isfinite(t.flush_pending_loss())
+        assert not np.array_equal(t.get("ft_w"), w0)

@@ -348,3 +348,31 @@ def test_progress_matches_brute_force():
         assert o["progress"][i] == p
         assert o["bucket"][i] == min(7, max(0, int(np.floor(np.float32(p * np.float32(8))))))
     assert len(set(o["bucket"].tolist())) > 2
+
+
+def test_records_king_blocked():
+    """A PSV batch is certified king-blocked unless, in a feature set with
+    merged king planes, a record has both kings on one square (its decoded
+    rows then hold the king feature twice, which the oracle confirms)."""
+    from tatara_amd.dataloader import king_squares, records_king_blocked
+    from tatara_amd.psv import synthetic_psv
+
+    rec = synthetic_psv(256, seed=77)
+    a, b = king_squares(rec)
+    dec = of.psv_decode(rec)
+    assert np.array_equal(a, dec["bking"]) and np.array_equal(b, dec["wking"])
+    for fs in of.FEATURE_SETS:
+        assert records_king_blocked(rec, fs)
+    bad = rec.copy()
+    w = int(bad[9, 0]) | (int(bad[9, 1]) << 8)
+    k0 = (w >> 1) & 127
+    w = (w & ~(127 << 8)) | (k0 << 8)
+    bad[9, 0], bad[9, 1] = w & 255, (w >> 8) & 255
+    assert king_squares(bad)[1][9] == k0
+    for fs in of.FEATURE_SETS:
+        merged = fs in ("halfka-merged", "halfka-hm-merged")
+        assert records_king_blocked(bad, fs) == (not merged), fs
+        rows = of.psv_to_batch(bad[9:10], fs)
+        for persp in ("stm", "nstm"):
+            r = rows[persp][0][: rows["nnz"][0]]
+            assert (len(np.unique(r)) < len(r)) == merged, (fs, persp)
