@@ -1092,8 +1092,9 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
 // gather_and_sum_per_feature_*_fp16 (native_kernels.cu:1030-1100) adds them:
 // a cell equals the sequential sum to within f32 summation error.  Rows past
 // the list are zero and the dft is clamped to +-65504, so every zero of H
-// multiplies a finite value unless a row of the block holds a NaN (which
-// then reaches every feature of its tile, not only the row's own).
+// multiplies a finite value unless a row of the block holds a NaN or an
+// infinity; a wave whose sums come out non-finite then takes the sequential
+// per-hit sums instead (below), which keep the value to its row's features.
 //
 // Workgroups take (block, chunk, feature group, column half) in the block
 // scan's order (the two halves of a chunk next to each other).  Wave w of
@@ -1274,6 +1275,41 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
         __syncthreads();
     }
 
+    // A non-finite dft value in one of the block's rows makes its column
+    // non-finite in every tile (H multiplies it by 1 or by 0, and 0 x NaN,
+    // 0 x Inf are NaN), while finite rows (|D| <= 65504, a few thousand per
+    // block) cannot overflow an f32 sum.  A wave that finds one recomputes
+    // its cells as the sequential per-hit sums, table stage by stage and row
+    // by row (the block scan's order, equal bit for bit to the reference's
+    // per-feature gather), so that a NaN reaches only the features of the
+    // rows that hold it.
+    bool nonfinite = false;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) nonfinite |= !__builtin_isfinite(acc[i][j][r]);
+    const bool sequential = __builtin_amdgcn_ballot_w64(nonfinite) != 0;
+    // the sequential sums of tile i's cells (feature 4 oct + r of mask word
+    // 2 wave + i, column 16 j + m), r and j as in the accumulators
+    const uint32_t* mrow = s.stage_masks + (uint64_t)(g * kScanWaves + 2 * wave) * kScanFeat + 4 * oct;
+    auto sequential_sums = [&](int i, int r, float (&sum)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum[j] = 0.0f;
+        for (uint32_t ts = 0; ts < n32; ++ts) {
+            uint32_t mk = mrow[(uint64_t)(sb + ts) * geom.words * kScanFeat + i * kScanFeat + r];
+            const uint32_t* tr = trow + 32 * ts;
+            while (mk) {  // the lane's hits, in row order
+                const uint32_t e = __builtin_ctz(mk);
+                mk &= mk - 1;
+                const _Float16* dr = d16 + (uint64_t)tr[e] * kDftChunk + m;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sum[j] += (float)dr[16 * j];
+            }
+        }
+    };
+
     // Update, 16 features x 128 columns at a time: the wave's tiles go
     // through its own LDS rows so that each lane then updates four
     // consecutive columns of a feature row, four rows' state loaded before
@@ -1290,10 +1326,20 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
     for (int i = 0; i < 2; ++i) {
         {
             const uint32_t col = chunk * kDftChunk + half * kMfmaCols + 4 * (lane % 32);
+            if (sequential) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+                for (int r = 0; r < 4; ++r) {
+                    float sum[8];
+                    sequential_sums(i, r, sum);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = acc[i][j][r];
+                    for (int j = 0; j < 8; ++j) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = sum[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s_u[(oct * 4 + r) * kMfmaUpdRow + j * 16 + m] = acc[i][j][r];
+            }
             __syncthreads();
             // the lane's rows 2 j + lane / 32 of the tile (j < 8): features
             // first + 2 j of the group, nfl of them real (none past the
