@@ -47,18 +47,30 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 // MFMAs, which permutes the K order consistently for A and B.
 // ---------------------------------------------------------------------------
 // T (1 or 2) consecutive tiles of bucket `bin`: the weights of each K-block
-// are loaded once for all T tiles.
-template <int T>
+// are loaded once for all T tiles.  NJ (1 or 2) blocks of 16 L1 outputs:
+// lane i computes outputs i and 16 + i (l1 = 32) from the same row loads.
+template <int T, int NJ>
 __device__ __forceinline__ void ls_l1_fwd_tiles(const LsDenseArgs& a, uint32_t tile0, int32_t bin, uint32_t lane) {
     const uint32_t i = lane % 16, q = lane / 16;
     const uint32_t ft_out = a.ft_out, l1 = a.l1;
     const bool bvalid = (uint32_t)bin < a.nb;
-    const bool jvalid = i < l1;
     // Operands are loaded unconditionally from always-valid addresses (row 0,
     // bucket 0, column l1-1) and masked afterwards: a guarded load would be
     // split into predicated dword loads and lose the 16-byte accesses.
-    const bool wbvalid = bvalid && jvalid;
-    const uint32_t ic = jvalid ? i : l1 - 1;
+    bool jvalid[NJ], wbvalid[NJ];
+    const float4* W1[NJ];
+    const float* Ws[NJ];
+    float binit[NJ];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) {
+        const uint32_t j = 16 * jt + i;
+        jvalid[jt] = j < l1;
+        wbvalid[jt] = bvalid && jvalid[jt];
+        const uint32_t ic = jvalid[jt] ? j : l1 - 1;
+        W1[jt] = reinterpret_cast<const float4*>(a.l1_w + ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
+        Ws[jt] = a.l1s_w + ic;
+        binit[jt] = wbvalid[jt] ? a.l1_b[bin * l1 + j] : 0.0f;
+    }
     const float4* X[T];
     bool xvalid[T];
 #pragma unroll
@@ -67,65 +79,72 @@ __device__ __forceinline__ void ls_l1_fwd_tiles(const LsDenseArgs& a, uint32_t t
         xvalid[t] = orig >= 0;
         X[t] = reinterpret_cast<const float4*>(a.combined + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
     }
-    const float4* W1 = reinterpret_cast<const float4*>(
-        a.l1_w + ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
-    const float* Ws = a.l1s_w + ic;
-    const float binit = (bvalid && jvalid) ? a.l1_b[bin * l1 + i] : 0.0f;
-    floatx4 accb[T], accs[T];
+    floatx4 accb[T][NJ], accs[T][NJ];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        accb[t] = floatx4{binit, binit, binit, binit};
-        accs[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int jt = 0; jt < NJ; ++jt) {
+            accb[t][jt] = floatx4{binit[jt], binit[jt], binit[jt], binit[jt]};
+            accs[t][jt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
     // ft_out % 64 == 0: whole groups of kU K-blocks; a group's operands are
     // loaded before its MFMAs so each wave keeps several loads in flight
     const uint32_t nk = ft_out / 16;
-    constexpr uint32_t kU = T == 1 ? 4 : 2;
+    constexpr uint32_t kU = T * NJ == 1 ? 4 : 2;
     for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
-        float4 x[kU][T], wb[kU];
-        float ws[kU][4];
+        float4 x[kU][T], wb[kU][NJ];
+        float ws[kU][NJ][4];
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
             const uint32_t kb = kb0 + u;
 #pragma unroll
             for (int t = 0; t < T; ++t) x[u][t] = X[t][kb * 4 + q];
-            wb[u] = W1[kb * 4 + q];
             const uint32_t k = kb * 16 + 4 * q;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) ws[u][c] = Ws[(uint64_t)(k + c) * l1];
-        }
+            for (int jt = 0; jt < NJ; ++jt) {
+                wb[u][jt] = W1[jt][kb * 4 + q];
 #pragma unroll
-        for (uint32_t u = 0; u < kU; ++u) {
-            const float4 wv = wbvalid ? wb[u] : zero4;
-            const float w0 = jvalid ? ws[u][0] : 0.f, w1 = jvalid ? ws[u][1] : 0.f;
-            const float w2 = jvalid ? ws[u][2] : 0.f, w3 = jvalid ? ws[u][3] : 0.f;
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const float4 xv = xvalid[t] ? x[u][t] : zero4;
-                accb[t] = mfma4(xv.x, wv.x, accb[t]);
-                accs[t] = mfma4(xv.x, w0, accs[t]);
-                accb[t] = mfma4(xv.y, wv.y, accb[t]);
-                accs[t] = mfma4(xv.y, w1, accs[t]);
-                accb[t] = mfma4(xv.z, wv.z, accb[t]);
-                accs[t] = mfma4(xv.z, w2, accs[t]);
-                accb[t] = mfma4(xv.w, wv.w, accb[t]);
-                accs[t] = mfma4(xv.w, w3, accs[t]);
+                for (int c = 0; c < 4; ++c) ws[u][jt][c] = Ws[jt][(uint64_t)(k + c) * l1];
             }
         }
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u)
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                const float4 wv = wbvalid[jt] ? wb[u][jt] : zero4;
+                const bool jv = jvalid[jt];
+                const float w0 = jv ? ws[u][jt][0] : 0.f, w1 = jv ? ws[u][jt][1] : 0.f;
+                const float w2 = jv ? ws[u][jt][2] : 0.f, w3 = jv ? ws[u][jt][3] : 0.f;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float4 xv = xvalid[t] ? x[u][t] : zero4;
+                    accb[t][jt] = mfma4(xv.x, wv.x, accb[t][jt]);
+                    accs[t][jt] = mfma4(xv.x, w0, accs[t][jt]);
+                    accb[t][jt] = mfma4(xv.y, wv.y, accb[t][jt]);
+                    accs[t][jt] = mfma4(xv.y, w1, accs[t][jt]);
+                    accb[t][jt] = mfma4(xv.z, wv.z, accb[t][jt]);
+                    accs[t][jt] = mfma4(xv.z, w2, accs[t][jt]);
+                    accb[t][jt] = mfma4(xv.w, wv.w, accb[t][jt]);
+                    accs[t][jt] = mfma4(xv.w, w3, accs[t][jt]);
+                }
+            }
     }
-    const uint32_t j = lane % 16;
-    if (j >= l1) return;
-    const float bs = a.l1s_b[j];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+    for (int jt = 0; jt < NJ; ++jt) {
+        const uint32_t j = 16 * jt + lane % 16;
+        if (j >= l1) continue;
+        const float bs = a.l1s_b[j];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint64_t row = (uint64_t)(tile0 + t) * 16 + 4 * q + r;
-            float* o = a.l1_sorted + row * 2 * l1;
-            o[j] = bvalid ? accb[t][r] : 0.0f;
-            o[l1 + j] = accs[t][r] + bs;
-        }
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint64_t row = (uint64_t)(tile0 + t) * 16 + 4 * q + r;
+                float* o = a.l1_sorted + row * 2 * l1;
+                o[j] = bvalid ? accb[t][jt][r] : 0.0f;
+                o[l1 + j] = accs[t][jt][r] + bs;
+            }
+    }
 }
 
 // The TF32 L1 forward's weight operands, once per forward: f16 copies of
@@ -147,6 +166,7 @@ __global__ __launch_bounds__(256) void ls_l1_weights_f16_kernel(LsDenseArgs a) {
 // One wave per pair of 16-row sorted tiles: both in one pass when they
 // belong to one bucket, else (at a bucket boundary) one pass each; a tile
 // of bin -1 (all padding) is skipped.
+template <int NJ>
 __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t tile0 = (blockIdx.x * 4 + wave) * 2;
@@ -155,10 +175,10 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
     const int32_t bin0 = scalar_load(a.sorted_bin + (uint64_t)tile0 * 16);
     const int32_t bin1 = tile0 + 1 < n_tiles ? scalar_load(a.sorted_bin + (uint64_t)(tile0 + 1) * 16) : -1;
     if (bin0 >= 0 && bin0 == bin1) {
-        ls_l1_fwd_tiles<2>(a, tile0, bin0, lane);
+        ls_l1_fwd_tiles<2, NJ>(a, tile0, bin0, lane);
     } else {
-        if (bin0 >= 0) ls_l1_fwd_tiles<1>(a, tile0, bin0, lane);
-        if (bin1 >= 0) ls_l1_fwd_tiles<1>(a, tile0 + 1, bin1, lane);
+        if (bin0 >= 0) ls_l1_fwd_tiles<1, NJ>(a, tile0, bin0, lane);
+        if (bin1 >= 0) ls_l1_fwd_tiles<1, NJ>(a, tile0 + 1, bin1, lane);
     }
 }
 
@@ -171,6 +191,7 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_kernel(LsDenseArgs a) {
 // reference's tf32 path (per-bucket sgemm, then the bias,
 // trainer_layerstack.rs:2388-2480) the bucket bias is added after the sum.
 // ---------------------------------------------------------------------------
+template <int NJ>
 __global__ __launch_bounds__(256) void ls_l1_fwd_tf32_kernel(LsDenseArgs a) {
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t tile = blockIdx.x * 4 + wave;
@@ -181,47 +202,64 @@ __global__ __launch_bounds__(256) void ls_l1_fwd_tf32_kernel(LsDenseArgs a) {
     const uint32_t ft_out = a.ft_out, l1 = a.l1;
     const int32_t orig = a.perm[tile * 16 + i];
     const bool bvalid = (uint32_t)bin < a.nb;
-    const bool jvalid = i < l1;
     // unconditional loads from always-valid addresses, masked afterwards
-    const bool xvalid = orig >= 0, wbvalid = bvalid && jvalid;
-    const uint32_t ic = jvalid ? i : l1 - 1;
+    const bool xvalid = orig >= 0;
     const half8* X = reinterpret_cast<const half8*>(
         reinterpret_cast<const _Float16*>(a.combined16) + (uint64_t)(orig >= 0 ? orig : 0) * ft_out);
-    const half8* W1 = reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(a.l1_w16) +
-                                                     ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
-    const half8* Ws = reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(a.l1s_wt16) +
-                                                     (uint64_t)ic * ft_out);
-    floatx4 accb = {0.f, 0.f, 0.f, 0.f}, accs = accb;
+    bool jvalid[NJ], wbvalid[NJ];
+    const half8 *W1[NJ], *Ws[NJ];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) {
+        const uint32_t j = 16 * jt + i;
+        jvalid[jt] = j < l1;
+        wbvalid[jt] = bvalid && jvalid[jt];
+        const uint32_t ic = jvalid[jt] ? j : l1 - 1;
+        W1[jt] = reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(a.l1_w16) +
+                                                ((uint64_t)(bvalid ? bin : 0) * l1 + ic) * ft_out);
+        Ws[jt] = reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(a.l1s_wt16) + (uint64_t)ic * ft_out);
+    }
+    floatx4 accb[NJ], accs[NJ];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) accb[jt] = accs[jt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const half8 zero8 = {};
     // ft_out % 64 == 0: K blocks of 32, four loaded before their MFMAs
     const uint32_t nk = ft_out / 32;
     constexpr uint32_t kU = 4;
     for (uint32_t kb0 = 0; kb0 < nk; kb0 += kU) {
-        half8 x[kU], wb[kU], wsh[kU];
+        half8 x[kU], wb[kU][NJ], wsh[kU][NJ];
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
             const uint32_t k8 = (kb0 + u) * 4 + q;
             x[u] = X[k8];
-            wb[u] = W1[k8];
-            wsh[u] = Ws[k8];
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                wb[u][jt] = W1[jt][k8];
+                wsh[u][jt] = Ws[jt][k8];
+            }
         }
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
             const half8 xv = xvalid ? x[u] : zero8;
-            accb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wbvalid ? wb[u] : zero8, accb, 0, 0, 0);
-            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, jvalid ? wsh[u] : zero8, accs, 0, 0, 0);
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                accb[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wbvalid[jt] ? wb[u][jt] : zero8, accb[jt], 0, 0, 0);
+                accs[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, jvalid[jt] ? wsh[u][jt] : zero8, accs[jt], 0, 0, 0);
+            }
         }
     }
-    const uint32_t j = lane % 16;
-    if (j >= l1) return;
-    const float bb = bvalid ? a.l1_b[bin * l1 + j] : 0.0f;
-    const float bs = a.l1s_b[j];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint64_t row = (uint64_t)tile * 16 + 4 * q + r;
-        float* o = a.l1_sorted + row * 2 * l1;
-        o[j] = bvalid ? accb[r] + bb : 0.0f;
-        o[l1 + j] = accs[r] + bs;
+    for (int jt = 0; jt < NJ; ++jt) {
+        const uint32_t j = 16 * jt + lane % 16;
+        if (j >= l1) continue;
+        const float bb = bvalid ? a.l1_b[bin * l1 + j] : 0.0f;
+        const float bs = a.l1s_b[j];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint64_t row = (uint64_t)tile * 16 + 4 * q + r;
+            float* o = a.l1_sorted + row * 2 * l1;
+            o[j] = bvalid ? accb[jt][r] + bb : 0.0f;
+            o[l1 + j] = accs[jt][r] + bs;
+        }
     }
 }
 
@@ -559,7 +597,7 @@ void reduce_rows(const float* P, uint32_t n_rows, uint32_t n_cols, const uint32_
 // TF32: `combined` read as f16 (as the forward stored it); dl1 and the
 // products stay f32.
 // ---------------------------------------------------------------------------
-template <bool TF32>
+template <bool TF32, int NJ>
 __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t n_chunks = a.chunk_info[3 * a.max_chunks];
@@ -570,17 +608,27 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
     const uint32_t t0 = a.chunk_info[3 * chunk + 1], nt = a.chunk_info[3 * chunk + 2];
     const uint32_t o = lane % 16, q = lane / 16, kk = lane % 16;
     const uint32_t l1 = a.l1, ft_out = a.ft_out;
-    const bool ovalid = o < l1;
     const bool kvalid = k0 + 4 * kk < ft_out;
-    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+    // NJ blocks of 16 L1 outputs (lane o: outputs o and 16 + o)
+    bool ovalid[NJ];
+    uint32_t oc[NJ];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) {
+        ovalid[jt] = 16 * jt + o < l1;
+        oc[jt] = ovalid[jt] ? 16 * jt + o : 0;
+    }
+    floatx4 acc[NJ][4];
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[jt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
     const uint32_t kc = kvalid ? k0 + 4 * kk : 0;  // always-valid column, masked below
-    const uint32_t oc = ovalid ? o : 0;
     for (uint32_t tt = 0; tt < nt; ++tt) {
         // the tile's 16 rows are loaded before its 16 MFMAs (unconditional
         // loads from valid addresses, masked after the load)
         float4 xs[4];
-        float ds[4];
+        float ds[4][NJ];
         bool rvs[4];
 #pragma unroll
         for (uint32_t s = 0; s < 4; ++s) {
@@ -595,30 +643,36 @@ __global__ __launch_bounds__(256) void ls_l1_wgrad_kernel(LsDenseArgs a) {
             } else {
                 xs[s] = *reinterpret_cast<const float4*>(a.combined + xo);
             }
-            ds[s] = a.dl1_sorted[row * l1 + oc];
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) ds[s][jt] = a.dl1_sorted[row * l1 + oc[jt]];
         }
 #pragma unroll
         for (uint32_t s = 0; s < 4; ++s) {
-            const float d = ovalid ? ds[s] : 0.0f;
             const float4 x = (rvs[s] && kvalid) ? xs[s] : zero4;
-            acc0 = mfma4(d, x.x, acc0);
-            acc1 = mfma4(d, x.y, acc1);
-            acc2 = mfma4(d, x.z, acc2);
-            acc3 = mfma4(d, x.w, acc3);
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                const float d = ovalid[jt] ? ds[s][jt] : 0.0f;
+                acc[jt][0] = mfma4(d, x.x, acc[jt][0]);
+                acc[jt][1] = mfma4(d, x.y, acc[jt][1]);
+                acc[jt][2] = mfma4(d, x.z, acc[jt][2]);
+                acc[jt][3] = mfma4(d, x.w, acc[jt][3]);
+            }
         }
     }
     if (!kvalid) return;
     float* P = a.w1_partial + (uint64_t)chunk * l1 * ft_out;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint32_t oo = 4 * q + r;
-        if (oo >= l1) continue;
-        float* dst = P + (uint64_t)oo * ft_out + k0 + 4 * kk;
-        dst[0] = acc0[r];
-        dst[1] = acc1[r];
-        dst[2] = acc2[r];
-        dst[3] = acc3[r];
-    }
+    for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t oo = 16 * jt + 4 * q + r;
+            if (oo >= l1) continue;
+            float* dst = P + (uint64_t)oo * ft_out + k0 + 4 * kk;
+            dst[0] = acc[jt][0][r];
+            dst[1] = acc[jt][1][r];
+            dst[2] = acc[jt][2][r];
+            dst[3] = acc[jt][3][r];
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -669,8 +723,9 @@ template <int L1, int CPL, int RB, bool H16>
 __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) {
     static_assert(16 % RB == 0 && (16 / RB) % 2 == 0, "an even number of RB-row groups per tile");
     constexpr int G = 16 / RB;
-    constexpr int DL = 16 * L1 / 4;  // float4 of a tile's dl1 rows
-    static_assert(DL <= 64, "a tile's dl1 rows in one float4 per lane");
+    constexpr int DL = 16 * L1 / 4;          // float4 of a tile's dl1 rows
+    constexpr int NDL = (DL + 63) / 64;      // of them per lane
+    static_assert(L1 % 4 == 0, "whole float4 of dl1 per row");
     const uint32_t ft_out = a.ft_out, half = ft_out / 2;
     const uint64_t batch = a.batch;
     const uint32_t c = (blockIdx.x * 128 + threadIdx.x) * CPL;
@@ -704,8 +759,16 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
     const uint32_t tiles_total = (uint32_t)(a.padded_b / 16);
     const uint32_t n_tiles = tile0 < tiles_total ? min((uint32_t)kPostTiles, tiles_total - tile0) : 0u;
     auto tile_perm = [&](uint32_t tile) -> int32_t { return a.perm[(uint64_t)tile * 16 + (lane & 15u)]; };
-    auto tile_dl1 = [&](uint32_t tile) -> float4 {
-        return reinterpret_cast<const float4*>(a.dl1_sorted + (uint64_t)tile * 16 * L1)[lane % DL];
+    struct Dl1 {
+        float4 v[NDL];
+    };
+    // float4 f of the tile's dl1 rows is element f / 64 of lane f % 64
+    auto tile_dl1 = [&](uint32_t tile) -> Dl1 {
+        Dl1 d;
+        const float4* src = reinterpret_cast<const float4*>(a.dl1_sorted + (uint64_t)tile * 16 * L1);
+#pragma unroll
+        for (int k = 0; k < NDL; ++k) d.v[k] = src[(64 * k + lane) % DL];
+        return d;
     };
     auto bcast_i = [](int32_t v, int l) -> int32_t { return __builtin_amdgcn_readlane(v, l); };
     auto bcast_f = [](float v, int l) -> float {
@@ -738,7 +801,7 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
         }                                                                                     \
     }
     int32_t perm_c = 0, bin_c = -1;
-    float4 dl1_c = make_float4(0.f, 0.f, 0.f, 0.f);
+    Dl1 dl1_c = {};
     if (n_tiles) {
         perm_c = tile_perm(tile0);
         dl1_c = tile_dl1(tile0);
@@ -750,7 +813,7 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
         const bool has_next = t + 1 < n_tiles;
         const uint32_t tn = has_next ? tile + 1 : tile;  // the last tile re-reads itself, unused
         const int32_t perm_n = tile_perm(tn);
-        const float4 dl1_n = tile_dl1(tn);
+        const Dl1 dl1_n = tile_dl1(tn);
         const int32_t bin_n = has_next ? scalar_load(a.sorted_bin + (uint64_t)tn * 16) : -1;
         const int32_t bin = bin_c;  // < 0: a trailing all-padding tile
         if (bin >= 0 && bin != cur_bin) {
@@ -785,9 +848,10 @@ __global__ __launch_bounds__(128) void ls_l1_input_post_c_kernel(LsDenseArgs a) 
                 float d[L1];
 #pragma unroll
                 for (int o = 0; o < L1; ++o) {
-                    const int e = row_in_tile * L1 + o;
-                    const float comp = (e & 3) == 0 ? dl1_c.x : (e & 3) == 1 ? dl1_c.y : (e & 3) == 2 ? dl1_c.z : dl1_c.w;
-                    d[o] = bcast_f(comp, e >> 2);
+                    const int e = row_in_tile * L1 + o, f4 = e >> 2;
+                    const float4& v = dl1_c.v[f4 / 64];
+                    const float comp = (e & 3) == 0 ? v.x : (e & 3) == 1 ? v.y : (e & 3) == 2 ? v.z : v.w;
+                    d[o] = bcast_f(comp, f4 % 64);
                 }
                 float ga[CPL], gb[CPL];
 #pragma unroll
@@ -938,8 +1002,9 @@ uint32_t ls_max_chunks(uint32_t padded_b, uint32_t nb) {
 }
 
 int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream) {
-    TATARA_REQUIRE(a.l1 >= 2 && a.l1 <= 16, "l1 must be in [2, 16]");
+    TATARA_REQUIRE(a.l1 >= 2 && a.l1 <= 32, "l1 must be in [2, 32]");
     TATARA_REQUIRE(a.ft_out % 64 == 0, "ft_out must be a multiple of 64");
+    const bool two = a.l1 > 16;  // two blocks of 16 outputs
     TATARA_REQUIRE(!a.combined16 || (a.l1_w16 && a.l1s_wt16), "the TF32 L1 forward needs its f16 weights");
     const uint32_t tiles = a.padded_b / 16;
     if (tiles == 0) return kOk;
@@ -947,10 +1012,14 @@ int32_t launch_ls_l1_forward(const LsDenseArgs& a, hipStream_t stream) {
         const uint64_t n_w = (uint64_t)a.nb * a.l1 * a.ft_out;
         ls_l1_weights_f16_kernel<<<ceil_div(n_w, 256), 256, 0, stream>>>(a);
         TATARA_LAUNCHED("ls_l1_weights_f16");
-        TATARA_REQUIRE(a.l1 <= 16, "l1 must be <= 16");
-        ls_l1_fwd_tf32_kernel<<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+        if (two)
+            ls_l1_fwd_tf32_kernel<2><<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+        else
+            ls_l1_fwd_tf32_kernel<1><<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    } else if (two) {
+        ls_l1_fwd_kernel<2><<<ceil_div(tiles, 8), 256, 0, stream>>>(a);
     } else {
-        ls_l1_fwd_kernel<<<ceil_div(tiles, 8), 256, 0, stream>>>(a);
+        ls_l1_fwd_kernel<1><<<ceil_div(tiles, 8), 256, 0, stream>>>(a);
     }
     TATARA_LAUNCHED("ls_l1_forward");
     return kOk;
@@ -973,14 +1042,24 @@ int32_t launch_ls_tail(const LsDenseArgs& a, int32_t train, hipStream_t stream) 
     TATARA_REQUIRE(a.padded_b % 16 == 0, "the sorted batch is whole 16-row tiles");
     const uint32_t blocks = ls_tail_workgroups(a.padded_b);
     if (blocks == 0) return kOk;
-    if (a.l1 == 16 && a.l2 == 32) {
-        ls_tail_kernel<16, 32><<<blocks, 64, 0, stream>>>(a, train);
-    } else if (a.l1 == 8 && a.l2 == 32) {
-        ls_tail_kernel<8, 32><<<blocks, 64, 0, stream>>>(a, train);
-    } else {
-        TATARA_REQUIRE(false, "LayerStack (l1, l2) must be (16, 32) or (8, 32)");
+    // one instantiation per accepted (l1, l2)
+#define TATARA_TAIL(L1_, L2_)                                            \
+    if (a.l1 == L1_ && a.l2 == L2_) {                                    \
+        ls_tail_kernel<L1_, L2_><<<blocks, 64, 0, stream>>>(a, train);   \
+        TATARA_LAUNCHED("ls_tail");                                      \
+        return kOk;                                                      \
     }
-    TATARA_LAUNCHED("ls_tail");
+    TATARA_TAIL(8, 16)
+    TATARA_TAIL(8, 32)
+    TATARA_TAIL(8, 64)
+    TATARA_TAIL(16, 16)
+    TATARA_TAIL(16, 32)
+    TATARA_TAIL(16, 64)
+    TATARA_TAIL(32, 16)
+    TATARA_TAIL(32, 32)
+    TATARA_TAIL(32, 64)
+#undef TATARA_TAIL
+    TATARA_REQUIRE(false, kLsDenseShapes);
     return kOk;
 }
 
@@ -989,10 +1068,12 @@ int32_t launch_ls_l1_weight_grad(const LsDenseArgs& a, hipStream_t stream) {
                                                a.chunk_info);
     TATARA_LAUNCHED("ls_chunk_table");
     dim3 grid(a.max_chunks, ceil_div(a.ft_out, 256));
+    TATARA_REQUIRE(a.l1 >= 2 && a.l1 <= 32, "l1 must be in [2, 32]");
+    const bool two = a.l1 > 16;
     if (a.combined16)
-        ls_l1_wgrad_kernel<true><<<grid, 256, 0, stream>>>(a);
+        (two ? ls_l1_wgrad_kernel<true, 2> : ls_l1_wgrad_kernel<true, 1>)<<<grid, 256, 0, stream>>>(a);
     else
-        ls_l1_wgrad_kernel<false><<<grid, 256, 0, stream>>>(a);
+        (two ? ls_l1_wgrad_kernel<false, 2> : ls_l1_wgrad_kernel<false, 1>)<<<grid, 256, 0, stream>>>(a);
     TATARA_LAUNCHED("ls_l1_weight_grad");
     return kOk;
 }
@@ -1003,18 +1084,22 @@ int32_t launch_ls_l1_input_post(const LsDenseArgs& a, hipStream_t stream) {
     const uint32_t rows = ls_post_workgroups(a.padded_b);
     if (rows == 0) return kOk;
     TATARA_REQUIRE(a.ft_out % 128 == 0, "ft_out must be a multiple of 128");
-    TATARA_REQUIRE(a.l1 == 16 || a.l1 == 8, "l1 must be 16 or 8");
-    // two columns per lane (f32) where the 256-column blocks tile ft_out
-    const bool two = !a.dft16 && a.ft_out % 256 == 0;
+    TATARA_REQUIRE(a.l1 == 8 || a.l1 == 16 || a.l1 == 32, kLsDenseShapes);
+    // two columns per lane (f32, l1 <= 16) where the 256-column blocks tile
+    // ft_out; l1 = 32 keeps one column per lane (its 64 weights per column
+    // stay in registers)
+    const bool two = !a.dft16 && a.ft_out % 256 == 0 && a.l1 <= 16;
     const dim3 grid(a.ft_out / (two ? 256 : 128), rows);
     // f32: two columns per lane, rows four at a time; f16: one column per
     // lane, all 16 rows of a tile ahead (each measured fastest for its type)
-    auto kernel = a.dft16 ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 8, true>
-                                        : ls_l1_input_post_c_kernel<8, 1, 8, true>)
-                          : two ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 2, 4, false>
-                                              : ls_l1_input_post_c_kernel<8, 2, 4, false>)
-                                : (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 4, false>
-                                              : ls_l1_input_post_c_kernel<8, 1, 4, false>);
+    auto kernel = a.dft16 ? (a.l1 == 32   ? ls_l1_input_post_c_kernel<32, 1, 8, true>
+                             : a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 8, true>
+                                          : ls_l1_input_post_c_kernel<8, 1, 8, true>)
+                  : two   ? (a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 2, 4, false>
+                                        : ls_l1_input_post_c_kernel<8, 2, 4, false>)
+                          : (a.l1 == 32   ? ls_l1_input_post_c_kernel<32, 1, 4, false>
+                             : a.l1 == 16 ? ls_l1_input_post_c_kernel<16, 1, 4, false>
+                                          : ls_l1_input_post_c_kernel<8, 1, 4, false>);
     kernel<<<grid, 128, 0, stream>>>(a);
     TATARA_LAUNCHED("ls_l1_input_post");
     return kOk;

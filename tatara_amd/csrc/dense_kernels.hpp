@@ -10,6 +10,13 @@
 
 namespace tatara {
 
+// The LayerStack dense shapes with kernels: l1 (L1 outputs, the last one the
+// skip output) in {8, 16, 32}, l2 (L2 outputs) in {16, 32, 64}.
+constexpr const char* kLsDenseShapes = "LayerStack l1 must be 8, 16 or 32 and l2 16, 32 or 64";
+inline bool ls_dense_shape_ok(int64_t l1, int64_t l2) {
+    return (l1 == 8 || l1 == 16 || l1 == 32) && (l2 == 16 || l2 == 32 || l2 == 64);
+}
+
 // Layout of the per-workgroup gradient partials written by the tail kernel.
 struct TailDims {
     uint32_t l1, l2, nb;

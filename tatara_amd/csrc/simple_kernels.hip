@@ -31,7 +31,8 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 }
 
 // ---------------------------------------------------------------------------
-// L1 forward: one wave per 16-row tile, L1/16 output blocks of 16 columns.
+// L1 forward: one wave per 16-row tile, ceil(L1/16) output blocks of 16
+// columns (l1 = 8: the lanes of outputs 8..15 load column 7 and drop it).
 // MFMA operand layout (16x16x4 f32): lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; element r of the result is D[4*(l/16)+r][l%16].  Lane (i, q)
 // loads a float4 of row i at k = 16*kb + 4q and feeds its components to four
@@ -39,7 +40,7 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 // ---------------------------------------------------------------------------
 template <int L1>
 __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
-    constexpr int NB = L1 / 16;
+    constexpr int NB = (L1 + 15) / 16;
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t tile = blockIdx.x * 4 + wave;
     const uint32_t batch = a.batch;
@@ -51,10 +52,14 @@ __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
     // load: a guarded load would be split into predicated dword loads
     const bool xvalid = row_a < batch;
     const float4* X = reinterpret_cast<const float4*>(a.combined + (uint64_t)(xvalid ? row_a : 0) * K);
+    // lane i's output in block nb (always-valid column; outputs >= L1 are
+    // computed from zeroed weights and not stored)
+    const uint32_t ic = i < (uint32_t)L1 ? i : L1 - 1;
+    const bool ivalid = i < (uint32_t)L1;
     floatx4 acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-        const float b = a.l1_b[16 * nb + i];  // dense_mm_fwd_cpu: the sum starts at the bias
+        const float b = a.l1_b[16 * nb + ic];  // dense_mm_fwd_cpu: the sum starts at the bias
         acc[nb] = floatx4{b, b, b, b};
     }
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -69,11 +74,14 @@ __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
         for (uint32_t u = 0; u < kU; ++u) {
             const uint32_t kb = kb0 + u;
             x[u] = X[kb * 4 + q];
-            const float* wp = a.l1_w + (uint64_t)(kb * 16 + 4 * q) * L1 + i;
+            const float* wp = a.l1_w + (uint64_t)(kb * 16 + 4 * q) * L1 + ic;
 #pragma unroll
             for (int c = 0; c < 4; ++c)
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) w[u][c][nb] = wp[c * L1 + 16 * nb];
+                for (int nb = 0; nb < NB; ++nb) {
+                    const float wv = wp[c * L1 + 16 * nb];
+                    w[u][c][nb] = (L1 % 16 == 0 || ivalid) ? wv : 0.0f;
+                }
         }
 #pragma unroll
         for (uint32_t u = 0; u < kU; ++u) {
@@ -93,7 +101,8 @@ __global__ __launch_bounds__(256) void simple_l1_fwd_kernel(SimpleDenseArgs a) {
         const uint32_t row = tile * 16 + 4 * q + r;
         if (row >= batch) continue;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) a.l1_pre[(uint64_t)row * L1 + 16 * nb + i] = acc[nb][r];
+        for (int nb = 0; nb < NB; ++nb)
+            if (L1 % 16 == 0 || ivalid) a.l1_pre[(uint64_t)row * L1 + 16 * nb + i] = acc[nb][r];
     }
 }
 
@@ -237,7 +246,7 @@ __global__ __launch_bounds__(64) void simple_tail_kernel(SimpleDenseArgs a, int3
 // ---------------------------------------------------------------------------
 template <int L1>
 __global__ __launch_bounds__(256) void simple_l1_wgrad_kernel(SimpleDenseArgs a) {
-    constexpr int NB = L1 / 16;
+    constexpr int NB = (L1 + 15) / 16;  // l1 = 8: outputs 8..15 of the block are zero and dropped
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t K = 2 * a.ft_out;
     const uint32_t k0 = (blockIdx.y * 4 + wave) * 64;
@@ -262,8 +271,9 @@ __global__ __launch_bounds__(256) void simple_l1_wgrad_kernel(SimpleDenseArgs a)
         const float4 x = (rv && kvalid) ? xl : zero4;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const float dl = a.dl1[(uint64_t)rc * L1 + 16 * nb + o];
-            const float d = rv ? dl : 0.0f;
+            const bool ov = L1 % 16 == 0 || o < (uint32_t)L1;
+            const float dl = a.dl1[(uint64_t)rc * L1 + 16 * nb + (ov ? o : 0)];
+            const float d = (rv && ov) ? dl : 0.0f;
             acc[nb][0] = mfma4(d, x.x, acc[nb][0]);
             acc[nb][1] = mfma4(d, x.y, acc[nb][1]);
             acc[nb][2] = mfma4(d, x.z, acc[nb][2]);
@@ -278,7 +288,8 @@ __global__ __launch_bounds__(256) void simple_l1_wgrad_kernel(SimpleDenseArgs a)
         for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                P[(uint64_t)(k0 + 4 * kk + c) * L1 + 16 * nb + 4 * q + r] = acc[nb][c][r];
+                if (L1 % 16 == 0 || 4 * q + r < (uint32_t)L1)
+                    P[(uint64_t)(k0 + 4 * kk + c) * L1 + 16 * nb + 4 * q + r] = acc[nb][c][r];
 }
 
 // ---------------------------------------------------------------------------
@@ -386,21 +397,28 @@ uint32_t simple_chunks(uint32_t batch) { return ceil_div(batch, kSimpleChunkRows
 uint32_t simple_post_workgroups(uint32_t batch) { return ceil_div(batch, kSimplePostRows); }
 
 static int32_t check_dims(const SimpleDenseArgs& a) {
-    TATARA_REQUIRE(a.l1 == 16 || a.l1 == 32, "Simple l1 must be 16 or 32");
-    TATARA_REQUIRE(a.l2 == 32, "Simple l2 must be 32");
+    TATARA_REQUIRE(simple_dense_shape_ok(a.l1, a.l2), kSimpleDenseShapes);
     TATARA_REQUIRE(a.ft_out % 32 == 0, "Simple ft_out must be a multiple of 32");
     return kOk;
 }
+
+// kernel<L1>(...) for the accepted l1
+#define TATARA_BY_L1(KERNEL, GRID, BLOCK, ...)                                  \
+    do {                                                                        \
+        if (a.l1 == 32)                                                         \
+            KERNEL<32><<<GRID, BLOCK, 0, stream>>>(__VA_ARGS__);                \
+        else if (a.l1 == 16)                                                    \
+            KERNEL<16><<<GRID, BLOCK, 0, stream>>>(__VA_ARGS__);                \
+        else                                                                    \
+            KERNEL<8><<<GRID, BLOCK, 0, stream>>>(__VA_ARGS__);                 \
+    } while (0)
 
 int32_t launch_simple_l1_forward(const SimpleDenseArgs& a, hipStream_t stream) {
     int32_t st = check_dims(a);
     if (st) return st;
     const uint32_t tiles = ceil_div(a.batch, 16);
     if (tiles == 0) return kOk;
-    if (a.l1 == 32)
-        simple_l1_fwd_kernel<32><<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
-    else
-        simple_l1_fwd_kernel<16><<<ceil_div(tiles, 4), 256, 0, stream>>>(a);
+    TATARA_BY_L1(simple_l1_fwd_kernel, ceil_div(tiles, 4), 256, a);
     TATARA_LAUNCHED("simple_l1_forward");
     return kOk;
 }
@@ -410,11 +428,24 @@ int32_t launch_simple_tail(const SimpleDenseArgs& a, int32_t train, hipStream_t 
     if (st) return st;
     const uint32_t blocks = simple_tail_workgroups(a.batch);
     if (blocks == 0) return kOk;
-    if (a.l1 == 32)
-        simple_tail_kernel<32, 32><<<blocks, 64, 0, stream>>>(a, train);
-    else
-        simple_tail_kernel<16, 32><<<blocks, 64, 0, stream>>>(a, train);
-    TATARA_LAUNCHED("simple_tail");
+    // one instantiation per accepted (l1, l2)
+#define TATARA_TAIL(L1_, L2_)                                                 \
+    if (a.l1 == L1_ && a.l2 == L2_) {                                         \
+        simple_tail_kernel<L1_, L2_><<<blocks, 64, 0, stream>>>(a, train);    \
+        TATARA_LAUNCHED("simple_tail");                                       \
+        return kOk;                                                           \
+    }
+    TATARA_TAIL(8, 16)
+    TATARA_TAIL(8, 32)
+    TATARA_TAIL(8, 64)
+    TATARA_TAIL(16, 16)
+    TATARA_TAIL(16, 32)
+    TATARA_TAIL(16, 64)
+    TATARA_TAIL(32, 16)
+    TATARA_TAIL(32, 32)
+    TATARA_TAIL(32, 64)
+#undef TATARA_TAIL
+    TATARA_REQUIRE(false, kSimpleDenseShapes);
     return kOk;
 }
 
@@ -424,10 +455,7 @@ int32_t launch_simple_l1_weight_grad(const SimpleDenseArgs& a, hipStream_t strea
     const uint32_t chunks = simple_chunks(a.batch);
     if (chunks == 0) return kOk;
     const dim3 grid(chunks, ceil_div(2 * a.ft_out, 256));
-    if (a.l1 == 32)
-        simple_l1_wgrad_kernel<32><<<grid, 256, 0, stream>>>(a);
-    else
-        simple_l1_wgrad_kernel<16><<<grid, 256, 0, stream>>>(a);
+    TATARA_BY_L1(simple_l1_wgrad_kernel, grid, 256, a);
     TATARA_LAUNCHED("simple_l1_weight_grad");
     return kOk;
 }
@@ -438,10 +466,7 @@ int32_t launch_simple_l1_input_post(const SimpleDenseArgs& a, hipStream_t stream
     const uint32_t rows = simple_post_workgroups(a.batch);
     if (rows == 0) return kOk;
     const dim3 grid(ceil_div(a.ft_out, 256), rows);
-    if (a.l1 == 32)
-        simple_l1_input_post_kernel<32><<<grid, 256, 0, stream>>>(a);
-    else
-        simple_l1_input_post_kernel<16><<<grid, 256, 0, stream>>>(a);
+    TATARA_BY_L1(simple_l1_input_post_kernel, grid, 256, a);
     TATARA_LAUNCHED("simple_l1_input_post");
     return kOk;
 }

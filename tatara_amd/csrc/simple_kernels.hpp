@@ -10,6 +10,13 @@
 
 namespace tatara {
 
+// The Simple dense shapes with kernels: l1 (first hidden layer) in
+// {8, 16, 32}, l2 (second) in {16, 32, 64}; "512x2-8-64" is (8, 64).
+constexpr const char* kSimpleDenseShapes = "Simple l1 must be 8, 16 or 32 and l2 16, 32 or 64";
+inline bool simple_dense_shape_ok(int64_t l1, int64_t l2) {
+    return (l1 == 8 || l1 == 16 || l1 == 32) && (l2 == 16 || l2 == 32 || l2 == 64);
+}
+
 // Per-workgroup gradient partials of the Simple output kernel, in this order:
 // l2_w [l1][l2], l2_b [l2], l3_w [l2], l3_b [1], l1_b [l1].
 struct SimpleTailDims {

@@ -19,6 +19,7 @@
 
 #include <cstring>
 #include <limits>
+#include <string>
 #include <vector>
 
 #include "binsort.hpp"
@@ -74,8 +75,9 @@ class SimpleTrainer final : public TrainerBase {
         TATARA_REQUIRE(c.max_batch > 0, "max_batch must be positive");
         TATARA_REQUIRE(c.ft_in > 0 && c.max_active > 0 && c.max_active <= 64, "ft_in > 0, 0 < max_active <= 64");
         TATARA_REQUIRE(c.ft_out > 0 && c.ft_out % 32 == 0, "ft_out must be a positive multiple of 32");
-        TATARA_REQUIRE((c.l1_out == 32 || c.l1_out == 16) && c.l2_out == 32,
-                       "Simple (l1, l2) must be (32, 32) or (16, 32)");
+        TATARA_REQUIRE(simple_dense_shape_ok(c.l1_out, c.l2_out),
+                       std::string(kSimpleDenseShapes) + " (got " + std::to_string(c.l1_out) + ", " +
+                           std::to_string(c.l2_out) + ")");
         TATARA_REQUIRE(c.optimizer >= 0 && c.optimizer <= 2, "unknown optimizer");
         TATARA_REQUIRE(c.piece_inputs >= 0, "piece_inputs >= 0");
         TATARA_REQUIRE(!c.ft_fp16 && !c.ft_fp16_out && !c.fp16_opt_state && !c.tf32,

@@ -128,8 +128,9 @@ class LayerStackTrainer final : public TrainerBase {
         TATARA_REQUIRE(c.max_batch > 0 && c.max_batch % 16 == 0, "max_batch must be a positive multiple of 16");
         TATARA_REQUIRE(c.ft_in > 0 && c.max_active > 0 && c.max_active <= 64, "ft_in > 0, 0 < max_active <= 64");
         TATARA_REQUIRE(c.ft_out > 0 && c.ft_out % 128 == 0, "ft_out must be a positive multiple of 128");
-        TATARA_REQUIRE((c.l1_out == 16 || c.l1_out == 8) && c.l2_out == 32,
-                       "(l1, l2) must be (16, 32) or (8, 32)");
+        TATARA_REQUIRE(ls_dense_shape_ok(c.l1_out, c.l2_out),
+                       std::string(kLsDenseShapes) + " (got " + std::to_string(c.l1_out) + ", " +
+                           std::to_string(c.l2_out) + ")");
         TATARA_REQUIRE(c.num_buckets >= 2 && c.num_buckets <= 9, "num_buckets must be in [2, 9]");
         TATARA_REQUIRE(c.optimizer >= 0 && c.optimizer <= 2, "unknown optimizer");
         TATARA_REQUIRE(c.piece_inputs >= 0, "piece_inputs >= 0");

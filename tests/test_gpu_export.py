@@ -50,10 +50,10 @@ def test_op_quantise_matches_oracle(gpu, rows, cols, pi):
     assert quantise_op(w, rows, cols, pi, True) == ox.leb128_encode(q)
 
 
-def _ls_trainer(pi):
+def _ls_trainer(pi, l1=16, l2=32):
     info = of.feature_set_info("halfka-hm-merged")  # 45 x 1629 rows
     cfg = LayerStackConfig(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=pi, ft_out=128,
-                           l1_out=16, l2_out=32, num_buckets=9, max_batch=1024, optimizer="ranger")
+                           l1_out=l1, l2_out=l2, num_buckets=9, max_batch=1024, optimizer="ranger")
     return info, LayerStackTrainer(cfg)
 
 
@@ -63,9 +63,10 @@ def _plant(t, name, idx, values):
     t.set(name, w)
 
 
-@pytest.mark.parametrize("factorized,fv", [(True, 28), (False, None)])
-def test_layerstack_export_bytes(gpu, tmp_path, factorized, fv):
-    info, t = _ls_trainer(1629 if factorized else 0)
+@pytest.mark.parametrize("factorized,fv,l1,l2", [(True, 28, 16, 32), (False, None, 16, 32), (True, 28, 32, 64),
+                                                 (False, 28, 8, 16)])
+def test_layerstack_export_bytes(gpu, tmp_path, factorized, fv, l1, l2):
+    info, t = _ls_trainer(1629 if factorized else 0, l1, l2)
     ft_in, pi = info["ft_in"], 1629 if factorized else 0
     with t:
         for s in range(3):
@@ -83,12 +84,12 @@ def test_layerstack_export_bytes(gpu, tmp_path, factorized, fv):
         got = path.read_bytes()
         w = {g: t.get(g) for g in t.GROUPS}
     w["ft_w"] = ox.coalesce(w["ft_w"], ft_in, pi, 128)
-    want = ox.ls_save_quantised(4, info_hash("halfka-hm-merged"), ft_in, 128, 16, 32, 9, w, fv_scale=fv)
+    want = ox.ls_save_quantised(4, info_hash("halfka-hm-merged"), ft_in, 128, l1, l2, 9, w, fv_scale=fv)
     assert len(got) == len(want)
     if got != want:
         bad = np.nonzero(np.frombuffer(got, np.uint8) != np.frombuffer(want, np.uint8))[0]
         raise AssertionError(f"{bad.size} bytes differ, first at {bad[:8]}")
-    d = ox.parse_layerstack(got, 128, 16, 32)
+    d = ox.parse_layerstack(got, 128, l1, l2)
     assert d["trailing"] == 0 and ("fv_scale=28" in d["arch"]) == (fv is not None)
 
 
@@ -98,12 +99,13 @@ def info_hash(fs):
     return h.value
 
 
-@pytest.mark.parametrize("factorized", [True, False])
-def test_simple_export_bytes(gpu, tmp_path, factorized):
+# 256x2-32-32 and the README's 512x2-8-64
+@pytest.mark.parametrize("factorized,ft_out,l1,l2", [(True, 256, 32, 32), (False, 256, 32, 32), (True, 512, 8, 64)])
+def test_simple_export_bytes(gpu, tmp_path, factorized, ft_out, l1, l2):
     info = of.feature_set_info("halfkp")
     ft_in, pi = info["ft_in"], 1548 if factorized else 0
-    cfg = SimpleConfig(ft_in=ft_in, max_active=info["max_active"], piece_inputs=pi, ft_out=256, l1_out=32,
-                       l2_out=32, max_batch=1024, optimizer="adamw", weight_decay=0.01)
+    cfg = SimpleConfig(ft_in=ft_in, max_active=info["max_active"], piece_inputs=pi, ft_out=ft_out, l1_out=l1,
+                       l2_out=l2, max_batch=1024, optimizer="adamw", weight_decay=0.01)
     fv = simple_fv_scale(290.0)
     with SimpleTrainer(cfg) as t:
         for s in range(3):
@@ -117,17 +119,17 @@ def test_simple_export_bytes(gpu, tmp_path, factorized):
         t.save_quantised(path, "halfkp", fv_scale=fv)
         got = path.read_bytes()
         w = {g: t.get(g) for g in t.GROUPS}
-    w["ft_w"] = ox.coalesce(w["ft_w"], ft_in, pi, 256)
+    w["ft_w"] = ox.coalesce(w["ft_w"], ft_in, pi, ft_out)
     # to_simple_weights: the device's in-major dense tables become out-major
-    w["l1_w"] = w["l1_w"].reshape(512, 32).T.copy()
-    w["l2_w"] = w["l2_w"].reshape(32, 32).T.copy()
-    want = ox.simple_save_quantised(0, 0x5D69D5B8, ft_in, 256, 32, 32, w, fv_scale=fv)
+    w["l1_w"] = w["l1_w"].reshape(2 * ft_out, l1).T.copy()
+    w["l2_w"] = w["l2_w"].reshape(l1, l2).T.copy()
+    want = ox.simple_save_quantised(0, 0x5D69D5B8, ft_in, ft_out, l1, l2, w, fv_scale=fv)
     assert len(got) == len(want)
     if got != want:
         bad = np.nonzero(np.frombuffer(got, np.uint8) != np.frombuffer(want, np.uint8))[0]
         raise AssertionError(f"{bad.size} bytes differ, first at {bad[:8]}")
-    d = ox.parse_simple(got, ft_in, 256, 32, 32)
-    assert d["trailing"] == 0 and d["network_hash"] == ox.simple_network_hash(0x5D69D5B8, 256, 32, 32)
+    d = ox.parse_simple(got, ft_in, ft_out, l1, l2)
+    assert d["trailing"] == 0 and d["network_hash"] == ox.simple_network_hash(0x5D69D5B8, ft_out, l1, l2)
 
 
 def test_export_rejects_wrong_feature_set(gpu, tmp_path):

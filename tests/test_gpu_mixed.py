@@ -151,6 +151,35 @@ def test_one_step_matches_oracle(gpu, mode, factorize, ft_out):
         assert clamps == 0
 
 
+@pytest.mark.parametrize("l1,l2,ft_out", [(32, 64, 512), (8, 16, 512), (32, 16, 256)])
+def test_all_optim_dense_shapes(gpu, l1, l2, ft_out):
+    """--all-optim at l1 = 32 (two 16-output blocks in the TF32 L1 forward,
+    the f16-dft L1 input gradient with 32 weights per column) and l1 = 8:
+    one step against the oracle with the same bars as the other shapes."""
+    prec = FLAGS["all_optim"]
+    sh, cfg = mixed(prec, ft_out=ft_out, l1=l1, l2=l2)
+    b = cfg.max_batch
+    batch, bucket = batch_for(17, b, sh.nb)
+    with LayerStackTrainer(cfg) as t:
+        t.train_step(batch, bucket, 8.75e-4, 0.25, Sigmoid())
+        st = oracle_state(sh, prec)
+        opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+        acc, a, g = ols.train_step(sh, st, as_dict(batch, bucket), opt, 8.75e-4, 0.25, loss_dict(Sigmoid()), 1,
+                                   prec)
+        bf = b * sh.ft_out
+        assert np.array_equal(t.activation("combined", bf), a["combined"])
+        close(t.activation("net_output", b), a["net"], 1e-5, atol=1e-6, what="net_output")
+        for k in ("dft_stm", "dft_nstm"):
+            close(t.activation(k, bf), a[k + "16"], 2e-3, atol=SUB16, what=k + " (f16, scaled)")
+        bd = as_dict(batch, bucket)
+        gb = f16_grad_bound(sh, bd, a, b, mfma=ft_out >= 512)
+        close(t.get("ft_w", "grad"), g["ft_w"], 1e-3, atol_frac=1e-5, atol=gb, what="grad ft_w")
+        for name in GROUPS:
+            close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"{name}.w")
+        check_moments(t, st, prec, "step 1", g=g["ft_w"], g_bound=gb, opt=opt)
+        close([t.flush_pending_loss()], [acc], 1e-6, what="loss")
+
+
 @pytest.mark.parametrize("ft_out", [256, 512])
 def test_all_optim_seven_steps_with_lookahead(gpu, ft_out):
     prec = ols.Precision.all_optim()

@@ -36,12 +36,12 @@ def close(got, exp, rtol, atol_frac=0.0, atol=0.0, what=""):
     )
 
 
-def make(ft_out=128, l1=32, optimizer="adamw", b=256, keep=True, factorize=True):
+def make(ft_out=128, l1=32, optimizer="adamw", b=256, keep=True, factorize=True, l2=32):
     sh = osi.SimpleShape(ft_in=SPEC["ft_in"], max_active=SPEC["max_active"],
                          piece_inputs=SPEC["piece_inputs"] if factorize else 0, ft_out=ft_out, l1=l1,
-                         l2=32)
+                         l2=l2)
     cfg = SimpleConfig(ft_in=sh.ft_in, max_active=sh.max_active, piece_inputs=sh.piece_inputs,
-                       ft_out=ft_out, l1_out=l1, l2_out=32, max_batch=b, optimizer=optimizer,
+                       ft_out=ft_out, l1_out=l1, l2_out=l2, max_batch=b, optimizer=optimizer,
                        weight_decay=0.01, keep_grads=keep)
     return sh, cfg
 
@@ -171,6 +171,40 @@ def test_unfactorized_l1_16_ragged_batch(gpu):
         for name in SIMPLE_GROUPS:
             close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=name)
         close([t.flush_pending_loss()], [acc], 1e-6, what="loss")
+
+
+# (ft_out, l1, l2): the README's 512x2-8-64, and the other l1 / l2 with kernels
+SIMPLE_SHAPES = [(512, 8, 64), (128, 8, 16), (128, 16, 16), (128, 16, 64), (128, 32, 16), (256, 32, 64),
+                 (128, 8, 32)]
+
+
+@pytest.mark.parametrize("ft_out,l1,l2", SIMPLE_SHAPES, ids=[f"{a}x2-{b}-{c}" for a, b, c in SIMPLE_SHAPES])
+def test_dense_shapes_match_oracle(gpu, ft_out, l1, l2):
+    """Two Ranger steps at each shape against the oracle (one-step bars)."""
+    sh, cfg = make(ft_out=ft_out, l1=l1, l2=l2, optimizer="ranger")
+    b = cfg.max_batch
+    st = osi.default_init(sh)
+    opt = osi.OptConfig(optimizer="ranger", weight_decay=0.01)
+    with SimpleTrainer(cfg) as t:
+        for step in (1, 2):
+            batch = batch_for(40 + step, b)
+            t.train_step(batch, 1e-3, 0.25, WRM290)
+            acc, a, g = osi.train_step(sh, st, as_dict(batch), opt, 1e-3, 0.25, loss_dict(WRM290), step)
+            bf = b * sh.ft_out
+            assert np.array_equal(t.activation("combined", 2 * bf), a["combined"])
+            close(t.activation("l1_pre", b * l1), a["l1_pre"], 1e-5, atol=1e-6, what=f"step {step} l1_pre")
+            close(t.activation("net_output", b), a["net"], 1e-5, atol=1e-6, what=f"step {step} net_output")
+            for name in SIMPLE_GROUPS:
+                close(t.get(name, "grad"), g[name], 1e-4, atol_frac=1e-5, what=f"step {step} grad {name}")
+                close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"step {step} {name}.w")
+
+
+@pytest.mark.parametrize("l1,l2", [(4, 32), (24, 32), (32, 48), (64, 64)])
+def test_dense_shapes_without_kernels_are_rejected(gpu, l1, l2):
+    from tatara_amd._lib import TataraError
+    _, cfg = make(l1=l1, l2=l2)
+    with pytest.raises(TataraError, match="l1 must be 8, 16 or 32 and l2 16, 32 or 64"):
+        SimpleTrainer(cfg)
 
 
 def test_validate_step(gpu):

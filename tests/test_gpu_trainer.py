@@ -36,12 +36,12 @@ def close(got, exp, rtol, atol_frac=0.0, atol=0.0, what=""):
             f"(largest abs err {err.max():.3e})")
 
 
-def make(nb=8, ft_out=256, l1=16, optimizer="ranger", b=256, keep=True, factorize=True):
+def make(nb=8, ft_out=256, l1=16, optimizer="ranger", b=256, keep=True, factorize=True, l2=32):
     sh = ols.LsShape(ft_in=SPEC["ft_in"], max_active=SPEC["max_active"],
                      piece_inputs=SPEC["piece_inputs"] if factorize else 0, ft_out=ft_out, l1=l1,
-                     l2=32, nb=nb)
+                     l2=l2, nb=nb)
     cfg = LayerStackConfig(ft_in=sh.ft_in, max_active=sh.max_active, piece_inputs=sh.piece_inputs,
-                           ft_out=ft_out, l1_out=l1, l2_out=32, num_buckets=nb, max_batch=b,
+                           ft_out=ft_out, l1_out=l1, l2_out=l2, num_buckets=nb, max_batch=b,
                            optimizer=optimizer, keep_grads=keep)
     return sh, cfg
 
@@ -174,6 +174,43 @@ def test_unfactorized_and_l1_8(gpu):
         assert np.array_equal(t.activation("combined", b * sh.ft_out), a["combined"])
         for name in GROUPS:
             close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=name)
+
+
+SHAPES = [(l1, l2) for l1 in (8, 16, 32) for l2 in (16, 32, 64)]
+
+
+@pytest.mark.parametrize("l1,l2", SHAPES, ids=[f"l1_{a}-l2_{b}" for a, b in SHAPES])
+def test_dense_shapes_match_oracle(gpu, l1, l2):
+    """Every (l1, l2) with kernels (l1 in {8, 16, 32}, l2 in {16, 32, 64}):
+    two Ranger steps against the oracle, with the one-step bars for the
+    activations, gradients and post-step weights."""
+    sh, cfg = make(l1=l1, l2=l2)
+    b = cfg.max_batch
+    st = ols.default_init(sh)
+    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+    loss = Sigmoid()
+    with LayerStackTrainer(cfg) as t:
+        for step in (1, 2):
+            batch, bucket = batch_for(30 + step, b, sh.nb)
+            t.train_step(batch, bucket, 8.75e-4, 0.25, loss)
+            acc, a, g = ols.train_step(sh, st, as_dict(batch, bucket), opt, 8.75e-4, 0.25, loss_dict(loss), step)
+            bf = b * sh.ft_out
+            assert np.array_equal(t.activation("combined", bf), a["combined"])
+            close(t.activation("net_output", b), a["net"], 1e-5, atol=1e-6, what=f"step {step} net_output")
+            dmax = max(np.abs(a["dft_stm"]).max(), 1e-30)
+            close(t.activation("dft_stm", bf), a["dft_stm"], 1e-4, atol=1e-5 * dmax, what=f"step {step} dft_stm")
+            for name in GROUPS:
+                close(t.get(name, "grad"), g[name], 1e-4, atol_frac=1e-5, what=f"step {step} grad {name}")
+                close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"step {step} {name}.w")
+        assert t.tensor_size("l2_w") == sh.nb * l2 * 2 * (l1 - 1)
+
+
+@pytest.mark.parametrize("l1,l2", [(24, 32), (16, 48), (4, 32), (64, 32), (16, 128)])
+def test_dense_shapes_without_kernels_are_rejected(gpu, l1, l2):
+    from tatara_amd._lib import TataraError
+    _, cfg = make(l1=l1, l2=l2)
+    with pytest.raises(TataraError, match="l1 must be 8, 16 or 32 and l2 16, 32 or 64"):
+        LayerStackTrainer(cfg)
 
 
 def test_validate_step_and_ragged_batch(gpu):
