@@ -80,22 +80,24 @@ WORKLOADS = {
 
 
 def hbm_traffic(workload: str, kernel: str):
-    """HBM bytes per launch of a kernel from the committed counter summary.
+    """(HBM bytes per launch, commit, kernel-source digest) of a kernel from
+    the committed counter summary.
 
     profiles/hbm_traffic.md holds FETCH_SIZE / WRITE_SIZE per dispatch from
     two rocprofv3 --pmc passes of this script, scaled by a plain-copy
-    calibration; returns None when the kernel was not profiled.
+    calibration, with the commit and the `source_digest` of the kernels
+    measured; (None, None, None) when the kernel was not profiled.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.md")
     try:
         with open(path) as f:
             for line in f:
                 cells = [c.strip() for c in line.strip().strip("|").split("|")]
-                if len(cells) == 7 and cells[0] == workload and cells[1].startswith(kernel):
-                    return int(cells[6])
+                if len(cells) == 9 and cells[0] == workload and cells[1].startswith(kernel):
+                    return int(cells[6]), cells[7], cells[8]
     except OSError:
-        return None
-    return None
+        pass
+    return None, None, None
 
 
 def log(msg: str) -> None:
@@ -527,6 +529,84 @@ def time_export(t, w: dict, spec: dict, args) -> dict:
     return out
 
 
+def run_loop_throughput(w: dict, cfg, records: list, b: int, pw, superbatches: int = 2) -> dict:
+    """End-to-end training throughput through tatara_train_run (the superbatch
+    driver, trainer.rs:759-1211): the bench's PSV batches written to one file
+    under /tmp, read back by the driver's reader thread into a pinned
+    two-slot ring, uploaded (40 B per position), decoded to indices and
+    buckets on the GPU, and trained, `superbatches` superbatches of
+    len(records) batches from a fresh trainer.  `value` is positions over the
+    superbatches' own seconds, as the reference's `[train] ... pos/s` line
+    reports it (trainer.rs:1080-1096: the file read, upload, decode and steps
+    of the superbatch, up to its loss flush); `with_checkpoints` adds the
+    final .bin export and resume checkpoint the driver writes at the end."""
+    import shutil
+    import tempfile
+
+    from tatara_amd import run as R
+    from tatara_amd.trainer import LayerStackTrainer, Sigmoid, SimpleTrainer, Wrm, simple_fv_scale
+
+    d = tempfile.mkdtemp(prefix="tatara_bench_run_", dir="/tmp")
+    try:
+        path = os.path.join(d, "bench.psv")
+        with open(path, "wb") as f:
+            for r in records:
+                f.write(np.ascontiguousarray(r).tobytes())
+        layerstack = w["arch"] == "layerstack"
+        rc = R.TrainingConfig(net_id="bench", feature_set=w["spec"], output_dir=os.path.join(d, "out"),
+                              start_superbatch=1, end_superbatch=superbatches,
+                              batches_per_superbatch=len(records), batch_size=b, save_rate=1 << 30,
+                              fv_scale=None if layerstack else simple_fv_scale(290.0),
+                              bucket_mode=w["bucket_mode"], num_buckets=w["nb"],
+                              progress_weights=pw.dev if pw is not None else None, print_progress=False)
+        if layerstack:
+            trainer, loss = LayerStackTrainer(cfg), Sigmoid(1.0 / 290.0)
+        else:
+            trainer = SimpleTrainer(cfg)
+            loss = Wrm(nnue2score=290.0, in_scaling=290.0, in_offset=0.0, target_offset=0.0, target_scaling=290.0)
+        with trainer as t:
+            t0 = time.perf_counter()
+            res = R.run(t, path, R.ConstantLR(w["lr"]), R.ConstantWDL(0.0), rc, loss)
+            wall = time.perf_counter() - t0
+        sbs = res.superbatches
+        pos = sum(r["positions"] for r in sbs)
+        secs = sum(r["seconds"] for r in sbs)
+        return {"value": round(pos / secs, 1), "unit": "pos/s",
+                "per_superbatch_pos_s": [round(r["positions"] / r["seconds"], 1) for r in sbs],
+                "with_checkpoints": {"value": round(pos / wall, 1), "unit": "pos/s", "seconds": round(wall, 3)},
+                "positions": pos, "superbatches": len(sbs), "batches_per_superbatch": len(records),
+                "mean_loss_last": round(sbs[-1]["mean_loss"], 6),
+                "path": "tatara_train_run: PSV file in /tmp -> pinned ring -> H2D 40 B/pos -> GPU decode "
+                        "-> king-blocked train_step; a fresh trainer"}
+    except Exception as e:  # the run figure must not hide the resident result
+        return {"value": None, "error": repr(e)}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def git_commit() -> str:
+    """The commit of this checkout (.git/HEAD read directly; git may be absent),
+    or "unknown"."""
+    root = os.path.dirname(os.path.abspath(__file__))
+    try:
+        with open(os.path.join(root, ".git", "HEAD")) as f:
+            head = f.read().strip()
+        if head.startswith("ref: "):
+            ref = head[5:]
+            p = os.path.join(root, ".git", ref)
+            if os.path.exists(p):
+                with open(p) as f:
+                    return f.read().strip()[:12]
+            with open(os.path.join(root, ".git", "packed-refs")) as f:
+                for line in f:
+                    if line.strip().endswith(" " + ref):
+                        return line.split()[0][:12]
+            return "unknown"
+        return head[:12]
+    except OSError:
+        return "unknown"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -548,6 +628,8 @@ def main() -> int:
                     help="also time this many quantised exports (.bin) of the trained weights")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
+    ap.add_argument("--no-run-loop", action="store_true",
+                    help="skip the end-to-end tatara_train_run figure (PSV file -> decode -> steps)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -661,6 +743,11 @@ def main() -> int:
         t.set_profiling(False)
         step_count = t.step_count
         export = time_export(t, w, spec, args) if args.export_reps > 0 else None
+    run_loop = None
+    if not args.no_run_loop:
+        log(f"run loop: tatara_train_run, 2 superbatches of {len(records)} batches from a PSV file")
+        run_loop = run_loop_throughput(w, cfg, records, b, pw)
+        log(f"run loop: {run_loop.get('value')} pos/s")
     phase_avg = {k: v / max(nprof, 1) for k, v in phases.items()}
     drift = None
     if args.drift and w.get("all_optim"):
@@ -698,7 +785,10 @@ def main() -> int:
     achieved = byts / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
     if achieved > HBM_PEAK_GBS:
         raise SystemExit(f"{dom}: compulsory bytes / launch time = {achieved:.0f} GB/s exceeds the HBM peak")
-    traffic = hbm_traffic(args.workload, dom)
+    traffic, traffic_commit, traffic_digest = hbm_traffic(args.workload, dom)
+    from tatara_amd.build import source_digest
+
+    digest = source_digest()
     roofline = {
         "bound": "hbm",
         "kernel": dom,
@@ -716,12 +806,19 @@ def main() -> int:
         "traffic_over_compulsory": round(traffic / byts, 3) if traffic else None,
         "logical_GBps": round(logical / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
         "traffic_source": "profiles/hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
+        # the commit and kernel-source digest the traffic row was measured
+        # with, beside this run's: a stale row shows as traffic_current false
+        "traffic_commit": traffic_commit,
+        "traffic_source_digest": traffic_digest,
+        "source_digest": digest,
+        "traffic_current": traffic_digest == digest,
+        "commit": git_commit(),
     }
     other = {k: {"avg_launch_ms": round(v[0], 4),
                  "compulsory_GB": round(v[1] / 1e9, 4),
                  "compulsory_frac": round(v[1] / (v[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if v[0] > 0 else None,
                  "logical_GBps": round(v[2] / (v[0] * 1e-3) / 1e9, 1) if v[0] > 0 else None,
-                 "hbm_bytes": hbm_traffic(args.workload, k)}
+                 "hbm_bytes": hbm_traffic(args.workload, k)[0]}
              for k, v in kernels.items()}
     phases_out = {k: {"ms": round(v, 4), "compulsory_GB": round(comp[k] / 1e9, 4),
                       "compulsory_frac": round(comp[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if v > 0 else None}
@@ -776,6 +873,8 @@ def main() -> int:
         line["export"] = export
     if drift is not None:
         line["drift_vs_f32"] = drift
+    if run_loop is not None:
+        line["run_loop"] = run_loop
     print(json.dumps(line), flush=True)
     return 0
 

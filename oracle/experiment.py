@@ -23,7 +23,13 @@ SCHEMA_VERSION = 2
 
 
 def civil_from_epoch(epoch_secs: int) -> tuple[int, int, int, int, int, int]:
-    """(year, month, day, hour, minute, second) UTC of a UNIX time in seconds."""
+    """(year, month, day, hour, minute, second) UTC of a UNIX time in seconds.
+
+    The date is Howard Hinnant's published civil_from_days algorithm
+    ("chrono-Compatible Low-Level Date Algorithms"; the reference names it at
+    crates/nnue-train/src/experiment.rs:577): 400-year eras from 0000-03-01,
+    the year of the era, the day of a March-based year, and the month from the
+    153-day five-month pattern."""
     days, rem = divmod(epoch_secs, 86400)
     hour, minute, second = rem // 3600, rem % 3600 // 60, rem % 60
     z = days + 719468

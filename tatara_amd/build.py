@@ -41,6 +41,20 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def source_digest() -> str:
+    """A short SHA-256 over the kernel sources (every csrc file and the C
+    header, by name and content): it names the kernels a measurement was
+    taken with where no git metadata travels with the tree."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.hpp")) + [PKG.parent / "include" / "tatara_hip.h"])
+    for f in files:
+        h.update(f.name.encode() + b"\0")
+        h.update(f.read_bytes())
+    return h.hexdigest()[:12]
+
+
 def build(jobs: int | None = None) -> Path:
     """Compiles every source and links the shared library; returns its path."""
     BUILD.mkdir(exist_ok=True)

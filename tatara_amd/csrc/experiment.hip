@@ -21,8 +21,11 @@
 
 namespace tatara {
 
-// Days since 1970-01-01 to the proleptic Gregorian date, by 400-year eras
-// counted from 0000-03-01 (so the leap day ends each era's year): the era,
+// Days since 1970-01-01 to the proleptic Gregorian date: Howard Hinnant's
+// published civil_from_days algorithm ("chrono-Compatible Low-Level Date
+// Algorithms"), which the reference also names (experiment.rs:577).  It
+// works in 400-year eras counted from 0000-03-01 (so the leap day ends each
+// era's year): the era,
 // the day within it, the year within it, the day of that March-based year,
 // and the month from the five-month 153-day pattern of March..July and
 // August..December.
