@@ -628,6 +628,9 @@ def main() -> int:
                     help="also time this many quantised exports (.bin) of the trained weights")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
+    ap.add_argument("--chain-ab-rounds", type=int, default=4,
+                    help="alternating rounds of --steps steps with the occurrence-list sort chain skipped "
+                         "(king-blocked batches) and queued (gated off on the device); 0 skips the comparison")
     ap.add_argument("--no-run-loop", action="store_true",
                     help="skip the end-to-end tatara_train_run figure (PSV file -> decode -> steps)")
     args = ap.parse_args()
@@ -709,6 +712,31 @@ def main() -> int:
         ms_per_step = 1000.0 * elapsed / args.steps
         pos_s = b * args.steps / elapsed
         log(f"{pos_s:,.0f} pos/s  ({ms_per_step:.3f} ms/step), last loss {last:.4f}")
+
+        # the same resident batches without the king-blocked statement
+        # (on_device = 1): the step also queues the occurrence-list sort chain
+        # (keys, radix passes, offsets), which the device flag then gates
+        # off.  Alternating rounds of each, medians compared.
+        import dataclasses
+
+        gated = [dataclasses.replace(d, king_blocked=False) for d in dev]
+        ab = {"skipped": [], "queued": []}
+        for rnd in range(args.chain_ab_rounds):
+            order = (("skipped", dev), ("queued", gated)) if rnd % 2 == 0 else (("queued", gated), ("skipped", dev))
+            for name, bs in order:
+                for i in range(args.warmup):
+                    step(t, bs[i % len(bs)])
+                t.flush_pending_loss()
+                _lib.check(lib.tatara_synchronize())
+                t0 = time.perf_counter()
+                for i in range(args.steps):
+                    step(t, bs[i % len(bs)])
+                t.flush_pending_loss()
+                _lib.check(lib.tatara_synchronize())
+                ab[name].append(1000.0 * (time.perf_counter() - t0) / args.steps)
+        if args.chain_ab_rounds:
+            log(f"sort chain skipped / queued: {np.median(ab['skipped']):.4f} / {np.median(ab['queued']):.4f} "
+                f"ms/step (medians of {args.chain_ab_rounds} alternating rounds)")
 
         # the drop-in path: host batches (on_device = 0) every step, copied into
         # the trainer's pinned upload ring and uploaded on its copy stream, as
@@ -864,6 +892,15 @@ def main() -> int:
                          "h2d_MB_per_step": round(h2d / 1e6, 2),
                          "path": "host arrays every step (on_device = 0): pinned two-slot upload ring, "
                                  "copy stream, event-gated"},
+        "sort_chain_ab": None if not args.chain_ab_rounds else {
+            "skipped_ms_median": round(float(np.median(ab["skipped"])), 4),
+            "queued_ms_median": round(float(np.median(ab["queued"])), 4),
+            "skipped_ms": [round(x, 4) for x in ab["skipped"]],
+            "queued_ms": [round(x, 4) for x in ab["queued"]],
+            "rounds": args.chain_ab_rounds, "steps_per_round": args.steps,
+            "path": "the resident batches passed as on_device = 2 (king-blocked: no occurrence-list sort "
+                    "chain queued, as `value` runs them) and as on_device = 1 (the chain queued each step "
+                    "and gated off on the device), in alternating rounds"},
         "kernels": other,
         "phases": phases_out,
         "psv_decode_ms_per_batch": round(decode_ms, 3),
