@@ -36,6 +36,7 @@ Prints ONE JSON line.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -416,21 +417,47 @@ def quantised_view(t) -> dict:
             "l1_i8": np.clip(rnd(64.0 * merged), -128, 127)}
 
 
-def drift_report(w: dict, spec: dict, dev: list, b: int, steps_per_sb: int) -> dict:
+def teacher_scores(hb: dict, ft_in: int, seed: int = 11, scale: float = 60.0) -> np.ndarray:
+    """A learnable stand-in for the PSV scores (the synthetic ones are noise):
+    a fixed random piece-square teacher, score = scale * (sum of t[f] over the
+    side to move's active features - the same over the other side's), clipped
+    to +-3000, t ~ N(0, 1) per feature index (seeded)."""
+    t = np.random.default_rng(seed).standard_normal(ft_in)
+    b = hb["nnz"].size
+    stm, nstm = hb["stm"].reshape(b, -1), hb["nstm"].reshape(b, -1)
+    valid = np.arange(stm.shape[1])[None, :] < hb["nnz"][:, None]
+
+    def side(idx):
+        ok = valid & (idx >= 0) & (idx < ft_in)
+        return np.where(ok, t[np.clip(idx, 0, ft_in - 1)], 0.0).sum(axis=1)
+
+    return np.clip(scale * (side(stm) - side(nstm)), -3000.0, 3000.0).astype(np.float32)
+
+
+def drift_report(w: dict, spec: dict, dev: list, host_batches: list, b: int, steps_per_sb: int) -> dict:
     """f32 vs mixed precision over 8 superbatches from the same initial weights and
-    batches.  The synthetic labels carry no signal the net can learn, and at the
-    initial weight scale the net output is ~1e-3, so the per-superbatch loss moves
-    little and f32 rounding of sigmoid(net / 290) hides most precision effects.
-    The drift is therefore also reported where it is visible: the f32 master
-    weights of every group after training, and the raw net outputs on a held-out
-    batch (the last batch of the set, never trained on)."""
-    from tatara_amd.trainer import GROUPS, LayerStackConfig, LayerStackTrainer, Sigmoid
+    batches.  The synthetic PSV scores carry nothing the net can learn (the loss
+    stays flat and the weights barely leave their initial scale, where the FT
+    table quantises to all zeros), so the batches' scores are replaced by a
+    fixed piece-square teacher (teacher_scores): the positions, features,
+    buckets, shape, optimizer and lr stay configs[4]'s.  Reported: both loss
+    curves, the exported-net integer tables (FT i16, merged L1 i8) of both runs
+    and how many of them differ, the f32 master weights' relative drift per
+    group, and the raw net outputs on a held-out batch (the last of the set,
+    never trained on), with the mixed-minus-f32 difference set against the
+    f32 run's own change from its initial outputs."""
+    from tatara_amd.trainer import GROUPS, DeviceArray, LayerStackConfig, LayerStackTrainer, Sigmoid
 
     base = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"], piece_inputs=spec["piece_inputs"],
                             ft_out=w["ft_out"], l1_out=w["l1"], l2_out=w["l2"], num_buckets=w["nb"], max_batch=b,
                             optimizer=w["optimizer"], weight_decay=0.01)
     loss = Sigmoid(1.0 / 290.0)
-    train, held = (dev[:-1], dev[-1]) if len(dev) > 1 else (dev, dev[0])
+    taught = []
+    for d, hb in zip(dev, host_batches):
+        arrays = dict(d.arrays)
+        arrays["score"] = DeviceArray(teacher_scores(hb, spec["ft_in"]))
+        taught.append(dataclasses.replace(d, arrays=arrays))
+    train, held = (taught[:-1], taught[-1]) if len(taught) > 1 else (taught, taught[0])
     curves, views, weights, nets, start, init = {}, {}, {}, {}, {}, {}
     for name, cfg in (("f32", base), ("mixed", base.all_optim())):
         with LayerStackTrainer(cfg) as t:
@@ -462,8 +489,15 @@ def drift_report(w: dict, spec: dict, dev: list, b: int, steps_per_sb: int) -> d
     rel = [abs(m - f) / f for f, m in zip(curves["f32"], curves["mixed"]) if f]
     net_d = nets["mixed"] - nets["f32"]
     net_move = nets["f32"] - start["f32"].astype(np.float64)
+    move_rms = float(np.sqrt(np.mean(net_move ** 2)))
+    drift_rms = float(np.sqrt(np.mean(net_d ** 2)))
+    ft_nz = float(np.count_nonzero(views["f32"]["ft_i16"])) / ft_diff.size
     return {
         "superbatches": 8, "steps_per_superbatch": steps_per_sb, "positions_per_superbatch": steps_per_sb * b,
+        "lr": w["lr"], "optimizer": w["optimizer"],
+        "target": "teacher scores: 60 x (sum of N(0,1) piece-square values over the side to move's active "
+                  "features - the other side's), clipped to +-3000, wdl_lambda 0 (the PSV positions, features "
+                  "and buckets of the bench; the synthetic PSV scores are noise)",
         "loss_f32": [float(f"{x:.9g}") for x in curves["f32"]],
         "loss_mixed": [float(f"{x:.9g}") for x in curves["mixed"]],
         "loss_rel_diff_max": float(f"{max(rel):.3g}"),
@@ -471,14 +505,19 @@ def drift_report(w: dict, spec: dict, dev: list, b: int, steps_per_sb: int) -> d
         "weights_rel_l2_f32_trained_vs_init": f32_move,
         "net_output_heldout": {
             "f32_rms": float(np.sqrt(np.mean(nets["f32"] ** 2))),
-            "f32_rms_change_from_init": float(np.sqrt(np.mean(net_move ** 2))),
-            "mixed_minus_f32_rms": float(np.sqrt(np.mean(net_d ** 2))),
+            "f32_rms_change_from_init": move_rms,
+            "mixed_minus_f32_rms": drift_rms,
             "mixed_minus_f32_max_abs": float(np.max(np.abs(net_d))),
+            "drift_over_f32_change": float(f"{drift_rms / move_rms:.4g}") if move_rms else None,
             "corr_of_training_change": float(np.corrcoef(net_move, nets["mixed"] - start["mixed"])[0, 1]),
         },
+        "ft_i16_nonzero_frac": ft_nz,
+        "ft_i16_nonzero_frac_mixed": float(np.count_nonzero(views["mixed"]["ft_i16"])) / ft_diff.size,
         "ft_i16_differing_frac": float(np.count_nonzero(ft_diff)) / ft_diff.size,
-        "ft_i16_nonzero_frac": float(np.count_nonzero(views["f32"]["ft_i16"])) / ft_diff.size,
+        "ft_i16_differing_frac_of_nonzero": (float(np.count_nonzero(ft_diff)) /
+                                             max(1, int(np.count_nonzero(views["f32"]["ft_i16"])))),
         "ft_i16_max_abs_diff": int(ft_diff.max()),
+        "l1_i8_nonzero_frac": float(np.count_nonzero(views["f32"]["l1_i8"])) / l1_diff.size,
         "l1_i8_differing_frac": float(np.count_nonzero(l1_diff)) / l1_diff.size,
         "l1_i8_max_abs_diff": int(l1_diff.max()),
         "dft_clamps": int(clamps), "dft_values_written": int(elems),
@@ -717,8 +756,6 @@ def main() -> int:
         # (on_device = 1): the step also queues the occurrence-list sort chain
         # (keys, radix passes, offsets), which the device flag then gates
         # off.  Alternating rounds of each, medians compared.
-        import dataclasses
-
         gated = [dataclasses.replace(d, king_blocked=False) for d in dev]
         ab = {"skipped": [], "queued": []}
         for rnd in range(args.chain_ab_rounds):
@@ -780,7 +817,7 @@ def main() -> int:
     drift = None
     if args.drift and w.get("all_optim"):
         log(f"drift: f32 vs mixed, 8 superbatches of {args.drift} steps")
-        drift = drift_report(w, spec, dev, b, args.drift)
+        drift = drift_report(w, spec, dev, host_batches, b, args.drift)
     log("phases (ms/step): " + ", ".join(f"{k} {v:.3f}" for k, v in phase_avg.items()))
 
     la = 1.0 / 6.0 if w["optimizer"] == "ranger" else 0.0
