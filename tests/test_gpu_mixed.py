@@ -151,11 +151,12 @@ def test_one_step_matches_oracle(gpu, mode, factorize, ft_out):
         assert clamps == 0
 
 
-@pytest.mark.parametrize("l1,l2,ft_out", [(32, 64, 512), (8, 16, 512), (32, 16, 256)])
+@pytest.mark.parametrize("l1,l2,ft_out", [(32, 64, 512), (8, 16, 512), (32, 16, 256), (16, 32, 640)])
 def test_all_optim_dense_shapes(gpu, l1, l2, ft_out):
     """--all-optim at l1 = 32 (two 16-output blocks in the TF32 L1 forward,
-    the f16-dft L1 input gradient with 32 weights per column) and l1 = 8:
-    one step against the oracle with the same bars as the other shapes."""
+    the f16-dft L1 input gradient with 32 weights per column), l1 = 8, and
+    ft_out 640 (the matrix-core backward's last chunk half empty): one step
+    against the oracle with the same bars as the other shapes."""
     prec = FLAGS["all_optim"]
     sh, cfg = mixed(prec, ft_out=ft_out, l1=l1, l2=l2)
     b = cfg.max_batch

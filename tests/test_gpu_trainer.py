@@ -205,6 +205,30 @@ def test_dense_shapes_match_oracle(gpu, l1, l2):
         assert t.tensor_size("l2_w") == sh.nb * l2 * 2 * (l1 - 1)
 
 
+@pytest.mark.parametrize("ft_out", [384, 640, 1152])
+def test_ft_out_multiples_of_128(gpu, ft_out):
+    """ft_out a multiple of 128 but not of 256 (the reference's --ft-out rule,
+    training.rs:497-503): the last 256-column chunk of the dft is half
+    empty (the block scan from 512 up, the occurrence lists below), and the
+    FT-post gradient takes one column per lane.  Two Ranger steps against
+    the oracle."""
+    sh, cfg = make(ft_out=ft_out)
+    b = cfg.max_batch
+    st = ols.default_init(sh)
+    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+    with LayerStackTrainer(cfg) as t:
+        for step in (1, 2):
+            batch, bucket = batch_for(50 + step, b, sh.nb)
+            t.train_step(batch, bucket, 8.75e-4, 0.25, Sigmoid())
+            _, a, g = ols.train_step(sh, st, as_dict(batch, bucket), opt, 8.75e-4, 0.25, loss_dict(Sigmoid()), step)
+            bf = b * sh.ft_out
+            assert np.array_equal(t.activation("ft_stm_out", bf), a["ft_stm"])
+            assert np.array_equal(t.activation("combined", bf), a["combined"])
+            for name in GROUPS:
+                close(t.get(name, "grad"), g[name], 1e-4, atol_frac=1e-5, what=f"step {step} grad {name}")
+                close(t.get(name, "w"), st[name]["w"], 1e-5, atol=1e-6, what=f"step {step} {name}.w")
+
+
 @pytest.mark.parametrize("l1,l2", [(24, 32), (16, 48), (4, 32), (64, 32), (16, 128)])
 def test_dense_shapes_without_kernels_are_rejected(gpu, l1, l2):
     from tatara_amd._lib import TataraError
