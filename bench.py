@@ -24,7 +24,8 @@ read once, each output written once, a gathered table counted once;
 `compulsory_bytes`).  `roofline.achieved` is the dominant FT kernel's
 compulsory bytes over its average launch time; `traffic` is the HBM bytes it
 actually moves (rocprofv3 counters, profiles/hbm_traffic.md); the logical
-rate of SURVEY's per-occurrence formula is kept as `logical_GBps`.  The run
+rate of the per-occurrence count (every gathered row once per occurrence) is
+kept as `logical_GBps`.  The run
 fails loudly if compulsory bytes / time exceed the HBM peak for the dominant
 kernel or the whole step.  The CPU baseline is the oracle step (restated
 reference CPU kernels, OpenMP) timed on bounded samples on this host: all
@@ -47,7 +48,7 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 
 # name -> workload; ref = the reference's published fp32 pos/s at b=65536 on
-# RTX 5090 (README.md:41-43)
+# RTX 5090 (the reference's README.md:41-43)
 WORKLOADS = {
     "ls1536": dict(
         metric="train pos/s @ batch 65536 (LayerStack ft-1536, 1 GPU); FT gather % HBM peak",
@@ -107,7 +108,7 @@ def log(msg: str) -> None:
 
 def logical_bytes(host_batches, ft_out, ft_in, max_active, lookahead_frac, out_rows, f16=False):
     """Per-launch logical bytes of the two FT kernels (every gathered row counted
-    once per occurrence, as SURVEY's per-position formula counts them), averaged
+    once per occurrence), averaged
     over the batches.  Rows served by L2 / Infinity Cache are counted, so this
     rate can exceed the HBM peak; it is reported beside the roofline, not as it.
 
@@ -677,7 +678,7 @@ def main() -> int:
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build targets a single MI355X "
               f"(--gpus {args.gpus} is not supported; multi-GPU sharding is a design "
-              f"note in DESIGN.md)", file=sys.stderr)
+              f"note only)", file=sys.stderr)
         return 2
 
     from tatara_amd import _lib
@@ -864,9 +865,9 @@ def main() -> int:
         "traffic": traffic,
         "avg_launch_ms": round(ms, 4),
         "compulsory_bytes_per_launch": int(byts),
-        # the HBM bytes the kernel actually moves (rocprofv3 counters) and the
-        # logical bytes of the SURVEY formula (every gathered row once per
-        # occurrence, L2 / Infinity Cache hits included)
+        # the HBM bytes the kernel actually moves (rocprofv3 counters) and its
+        # logical bytes (every gathered row once per occurrence, L2 /
+        # Infinity Cache hits included)
         "hbm_GBps": round(traffic / (ms * 1e-3) / 1e9, 1) if (traffic and ms > 0) else None,
         "traffic_over_compulsory": round(traffic / byts, 3) if traffic else None,
         "logical_GBps": round(logical / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
@@ -916,7 +917,7 @@ def main() -> int:
             "global_batch": b,
             "ft_out": w["ft_out"], "l1": w["l1"], "l2": w["l2"], "num_buckets": w["nb"],
             "n_batches_cycled": args.n_batches,
-            "vs_baseline_ref": f"RTX 5090 fp32 {w['ref'] / 1e6:.2f}M pos/s (BASELINE.md, {w['ref_src']})",
+            "vs_baseline_ref": f"RTX 5090 fp32 {w['ref'] / 1e6:.2f}M pos/s (reference {w['ref_src']})",
             "step_count_end": step_count,
         },
         "roofline": roofline,

@@ -2,7 +2,7 @@
  *
  * Compiled with the host C compiler by tests/test_abi_layout.py (no GPU, no
  * HIP): the static assertions pin the size and field offsets a foreign-language
- * binding must reproduce (the Rust #[repr(C)] structs of INTEGRATION.md, the
+ * binding must reproduce (the Rust #[repr(C)] structs of the integration guide, the
  * ctypes structs of tatara_amd/_lib.py), and main() prints every field's
  * offset and size so the test can compare those bindings field by field. */
 #include <assert.h>
