@@ -339,6 +339,313 @@ __global__ __launch_bounds__(256) void ft_forward_pair16_kernel(
         __builtin_nontemporal_store(c, reinterpret_cast<f8v*>(combined + co) + qp);
 }
 
+// The king block of rank `rank` when the blocks are ordered by descending
+// row count over both perspectives (ties: lower block first), from the
+// schedule's bins start[0 .. 2*nb] (perspective-major); up to 128 blocks,
+// two per lane.
+__device__ __forceinline__ uint32_t block_of_rank(const uint32_t* __restrict__ start, uint32_t nb, uint32_t rank,
+                                                  uint32_t lane) {
+    auto block_rows = [&](uint32_t k) -> uint32_t {
+        return k < nb ? (start[k + 1] - start[k]) + (start[nb + k + 1] - start[nb + k]) : 0u;
+    };
+    const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
+    uint32_t r0 = 0, r1 = 0;
+    for (uint32_t m = 0; m < nb; ++m) {
+        const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
+        r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
+        r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
+    }
+    const uint64_t h0 = __ballot(lane < nb && r0 == rank);
+    const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
+    return __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
+}
+
+// ---------------------------------------------------------------------------
+// Forward gather with the king block's table slice resident in LDS.
+//
+// For a king-blocked schedule every row of block K reads only rows
+// K*pi .. K*pi + pi - 1 of the table.  Workgroup (K, slice) copies those
+// rows' slice (64 bytes each: 16 f32 or 32 f16 columns) into LDS once and
+// then sums every row of the block from there, so the gather reads LDS (about
+// 100 bytes per clock per CU for these 64-byte rows) instead of issuing one
+// 16-byte vector-memory request per lane and row (64 bytes per clock per CU
+// through the texture-address unit).  A row's four lanes (quads q = 0..3)
+// each own one 16-byte quad of the slice: pairwise mode, quads 0-1 hold
+// first-half columns and quads 2-3 their partners in the second half;
+// concat mode, four consecutive quads.  Each lane sums its row's slots in
+// slot order from +0.0, as the row gather does; an empty or invalid slot
+// reads a zero row (adding +0.0 to a sum that started at +0.0 changes
+// nothing), so the sums are bit-identical to the row gather's.  The slot
+// indices are read once per row: slot 4u + q is held by lane q in register
+// u and handed to the row's other lanes by a quad permute.  A row with a
+// valid index outside its block (possible only when the caller's rows are
+// not king-blocked) is summed again by its own lanes from global memory.
+//
+// Workgroups: (block rank, slice) with blocks by descending row count, and
+// four consecutive slices (one 128-byte line of each output row) on one XCD
+// at once, so an output line is filled in one L2.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kFbThreads = 1024;
+constexpr uint32_t kFbWaves = kFbThreads / 64;
+constexpr uint32_t kFbSlots = 48;           // index slots per row read (12 per lane)
+constexpr uint32_t kFbMaxPi = 1791;         // rows of a block slice held in LDS (plus the zero row)
+constexpr uint32_t kFbQuadBytes = 16;
+
+struct FtBlockFwd {
+    const void* W;  // f32 or f16 table [cols][ft_out]
+    const int32_t* idx_stm;
+    const int32_t* idx_nstm;
+    const int32_t* nnz;
+    const int32_t* schedule;
+    const uint32_t* sched_start;
+    const uint32_t* slot_off;  // [2*batch][4 * NU] LDS byte offset of each slot
+    const uint8_t* row_bad;    // [2*batch] row has an index outside its block
+    const float* bias;
+    float* out_stm;
+    float* out_nstm;
+    _Float16* out16_stm;
+    _Float16* out16_nstm;
+    float* combined;
+    _Float16* combined16;
+    uint32_t batch, ft_out, cols, max_active, n_blocks, piece_inputs, n_slices;
+    float scale;
+};
+
+// acc + (f32) the low / high f16 half of h2, rounded once: a mixed-precision
+// FMA by 1.0 (the product is exact), one instruction where a conversion and
+// an add take two.
+__device__ __forceinline__ float add_f16_lo(uint32_t h2, float acc) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h2), "v"(acc));
+    return d;
+}
+__device__ __forceinline__ float add_f16_hi(uint32_t h2, float acc) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h2), "v"(acc));
+    return d;
+}
+
+// A quad-permute broadcast of lane `src` of every group of four lanes.
+template <int SRC>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, SRC * 0x55, 0xF, 0xF, true);
+}
+
+// NU: slot quads read per row (4 * NU >= max_active; slots past max_active
+// are empty and read the zero row).
+template <int MODE, typename T, bool HOUT, int NU>
+__global__ __launch_bounds__(kFbThreads) void ft_forward_block_kernel(FtBlockFwd a) {
+    static_assert(4 * NU <= (int)kFbSlots, "slot quads");
+    constexpr bool H16 = sizeof(T) == 2;
+    constexpr uint32_t QC = H16 ? 8 : 4;  // columns per quad
+    typedef float accv __attribute__((ext_vector_type(QC)));
+    typedef T rowv __attribute__((ext_vector_type(QC)));
+    static_assert(sizeof(rowv) == kFbQuadBytes, "a quad is 16 bytes");
+    __shared__ uint4 s_w[(kFbMaxPi + 1) * 4];  // feature f's quad q at 4f + q; row pi is zero
+
+    const uint32_t lane = threadIdx.x % 64, q = lane & 3u, r = lane >> 2;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t nb = a.n_blocks;
+    const uint32_t xcd = blockIdx.x % kNumXcd, j = blockIdx.x / kNumXcd;
+    const uint32_t n_sg = (a.n_slices + 3) / 4;
+    const uint32_t item = (j / 4) * kNumXcd + xcd;
+    if (item >= nb * n_sg) return;
+    const uint32_t slice = (item % n_sg) * 4 + j % 4;
+    if (slice >= a.n_slices) return;
+    const uint32_t K = block_of_rank(a.sched_start, nb, item / n_sg, lane);
+    const uint32_t a0 = a.sched_start[K], na = a.sched_start[K + 1] - a0;
+    const uint32_t b0 = a.sched_start[nb + K];
+    const uint32_t n = na + (a.sched_start[nb + K + 1] - b0);
+    if (n == 0) return;
+
+    // the columns of quad q in this slice
+    const uint32_t H = a.ft_out / 2;
+    auto quad_col = [&](uint32_t qq) -> uint32_t {
+        return MODE == kPair ? (qq >= 2 ? H : 0u) + slice * 2 * QC + (qq & 1u) * QC : slice * 4 * QC + qq * QC;
+    };
+    const uint32_t col = quad_col(q);
+    const T* W = reinterpret_cast<const T*>(a.W);
+    const uint32_t PI = a.piece_inputs, blk_lo = K * PI;
+    const uint32_t nfeat = a.cols > blk_lo ? (a.cols - blk_lo < PI ? a.cols - blk_lo : PI) : 0u;
+    for (uint32_t i = threadIdx.x; i < (PI + 1) * 4; i += kFbThreads) {
+        const uint32_t f = i / 4;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (f < nfeat) v = *reinterpret_cast<const uint4*>(W + (uint64_t)(blk_lo + f) * a.ft_out + quad_col(i % 4));
+        s_w[i] = v;
+    }
+
+    // bias of the lane's columns (and of their partners: quad q ^ 2)
+    accv b_own, b_par;
+    const uint32_t col_par = MODE == kPair ? quad_col(q ^ 2u) : col;
+#pragma unroll
+    for (uint32_t e = 0; e < QC; ++e) {
+        b_own[e] = a.bias[col + e];
+        b_par[e] = a.bias[col_par + e];
+    }
+    __syncthreads();
+
+    // Rows go in groups of 16 (one per four lanes), wave w taking groups w,
+    // w + 16, ...  A group's slot offsets are loaded while the wave sums the
+    // group before it, and its schedule entry a group earlier still, so the
+    // sums never wait for the chain entry -> position -> slots.  Each half
+    // iteration issues the position two groups ahead, then the eleven slot
+    // loads of the next group (unconditional, so every wait leaves at least
+    // eleven loads in flight rather than waiting for the stores).  Group rows
+    // past the block's list take its first entry and are empty.
+    const uint32_t n_groups = (n + 15) / 16;
+    const char* s_bytes = reinterpret_cast<const char*>(s_w);
+    auto entry = [&](uint32_t gg) -> uint32_t {
+        const uint32_t jr = gg * 16 + r;
+        const uint32_t e = (jr < na ? a0 : b0 - na) + jr;
+        return jr < n ? e : a0;
+    };
+    auto row_ptr = [&](uint32_t e, uint32_t pos) -> const int32_t* {
+        return (e >= a.batch ? a.idx_nstm : a.idx_stm) + (uint64_t)pos * a.max_active;
+    };
+    struct Slots {
+        uint32_t off[NU];  // slot 4u + q: its row's LDS byte offset
+        uint32_t bad;
+    };
+    auto load_slots = [&](uint32_t e, uint32_t pos, Slots& s) {
+        const uint32_t i = (e >= a.batch ? a.batch : 0u) + pos;
+        const uint32_t* so = a.slot_off + (uint64_t)i * (4 * NU) + q;
+        s.bad = a.row_bad[i];
+#pragma unroll
+        for (uint32_t u = 0; u < (uint32_t)NU; ++u) s.off[u] = so[4 * u];
+    };
+    // One group: sums of group gg from its slots s_c (position pos).
+    auto group = [&](uint32_t gg, const Slots& s_c, uint32_t pos) {
+        const bool live = gg * 16 + r < n;
+        const uint32_t e_c = entry(gg);
+        const uint32_t persp = e_c >= a.batch ? 1u : 0u;
+        // slot 4u + q: its row's byte offset in LDS (the zero row for an
+        // empty or invalid slot, and for slots past max_active)
+        const uint32_t* off = s_c.off;
+        const bool bad = live && s_c.bad != 0;
+        accv acc = 0.0f;
+#define TATARA_FB_SLOT(U, SRC)                                                           \
+    {                                                                                    \
+        const uint32_t o = quad_bcast<SRC>(off[U]) + q * kFbQuadBytes;                   \
+        if constexpr (H16) {                                                             \
+            const uint4 w = *reinterpret_cast<const uint4*>(s_bytes + o);                \
+            acc[0] = add_f16_lo(w.x, acc[0]);                                            \
+            acc[1] = add_f16_hi(w.x, acc[1]);                                            \
+            acc[2] = add_f16_lo(w.y, acc[2]);                                            \
+            acc[3] = add_f16_hi(w.y, acc[3]);                                            \
+            acc[4] = add_f16_lo(w.z, acc[4]);                                            \
+            acc[5] = add_f16_hi(w.z, acc[5]);                                            \
+            acc[6] = add_f16_lo(w.w, acc[6]);                                            \
+            acc[7] = add_f16_hi(w.w, acc[7]);                                            \
+        } else {                                                                         \
+            acc += *reinterpret_cast<const rowv*>(s_bytes + o);                          \
+        }                                                                                \
+    }
+#pragma unroll
+        for (uint32_t u = 0; u < (uint32_t)NU; ++u) {
+            TATARA_FB_SLOT(u, 0)
+            TATARA_FB_SLOT(u, 1)
+            TATARA_FB_SLOT(u, 2)
+            TATARA_FB_SLOT(u, 3)
+        }
+#undef TATARA_FB_SLOT
+        // a row with an index outside its block: its lanes sum it again from
+        // global memory, valid slots in slot order
+        const uint64_t bad_lanes = __ballot(bad);
+        if (bad_lanes) {
+            if ((bad_lanes >> (4 * r)) & 0xFull) {
+                const int32_t* idx = row_ptr(e_c, pos);
+                const int32_t nz = a.nnz[pos];
+                const uint32_t nv = nz <= 0 ? 0u : ((uint32_t)nz < a.max_active ? (uint32_t)nz : a.max_active);
+                acc = 0.0f;
+                for (uint32_t k = 0; k < nv; ++k) {
+                    const int32_t v = idx[k];
+                    if (v < 0 || (uint32_t)v >= a.cols) continue;
+                    acc += __builtin_convertvector(*reinterpret_cast<const rowv*>(W + (uint64_t)v * a.ft_out + col),
+                                                   accv);
+                }
+            }
+        }
+
+        if (MODE == kPair) {
+            rowv r16;
+            if (HOUT) {
+                r16 = __builtin_convertvector(acc, rowv);
+                acc = __builtin_convertvector(r16, accv);
+            }
+            // the partner columns' sums, from lane q ^ 2 of the row (each
+            // element copied to a scalar first: a bit cast of a vector
+            // element reads element 0)
+            accv p;
+#pragma unroll
+            for (uint32_t e2 = 0; e2 < QC; ++e2) {
+                const float x = acc[e2];
+                p[e2] = __int_as_float(
+                    __builtin_amdgcn_mov_dpp(__float_as_int(x), 2 | 3 << 2 | 0 << 4 | 1 << 6, 0xF, 0xF, true));
+            }
+            if (live) {
+                // plain stores: four workgroups fill each 128-byte line, which
+                // L2 assembles before it writes the line back
+                if (HOUT) {
+                    _Float16* o = persp ? a.out16_nstm : a.out16_stm;
+                    *reinterpret_cast<rowv*>(o + (uint64_t)pos * a.ft_out + col) = r16;
+                } else {
+                    float* o = persp ? a.out_nstm : a.out_stm;
+                    *reinterpret_cast<accv*>(o + (uint64_t)pos * a.ft_out + col) = acc;
+                }
+                if (q < 2) {
+                    accv c;
+#pragma unroll
+                    for (uint32_t e2 = 0; e2 < QC; ++e2)
+                        c[e2] = crelu01(acc[e2] + b_own[e2]) * crelu01(p[e2] + b_par[e2]) * a.scale;
+                    const uint64_t co = (uint64_t)pos * a.ft_out + persp * H + col;
+                    if (a.combined16) {
+                        typedef _Float16 hv __attribute__((ext_vector_type(QC)));
+                        *reinterpret_cast<hv*>(a.combined16 + co) = __builtin_convertvector(c, hv);
+                    } else {
+                        *reinterpret_cast<accv*>(a.combined + co) = c;
+                    }
+                }
+            }
+        } else if (live) {
+            // Simple: ft_out += bias in place, combined[off + c] = crelu(x)
+            const accv x = acc + b_own;
+            float* o = persp ? a.out_nstm : a.out_stm;
+            *reinterpret_cast<accv*>(o + (uint64_t)pos * a.ft_out + col) = x;
+            accv c;
+#pragma unroll
+            for (uint32_t e2 = 0; e2 < QC; ++e2) c[e2] = crelu01(x[e2]);
+            *reinterpret_cast<accv*>(a.combined + (uint64_t)pos * 2 * a.ft_out + persp * a.ft_out + col) = c;
+        }
+    };
+    // Two register sets: set X sums group g while set Y's slots (group
+    // g + 16) are loaded; X's position register is reloaded with group
+    // g + 32's first (its old value copied once its load is long done).
+    uint32_t g = wave;
+    if (g >= n_groups) return;
+    uint32_t pA = (uint32_t)a.schedule[entry(g)];
+    uint32_t pB = (uint32_t)a.schedule[entry(g + kFbWaves)];
+    __builtin_amdgcn_sched_barrier(0);
+    Slots sA, sB;
+    load_slots(entry(g), pA, sA);
+    auto half = [&](uint32_t gg, Slots& sx, uint32_t& px, Slots& sy, const uint32_t& py) {
+        const uint32_t pos = px;
+        px = (uint32_t)a.schedule[entry(gg + 2 * kFbWaves)];
+        __builtin_amdgcn_sched_barrier(0);
+        load_slots(entry(gg + kFbWaves), py, sy);
+        __builtin_amdgcn_sched_barrier(0);
+        group(gg, sx, pos);
+    };
+    for (;;) {
+        half(g, sA, pA, sB, pB);
+        g += kFbWaves;
+        if (g >= n_groups) break;
+        half(g, sB, pB, sA, pA);
+        g += kFbWaves;
+        if (g >= n_groups) break;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Forward schedule keys: item p*batch + b gets key p*n_bins + (king block of
 // position b in perspective p), where the king block is the first valid
@@ -367,6 +674,43 @@ __global__ void king_block_keys_kernel(const int32_t* __restrict__ idx_stm,
         }
     }
     keys[i] = (uint8_t)(persp * n_bins + k);
+}
+
+// The same keys (one wave per row, lane = slot) and, for the block-resident
+// forward, every slot's LDS byte offset in rows of `stride` >= max_active
+// slots: (v - k * pi) * 64 for a valid index v of the row's block k, pi * 64
+// (the zero row) for an empty or invalid slot, an index outside the block
+// and the padding past max_active; row_bad[i] = 1 when the row has a valid
+// index outside its block.
+__global__ void king_block_rows_kernel(const int32_t* __restrict__ idx_stm, const int32_t* __restrict__ idx_nstm,
+                                       const int32_t* __restrict__ nnz, uint8_t* __restrict__ keys,
+                                       uint32_t* __restrict__ slot_off, uint8_t* __restrict__ row_bad,
+                                       uint32_t batch, uint32_t max_active, uint32_t stride, uint32_t cols,
+                                       uint32_t piece_inputs, uint32_t n_bins) {
+    const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    if (i >= 2ull * batch) return;
+    const uint32_t persp = i >= batch ? 1u : 0u;
+    const uint32_t b = (uint32_t)(i - (uint64_t)persp * batch);
+    const int32_t nz = nnz[b];
+    const uint32_t n = nz <= 0 ? 0u : ((uint32_t)nz < max_active ? (uint32_t)nz : max_active);
+    const int32_t v = lane < n ? ((persp ? idx_nstm : idx_stm) + (uint64_t)b * max_active)[lane] : -1;
+    const bool valid = v >= 0 && (uint32_t)v < cols;
+    const uint64_t vm = __ballot(valid);
+    uint32_t k = 0;
+    if (vm) {
+        const uint32_t v0 = (uint32_t)__builtin_amdgcn_readlane(v, (int)__builtin_ctzll(vm));
+        k = piece_inputs ? v0 / piece_inputs : 0u;
+        if (k >= n_bins) k = n_bins - 1;
+    }
+    const uint32_t local = (uint32_t)v - k * piece_inputs;
+    const bool in_block = valid && local < piece_inputs;
+    if (lane < stride) slot_off[i * stride + lane] = (in_block ? local : piece_inputs) * 64u;
+    const uint64_t bad = __ballot(valid && !in_block);
+    if (lane == 0) {
+        keys[i] = (uint8_t)(persp * n_bins + k);
+        row_bad[i] = bad ? 1u : 0u;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -786,24 +1130,8 @@ __host__ __device__ inline ScanGeom scan_geom(uint32_t piece_inputs) {
     return g;
 }
 
-// The king block of rank `rank` when the blocks are ordered by descending
-// row count (ties: lower block first); up to 128 blocks, two per lane.
 __device__ __forceinline__ uint32_t block_of_rank(const FtBlockScan& s, uint32_t rank, uint32_t lane) {
-    const uint32_t nb = s.n_blocks;
-    auto block_rows = [&](uint32_t k) -> uint32_t {
-        return k < nb ? (s.sched_start[k + 1] - s.sched_start[k]) + (s.sched_start[nb + k + 1] - s.sched_start[nb + k])
-                      : 0u;
-    };
-    const uint32_t z0 = block_rows(lane), z1 = block_rows(lane + 64);
-    uint32_t r0 = 0, r1 = 0;
-    for (uint32_t m = 0; m < nb; ++m) {
-        const uint32_t zm = m < 64 ? __builtin_amdgcn_readlane(z0, m) : __builtin_amdgcn_readlane(z1, m - 64);
-        r0 += (zm > z0 || (zm == z0 && m < lane)) ? 1u : 0u;
-        r1 += (zm > z1 || (zm == z1 && m < lane + 64)) ? 1u : 0u;
-    }
-    const uint64_t h0 = __ballot(lane < nb && r0 == rank);
-    const uint64_t h1 = __ballot(lane + 64 < nb && r1 == rank);
-    return __builtin_amdgcn_readfirstlane(h0 ? (uint32_t)__builtin_ctzll(h0) : 64u + (uint32_t)__builtin_ctzll(h1));
+    return block_of_rank(s.sched_start, s.n_blocks, rank, lane);
 }
 
 // The first stage of block K in the stage tables: the blocks before it
@@ -1510,6 +1838,15 @@ __global__ void lerp_kernel(float* __restrict__ w, float* __restrict__ slow, uin
 // host launchers
 // ---------------------------------------------------------------------------
 
+uint32_t ft_block_slot_stride(uint32_t max_active) { return max_active <= 40 ? 40u : 48u; }
+
+bool ft_forward_block_ok(int mode, bool f16_table, uint32_t ft_out, uint32_t piece_inputs, uint32_t max_active) {
+    if (piece_inputs == 0 || piece_inputs > kFbMaxPi || max_active > kFbSlots) return false;
+    if (mode == kPair) return ft_out % (f16_table ? 32u : 16u) == 0;
+    if (mode == kConcat) return !f16_table && ft_out % 16 == 0;
+    return false;
+}
+
 int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.max_active <= (uint32_t)kMaxActive, "max_active must be <= 64");
     TATARA_REQUIRE(a.ft_out % 8 == 0, "ft_out must be a multiple of 8");
@@ -1518,6 +1855,53 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(!h_out || (a.mode == kPair && a.W16), "f16 raw sums need the pairwise mode and an f16 table");
     TATARA_REQUIRE(!a.W16 || a.mode == kPair, "an f16 table is read by the pairwise mode only");
     if (a.batch == 0) return kOk;
+    if (a.sched_start && a.schedule && a.slot_off && a.row_bad && a.n_persp == 2 && a.n_blocks >= 1 &&
+        a.n_blocks <= 128 &&
+        ft_forward_block_ok(a.mode, a.W16 != nullptr, a.ft_out, a.piece_inputs, a.max_active)) {
+        FtBlockFwd f{};
+        f.W = a.W16 ? static_cast<const void*>(a.W16) : static_cast<const void*>(a.W);
+        f.idx_stm = a.idx_stm;
+        f.idx_nstm = a.idx_nstm;
+        f.nnz = a.nnz;
+        f.schedule = a.schedule;
+        f.sched_start = a.sched_start;
+        f.slot_off = a.slot_off;
+        f.row_bad = a.row_bad;
+        f.bias = a.bias;
+        f.out_stm = a.out_stm;
+        f.out_nstm = a.out_nstm;
+        f.out16_stm = reinterpret_cast<_Float16*>(a.out_stm16);
+        f.out16_nstm = reinterpret_cast<_Float16*>(a.out_nstm16);
+        f.combined = a.combined;
+        f.combined16 = reinterpret_cast<_Float16*>(a.combined16);
+        f.batch = a.batch;
+        f.ft_out = a.ft_out;
+        f.cols = a.cols;
+        f.max_active = a.max_active;
+        f.n_blocks = a.n_blocks;
+        f.piece_inputs = a.piece_inputs;
+        f.n_slices = a.ft_out / (a.W16 ? 32u : 16u);
+        f.scale = a.scale;
+        const uint32_t items = a.n_blocks * ((f.n_slices + 3) / 4);
+        const uint32_t grid = ceil_div(items, kNumXcd) * kNumXcd * 4;
+#define TATARA_FB(NU)                                                                         \
+    if (a.mode == kConcat)                                                                    \
+        ft_forward_block_kernel<kConcat, float, false, NU><<<grid, kFbThreads, 0, stream>>>(f);  \
+    else if (!a.W16)                                                                          \
+        ft_forward_block_kernel<kPair, float, false, NU><<<grid, kFbThreads, 0, stream>>>(f);    \
+    else if (h_out)                                                                           \
+        ft_forward_block_kernel<kPair, _Float16, true, NU><<<grid, kFbThreads, 0, stream>>>(f);  \
+    else                                                                                      \
+        ft_forward_block_kernel<kPair, _Float16, false, NU><<<grid, kFbThreads, 0, stream>>>(f);
+        if (a.max_active <= 40) {
+            TATARA_FB(10)
+        } else {
+            TATARA_FB(12)
+        }
+#undef TATARA_FB
+        TATARA_LAUNCHED("ft_forward_block");
+        return kOk;
+    }
     const uint32_t n_chunks = a.mode == kPair ? ceil_div(a.ft_out / 8, 32) : ceil_div(a.ft_out / 4, kWave);
     const uint64_t tasks = (uint64_t)a.n_persp * n_chunks * a.batch;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
@@ -1567,11 +1951,19 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
 int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm,
                                const int32_t* nnz, uint8_t* keys, uint32_t batch,
                                uint32_t max_active, uint32_t cols, uint32_t piece_inputs,
-                               uint32_t n_bins, hipStream_t stream) {
+                               uint32_t n_bins, hipStream_t stream, uint32_t* slot_off, uint8_t* row_bad) {
     if (batch == 0) return kOk;
     TATARA_REQUIRE(2 * n_bins <= 256, "king block keys: 2*n_bins <= 256");
-    king_block_keys_kernel<<<ceil_div(2ull * batch, 256), 256, 0, stream>>>(
-        idx_stm, idx_nstm, nnz, keys, batch, max_active, cols, piece_inputs, n_bins);
+    TATARA_REQUIRE((slot_off == nullptr) == (row_bad == nullptr), "slot offsets and row flags go together");
+    if (slot_off) {
+        TATARA_REQUIRE(max_active <= 64, "king block rows: max_active <= 64");
+        king_block_rows_kernel<<<ceil_div(2ull * batch, 4), 256, 0, stream>>>(
+            idx_stm, idx_nstm, nnz, keys, slot_off, row_bad, batch, max_active, ft_block_slot_stride(max_active),
+            cols, piece_inputs, n_bins);
+    } else {
+        king_block_keys_kernel<<<ceil_div(2ull * batch, 256), 256, 0, stream>>>(
+            idx_stm, idx_nstm, nnz, keys, batch, max_active, cols, piece_inputs, n_bins);
+    }
     TATARA_LAUNCHED("king_block_keys");
     return kOk;
 }

@@ -31,7 +31,25 @@ struct FtForwardArgs {
     uint16_t* combined16;  // pairwise mode: `combined` rounded to f16, written instead when non-null
     uint32_t batch, ft_out, cols, max_active, n_persp;
     float scale;
+    // Optional king-block statement of the schedule: bins [2*n_blocks + 1]
+    // (perspective-major, as FtBlockScan::sched_start) and the block width.
+    // When set (and the shape fits), the gather holds each block's table
+    // slice in LDS (ft_forward_block_kernel) instead of reading rows through
+    // the vector memory path.
+    const uint32_t* sched_start;
+    uint32_t n_blocks, piece_inputs;
+    // ... with the per-slot LDS offsets and out-of-block row flags of
+    // launch_king_block_keys (both required for the LDS-resident gather)
+    const uint32_t* slot_off;
+    const uint8_t* row_bad;
 };
+
+// Whether the LDS-resident forward serves this shape (mode, table type,
+// ft_out, piece_inputs, max_active); otherwise the row gather runs.
+bool ft_forward_block_ok(int mode, bool f16_table, uint32_t ft_out, uint32_t piece_inputs, uint32_t max_active);
+// Slots per row of FtForwardArgs::slot_off (max_active rounded up to 40 or 48;
+// the padding holds the zero row's offset).
+uint32_t ft_block_slot_stride(uint32_t max_active);
 
 struct OccurrenceSortArgs {
     const int32_t* idx_stm;
@@ -103,9 +121,13 @@ constexpr uint32_t kDftChunk = 256;
 
 
 int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream);
+// Schedule keys; with slot_off [2*batch*ft_block_slot_stride(max_active)] and row_bad [2*batch]
+// also the block-resident forward's LDS slot offsets and out-of-block row
+// flags (FtForwardArgs::slot_off, row_bad).
 int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm, const int32_t* nnz,
                                uint8_t* keys, uint32_t batch, uint32_t max_active, uint32_t cols,
-                               uint32_t piece_inputs, uint32_t n_bins, hipStream_t stream);
+                               uint32_t piece_inputs, uint32_t n_bins, hipStream_t stream,
+                               uint32_t* slot_off = nullptr, uint8_t* row_bad = nullptr);
 uint32_t occurrence_key_bits(uint32_t cols);
 size_t occurrence_sort_temp_bytes(uint64_t n_items, uint32_t cols);
 int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream);

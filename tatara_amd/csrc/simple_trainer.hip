@@ -50,6 +50,8 @@ class SimpleTrainer final : public TrainerBase {
     // gather schedule
     uint32_t n_king_bins = 1;
     uint8_t* sched_keys = nullptr;
+    uint32_t* fb_off = nullptr;  // LDS slot offsets of the block-resident gather, or null
+    uint8_t* fb_bad = nullptr;
     int32_t* schedule = nullptr;
     uint32_t *sched_hist = nullptr, *sched_start = nullptr, *sched_count = nullptr;
     // occurrence sort
@@ -151,6 +153,11 @@ class SimpleTrainer final : public TrainerBase {
             (st = arena.alloc(&sched_start, 2 * n_king_bins + 1)) ||
             (st = arena.alloc(&sched_count, 2 * n_king_bins)))
             return st;
+        if (factorized && n_king_bins == ceil_div(ft_in, pi) &&
+            ft_forward_block_ok(2, false, ft_out, pi, max_active)) {
+            if ((st = arena.alloc(&fb_off, 2 * B * ft_block_slot_stride(max_active), false)) || (st = arena.alloc(&fb_bad, 2 * B, false)))
+                return st;
+        }
         const uint64_t n_items = 2 * B * max_active;
         occ_tmp_bytes = occurrence_sort_temp_bytes(n_items, ft_in);
         if ((st = arena.alloc(&occ_ki, n_items, false)) || (st = arena.alloc(&occ_vi, n_items, false)) ||
@@ -356,7 +363,7 @@ class SimpleTrainer final : public TrainerBase {
         const int32_t* sched = nullptr;
         if (factorized) {
             if ((st = launch_king_block_keys(p.stm, p.nstm, p.nnz, sched_keys, b, max_active, ft_in, pi,
-                                             n_king_bins, stream)))
+                                             n_king_bins, stream, fb_off, fb_bad)))
                 return st;
             BinSortArgs bs{};
             bs.keys = sched_keys;
@@ -390,6 +397,14 @@ class SimpleTrainer final : public TrainerBase {
         fa.idx_nstm = p.nstm;
         fa.nnz = p.nnz;
         fa.schedule = sched;
+        if (sched && fb_off) {
+            // the schedule's bins: the gather holds each king block's slice in LDS
+            fa.sched_start = sched_start;
+            fa.n_blocks = n_king_bins;
+            fa.piece_inputs = pi;
+            fa.slot_off = fb_off;
+            fa.row_bad = fb_bad;
+        }
         fa.bias = small[0].w;
         fa.out_stm = ft_stm;
         fa.out_nstm = ft_nstm;

@@ -132,7 +132,13 @@ def test_rows_across_king_blocks_and_repeated_features(gpu):
     with LayerStackTrainer(cfg) as t:
         for step, (bt, bk) in enumerate([(mixed, bucket), batch_for(3, b, sh.nb)], start=1):
             t.train_step(bt, bk, 1e-3, 0.0, Sigmoid())
-            ols.train_step(sh, st, as_dict(bt, bk), opt, 1e-3, 0.0, loss_dict(Sigmoid()), step)
+            _, a, _ = ols.train_step(sh, st, as_dict(bt, bk), opt, 1e-3, 0.0, loss_dict(Sigmoid()), step)
+            # the forward's rows with a feature outside their king block are
+            # summed from global memory: still bit-exact
+            bf = b * sh.ft_out
+            assert np.array_equal(t.activation("ft_stm_out", bf), a["ft_stm"]), step
+            assert np.array_equal(t.activation("ft_nstm_out", bf), a["ft_nstm"]), step
+            assert np.array_equal(t.activation("combined", bf), a["combined"]), step
             for name in ("ft_w", "ft_b"):
                 for k in ("w", "m", "v"):
                     close(t.get(name, k), st[name][k], 1e-5, atol=1e-6 if k == "w" else 0.0,
