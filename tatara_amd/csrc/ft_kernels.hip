@@ -524,31 +524,42 @@ __global__ __launch_bounds__(kFbThreads) void ft_forward_block_kernel(FtBlockFwd
         const uint32_t* off = s_c.off;
         const bool bad = live && s_c.bad != 0;
         accv acc = 0.0f;
-#define TATARA_FB_SLOT(U, SRC)                                                           \
-    {                                                                                    \
-        const uint32_t o = quad_bcast<SRC>(off[U]) + q * kFbQuadBytes;                   \
-        if constexpr (H16) {                                                             \
-            const uint4 w = *reinterpret_cast<const uint4*>(s_bytes + o);                \
-            acc[0] = add_f16_lo(w.x, acc[0]);                                            \
-            acc[1] = add_f16_hi(w.x, acc[1]);                                            \
-            acc[2] = add_f16_lo(w.y, acc[2]);                                            \
-            acc[3] = add_f16_hi(w.y, acc[3]);                                            \
-            acc[4] = add_f16_lo(w.z, acc[4]);                                            \
-            acc[5] = add_f16_hi(w.z, acc[5]);                                            \
-            acc[6] = add_f16_lo(w.w, acc[6]);                                            \
-            acc[7] = add_f16_hi(w.w, acc[7]);                                            \
-        } else {                                                                         \
-            acc += *reinterpret_cast<const rowv*>(s_bytes + o);                          \
-        }                                                                                \
-    }
+        // Slots four at a time: the four reads of slot quad u + 1 are issued
+        // before the adds of quad u, so eight reads can be in flight.
+        auto read4 = [&](uint32_t u, uint4 (&d)[4]) {
+            d[0] = *reinterpret_cast<const uint4*>(s_bytes + quad_bcast<0>(off[u]) + q * kFbQuadBytes);
+            d[1] = *reinterpret_cast<const uint4*>(s_bytes + quad_bcast<1>(off[u]) + q * kFbQuadBytes);
+            d[2] = *reinterpret_cast<const uint4*>(s_bytes + quad_bcast<2>(off[u]) + q * kFbQuadBytes);
+            d[3] = *reinterpret_cast<const uint4*>(s_bytes + quad_bcast<3>(off[u]) + q * kFbQuadBytes);
+        };
+        auto add4 = [&](const uint4 (&d)[4]) {
 #pragma unroll
-        for (uint32_t u = 0; u < (uint32_t)NU; ++u) {
-            TATARA_FB_SLOT(u, 0)
-            TATARA_FB_SLOT(u, 1)
-            TATARA_FB_SLOT(u, 2)
-            TATARA_FB_SLOT(u, 3)
+            for (int s = 0; s < 4; ++s) {
+                if constexpr (H16) {
+                    acc[0] = add_f16_lo(d[s].x, acc[0]);
+                    acc[1] = add_f16_hi(d[s].x, acc[1]);
+                    acc[2] = add_f16_lo(d[s].y, acc[2]);
+                    acc[3] = add_f16_hi(d[s].y, acc[3]);
+                    acc[4] = add_f16_lo(d[s].z, acc[4]);
+                    acc[5] = add_f16_hi(d[s].z, acc[5]);
+                    acc[6] = add_f16_lo(d[s].w, acc[6]);
+                    acc[7] = add_f16_hi(d[s].w, acc[7]);
+                } else {
+                    acc += __builtin_bit_cast(accv, d[s]);
+                }
+            }
+        };
+        uint4 w0[4], w1[4];
+        read4(0, w0);
+#pragma unroll
+        for (uint32_t u = 0; u < (uint32_t)NU; u += 2) {
+            if (u + 1 < (uint32_t)NU) read4(u + 1, w1);
+            add4(w0);
+            if (u + 1 < (uint32_t)NU) {
+                if (u + 2 < (uint32_t)NU) read4(u + 2, w0);
+                add4(w1);
+            }
         }
-#undef TATARA_FB_SLOT
         // a row with an index outside its block: its lanes sum it again from
         // global memory, valid slots in slot order
         const uint64_t bad_lanes = __ballot(bad);
