@@ -687,40 +687,46 @@ __global__ void king_block_keys_kernel(const int32_t* __restrict__ idx_stm,
     keys[i] = (uint8_t)(persp * n_bins + k);
 }
 
-// The same keys (one wave per row, lane = slot) and, for the block-resident
+// The same keys (a wave per kKeyRowsPerWave rows, lane = slot) and, for the block-resident
 // forward, every slot's LDS byte offset in rows of `stride` >= max_active
 // slots: (v - k * pi) * 64 for a valid index v of the row's block k, pi * 64
 // (the zero row) for an empty or invalid slot, an index outside the block
 // and the padding past max_active; row_bad[i] = 1 when the row has a valid
 // index outside its block.
+constexpr uint32_t kKeyRowsPerWave = 8;
+
 __global__ void king_block_rows_kernel(const int32_t* __restrict__ idx_stm, const int32_t* __restrict__ idx_nstm,
                                        const int32_t* __restrict__ nnz, uint8_t* __restrict__ keys,
                                        uint32_t* __restrict__ slot_off, uint8_t* __restrict__ row_bad,
                                        uint32_t batch, uint32_t max_active, uint32_t stride, uint32_t cols,
                                        uint32_t piece_inputs, uint32_t n_bins) {
-    const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
+    const uint64_t w = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
     const uint32_t lane = threadIdx.x % 64;
-    if (i >= 2ull * batch) return;
-    const uint32_t persp = i >= batch ? 1u : 0u;
-    const uint32_t b = (uint32_t)(i - (uint64_t)persp * batch);
-    const int32_t nz = nnz[b];
-    const uint32_t n = nz <= 0 ? 0u : ((uint32_t)nz < max_active ? (uint32_t)nz : max_active);
-    const int32_t v = lane < n ? ((persp ? idx_nstm : idx_stm) + (uint64_t)b * max_active)[lane] : -1;
-    const bool valid = v >= 0 && (uint32_t)v < cols;
-    const uint64_t vm = __ballot(valid);
-    uint32_t k = 0;
-    if (vm) {
-        const uint32_t v0 = (uint32_t)__builtin_amdgcn_readlane(v, (int)__builtin_ctzll(vm));
-        k = piece_inputs ? v0 / piece_inputs : 0u;
-        if (k >= n_bins) k = n_bins - 1;
-    }
-    const uint32_t local = (uint32_t)v - k * piece_inputs;
-    const bool in_block = valid && local < piece_inputs;
-    if (lane < stride) slot_off[i * stride + lane] = (in_block ? local : piece_inputs) * 64u;
-    const uint64_t bad = __ballot(valid && !in_block);
-    if (lane == 0) {
-        keys[i] = (uint8_t)(persp * n_bins + k);
-        row_bad[i] = bad ? 1u : 0u;
+#pragma unroll
+    for (uint32_t rr = 0; rr < kKeyRowsPerWave; ++rr) {
+        const uint64_t i = w * kKeyRowsPerWave + rr;
+        if (i >= 2ull * batch) return;
+        const uint32_t persp = i >= batch ? 1u : 0u;
+        const uint32_t b = (uint32_t)(i - (uint64_t)persp * batch);
+        const int32_t nz = nnz[b];
+        const uint32_t n = nz <= 0 ? 0u : ((uint32_t)nz < max_active ? (uint32_t)nz : max_active);
+        const int32_t v = lane < n ? ((persp ? idx_nstm : idx_stm) + (uint64_t)b * max_active)[lane] : -1;
+        const bool valid = v >= 0 && (uint32_t)v < cols;
+        const uint64_t vm = __ballot(valid);
+        uint32_t k = 0;
+        if (vm) {
+            const uint32_t v0 = (uint32_t)__builtin_amdgcn_readlane(v, (int)__builtin_ctzll(vm));
+            k = piece_inputs ? v0 / piece_inputs : 0u;
+            if (k >= n_bins) k = n_bins - 1;
+        }
+        const uint32_t local = (uint32_t)v - k * piece_inputs;
+        const bool in_block = valid && local < piece_inputs;
+        if (lane < stride) slot_off[i * stride + lane] = (in_block ? local : piece_inputs) * 64u;
+        const uint64_t bad = __ballot(valid && !in_block);
+        if (lane == 0) {
+            keys[i] = (uint8_t)(persp * n_bins + k);
+            row_bad[i] = bad ? 1u : 0u;
+        }
     }
 }
 
@@ -1968,7 +1974,7 @@ int32_t launch_king_block_keys(const int32_t* idx_stm, const int32_t* idx_nstm,
     TATARA_REQUIRE((slot_off == nullptr) == (row_bad == nullptr), "slot offsets and row flags go together");
     if (slot_off) {
         TATARA_REQUIRE(max_active <= 64, "king block rows: max_active <= 64");
-        king_block_rows_kernel<<<ceil_div(2ull * batch, 4), 256, 0, stream>>>(
+        king_block_rows_kernel<<<ceil_div(2ull * batch, 4 * kKeyRowsPerWave), 256, 0, stream>>>(
             idx_stm, idx_nstm, nnz, keys, slot_off, row_bad, batch, max_active, ft_block_slot_stride(max_active),
             cols, piece_inputs, n_bins);
     } else {
