@@ -315,3 +315,32 @@ def test_king_blocked_batches(gpu):
         with pytest.raises(_lib.TataraError) as ei:
             t.flush_pending_loss()
         assert ei.value.status == -4
+
+
+@pytest.mark.parametrize("ma", [44, 38], ids=["max_active_44", "max_active_38"])
+def test_forward_slot_padding_and_rows_across_blocks(gpu, ma):
+    """The block-resident concat forward with rows padded to 48 slots
+    (max_active 44) and to 40 (38), including a row with a feature outside
+    its king block (summed again from global memory): bit-exact, and the
+    post-step FT weights within tolerance."""
+    from tatara_amd.trainer import Batch
+    spec = small_spec(king_buckets=10, piece_inputs=64, max_active=ma)
+    sh = osi.SimpleShape(ft_in=spec["ft_in"], max_active=ma, piece_inputs=64, ft_out=128, l1=32, l2=32)
+    cfg = SimpleConfig(ft_in=sh.ft_in, max_active=ma, piece_inputs=64, ft_out=128, l1_out=32, l2_out=32,
+                       max_batch=256, optimizer="adamw", weight_decay=0.01, keep_grads=True)
+    batch, _ = structured_batch(256, spec, num_buckets=1, seed=41, nnz_min=ma - 10)
+    stm = batch.stm_indices.copy()
+    stm[9, 1] = (int(stm[9, 0]) // 64 + 1) % 10 * 64 + 5  # a feature of another block
+    batch = Batch(stm, batch.nstm_indices, batch.nnz, batch.score, batch.wdl)
+    st = osi.default_init(sh)
+    opt = osi.OptConfig(optimizer="adamw", weight_decay=0.01)
+    with SimpleTrainer(cfg) as t:
+        t.train_step(batch, 1e-3, 0.0, WRM290)
+        _, a, _ = osi.train_step(sh, st, as_dict(batch), opt, 1e-3, 0.0, loss_dict(WRM290), 1)
+        bf = 256 * sh.ft_out
+        assert np.array_equal(t.activation("ft_stm_out", bf), a["ft_stm"])
+        assert np.array_equal(t.activation("ft_nstm_out", bf), a["ft_nstm"])
+        assert np.array_equal(t.activation("combined", 2 * bf), a["combined"])
+        for k in ("w", "m", "v"):
+            close(t.get("ft_w", k), st["ft_w"][k], 1e-5, atol=1e-6 if k == "w" else 0.0,
+                  atol_frac=1e-5 if k != "w" else 0.0, what=f"ft_w.{k}")

@@ -381,3 +381,29 @@ def test_king_blocked_batch_that_is_not_is_reported(gpu):
         t.train_step(good, None, 1e-3, 0.0, Sigmoid())
         assert np.isfinite(t.flush_pending_loss())
         assert not np.array_equal(t.get("ft_w"), w0)
+
+
+@pytest.mark.parametrize("kb,pi,ma", [(10, 64, 44), (2, 1791, 40), (2, 1800, 40)],
+                         ids=["max_active_44", "pi_1791", "pi_1800_row_gather"])
+def test_forward_table_shapes(gpu, kb, pi, ma):
+    """The block-resident forward at its shape limits: max_active above 40
+    (twelve slot quads per row, rows padded to 48 slots), the largest king
+    block it holds in LDS (1791 rows), and one row more (the row gather runs
+    instead).  Forward bit-exact, post-step FT weights within tolerance."""
+    spec = small_spec(king_buckets=kb, piece_inputs=pi, max_active=ma)
+    sh = ols.LsShape(ft_in=spec["ft_in"], max_active=ma, piece_inputs=pi, ft_out=256, l1=16, l2=32, nb=8)
+    cfg = LayerStackConfig(ft_in=sh.ft_in, max_active=ma, piece_inputs=pi, ft_out=256, l1_out=16, l2_out=32,
+                           num_buckets=8, max_batch=256, optimizer="ranger", keep_grads=True)
+    batch, bucket = structured_batch(256, spec, num_buckets=8, seed=31, nnz_min=ma - 10)
+    st = ols.default_init(sh)
+    opt = ols.OptConfig(optimizer="ranger", weight_decay=0.01)
+    with LayerStackTrainer(cfg) as t:
+        t.train_step(batch, bucket, 1e-3, 0.0, Sigmoid())
+        _, a, _ = ols.train_step(sh, st, as_dict(batch, bucket), opt, 1e-3, 0.0, loss_dict(Sigmoid()), 1)
+        bf = 256 * 256
+        assert np.array_equal(t.activation("ft_stm_out", bf), a["ft_stm"])
+        assert np.array_equal(t.activation("ft_nstm_out", bf), a["ft_nstm"])
+        assert np.array_equal(t.activation("combined", bf), a["combined"])
+        for k in ("w", "m", "v"):
+            close(t.get("ft_w", k), st["ft_w"][k], 1e-5, atol=1e-6 if k == "w" else 0.0,
+                  atol_frac=1e-5 if k != "w" else 0.0, what=f"ft_w.{k}")
