@@ -339,6 +339,21 @@ __global__ __launch_bounds__(256) void ft_forward_pair16_kernel(
         __builtin_nontemporal_store(c, reinterpret_cast<f8v*>(combined + co) + qp);
 }
 
+// Element index of (row, col) of a forward table in layout `layout`
+// (FtTableLayout); qc: columns per 16-byte quad (4 for f32, 8 for f16).
+__host__ __device__ __forceinline__ uint64_t table_index(int layout, uint64_t row, uint32_t col, uint32_t ft_out,
+                                                         uint32_t pi, uint32_t qc) {
+    if (layout == kTableRows) return row * ft_out + col;
+    const uint64_t blk = row / pi;
+    const uint64_t f = row - blk * pi;
+    if (layout == kTablePairSlices) {
+        const uint32_t h = ft_out / 2, hw = 2 * qc, c = col >= h ? col - h : col, s = c / hw;
+        return ((blk * (h / hw) + s) * pi + f) * (4 * qc) + (col >= h ? 2 * qc : 0u) + (c - s * hw);
+    }
+    const uint32_t sw = 4 * qc, s = col / sw;
+    return ((blk * (ft_out / sw) + s) * pi + f) * sw + (col - s * sw);
+}
+
 // The king block of rank `rank` when the blocks are ordered by descending
 // row count over both perspectives (ties: lower block first), from the
 // schedule's bins start[0 .. 2*nb] (perspective-major); up to 128 blocks,
@@ -410,6 +425,7 @@ struct FtBlockFwd {
     _Float16* combined16;
     uint32_t batch, ft_out, cols, max_active, n_blocks, piece_inputs, n_slices;
     float scale;
+    int w_layout;  // FtTableLayout of W
 };
 
 // acc + (f32) the low / high f16 half of h2, rounded once: a mixed-precision
@@ -468,10 +484,16 @@ __global__ __launch_bounds__(kFbThreads) void ft_forward_block_kernel(FtBlockFwd
     const T* W = reinterpret_cast<const T*>(a.W);
     const uint32_t PI = a.piece_inputs, blk_lo = K * PI;
     const uint32_t nfeat = a.cols > blk_lo ? (a.cols - blk_lo < PI ? a.cols - blk_lo : PI) : 0u;
+    // a slice-major table holds this slice as one contiguous run of pi
+    // features x 64 bytes (quad i at element i * QC)
+    const T* Ws = W + (uint64_t)(K * a.n_slices + slice) * PI * (4 * QC);
     for (uint32_t i = threadIdx.x; i < (PI + 1) * 4; i += kFbThreads) {
         const uint32_t f = i / 4;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (f < nfeat) v = *reinterpret_cast<const uint4*>(W + (uint64_t)(blk_lo + f) * a.ft_out + quad_col(i % 4));
+        if (f < nfeat)
+            v = a.w_layout != kTableRows
+                    ? *reinterpret_cast<const uint4*>(Ws + (uint64_t)i * QC)
+                    : *reinterpret_cast<const uint4*>(W + (uint64_t)(blk_lo + f) * a.ft_out + quad_col(i % 4));
         s_w[i] = v;
     }
 
@@ -572,8 +594,9 @@ __global__ __launch_bounds__(kFbThreads) void ft_forward_block_kernel(FtBlockFwd
                 for (uint32_t k = 0; k < nv; ++k) {
                     const int32_t v = idx[k];
                     if (v < 0 || (uint32_t)v >= a.cols) continue;
-                    acc += __builtin_convertvector(*reinterpret_cast<const rowv*>(W + (uint64_t)v * a.ft_out + col),
-                                                   accv);
+                    acc += __builtin_convertvector(
+                        *reinterpret_cast<const rowv*>(W + table_index(a.w_layout, (uint32_t)v, col, a.ft_out, PI, QC)),
+                        accv);
                 }
             }
         }
@@ -1726,10 +1749,13 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
 // comb = w + w_virtual is rewritten for the piece's rows (ft_fold_virtual).
 // ---------------------------------------------------------------------------
 
+// With a slice-major pairwise table (layout kTablePairSlices) lane j < 32 of
+// a chunk takes float4 column 32c + j of the first half and lane j + 32 its
+// partner in the second half, so every store writes whole 64-byte slices.
 template <bool HSTATE, bool HCOMB>
 __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint32_t piece_inputs,
                                                               uint32_t n_chunks, float* __restrict__ comb,
-                                                              _Float16* __restrict__ comb16) {
+                                                              _Float16* __restrict__ comb16, int layout) {
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint64_t task = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
@@ -1738,8 +1764,15 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint
     const uint32_t p = (uint32_t)(task - (uint64_t)chunk * piece_inputs);
     const uint32_t ft_out = a.ft_out, ft_in = a.rows;
     const uint32_t row4 = ft_out / 4;
-    const uint32_t q = chunk * kWave + lane;
-    if (q >= row4) return;
+    uint32_t q;
+    if (layout == kTablePairSlices) {
+        const uint32_t qh = chunk * 32 + (lane & 31u);
+        if (qh >= row4 / 2) return;
+        q = (lane < 32 ? 0u : row4 / 2) + qh;
+    } else {
+        q = chunk * kWave + lane;
+        if (q >= row4) return;
+    }
     const uint32_t count = ft_in / piece_inputs;
     const float4* g4 = reinterpret_cast<const float4*>(a.grad);
     float4 vsum = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1762,12 +1795,13 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint
     // the forward rows of this piece: comb = w + w_virtual (f32 add), rounded
     // to f16 for an f16 forward table (ft_fold_virtual_f16, native_kernels.cu:262-300)
     const float4 wv = reinterpret_cast<const float4*>(a.w)[voff4];
-    auto put = [&](uint64_t off4, float4 wr) {
+    auto put = [&](uint64_t row, float4 wr) {
         const float4 c = f4add(wr, wv);
+        const uint64_t t4 = table_index(layout, row, 4 * q, ft_out, piece_inputs, HCOMB ? 8u : 4u) / 4;
         if constexpr (HCOMB)
-            reinterpret_cast<h4*>(comb16)[off4] = f4_to_h4(c);
+            reinterpret_cast<h4*>(comb16)[t4] = f4_to_h4(c);
         else
-            reinterpret_cast<float4*>(comb)[off4] = c;
+            reinterpret_cast<float4*>(comb)[t4] = c;
     };
     for (j = 0; j + U <= count; j += U) {
         float4 wr[U];
@@ -1775,11 +1809,11 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint
         for (int u = 0; u < U; ++u)
             wr[u] = reinterpret_cast<const float4*>(a.w)[(uint64_t)(p + (j + u) * piece_inputs) * row4 + q];
 #pragma unroll
-        for (int u = 0; u < U; ++u) put((uint64_t)(p + (j + u) * piece_inputs) * row4 + q, wr[u]);
+        for (int u = 0; u < U; ++u) put(p + (uint64_t)(j + u) * piece_inputs, wr[u]);
     }
     for (; j < count; ++j) {
-        const uint64_t off4 = (uint64_t)(p + j * piece_inputs) * row4 + q;
-        put(off4, reinterpret_cast<const float4*>(a.w)[off4]);
+        const uint64_t row = p + (uint64_t)j * piece_inputs;
+        put(row, reinterpret_cast<const float4*>(a.w)[row * row4 + q]);
     }
 }
 
@@ -1787,7 +1821,7 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint
 template <bool HCOMB>
 __global__ void ft_fold_kernel(const float* __restrict__ w, float* __restrict__ comb,
                                _Float16* __restrict__ comb16, uint32_t ft_in, uint32_t ft_out,
-                               uint32_t piece_inputs) {
+                               uint32_t piece_inputs, int layout) {
     const uint64_t n4 = (uint64_t)ft_in * ft_out / 4;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n4) return;
@@ -1797,10 +1831,11 @@ __global__ void ft_fold_kernel(const float* __restrict__ w, float* __restrict__ 
     const uint64_t vrow = ft_in + f % piece_inputs;
     const float4 x =
         f4add(reinterpret_cast<const float4*>(w)[i], reinterpret_cast<const float4*>(w)[vrow * row4 + c]);
+    const uint64_t t4 = table_index(layout, f, 4 * c, ft_out, piece_inputs, HCOMB ? 8u : 4u) / 4;
     if constexpr (HCOMB)
-        reinterpret_cast<h4*>(comb16)[i] = f4_to_h4(x);
+        reinterpret_cast<h4*>(comb16)[t4] = f4_to_h4(x);
     else
-        reinterpret_cast<float4*>(comb)[i] = x;
+        reinterpret_cast<float4*>(comb)[t4] = x;
 }
 
 __global__ void cast_f16_kernel(const float* __restrict__ src, _Float16* __restrict__ dst, uint64_t n) {
@@ -1857,6 +1892,15 @@ __global__ void lerp_kernel(float* __restrict__ w, float* __restrict__ slow, uin
 
 uint32_t ft_block_slot_stride(uint32_t max_active) { return max_active <= 40 ? 40u : 48u; }
 
+// A slice-major layout needs whole slices: 16-byte quads of 4 (f32) or 8
+// (f16) columns, four per slice.
+static bool table_layout_ok(int layout, bool f16, uint32_t ft_out) {
+    if (layout == kTableRows) return true;
+    if (layout == kTablePairSlices) return ft_out % (f16 ? 32u : 16u) == 0;
+    if (layout == kTableConcatSlices) return !f16 && ft_out % 16 == 0;
+    return false;
+}
+
 bool ft_forward_block_ok(int mode, bool f16_table, uint32_t ft_out, uint32_t piece_inputs, uint32_t max_active) {
     if (piece_inputs == 0 || piece_inputs > kFbMaxPi || max_active > kFbSlots) return false;
     if (mode == kPair) return ft_out % (f16_table ? 32u : 16u) == 0;
@@ -1872,9 +1916,14 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(!h_out || (a.mode == kPair && a.W16), "f16 raw sums need the pairwise mode and an f16 table");
     TATARA_REQUIRE(!a.W16 || a.mode == kPair, "an f16 table is read by the pairwise mode only");
     if (a.batch == 0) return kOk;
-    if (a.sched_start && a.schedule && a.slot_off && a.row_bad && a.n_persp == 2 && a.n_blocks >= 1 &&
-        a.n_blocks <= 128 &&
-        ft_forward_block_ok(a.mode, a.W16 != nullptr, a.ft_out, a.piece_inputs, a.max_active)) {
+    const bool block = a.sched_start && a.schedule && a.slot_off && a.row_bad && a.n_persp == 2 &&
+                       a.n_blocks >= 1 && a.n_blocks <= 128 &&
+                       ft_forward_block_ok(a.mode, a.W16 != nullptr, a.ft_out, a.piece_inputs, a.max_active);
+    TATARA_REQUIRE(a.w_layout == kTableRows ||
+                       (block && a.w_layout == (a.mode == kPair ? kTablePairSlices : kTableConcatSlices) &&
+                        a.cols == a.n_blocks * a.piece_inputs),
+                   "a slice-major forward table is read by the LDS-resident gather of its mode only");
+    if (block) {
         FtBlockFwd f{};
         f.W = a.W16 ? static_cast<const void*>(a.W16) : static_cast<const void*>(a.W);
         f.idx_stm = a.idx_stm;
@@ -1899,6 +1948,7 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
         f.piece_inputs = a.piece_inputs;
         f.n_slices = a.ft_out / (a.W16 ? 32u : 16u);
         f.scale = a.scale;
+        f.w_layout = a.w_layout;
         const uint32_t items = a.n_blocks * ((f.n_slices + 3) / 4);
         const uint32_t grid = ceil_div(items, kNumXcd) * kNumXcd * 4;
 #define TATARA_FB(NU)                                                                         \
@@ -2172,42 +2222,45 @@ int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream
 }
 
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
-                               hipStream_t stream) {
+                               hipStream_t stream, int layout) {
     TATARA_REQUIRE(piece_inputs > 0 && a.rows % piece_inputs == 0,
                    "virtual fold: rows must be a multiple of piece_inputs");
     TATARA_REQUIRE(a.grad, "virtual fold needs the real-row gradients");
     TATARA_REQUIRE(!(comb && comb16), "virtual fold writes one forward table");
-    const uint32_t n_chunks = ceil_div(a.ft_out / 4, kWave);
+    TATARA_REQUIRE(table_layout_ok(layout, comb16 != nullptr, a.ft_out), "virtual fold: table layout");
+    const uint32_t n_chunks = layout == kTablePairSlices ? ceil_div(a.ft_out / 8, 32) : ceil_div(a.ft_out / 4, kWave);
     const uint64_t tasks = (uint64_t)piece_inputs * n_chunks;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
     _Float16* c16 = reinterpret_cast<_Float16*>(comb16);
     if (a.m16) {
         if (comb16)
-            ft_virtual_fold_kernel<true, true><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+            ft_virtual_fold_kernel<true, true><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16, layout);
         else
-            ft_virtual_fold_kernel<true, false><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+            ft_virtual_fold_kernel<true, false><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16, layout);
     } else {
         if (comb16)
-            ft_virtual_fold_kernel<false, true><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+            ft_virtual_fold_kernel<false, true><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16, layout);
         else
-            ft_virtual_fold_kernel<false, false><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16);
+            ft_virtual_fold_kernel<false, false><<<blocks, 256, 0, stream>>>(a, piece_inputs, n_chunks, comb, c16, layout);
     }
     TATARA_LAUNCHED("ft_virtual_fold");
     return kOk;
 }
 
 int32_t launch_ft_fold(const float* w, float* comb, uint16_t* comb16, uint32_t ft_in, uint32_t ft_out,
-                       uint32_t piece_inputs, hipStream_t stream) {
+                       uint32_t piece_inputs, hipStream_t stream, int layout) {
     TATARA_REQUIRE(ft_out % 4 == 0 && piece_inputs > 0, "fold: ft_out%4==0, piece_inputs>0");
     TATARA_REQUIRE((comb != nullptr) != (comb16 != nullptr), "fold: exactly one of comb / comb16");
+    TATARA_REQUIRE(table_layout_ok(layout, comb16 != nullptr, ft_out) && ft_in % piece_inputs == 0,
+                   "fold: table layout");
     const uint64_t n4 = (uint64_t)ft_in * ft_out / 4;
     if (n4 == 0) return kOk;
     if (comb16)
         ft_fold_kernel<true><<<ceil_div(n4, 256), 256, 0, stream>>>(
-            w, nullptr, reinterpret_cast<_Float16*>(comb16), ft_in, ft_out, piece_inputs);
+            w, nullptr, reinterpret_cast<_Float16*>(comb16), ft_in, ft_out, piece_inputs, layout);
     else
         ft_fold_kernel<false><<<ceil_div(n4, 256), 256, 0, stream>>>(w, comb, nullptr, ft_in, ft_out,
-                                                                      piece_inputs);
+                                                                      piece_inputs, layout);
     TATARA_LAUNCHED("ft_fold");
     return kOk;
 }

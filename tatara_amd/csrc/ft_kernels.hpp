@@ -14,6 +14,14 @@ namespace tatara {
 // (the --ft-fp16 / --ft-fp16-out / --fp16-opt-state modes of the reference,
 // bins/nnue_train/src/trainer_common.rs:49-61).
 
+// Layout of a forward table (the factorizer's folded table): row-major
+// [rows][ft_out], or slice-major for the block-resident gather:
+// [king block][slice][feature][64 bytes], a slice being the columns one
+// ft_forward_block_kernel workgroup holds (pairwise: 2 x QC columns of each
+// half, concat: 4 x QC consecutive columns; QC = 4 for f32, 8 for f16), so
+// a workgroup stages its slice as one contiguous run.
+enum FtTableLayout : int { kTableRows = 0, kTablePairSlices = 1, kTableConcatSlices = 2 };
+
 struct FtForwardArgs {
     int mode;  // 0 raw sum, 1 LayerStack pairwise post, 2 Simple concat post
     const float* W;
@@ -42,6 +50,7 @@ struct FtForwardArgs {
     // launch_king_block_keys (both required for the LDS-resident gather)
     const uint32_t* slot_off;
     const uint8_t* row_bad;
+    int w_layout;  // FtTableLayout of W / W16 (slice-major only with the LDS-resident gather)
 };
 
 // Whether the LDS-resident forward serves this shape (mode, table type,
@@ -148,10 +157,10 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
 int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream_t stream, bool fallback = true);
 // comb or comb16 (f16) receives the rewritten forward rows; both may be null.
 int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float* comb, uint16_t* comb16,
-                               hipStream_t stream);
+                               hipStream_t stream, int layout = kTableRows);
 // comb = w + w_virtual (f32), or comb16 = f16(w + w_virtual) when comb is null.
 int32_t launch_ft_fold(const float* w, float* comb, uint16_t* comb16, uint32_t ft_in, uint32_t ft_out,
-                       uint32_t piece_inputs, hipStream_t stream);
+                       uint32_t piece_inputs, hipStream_t stream, int layout = kTableRows);
 // dst[i] = f16(src[i]), round to nearest even (cast_f32_to_f16).
 int32_t launch_cast_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream);
 int32_t launch_ft_reduce(float* grad, uint32_t ft_in, uint32_t ft_out, uint32_t piece_inputs,

@@ -52,6 +52,8 @@ class SimpleTrainer final : public TrainerBase {
     uint8_t* sched_keys = nullptr;
     uint32_t* fb_off = nullptr;  // LDS slot offsets of the block-resident gather, or null
     uint8_t* fb_bad = nullptr;
+    // layout of the folded forward table: slice-major for the block-resident gather
+    int table_layout() const { return fb_off ? kTableConcatSlices : kTableRows; }
     int32_t* schedule = nullptr;
     uint32_t *sched_hist = nullptr, *sched_start = nullptr, *sched_count = nullptr;
     // occurrence sort
@@ -218,7 +220,7 @@ class SimpleTrainer final : public TrainerBase {
 
     int32_t sync_forward_weights() override {
         if (!factorized) return kOk;
-        int32_t st = launch_ft_fold(ft.w, comb, nullptr, ft_in, ft_out, pi, stream);
+        int32_t st = launch_ft_fold(ft.w, comb, nullptr, ft_in, ft_out, pi, stream, table_layout());
         if (st) return st;
         TATARA_HIP(hipStreamSynchronize(stream), "sync_forward_weights");
         return kOk;
@@ -404,6 +406,7 @@ class SimpleTrainer final : public TrainerBase {
             fa.piece_inputs = pi;
             fa.slot_off = fb_off;
             fa.row_bad = fb_bad;
+            fa.w_layout = factorized ? table_layout() : kTableRows;
         }
         fa.bias = small[0].w;
         fa.out_stm = ft_stm;
@@ -464,7 +467,7 @@ class SimpleTrainer final : public TrainerBase {
         if ((st = join_side())) return st;
         if ((st = ft_gradient(p, fb))) return st;
         if ((st = prof_mark(5))) return st;
-        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, nullptr, stream))) return st;
+        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, nullptr, stream, table_layout()))) return st;
         if ((st = prof_mark(6))) return st;
         SimpleDenseGroup groups[7];
         for (int k = 0; k < 7; ++k) {

@@ -95,6 +95,8 @@ class LayerStackTrainer final : public TrainerBase {
     uint8_t* sched_keys = nullptr;
     uint32_t* fb_off = nullptr;  // LDS slot offsets of the block-resident gather, or null
     uint8_t* fb_bad = nullptr;
+    // layout of the folded forward table: slice-major for the block-resident gather
+    int table_layout() const { return fb_off ? kTablePairSlices : kTableRows; }
     int32_t* schedule = nullptr;
     uint32_t *sched_hist = nullptr, *sched_start = nullptr, *sched_count = nullptr;
     // bucket sort
@@ -319,11 +321,11 @@ class LayerStackTrainer final : public TrainerBase {
     int32_t sync_forward_weights() override {
         int32_t st = kOk;
         if (h_fwd && factorized)
-            st = launch_ft_fold(ft.w, nullptr, fwd16, ft_in, ft_out, pi, stream);
+            st = launch_ft_fold(ft.w, nullptr, fwd16, ft_in, ft_out, pi, stream, table_layout());
         else if (h_fwd)
             st = launch_cast_f16(ft.w, fwd16, (uint64_t)ft_in * ft_out, stream);
         else if (factorized)
-            st = launch_ft_fold(ft.w, comb, nullptr, ft_in, ft_out, pi, stream);
+            st = launch_ft_fold(ft.w, comb, nullptr, ft_in, ft_out, pi, stream, table_layout());
         else
             return kOk;
         if (st) return st;
@@ -541,6 +543,7 @@ class LayerStackTrainer final : public TrainerBase {
             fa.piece_inputs = pi;
             fa.slot_off = fb_off;
             fa.row_bad = fb_bad;
+            fa.w_layout = factorized ? table_layout() : kTableRows;
         }
         fa.bias = small[0].w;
         fa.out_stm = ft_stm;
@@ -615,7 +618,9 @@ class LayerStackTrainer final : public TrainerBase {
         if ((st = join_side())) return st;
         if ((st = ft_gradient(p, fb))) return st;
         if ((st = prof_mark(5))) return st;
-        if (factorized && (st = launch_ft_virtual_fold(fb, pi, comb, h_fwd ? fwd16 : nullptr, stream))) return st;
+        if (factorized &&
+            (st = launch_ft_virtual_fold(fb, pi, comb, h_fwd ? fwd16 : nullptr, stream, table_layout())))
+            return st;
         if (h_out) clamp_elems += 2ull * p.b * ft_out;
         if ((st = prof_mark(6))) return st;
         LsDenseGroup groups[9];
