@@ -1749,9 +1749,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void ft_grad_mfma_kernel(FtGradArg
 // comb = w + w_virtual is rewritten for the piece's rows (ft_fold_virtual).
 // ---------------------------------------------------------------------------
 
-// With a slice-major pairwise table (layout kTablePairSlices) lane j < 32 of
-// a chunk takes float4 column 32c + j of the first half and lane j + 32 its
-// partner in the second half, so every store writes whole 64-byte slices.
+// With a slice-major pairwise table (layout kTablePairSlices) a wave takes
+// two adjacent pieces: lane 32i + 16h + j holds piece 2u + i, float4 column
+// 16c + j of half h, so each store writes two adjacent features' whole
+// 64-byte slices, one 128-byte line per slice.
 template <bool HSTATE, bool HCOMB>
 __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint32_t piece_inputs,
                                                               uint32_t n_chunks, float* __restrict__ comb,
@@ -1759,17 +1760,21 @@ __global__ __launch_bounds__(256) void ft_virtual_fold_kernel(FtGradArgs a, uint
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint64_t task = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
-    if (task >= (uint64_t)piece_inputs * n_chunks) return;
-    const uint32_t chunk = (uint32_t)(task / piece_inputs);
-    const uint32_t p = (uint32_t)(task - (uint64_t)chunk * piece_inputs);
+    const bool paired = layout == kTablePairSlices;
+    const uint32_t n_units = paired ? (piece_inputs + 1) / 2 : piece_inputs;
+    if (task >= (uint64_t)n_units * n_chunks) return;
+    const uint32_t chunk = (uint32_t)(task / n_units);
+    const uint32_t unit = (uint32_t)(task - (uint64_t)chunk * n_units);
     const uint32_t ft_out = a.ft_out, ft_in = a.rows;
     const uint32_t row4 = ft_out / 4;
-    uint32_t q;
-    if (layout == kTablePairSlices) {
-        const uint32_t qh = chunk * 32 + (lane & 31u);
-        if (qh >= row4 / 2) return;
-        q = (lane < 32 ? 0u : row4 / 2) + qh;
+    uint32_t q, p;
+    if (paired) {
+        p = 2 * unit + (lane >> 5);
+        const uint32_t qh = chunk * 16 + (lane & 15u);
+        if (p >= piece_inputs || qh >= row4 / 2) return;
+        q = ((lane >> 4) & 1u ? row4 / 2 : 0u) + qh;
     } else {
+        p = unit;
         q = chunk * kWave + lane;
         if (q >= row4) return;
     }
@@ -2228,8 +2233,8 @@ int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float
     TATARA_REQUIRE(a.grad, "virtual fold needs the real-row gradients");
     TATARA_REQUIRE(!(comb && comb16), "virtual fold writes one forward table");
     TATARA_REQUIRE(table_layout_ok(layout, comb16 != nullptr, a.ft_out), "virtual fold: table layout");
-    const uint32_t n_chunks = layout == kTablePairSlices ? ceil_div(a.ft_out / 8, 32) : ceil_div(a.ft_out / 4, kWave);
-    const uint64_t tasks = (uint64_t)piece_inputs * n_chunks;
+    const uint32_t n_chunks = layout == kTablePairSlices ? ceil_div(a.ft_out / 8, 16) : ceil_div(a.ft_out / 4, kWave);
+    const uint64_t tasks = (uint64_t)(layout == kTablePairSlices ? (piece_inputs + 1) / 2 : piece_inputs) * n_chunks;
     const uint32_t blocks = (uint32_t)((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
     _Float16* c16 = reinterpret_cast<_Float16*>(comb16);
     if (a.m16) {
