@@ -346,12 +346,8 @@ __host__ __device__ __forceinline__ uint64_t table_index(int layout, uint64_t ro
     if (layout == kTableRows) return row * ft_out + col;
     const uint64_t blk = row / pi;
     const uint64_t f = row - blk * pi;
-    if (layout == kTablePairSlices) {
-        const uint32_t h = ft_out / 2, hw = 2 * qc, c = col >= h ? col - h : col, s = c / hw;
-        return ((blk * (h / hw) + s) * pi + f) * (4 * qc) + (col >= h ? 2 * qc : 0u) + (c - s * hw);
-    }
-    const uint32_t sw = 4 * qc, s = col / sw;
-    return ((blk * (ft_out / sw) + s) * pi + f) * sw + (col - s * sw);
+    const uint32_t h = ft_out / 2, hw = 2 * qc, c = col >= h ? col - h : col, s = c / hw;
+    return ((blk * (h / hw) + s) * pi + f) * (4 * qc) + (col >= h ? 2 * qc : 0u) + (c - s * hw);
 }
 
 // The king block of rank `rank` when the blocks are ordered by descending
@@ -1902,7 +1898,6 @@ uint32_t ft_block_slot_stride(uint32_t max_active) { return max_active <= 40 ? 4
 static bool table_layout_ok(int layout, bool f16, uint32_t ft_out) {
     if (layout == kTableRows) return true;
     if (layout == kTablePairSlices) return ft_out % (f16 ? 32u : 16u) == 0;
-    if (layout == kTableConcatSlices) return !f16 && ft_out % 16 == 0;
     return false;
 }
 
@@ -1925,9 +1920,9 @@ int32_t launch_ft_forward(const FtForwardArgs& a, hipStream_t stream) {
                        a.n_blocks >= 1 && a.n_blocks <= 128 &&
                        ft_forward_block_ok(a.mode, a.W16 != nullptr, a.ft_out, a.piece_inputs, a.max_active);
     TATARA_REQUIRE(a.w_layout == kTableRows ||
-                       (block && a.w_layout == (a.mode == kPair ? kTablePairSlices : kTableConcatSlices) &&
+                       (block && a.mode == kPair && a.w_layout == kTablePairSlices &&
                         a.cols == a.n_blocks * a.piece_inputs),
-                   "a slice-major forward table is read by the LDS-resident gather of its mode only");
+                   "a slice-major forward table is read by the pairwise LDS-resident gather only");
     if (block) {
         FtBlockFwd f{};
         f.W = a.W16 ? static_cast<const void*>(a.W16) : static_cast<const void*>(a.W);

@@ -15,12 +15,12 @@ namespace tatara {
 // bins/nnue_train/src/trainer_common.rs:49-61).
 
 // Layout of a forward table (the factorizer's folded table): row-major
-// [rows][ft_out], or slice-major for the block-resident gather:
+// [rows][ft_out], or slice-major for the pairwise block-resident gather:
 // [king block][slice][feature][64 bytes], a slice being the columns one
-// ft_forward_block_kernel workgroup holds (pairwise: 2 x QC columns of each
-// half, concat: 4 x QC consecutive columns; QC = 4 for f32, 8 for f16), so
-// a workgroup stages its slice as one contiguous run.
-enum FtTableLayout : int { kTableRows = 0, kTablePairSlices = 1, kTableConcatSlices = 2 };
+// ft_forward_block_kernel workgroup holds (2 x QC columns of each half;
+// QC = 4 for f32, 8 for f16), so a workgroup stages its slice as one
+// contiguous run.
+enum FtTableLayout : int { kTableRows = 0, kTablePairSlices = 1 };
 
 struct FtForwardArgs {
     int mode;  // 0 raw sum, 1 LayerStack pairwise post, 2 Simple concat post

@@ -52,8 +52,10 @@ class SimpleTrainer final : public TrainerBase {
     uint8_t* sched_keys = nullptr;
     uint32_t* fb_off = nullptr;  // LDS slot offsets of the block-resident gather, or null
     uint8_t* fb_bad = nullptr;
-    // layout of the folded forward table: slice-major for the block-resident gather
-    int table_layout() const { return fb_off ? kTableConcatSlices : kTableRows; }
+    // layout of the folded forward table: row-major also for the block-resident
+    // gather (the 256-column table stays in the Infinity Cache, where the
+    // slice-major form saved the forward less than it cost the fold)
+    int table_layout() const { return kTableRows; }
     int32_t* schedule = nullptr;
     uint32_t *sched_hist = nullptr, *sched_start = nullptr, *sched_count = nullptr;
     // occurrence sort
