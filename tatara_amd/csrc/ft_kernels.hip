@@ -15,6 +15,7 @@
 //   optimizer crates/gpu-kernels/src/pointwise/radam_step.rs:116-149
 #include "ft_kernels.hpp"
 
+#include <cmath>
 #include <type_traits>
 #include <utility>
 
@@ -913,16 +914,21 @@ __device__ __forceinline__ CellState<V, HSTATE> load_cells(const FtGradArgs& a, 
 // native_kernels.cu:1118-1170: read back as f16 / scale, stored as
 // f16(m * m_scale) clamped to +-65504 and f16(v * v_scale) clamped above at
 // 65504, a NaN staying NaN).
+// The scales are powers of two (the launchers check it), so x / scale is
+// x scaled by an exact power of two: v_ldexp_f32 rounds the same exact value,
+// bit for bit, without a division sequence.
 template <int V, bool HSTATE>
 __device__ __forceinline__ vecf<V> radam_cells(const FtGradArgs& a, vecf<V> g, CellState<V, HSTATE>& c) {
     const OptScalars& s = a.opt;
     vecf<V> W = c.w;
+    // scale = 2^(e - 1) with e the frexp exponent
+    const int m_shift = 1 - __builtin_amdgcn_frexp_expf(a.m_scale), v_shift = 1 - __builtin_amdgcn_frexp_expf(a.v_scale);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
         float w = W[k], m, v;
         if constexpr (HSTATE) {
-            m = (float)c.m[k] / a.m_scale;
-            v = (float)c.v[k] / a.v_scale;
+            m = __builtin_amdgcn_ldexpf((float)c.m[k], m_shift);
+            v = __builtin_amdgcn_ldexpf((float)c.v[k], v_shift);
         } else {
             m = c.m[k];
             v = c.v[k];
@@ -2103,6 +2109,16 @@ int32_t launch_occurrence_sort(const OccurrenceSortArgs& a, hipStream_t stream) 
     return kOk;
 }
 
+// f16 moments are read back as x / scale by an exact power-of-two scaling
+// (radam_cells): the scales must be powers of two with normal reciprocals.
+static bool moment_scales_ok(const FtGradArgs& a) {
+    auto pow2 = [](float x) {
+        int e = 0;
+        return x > 0.0f && std::isfinite(x) && std::frexp(x, &e) == 0.5f && e >= -124 && e <= 127;
+    };
+    return !a.m16 || (pow2(a.m_scale) && pow2(a.v_scale));
+}
+
 int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     constexpr int V = kFtGradLaneFloats;
     constexpr uint32_t kCols = kWave * V;
@@ -2110,6 +2126,7 @@ int32_t launch_ft_grad_update(const FtGradArgs& a, hipStream_t stream) {
     TATARA_REQUIRE(a.dft_row_stride % 4 == 0 && a.dft_chunk_stride % 4 == 0, "dft strides");
     const bool hdft = a.dft16 != nullptr, hstate = a.m16 != nullptr;
     TATARA_REQUIRE(!hstate || a.v16, "f16 moments need both m16 and v16");
+    TATARA_REQUIRE(moment_scales_ok(a), "f16 moment scales must be powers of two");
     const uint32_t n_chunks = ceil_div(a.ft_out, kCols);
     const uint64_t tasks = (uint64_t)a.rows * n_chunks;
     if (tasks == 0) return kOk;
@@ -2173,6 +2190,7 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
                    "block scan: chunk-major dft");
     TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "block scan: shapes");
+    TATARA_REQUIRE(moment_scales_ok(a), "f16 moment scales must be powers of two");
     const ScanGeom geom = scan_geom(s.piece_inputs);
     TATARA_REQUIRE(s.n_blocks <= 128, "block scan: at most 128 king blocks");
     const uint64_t pairs = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks;
@@ -2202,6 +2220,7 @@ int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream
     TATARA_REQUIRE(a.dft_row_stride == kDftChunk && a.dft_chunk_stride == 2ull * s.batch * kDftChunk,
                    "mfma backward: chunk-major dft");
     TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "mfma backward: shapes");
+    TATARA_REQUIRE(moment_scales_ok(a), "f16 moment scales must be powers of two");
     TATARA_REQUIRE(s.n_blocks <= 128, "mfma backward: at most 128 king blocks");
     const ScanGeom geom = scan_geom(s.piece_inputs);
     TATARA_REQUIRE(geom.group_size <= 128, "mfma backward: at most 128 features per group");
@@ -2226,6 +2245,7 @@ int32_t launch_ft_virtual_fold(const FtGradArgs& a, uint32_t piece_inputs, float
     TATARA_REQUIRE(piece_inputs > 0 && a.rows % piece_inputs == 0,
                    "virtual fold: rows must be a multiple of piece_inputs");
     TATARA_REQUIRE(a.grad, "virtual fold needs the real-row gradients");
+    TATARA_REQUIRE(moment_scales_ok(a), "f16 moment scales must be powers of two");
     TATARA_REQUIRE(!(comb && comb16), "virtual fold writes one forward table");
     TATARA_REQUIRE(table_layout_ok(layout, comb16 != nullptr, a.ft_out), "virtual fold: table layout");
     const uint32_t n_chunks = layout == kTablePairSlices ? ceil_div(a.ft_out / 8, 16) : ceil_div(a.ft_out / 4, kWave);
