@@ -1369,14 +1369,18 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
 #define TATARA_SUM_STAGE(BUF, M, T)                                       \
     do {                                                                  \
         if (nf) {                                                         \
+            /* bit k: feature k has a row in the stage (one compare for   \
+               all 16, so a feature without one costs a bit test) */      \
+            const uint32_t any = (uint32_t)__builtin_amdgcn_ballot_w64((M) != 0u) & 0xFFFFu; \
             _Pragma("unroll") for (int k = 0; k < kScanFeat; ++k) {       \
+                if (!(any & (1u << k))) continue;                         \
                 /* the stage's rows that hold feature k, ascending */     \
                 uint32_t rows = __builtin_amdgcn_readlane((M), k);        \
-                while (rows) {                                            \
+                do {                                                      \
                     const uint32_t jj = __builtin_ctz(rows);              \
                     rows &= rows - 1u;                                    \
                     acc[k] = f4add(acc[k], as_f4(s_rows[(BUF)][jj][lane])); \
-                }                                                         \
+                } while (rows);                                           \
             }                                                             \
         }                                                                 \
     } while (0)
