@@ -1369,6 +1369,9 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
 #define TATARA_SUM_STAGE(BUF, M, T)                                       \
     do {                                                                  \
         if (nf) {                                                         \
+            /* the hit loop's latency chain issues ahead of the other     \
+               workgroup's staging and update (about 1% of the kernel) */ \
+            __builtin_amdgcn_s_setprio(1);                                \
             /* bit k: feature k has a row in the stage (one compare for   \
                all 16, so a feature without one costs a bit test) */      \
             const uint32_t any = (uint32_t)__builtin_amdgcn_ballot_w64((M) != 0u) & 0xFFFFu; \
@@ -1382,6 +1385,7 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
                     acc[k] = f4add(acc[k], as_f4(s_rows[(BUF)][jj][lane])); \
                 } while (rows);                                           \
             }                                                             \
+            __builtin_amdgcn_s_setprio(0);                                \
         }                                                                 \
     } while (0)
 #define TATARA_STAGE(T, X, Y, BUF)                \
