@@ -624,6 +624,68 @@ def run_loop_throughput(w: dict, cfg, records: list, b: int, pw, superbatches: i
         shutil.rmtree(d, ignore_errors=True)
 
 
+def make_trainer(w: dict, spec: dict, b: int):
+    """The workload's trainer at batch capacity b: (config, trainer, loss,
+    step(trainer, device_batch))."""
+    from tatara_amd.trainer import (LayerStackConfig, LayerStackTrainer, Sigmoid, SimpleConfig,
+                                    SimpleTrainer, Wrm)
+
+    lr = w["lr"]
+    if w["arch"] == "layerstack":
+        cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
+                               piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
+                               l2_out=w["l2"], num_buckets=w["nb"], max_batch=b,
+                               optimizer=w["optimizer"], weight_decay=0.01)
+        if w.get("all_optim"):
+            cfg = cfg.all_optim()
+        loss = Sigmoid(1.0 / 290.0)
+        return cfg, LayerStackTrainer(cfg), loss, lambda t, db: t.train_step(db, None, lr, 0.0, loss)
+    cfg = SimpleConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
+                       piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
+                       l2_out=w["l2"], max_batch=b, optimizer=w["optimizer"], weight_decay=0.01)
+    loss = Wrm(nnue2score=290.0, in_scaling=290.0, in_offset=0.0, target_offset=0.0, target_scaling=290.0)
+    return cfg, SimpleTrainer(cfg), loss, lambda t, db: t.train_step(db, lr, 0.0, loss)
+
+
+def other_workloads(names: list, b: int, steps: int, warmup: int, n_batches: int = 2) -> dict:
+    """The other BASELINE workloads, measured the way `value` is: resident
+    GPU-decoded batches cycled, warm-up steps, then `steps` timed steps
+    bracketed by device synchronisations (host wall clock)."""
+    from tatara_amd import _lib
+    from tatara_amd.dataloader import ProgressWeights, feature_set_info, psv_to_device_batch
+    from tatara_amd.psv import synthetic_progress_weights, synthetic_psv
+
+    lib = _lib.load()
+    out = {}
+    for name in names:
+        w = WORKLOADS[name]
+        info = feature_set_info(w["spec"])
+        spec = dict(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"])
+        pw = ProgressWeights(synthetic_progress_weights(seed=7)) if w["bucket_mode"] == "progress8kpabs" else None
+        dev = [psv_to_device_batch(synthetic_psv(b, seed=1000 + i), w["spec"], w["bucket_mode"], w["nb"], pw)
+               for i in range(n_batches)]
+        _, trainer, _, step = make_trainer(w, spec, b)
+        with trainer as t:
+            for i in range(warmup):
+                step(t, dev[i % len(dev)])
+            t.flush_pending_loss()
+            _lib.check(lib.tatara_synchronize())
+            t0 = time.perf_counter()
+            for i in range(steps):
+                step(t, dev[i % len(dev)])
+            t.flush_pending_loss()
+            _lib.check(lib.tatara_synchronize())
+            elapsed = time.perf_counter() - t0
+        del dev
+        pos_s = b * steps / elapsed
+        out[name] = {"value": round(pos_s, 1), "unit": "pos/s", "ms_per_step": round(1000.0 * elapsed / steps, 4),
+                     "steps": steps, "warmup": warmup, "vs_baseline": round(pos_s / w["ref"], 4),
+                     "vs_baseline_ref": f"RTX 5090 {w['ref'] / 1e6:.2f}M pos/s (reference {w['ref_src']})",
+                     "dtype": "f16+f32" if w.get("all_optim") else "f32", "workload": w["desc"]}
+        log(f"{name}: {pos_s:,.0f} pos/s ({1000.0 * elapsed / steps:.3f} ms/step)")
+    return out
+
+
 def git_commit() -> str:
     """The commit of this checkout (.git/HEAD read directly; git may be absent),
     or "unknown"."""
@@ -673,6 +735,9 @@ def main() -> int:
                          "(king-blocked batches) and queued (gated off on the device); 0 skips the comparison")
     ap.add_argument("--no-run-loop", action="store_true",
                     help="skip the end-to-end tatara_train_run figure (PSV file -> decode -> steps)")
+    ap.add_argument("--no-other-workloads", action="store_true",
+                    help="skip the short throughput runs of the other BASELINE workloads "
+                         "(other_workloads in the JSON line)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -718,24 +783,7 @@ def main() -> int:
         f"mean nnz {np.mean([h['nnz'].mean() for h in host_batches]):.1f}; bucket histogram "
         f"{np.bincount(host_batches[0]['bucket'], minlength=w['nb']).tolist()}")
     lr = w["lr"]
-    if w["arch"] == "layerstack":
-        cfg = LayerStackConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
-                               piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
-                               l2_out=w["l2"], num_buckets=w["nb"], max_batch=b,
-                               optimizer=w["optimizer"], weight_decay=0.01)
-        if w.get("all_optim"):
-            cfg = cfg.all_optim()
-        trainer = LayerStackTrainer(cfg)
-        loss = Sigmoid(1.0 / 290.0)
-        step = lambda t, db: t.train_step(db, None, lr, 0.0, loss)  # noqa: E731
-    else:
-        cfg = SimpleConfig(ft_in=spec["ft_in"], max_active=spec["max_active"],
-                           piece_inputs=spec["piece_inputs"], ft_out=w["ft_out"], l1_out=w["l1"],
-                           l2_out=w["l2"], max_batch=b, optimizer=w["optimizer"], weight_decay=0.01)
-        trainer = SimpleTrainer(cfg)
-        loss = Wrm(nnue2score=290.0, in_scaling=290.0, in_offset=0.0, target_offset=0.0,
-                   target_scaling=290.0)
-        step = lambda t, db: t.train_step(db, lr, 0.0, loss)  # noqa: E731
+    cfg, trainer, loss, step = make_trainer(w, spec, b)
     with trainer as t:
         log(f"warm-up {args.warmup} steps")
         for i in range(args.warmup):
@@ -890,6 +938,10 @@ def main() -> int:
                       "compulsory_frac": round(comp[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if v > 0 else None}
                   for k, v in phase_avg.items()}
 
+    others = None
+    if not args.no_other_workloads:
+        others = other_workloads([n for n in WORKLOADS if n != args.workload], b, min(args.steps, 20),
+                                 args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle step)")
@@ -950,6 +1002,8 @@ def main() -> int:
         line["drift_vs_f32"] = drift
     if run_loop is not None:
         line["run_loop"] = run_loop
+    if others is not None:
+        line["other_workloads"] = others
     print(json.dumps(line), flush=True)
     return 0
 
