@@ -1262,9 +1262,12 @@ __global__ __launch_bounds__(256) void ft_scan_tables_kernel(FtBlockScan s, Scan
             }
             const uint32_t g = (uint32_t)local / geom.group_size;
             const uint32_t rr = (uint32_t)local - g * geom.group_size;
-            const uint32_t q = g * kScanWaves + rr / kScanFeat;
+            // the group's feature rr: wave rr / 16, entry rr % 16; dealt
+            // (s.dealt): wave rr % 8, entry rr / 8
+            const uint32_t q = g * kScanWaves + (s.dealt ? rr % kScanWaves : rr / kScanFeat);
+            const uint32_t e = s.dealt ? rr / kScanWaves : rr % kScanFeat;
             const uint32_t bit = 1u << (r0 + u);
-            const uint32_t old = atomicOr(&st[q * kScanFeat + rr % kScanFeat], bit);
+            const uint32_t old = atomicOr(&st[q * kScanFeat + e], bit);
             if (old & bit) multi = true;  // the feature is in the row twice
         }
     }
@@ -1280,10 +1283,14 @@ __global__ __launch_bounds__(256) void ft_scan_tables_kernel(FtBlockScan s, Scan
 // (512 bytes per 256-column chunk), each added value is converted to f32,
 // and the sum is multiplied by dft_inv_scale at the end, as the
 // occurrence-list kernel does.
-template <bool HDFT, bool HSTATE>
+//
+// DEALT (s.dealt): the tables deal a group's features to the waves
+// round-robin, so wave w owns the group's features w, w + 8, w + 16, ...
+// and adjacent (often equally frequent) features land on different waves,
+// which evens out the hits per wave and stage that the barrier waits for.
+template <bool HDFT, bool HSTATE, bool DEALT>
 __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void ft_grad_scan_kernel(
-    FtGradArgs a, FtBlockScan s,
-                                                                       ScanGeom geom) {
+    FtGradArgs a, FtBlockScan s, ScanGeom geom) {
     constexpr int R = kScanStage, RPW = kScanStage / kScanWaves;
     static_assert(R == 32 && (RPW == 2 || RPW == 4), "32 rows per stage, two or four per wave");
     if (__builtin_amdgcn_readfirstlane(*s.multi)) return;  // the occurrence-list kernel runs instead
@@ -1308,9 +1315,13 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t PI = s.piece_inputs;
     const uint32_t blk_lo = K * PI;
     const uint32_t blk_n = s.cols > blk_lo ? (s.cols - blk_lo < PI ? s.cols - blk_lo : PI) : 0u;
-    const uint32_t lo = g * geom.group_size + wave * kScanFeat;
+    // the wave's features: f0 + k * fstep (k < nf)
+    const uint32_t g_lo = g * geom.group_size;
     const uint32_t g_hi = (g + 1) * geom.group_size < blk_n ? (g + 1) * geom.group_size : blk_n;
-    const uint32_t nf = g_hi > lo ? (g_hi - lo < (uint32_t)kScanFeat ? g_hi - lo : (uint32_t)kScanFeat) : 0u;
+    const uint32_t lo = g_lo + (DEALT ? wave : wave * kScanFeat);
+    const uint32_t fstep = DEALT ? kScanWaves : 1u;
+    const uint32_t span = g_hi > lo ? (DEALT ? (g_hi - lo + kScanWaves - 1) / kScanWaves : g_hi - lo) : 0u;
+    const uint32_t nf = span < (uint32_t)kScanFeat ? span : (uint32_t)kScanFeat;
     const uint32_t f0 = blk_lo + lo;
     // the block's rows: its stm bin, then its nstm bin, as schedule entries
     const uint32_t a0 = s.sched_start[K], na = s.sched_start[K + 1] - a0;
@@ -1430,7 +1441,7 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     for (int k = 0; k < kScanFeat; ++k) {
         gv[k] = vecf<4>{acc[k].x, acc[k].y, acc[k].z, acc[k].w};
         if constexpr (HDFT) gv[k] *= a.dft_inv_scale;
-        if (a.grad && (uint32_t)k < nf) __builtin_nontemporal_store(gv[k], grad + off0 + k * row4);
+        if (a.grad && (uint32_t)k < nf) __builtin_nontemporal_store(gv[k], grad + off0 + (uint64_t)k * fstep * row4);
     }
     if (!a.apply_update) return;
     // The update loads each row's state two rows ahead of it (one on a
@@ -1449,11 +1460,15 @@ __global__ __launch_bounds__(kScanWaves * 64) __attribute__((amdgpu_waves_per_eu
     auto grad_lo = [&](int k) { return parked[k * 64]; };
     const uint32_t nf_lo = nf < (uint32_t)kParked ? nf : kParked;
     if (a.opt.lookahead) {
-        if (nf_hi) update_rows_pipelined<kScanFeat - kParked, 1, HSTATE, true>(a, f0 + kParked, 1, col, nf_hi, nf_hi, grad_hi);
-        update_rows_pipelined<kParked, 1, HSTATE, true>(a, f0, 1, col, nf_lo, nf_lo, grad_lo);
+        if (nf_hi)
+            update_rows_pipelined<kScanFeat - kParked, 1, HSTATE, true>(a, f0 + kParked * fstep, fstep, col, nf_hi, nf_hi,
+                                                                        grad_hi);
+        update_rows_pipelined<kParked, 1, HSTATE, true>(a, f0, fstep, col, nf_lo, nf_lo, grad_lo);
     } else {
-        if (nf_hi) update_rows_pipelined<kScanFeat - kParked, 2, HSTATE, false>(a, f0 + kParked, 1, col, nf_hi, nf_hi, grad_hi);
-        update_rows_pipelined<kParked, 2, HSTATE, false>(a, f0, 1, col, nf_lo, nf_lo, grad_lo);
+        if (nf_hi)
+            update_rows_pipelined<kScanFeat - kParked, 2, HSTATE, false>(a, f0 + kParked * fstep, fstep, col, nf_hi,
+                                                                         nf_hi, grad_hi);
+        update_rows_pipelined<kParked, 2, HSTATE, false>(a, f0, fstep, col, nf_lo, nf_lo, grad_lo);
     }
 }
 
@@ -2205,14 +2220,22 @@ int32_t launch_ft_grad_scan(const FtGradArgs& a, const FtBlockScan& s, hipStream
     const uint64_t grid = (pairs + kNumXcd - 1) / kNumXcd * kNumXcd * geom.n_groups;
     if (grid > 0) {
         const uint32_t g = (uint32_t)grid, t = kScanWaves * 64;
-        if (a.dft16 && a.m16)
-            ft_grad_scan_kernel<true, true><<<g, t, 0, stream>>>(a, s, geom);
-        else if (a.dft16)
-            ft_grad_scan_kernel<true, false><<<g, t, 0, stream>>>(a, s, geom);
-        else if (a.m16)
-            ft_grad_scan_kernel<false, true><<<g, t, 0, stream>>>(a, s, geom);
+#define TATARA_SCAN(D)                                                                  \
+    do {                                                                                \
+        if (a.dft16 && a.m16)                                                           \
+            ft_grad_scan_kernel<true, true, D><<<g, t, 0, stream>>>(a, s, geom);        \
+        else if (a.dft16)                                                               \
+            ft_grad_scan_kernel<true, false, D><<<g, t, 0, stream>>>(a, s, geom);       \
+        else if (a.m16)                                                                 \
+            ft_grad_scan_kernel<false, true, D><<<g, t, 0, stream>>>(a, s, geom);       \
+        else                                                                            \
+            ft_grad_scan_kernel<false, false, D><<<g, t, 0, stream>>>(a, s, geom);      \
+    } while (0)
+        if (s.dealt)
+            TATARA_SCAN(true);
         else
-            ft_grad_scan_kernel<false, false><<<g, t, 0, stream>>>(a, s, geom);
+            TATARA_SCAN(false);
+#undef TATARA_SCAN
         TATARA_LAUNCHED("ft_grad_scan");
     }
     if (!fallback) return kOk;
@@ -2230,6 +2253,7 @@ int32_t launch_ft_grad_mfma(const FtGradArgs& a, const FtBlockScan& s, hipStream
     TATARA_REQUIRE(a.ft_out % 4 == 0 && a.rows == s.cols, "mfma backward: shapes");
     TATARA_REQUIRE(moment_scales_ok(a), "f16 moment scales must be powers of two");
     TATARA_REQUIRE(s.n_blocks <= 128, "mfma backward: at most 128 king blocks");
+    TATARA_REQUIRE(!s.dealt, "mfma backward: stage tables with contiguous waves");
     const ScanGeom geom = scan_geom(s.piece_inputs);
     TATARA_REQUIRE(geom.group_size <= 128, "mfma backward: at most 128 features per group");
     const uint64_t pairs = (uint64_t)ceil_div(a.ft_out, kDftChunk) * s.n_blocks;

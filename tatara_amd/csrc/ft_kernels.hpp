@@ -123,6 +123,10 @@ struct FtBlockScan {
     // optional: also set (and never cleared by the kernels) with *multi, for
     // a batch whose caller said its rows are king-blocked
     uint32_t* multi_sticky;
+    // the tables deal a feature group to the block scan's waves round-robin
+    // (feature i of a group to wave i % 8) instead of in runs of 16; the
+    // matrix-core form needs the runs
+    uint32_t dealt;
 };
 
 // Columns per dft chunk in the chunk-major layout (one wave of float4 lanes).

@@ -353,6 +353,7 @@ static int32_t ft_weight_grad_blocked(const float* dft, const uint16_t* dft16, f
     sc.cols = cols;
     sc.piece_inputs = piece_inputs;
     sc.n_blocks = n_blocks;
+    sc.dealt = mfma ? 0u : 1u;
     if ((st = launch_ft_scan_tables(sc, 0))) return st;
     // occurrence lists for the fallback (a row with features of two blocks)
     const uint64_t n_items = two_b * max_active;

@@ -350,6 +350,7 @@ class SimpleTrainer final : public TrainerBase {
         sc.piece_inputs = pi;
         sc.n_blocks = n_king_bins;
         sc.multi_sticky = batch_king_blocked ? kb_broken_dev : nullptr;
+        sc.dealt = 1;
         return sc;
     }
 

@@ -459,6 +459,7 @@ class LayerStackTrainer final : public TrainerBase {
         sc.piece_inputs = pi;
         sc.n_blocks = n_king_bins;
         sc.multi_sticky = batch_king_blocked ? kb_broken_dev : nullptr;
+        sc.dealt = h_out ? 0u : 1u;  // the matrix-core form reads runs of 16
         return sc;
     }
 
