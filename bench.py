@@ -650,40 +650,49 @@ def make_trainer(w: dict, spec: dict, b: int):
 def other_workloads(names: list, b: int, steps: int, warmup: int, n_batches: int = 2) -> dict:
     """The other BASELINE workloads, measured the way `value` is: resident
     GPU-decoded batches cycled, warm-up steps, then `steps` timed steps
-    bracketed by device synchronisations (host wall clock)."""
+    bracketed by device synchronisations (host wall clock).  A workload
+    that fails is reported with its error; the headline line still prints."""
+    out = {}
+    for name in names:
+        try:
+            out[name] = one_workload(name, b, steps, warmup, n_batches)
+        except Exception as e:  # noqa: BLE001 - a secondary figure must not cost the headline line
+            out[name] = {"value": None, "error": repr(e)}
+            log(f"{name}: {e!r}")
+    return out
+
+
+def one_workload(name: str, b: int, steps: int, warmup: int, n_batches: int) -> dict:
+    """Resident-batch throughput of one workload (see other_workloads)."""
     from tatara_amd import _lib
     from tatara_amd.dataloader import ProgressWeights, feature_set_info, psv_to_device_batch
     from tatara_amd.psv import synthetic_progress_weights, synthetic_psv
 
     lib = _lib.load()
-    out = {}
-    for name in names:
-        w = WORKLOADS[name]
-        info = feature_set_info(w["spec"])
-        spec = dict(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"])
-        pw = ProgressWeights(synthetic_progress_weights(seed=7)) if w["bucket_mode"] == "progress8kpabs" else None
-        dev = [psv_to_device_batch(synthetic_psv(b, seed=1000 + i), w["spec"], w["bucket_mode"], w["nb"], pw)
-               for i in range(n_batches)]
-        _, trainer, _, step = make_trainer(w, spec, b)
-        with trainer as t:
-            for i in range(warmup):
-                step(t, dev[i % len(dev)])
-            t.flush_pending_loss()
-            _lib.check(lib.tatara_synchronize())
-            t0 = time.perf_counter()
-            for i in range(steps):
-                step(t, dev[i % len(dev)])
-            t.flush_pending_loss()
-            _lib.check(lib.tatara_synchronize())
-            elapsed = time.perf_counter() - t0
-        del dev
-        pos_s = b * steps / elapsed
-        out[name] = {"value": round(pos_s, 1), "unit": "pos/s", "ms_per_step": round(1000.0 * elapsed / steps, 4),
-                     "steps": steps, "warmup": warmup, "vs_baseline": round(pos_s / w["ref"], 4),
-                     "vs_baseline_ref": f"RTX 5090 {w['ref'] / 1e6:.2f}M pos/s (reference {w['ref_src']})",
-                     "dtype": "f16+f32" if w.get("all_optim") else "f32", "workload": w["desc"]}
-        log(f"{name}: {pos_s:,.0f} pos/s ({1000.0 * elapsed / steps:.3f} ms/step)")
-    return out
+    w = WORKLOADS[name]
+    info = feature_set_info(w["spec"])
+    spec = dict(ft_in=info["ft_in"], max_active=info["max_active"], piece_inputs=info["piece_inputs"])
+    pw = ProgressWeights(synthetic_progress_weights(seed=7)) if w["bucket_mode"] == "progress8kpabs" else None
+    dev = [psv_to_device_batch(synthetic_psv(b, seed=1000 + i), w["spec"], w["bucket_mode"], w["nb"], pw)
+           for i in range(n_batches)]
+    _, trainer, _, step = make_trainer(w, spec, b)
+    with trainer as t:
+        for i in range(warmup):
+            step(t, dev[i % len(dev)])
+        t.flush_pending_loss()
+        _lib.check(lib.tatara_synchronize())
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(t, dev[i % len(dev)])
+        t.flush_pending_loss()
+        _lib.check(lib.tatara_synchronize())
+        elapsed = time.perf_counter() - t0
+    pos_s = b * steps / elapsed
+    log(f"{name}: {pos_s:,.0f} pos/s ({1000.0 * elapsed / steps:.3f} ms/step)")
+    return {"value": round(pos_s, 1), "unit": "pos/s", "ms_per_step": round(1000.0 * elapsed / steps, 4),
+            "steps": steps, "warmup": warmup, "vs_baseline": round(pos_s / w["ref"], 4),
+            "vs_baseline_ref": f"RTX 5090 {w['ref'] / 1e6:.2f}M pos/s (reference {w['ref_src']})",
+            "dtype": "f16+f32" if w.get("all_optim") else "f32", "workload": w["desc"]}
 
 
 def git_commit() -> str:
