@@ -1132,8 +1132,9 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
 // bit.
 //
 // A workgroup owns one 256-column chunk and a group of GS features of one
-// block (wave w: features g*GS + 16w .. +15 of the block, accumulated in
-// registers, four columns per lane).  It stages each row's chunk in LDS once
+// block (wave w: 16 of them, accumulated in registers, four columns per
+// lane: features g*GS + 16w .. +15, or g*GS + w + 8k when the tables deal
+// the group round-robin, FtBlockScan::dealt).  It stages each row's chunk in LDS once
 // (a dft row is read once per group instead of once per occurrence) and
 // every wave adds it to those of its features whose bit is set in the row's
 // hit mask.  Per stage of 32 rows a wave reads 16 feature masks (bit r: the
@@ -1147,7 +1148,7 @@ __global__ __launch_bounds__(256) void ft_grad_update_kernel(FtGradArgs a, uint3
 // of its 32 slots (perspective * batch + position; slots past the block's
 // list repeat its last row) and, for mask word q = g*W + w and feature k,
 // a slot mask whose bit r is set when slot r's row holds block feature
-// g*GS + 16w + k.  A row with a feature outside its own block, or with one
+// g*GS + 16w + k (dealt: g*GS + w + 8k).  A row with a feature outside its own block, or with one
 // feature in two slots, sets *multi; the scan then leaves the step to the
 // occurrence-list kernel, which runs only in that case.
 // ---------------------------------------------------------------------------
